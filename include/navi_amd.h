@@ -1,0 +1,168 @@
+/*
+ * navi_amd.h - the C ABI between navi-tts's C++ host (Device, DeviceWeights,
+ * KvCache/Talker, Frame, Vocoder) and this library's gfx950 kernels.
+ *
+ * The reference has no FFI: its boundary is the pimpl `Impl` behind each C++
+ * class, which calls HIP directly. Each entry point below replaces one of those
+ * Impl operations (cited per function); the C++ classes in
+ * navi-tts_amd/csrc/host keep the reference's public signatures and call these.
+ *
+ * Conventions
+ *  - Plain C types only: opaque handles, pointers and sizes. Device buffers are
+ *    `void *` / typed device pointers that the caller owns unless stated.
+ *  - Every call returns a navi_status; no C++ exception crosses the ABI.
+ *    Functions taking (char *err, size_t errlen) write a NUL-terminated
+ *    message on failure (errlen may be 0).
+ *  - One host thread drives one handle at a time; all work is ordered on the
+ *    library's stream for the current device (runtime/device/device.cpp:96-97),
+ *    and every call that returns results to the host is synchronous on return.
+ */
+#ifndef NAVI_AMD_H
+#define NAVI_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define NAVI_AMD_ABI_VERSION 1
+
+typedef enum {
+    NAVI_OK = 0,
+    NAVI_ERR_TIMEOUT = 1,        /* a dataflow wait hit its spin cap (frame.hip:673 "timed out") */
+    NAVI_ERR_LAUNCH = 2,         /* cooperative launch refused (frame.hip:664) */
+    NAVI_ERR_KV_FULL = 3,        /* n_past >= max_pos (frame.hip:800) */
+    NAVI_ERR_INVALID = 4,        /* bad argument / shape / missing tensor */
+    NAVI_ERR_HIP = 5,            /* a HIP runtime call failed */
+    NAVI_ERR_UNSUPPORTED = 6     /* model shape or device this build does not run */
+} navi_status;
+
+/* ---- device (runtime/device/device.h:100-123) ---------------------------- */
+
+typedef struct {
+    int32_t index;
+    char    name[64];
+    char    arch[32];                 /* gcnArchName without feature suffix, e.g. "gfx950" */
+    int32_t multiprocessors;          /* CUs on CDNA */
+    int32_t warp_size;                /* 64 */
+    int32_t cooperative_launch;
+    int32_t max_threads_per_block;
+    uint64_t lds_per_block;
+    int32_t clock_khz, mem_clock_khz, mem_bus_width;
+    uint64_t vram_total, vram_free, l2_bytes;
+    int32_t hip_runtime_version;
+} navi_device_info;
+
+/* Device::open (device.cpp:77-108): first visible gfx950 GPU, made current,
+ * spin scheduling, one non-blocking stream owned by the library. */
+navi_status navi_device_open(navi_device_info *out, char *err, size_t errlen);
+/* The library stream (hipStream_t) for callers that enqueue their own work. */
+void *navi_device_stream(void);
+navi_status navi_device_synchronize(void);
+const char *navi_build_arch(void);    /* the offload arch the kernels were built for */
+
+/* ---- device memory (DeviceWeights arena, device_weights.cpp:245-299; Impl::alloc) */
+
+navi_status navi_mem_alloc(void **dptr, size_t bytes);   /* zero-filled */
+navi_status navi_mem_free(void *dptr);
+navi_status navi_mem_h2d(void *dst, const void *src, size_t bytes);
+navi_status navi_mem_d2h(void *dst, const void *src, size_t bytes);
+navi_status navi_mem_d2d(void *dst, const void *src, size_t bytes);
+navi_status navi_mem_zero(void *dptr, size_t bytes);
+
+/* ---- model description ----------------------------------------------------- */
+
+typedef struct {                       /* params.h:16-27 TransformerParams */
+    int32_t hidden, n_layer, n_head, n_kv_head, head_dim, ff, vocab;
+    float   rms_eps;
+    double  rope_theta;
+} navi_xformer_params;
+
+typedef struct {                       /* the fields of params.h:29-73 the path reads */
+    navi_xformer_params talker, cp;
+    int32_t n_code_groups;             /* 16 */
+    int32_t codec_eos_id;              /* 2050 */
+    int32_t text_hidden, text_vocab;   /* 2048, 151936 */
+    int32_t tts_bos_id, tts_eos_id, tts_pad_id;
+    int32_t codec_bos_id, codec_pad_id, codec_think_id, codec_nothink_id, codec_think_bos_id, codec_think_eos_id;
+} navi_model_params;
+
+typedef enum { NAVI_DT_F32 = 0, NAVI_DT_F16 = 1, NAVI_DT_BF16 = 2, NAVI_DT_I32 = 3, NAVI_DT_U8 = 4 } navi_dtype;
+
+/* One device-resident weight (DeviceTensor, device_weights.h:17-21): the C
+ * stand-in for DeviceWeights::get(name). Shapes are checked by each create(). */
+typedef struct {
+    const char *name;
+    const void *ptr;
+    int32_t     dtype;                 /* navi_dtype */
+    int32_t     ndim;
+    uint64_t    dims[4];
+} navi_tensor_ref;
+
+/* KV cache view (talker.h:20-24): per layer [max_pos][kv_dim] f16, caller-owned. */
+typedef struct {
+    int32_t   n_layer, max_pos, kv_dim;
+    uint16_t *const *k;
+    uint16_t *const *v;
+} navi_kv_view;
+
+/* ---- frame: talker step + cb0 sampling + code predictor (frame.h:24-71) ---- */
+
+typedef struct {                       /* frame.h:24-31 */
+    float   temperature;               /* <= 0: greedy */
+    int32_t top_k;
+    float   repetition_penalty;        /* <= 0: off */
+    float   cp_temperature;
+    int32_t cp_top_k;
+    int32_t min_frames;
+} navi_sampling;
+
+typedef struct {                       /* frame.h:33-36 */
+    int32_t  blocks_per_mp;            /* must be 1: one persistent block per CU */
+    uint64_t spin_cap;                 /* polls per wait before the frame is failed; 0 = default */
+} navi_frame_options;
+
+typedef struct {                       /* frame.h:38-44 */
+    int32_t ok;
+    int32_t eos;                       /* codes[0] == codec_eos */
+    int32_t codes[16];
+    double  us;                        /* device time of the launch (hipEvent) */
+    int32_t status;                    /* navi_status */
+    char    error[160];
+} navi_frame_result;
+
+typedef struct navi_frame navi_frame;
+
+/* Frame::create (frame.hip:684-774): binds weights by tensor name, allocates
+ * the work buffers, sizes the persistent grid (one block per CU). */
+navi_status navi_frame_create(const navi_model_params *p, const navi_tensor_ref *tensors, int32_t n_tensors,
+                              const navi_frame_options *opt, navi_frame **out, char *err, size_t errlen);
+void navi_frame_destroy(navi_frame *f);
+/* Frame::reset (frame.hip:783-785): clears the repetition set. */
+navi_status navi_frame_reset(navi_frame *f);
+/* Frame::run_first / Frame::run (frame.hip:787-810) with Impl::launch (653-681).
+ * skip_talker != 0: frame 0 from the prefill's post-norm hidden and logits
+ * (kv may be NULL); else a talker step on the previous frame's step embedding at
+ * position n_past (writes KV row n_past; the caller sets n_used = n_past + 1). */
+navi_status navi_frame_run(navi_frame *f, const navi_kv_view *kv, int32_t n_past, int32_t skip_talker,
+                           const float *d_hidden, const float *d_logits, const float *d_trailing,
+                           const navi_sampling *s, uint64_t seed, int32_t frame_index, navi_frame_result *out);
+/* Frame::d_step_out (frame.hip:812): next frame's step embedding, f32[hidden]. */
+float *navi_frame_step_out(navi_frame *f);
+int32_t navi_frame_grid_blocks(const navi_frame *f);
+int32_t navi_frame_occupancy_per_mp(const navi_frame *f);
+/* Test/diagnostic taps (no reference counterpart; off unless enabled): the talker's
+ * post-norm hidden f32[hidden], its logits f32[vocab] and the 15 cp logit rows
+ * f32[15][cp vocab] of the last frame run with taps on. */
+navi_status navi_frame_set_taps(navi_frame *f, int32_t enabled);
+const float *navi_frame_tap_hidden(const navi_frame *f);
+const float *navi_frame_tap_logits(const navi_frame *f);
+const float *navi_frame_tap_cp_logits(const navi_frame *f);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NAVI_AMD_H */

@@ -1,0 +1,83 @@
+// Device helpers shared by the gfx950 kernels: wave64 reductions, f16 unpacking
+// and the tagged-word mailboxes the persistent frame kernel communicates through.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace navi_amd {
+
+constexpr int WAVE = 64;
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, WAVE);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, WAVE));
+    return v;
+}
+
+__device__ __forceinline__ float h2f(uint16_t h) {
+    _Float16 f;
+    __builtin_memcpy(&f, &h, 2);
+    return static_cast<float>(f);
+}
+
+__device__ __forceinline__ uint16_t f2h(float v) {
+    const _Float16 h = static_cast<_Float16>(v);
+    uint16_t u;
+    __builtin_memcpy(&u, &h, 2);
+    return u;
+}
+
+// f32 -> f16 -> f32: the value a K/V cache entry holds.
+__device__ __forceinline__ float round_f16(float v) { return static_cast<float>(static_cast<_Float16>(v)); }
+
+// acc + sum_i w[i] * x[i] over one 16-byte weight fragment (8 f16), left to right.
+__device__ __forceinline__ float dot8(const uint4 w, const float *x, float acc) {
+    half8_t h;
+    __builtin_memcpy(&h, &w, 16);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc = fmaf(static_cast<float>(h[i]), x[i], acc);
+    return acc;
+}
+
+__device__ __forceinline__ uint4 ldg16(const uint16_t *p) { return *reinterpret_cast<const uint4 *>(p); }
+
+// ---------------------------------------------------------------------------
+// Tagged mailboxes. A 64-bit word holds {f32 value (low), u32 tag (high)} and
+// is written and read with device-scope relaxed atomics, which compile to
+// plain global stores/loads with the sc1 bit on gfx950: coherent across the
+// eight XCDs' L2s without any fence or cache flush. A consumer accepts a word
+// only when its tag is the tag of the phase it waits for, so the data and its
+// readiness travel in one store and one load.
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ void mb_put(uint64_t *p, float v, uint32_t tag) {
+    const uint64_t w = (static_cast<uint64_t>(tag) << 32) | __float_as_uint(v);
+    __hip_atomic_store(p, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ uint64_t mb_peek(uint64_t *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ uint32_t ctl_peek(uint32_t *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ void ctl_put(uint32_t *p, uint32_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ uint32_t tag_of(uint64_t w) { return static_cast<uint32_t>(w >> 32); }
+__device__ __forceinline__ float val_of(uint64_t w) { return __uint_as_float(static_cast<uint32_t>(w)); }
+
+} // namespace navi_amd

@@ -1,0 +1,1170 @@
+// The per-frame token loop on gfx950: talker decode step at n_past -> codebook-0
+// sampling -> 16-position code-predictor pass with 15 sampled codebooks ->
+// next step embedding, in one persistent cooperative launch.
+//
+// Replaces k_frame and its phases (model/qwen3tts/frame.hip:85-579) and the
+// host side of Frame (frame.hip:590-810). MI355X design:
+//
+//  * Grid: one 512-thread block (8 wave64s) per CU, 256 blocks. Every matrix
+//    is partitioned into fixed per-block row slices (q/k/v 16 rows, o 4, gate+up
+//    12+12, down 4, talker head 12, cp lm_head 8) so each block streams the same
+//    slice of every layer, and the slice of the NEXT layer for a phase is loaded
+//    into registers as soon as the current one has been consumed.
+//  * No grid barriers. Every activation vector is published as 64-bit tagged
+//    words {f32, u32 epoch} with device-scope relaxed stores; each consumer
+//    polls exactly the words it needs. A hop costs one store and one load
+//    instead of a barrier's fence + atomic + poll + data load.
+//  * Sampling (greedy argmax or exact top-k + PCG32 draw) runs redundantly in
+//    every block on identical inputs, so the sampled code never costs a hop.
+//  * Code-predictor positions 0 and 1 run as one 2-row pass (15 weight passes
+//    instead of 16); each attention block keeps its kv head's cp K/V in LDS.
+//  * Every wait has a spin cap; the first block to exceed it stamps the
+//    launch's epoch into the abort word and every other wait gives up, so a
+//    frame fails with "timed out" instead of hanging (frame.hip:78-99 contract).
+#include "dev_common.h"
+#include "host_util.h"
+
+#include <cmath>
+#include <cstring>
+#include <string>
+#include <vector>
+
+namespace navi_amd {
+namespace fk {
+
+constexpr int NB = 256, BT = 256, NW = BT / WAVE;   // one block per CU, one wave per SIMD
+constexpr int H = 1024, NH = 16, NKV = 8, HD = 128, FF = 3072, VT = 3072, VC = 2048;
+constexpr int QD = NH * HD, KVD = NKV * HD, QKV = QD + 2 * KVD;
+constexpr int NCB = 16, CPH = NCB - 1, GRP = NH / NKV;
+constexpr int MAX_TL = 32, MAX_CL = 5;
+constexpr int MAX_POS = 4096;          // talker KV positions the score buffer holds
+constexpr int VCH = 64;                // V rows staged in LDS per chunk
+constexpr float ATT_SCALE = 0.08838834764831845f;   // 1/sqrt(128)
+
+static_assert(QKV / NB == 4 * NW, "q/k/v: 4 rows per wave");
+static_assert(H / NB == NW, "o/down: 1 row per wave");
+static_assert(2 * FF / NB == 6 * NW, "gate+up: 6 rows per wave");
+static_assert(VT / NB == 3 * NW, "talker head: 3 rows per wave");
+static_assert(VC / NB == 2 * NW, "cp head: 2 rows per wave");
+
+// mailbox layout, in 64-bit words
+constexpr int MB_X = 0, MB_QKV = MB_X + 2 * H, MB_ATT = MB_QKV + 2 * QKV, MB_X2 = MB_ATT + 2 * QD,
+              MB_H = MB_X2 + 2 * H, MB_LG = MB_H + 2 * FF, MB_WORDS = MB_LG + VT;
+constexpr uint32_t EPOCH_STRIDE = 4096;   // > tags used by one launch
+
+struct LayerPtrs {
+    const uint16_t *wq, *wk, *wv, *wo, *wg, *wu, *wd;
+    const float *ln1, *ln2, *qn, *kn;
+};
+
+struct Weights {
+    LayerPtrs tl[MAX_TL];
+    LayerPtrs cp[MAX_CL];
+    const float *tl_norm, *cp_norm;
+    const uint16_t *codec_head, *codec_emb;
+    const uint16_t *cp_emb[CPH], *lm_head[CPH];
+    float invf_t[HD / 2], invf_c[HD / 2];
+    float eps_t, eps_c;
+};
+
+struct Args {
+    const Weights *W;
+    uint64_t *mb;
+    uint32_t *abort_word;
+    int32_t *codes_out;
+    uint16_t *const *kc, *const *vc;   // per talker layer, device arrays
+    int n_tl, n_cl, n_past, skip_talker;
+    const float *hidden_in, *logits_in, *step_in, *trailing;
+    float *step_out;
+    uint8_t *seen;
+    float temperature, rep_penalty, cp_temperature;
+    int top_k, cp_top_k, min_frames, frame_index, eos_id, suppress_from;
+    uint64_t talker_seed, cp_seed, spin_cap;
+    uint32_t epoch;
+    float *tap_hidden, *tap_logits, *tap_cp_logits;
+};
+
+// This block's slice of one layer (and of the heads), 160 registers per lane:
+// with one wave per SIMD the unified VGPR/AGPR file holds it without scratch.
+struct Regs {
+    uint4 qkv[4][2];   // [row][512-col chunk]
+    uint4 o[4];
+    uint4 gu[6][2];
+    uint4 dn[6];
+    uint4 th[3][2];    // talker head rows
+    uint4 lm[2][2];    // cp lm head rows
+};
+
+struct Smem {
+    float x[2][H];                  // residual stream rows
+    float xn[2][H];                 // normed rows
+    union {
+        float big[2 * FF];          // att [T][QD] | h [T][FF]
+        struct { float lg[VT]; int idx[VT]; } samp;
+        uint16_t vch[VCH][HD];      // V rows staged for the output sum
+    } u;
+    float part[2][6 * NW];          // gate/up dots before SiLU(g)*u
+    float red[4 * NW];
+    float q[2][HD], k[2][HD], v[2][HD];
+    float sc[MAX_POS];              // attention probabilities
+    float opart[NW][HD];
+    uint16_t ckv[2][MAX_CL][NCB][HD];   // this block's cp K/V (kv head blockIdx/2)
+    unsigned hist[256];
+    int isel[4];
+    int codes[NCB];
+    int fail;
+};
+
+__device__ __forceinline__ int tid() { return static_cast<int>(threadIdx.x); }
+__device__ __forceinline__ int lane() { return static_cast<int>(threadIdx.x) & (WAVE - 1); }
+__device__ __forceinline__ int wave() { return static_cast<int>(threadIdx.x) / WAVE; }
+__device__ __forceinline__ int blk() { return static_cast<int>(blockIdx.x); }
+
+// ---- block reductions (fixed order: every block gets bit-identical results) ----
+
+__device__ __forceinline__ float block_sum(float v, Smem &S) {
+    v = wave_sum(v);
+    if (lane() == 0) S.red[wave()] = v;
+    __syncthreads();
+    float r = 0.f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) r += S.red[w];
+    __syncthreads();
+    return r;
+}
+
+__device__ __forceinline__ float block_max(float v, Smem &S) {
+    v = wave_max(v);
+    if (lane() == 0) S.red[wave()] = v;
+    __syncthreads();
+    float r = S.red[0];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) r = fmaxf(r, S.red[w]);
+    __syncthreads();
+    return r;
+}
+
+// ---- waits ----------------------------------------------------------------
+
+__device__ __forceinline__ bool aborted(const Args &a) { return ctl_peek(a.abort_word) == a.epoch; }
+
+// Polls one word until it carries `tag`; false on spin cap or abort.
+__device__ __forceinline__ bool poll_word(const Args &a, uint64_t *p, uint32_t tag, uint64_t &w) {
+    uint64_t spins = 0;
+    while (tag_of(w) != tag) {
+        if (++spins >= a.spin_cap || ((spins & 63u) == 0 && aborted(a))) {
+            ctl_put(a.abort_word, a.epoch);
+            return false;
+        }
+        w = mb_peek(p);
+    }
+    return true;
+}
+
+// Block-wide: N tagged words at mailbox offset `off` -> dst (LDS f32). Uniform result.
+template <int N>
+__device__ __forceinline__ bool gather(const Args &a, int off, uint32_t tag, float *dst, Smem &S) {
+    static_assert(N % BT == 0, "gather size");
+    constexpr int PER = N / BT;
+    uint64_t w[PER];
+#pragma unroll
+    for (int k = 0; k < PER; ++k) w[k] = mb_peek(a.mb + off + tid() + k * BT);
+    bool ok = true;
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+        const int i = tid() + k * BT;
+        if (ok) ok = poll_word(a, a.mb + off + i, tag, w[k]);
+        dst[i] = val_of(w[k]);
+    }
+    if (!ok) S.fail = 1;
+    __syncthreads();
+    return S.fail == 0;
+}
+
+// T rows of N words each (row stride N in the mailbox and in dst), one row at a time.
+template <int T, int N>
+__device__ __forceinline__ bool gather_rows(const Args &a, int off, uint32_t tag, float *dst, Smem &S) {
+#pragma unroll
+    for (int t = 0; t < T; ++t)
+        if (!gather<N>(a, off + t * N, tag, dst + t * N, S)) return false;
+    return true;
+}
+
+// ---- RMSNorm of T rows (every block, redundantly) ---------------------------
+
+template <int T>
+__device__ __forceinline__ void rmsnorm_rows(const float (*x)[H], const float *w, float eps, float (*out)[H], Smem &S) {
+    constexpr int PER = H / BT;
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+        float e[PER], ss = 0.f;
+#pragma unroll
+        for (int k = 0; k < PER; ++k) { e[k] = x[t][tid() + k * BT]; ss = fmaf(e[k], e[k], ss); }
+        ss = block_sum(ss, S);
+        const float sc = rsqrtf(ss / static_cast<float>(H) + eps);
+#pragma unroll
+        for (int k = 0; k < PER; ++k) out[t][tid() + k * BT] = e[k] * sc * w[tid() + k * BT];
+    }
+    __syncthreads();
+}
+
+// x fragment a lane multiplies with 512-col chunks: cols base + c*512 + lane*8 .. +8
+template <int NC>
+__device__ __forceinline__ void xfrag(const float *x, int base, float (&xf)[NC][8]) {
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        const float4 p = *reinterpret_cast<const float4 *>(x + base + c * 512 + lane() * 8);
+        const float4 q = *reinterpret_cast<const float4 *>(x + base + c * 512 + lane() * 8 + 4);
+        xf[c][0] = p.x; xf[c][1] = p.y; xf[c][2] = p.z; xf[c][3] = p.w;
+        xf[c][4] = q.x; xf[c][5] = q.y; xf[c][6] = q.z; xf[c][7] = q.w;
+    }
+}
+
+// ---- weight prefetch: this block's slice of one layer -----------------------
+
+__device__ __forceinline__ void load_qkv(Regs &R, const LayerPtrs &L) {
+    const int rb = blk() * (QKV / NB);
+    const uint16_t *M;
+    int base;
+    if (rb < QD) { M = L.wq; base = rb; }
+    else if (rb < QD + KVD) { M = L.wk; base = rb - QD; }
+    else { M = L.wv; base = rb - QD - KVD; }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const uint16_t *p = M + static_cast<size_t>(base + wave() * 4 + r) * H + lane() * 8;
+        R.qkv[r][0] = ldg16(p);
+        R.qkv[r][1] = ldg16(p + 512);
+    }
+}
+
+__device__ __forceinline__ void load_o(Regs &R, const LayerPtrs &L) {
+    const uint16_t *p = L.wo + static_cast<size_t>(blk() * (H / NB) + wave()) * QD + lane() * 8;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) R.o[c] = ldg16(p + c * 512);
+}
+
+__device__ __forceinline__ void load_gu(Regs &R, const LayerPtrs &L) {
+    constexpr int RB = FF / NB;   // 12 gate + 12 up rows per block
+#pragma unroll
+    for (int r = 0; r < 6; ++r) {
+        const int vr = wave() * 6 + r;
+        const uint16_t *M = vr < RB ? L.wg : L.wu;
+        const int row = blk() * RB + (vr < RB ? vr : vr - RB);
+        const uint16_t *p = M + static_cast<size_t>(row) * H + lane() * 8;
+        R.gu[r][0] = ldg16(p);
+        R.gu[r][1] = ldg16(p + 512);
+    }
+}
+
+__device__ __forceinline__ void load_dn(Regs &R, const LayerPtrs &L) {
+    const uint16_t *p = L.wd + static_cast<size_t>(blk() * (H / NB) + wave()) * FF + lane() * 8;
+#pragma unroll
+    for (int c = 0; c < 6; ++c) R.dn[c] = ldg16(p + c * 512);
+}
+
+__device__ __forceinline__ void load_th(Regs &R, const uint16_t *head) {
+#pragma unroll
+    for (int r = 0; r < 3; ++r) {
+        const uint16_t *p = head + static_cast<size_t>(blk() * (VT / NB) + wave() * 3 + r) * H + lane() * 8;
+        R.th[r][0] = ldg16(p);
+        R.th[r][1] = ldg16(p + 512);
+    }
+}
+
+__device__ __forceinline__ void load_lm(Regs &R, const uint16_t *head) {
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+        const uint16_t *p = head + static_cast<size_t>(blk() * (VC / NB) + wave() * 2 + r) * H + lane() * 8;
+        R.lm[r][0] = ldg16(p);
+        R.lm[r][1] = ldg16(p + 512);
+    }
+}
+
+// ---- matvec phases --------------------------------------------------------
+
+template <int T>
+__device__ __forceinline__ void qkv_phase(const Args &a, const Regs &R, Smem &S, uint32_t tag) {
+    const int row0 = blk() * (QKV / NB) + wave() * 4;
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+        float xf[2][8];
+        xfrag<2>(S.xn[t], 0, xf);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const float d = wave_sum(dot8(R.qkv[r][1], xf[1], dot8(R.qkv[r][0], xf[0], 0.f)));
+            if (lane() == r) mb_put(a.mb + MB_QKV + t * QKV + row0 + r, d, tag);
+        }
+    }
+}
+
+// x2[row] = x[row] + Wo . att  (att gathered into S.u.big as [T][QD])
+template <int T>
+__device__ __forceinline__ void o_phase(const Args &a, const Regs &R, Smem &S, uint32_t tag) {
+    const int row = blk() * (H / NB) + wave();
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+        float acc = 0.f;
+#pragma unroll
+        for (int c2 = 0; c2 < 4; c2 += 2) {
+            float xf[2][8];
+            xfrag<2>(S.u.big + t * QD, c2 * 512, xf);
+            acc = dot8(R.o[c2 + 1], xf[1], dot8(R.o[c2], xf[0], acc));
+        }
+        const float d = wave_sum(acc);
+        if (lane() == 0) mb_put(a.mb + MB_X2 + t * H + row, S.x[t][row] + d, tag);
+    }
+}
+
+// h[row] = silu(Wg . xn) * (Wu . xn)
+template <int T>
+__device__ __forceinline__ void gu_phase(const Args &a, const Regs &R, Smem &S, uint32_t tag) {
+    constexpr int RB = FF / NB;
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+        float xf[2][8];
+        xfrag<2>(S.xn[t], 0, xf);
+#pragma unroll
+        for (int r = 0; r < 6; ++r) {
+            const float d = wave_sum(dot8(R.gu[r][1], xf[1], dot8(R.gu[r][0], xf[0], 0.f)));
+            if (lane() == 0) S.part[t][wave() * 6 + r] = d;
+        }
+    }
+    __syncthreads();
+    if (tid() < RB * T) {
+        const int t = tid() / RB, j = tid() % RB;
+        const float g = S.part[t][j], u = S.part[t][RB + j];
+        mb_put(a.mb + MB_H + t * FF + blk() * RB + j, g / (1.f + expf(-g)) * u, tag);
+    }
+}
+
+// x[row] = x2[row] + Wd . h  (x2 in S.x, h gathered into S.u.big as [T][FF])
+template <int T>
+__device__ __forceinline__ void down_phase(const Args &a, const Regs &R, Smem &S, uint32_t tag) {
+    const int row = blk() * (H / NB) + wave();
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+        float acc = 0.f;
+#pragma unroll
+        for (int c2 = 0; c2 < 6; c2 += 2) {
+            float xf[2][8];
+            xfrag<2>(S.u.big + t * FF, c2 * 512, xf);
+            acc = dot8(R.dn[c2 + 1], xf[1], dot8(R.dn[c2], xf[0], acc));
+        }
+        const float d = wave_sum(acc);
+        if (lane() == 0) mb_put(a.mb + MB_X + t * H + row, S.x[t][row] + d, tag);
+    }
+}
+
+// ---- attention --------------------------------------------------------------
+
+// q/k head RMSNorm over 128 dims for nvec vectors, two at a time (waves 0-1 and 2-3).
+__device__ __forceinline__ void head_norms(float *const *vec, const float *const *w, int nvec, float eps, Smem &S) {
+    for (int v0 = 0; v0 < nvec; v0 += 2) {
+        const int vi = v0 + (wave() >> 1), d = tid() & (HD - 1);
+        float e = 0.f;
+        if (vi < nvec) e = vec[vi][d];
+        const float ps = wave_sum(e * e);
+        if (lane() == 0) S.red[wave()] = ps;
+        __syncthreads();
+        if (vi < nvec) {
+            const float ss = S.red[(wave() >> 1) * 2] + S.red[(wave() >> 1) * 2 + 1];
+            vec[vi][d] = e * rsqrtf(ss / static_cast<float>(HD) + eps) * w[vi][d];
+        }
+        __syncthreads();
+    }
+}
+
+__device__ __forceinline__ void rope_pair(float *v, int i, float c, float s) {
+    const float x0 = v[i], x1 = v[i + HD / 2];
+    v[i] = x0 * c - x1 * s;
+    v[i + HD / 2] = x0 * s + x1 * c;
+}
+
+// Waits for q head h and kv head g of T rows: S.q/S.k/S.v[t].
+template <int T>
+__device__ __forceinline__ bool gather_head(const Args &a, int h, int g, uint32_t tag, Smem &S) {
+    bool ok = true;
+    for (int i = tid(); i < T * 3 * HD; i += BT) {
+        const int t = i / (3 * HD), seg = (i % (3 * HD)) / HD, d = i % HD;
+        const int off = MB_QKV + t * QKV + (seg == 0 ? h * HD : seg == 1 ? QD + g * HD : QD + KVD + g * HD) + d;
+        uint64_t w = mb_peek(a.mb + off);
+        if (ok) ok = poll_word(a, a.mb + off, tag, w);
+        (seg == 0 ? S.q[t] : seg == 1 ? S.k[t] : S.v[t])[d] = val_of(w);
+    }
+    if (!ok) S.fail = 1;
+    __syncthreads();
+    return S.fail == 0;
+}
+
+// Talker attention for q head h = blockIdx (one row at position pos):
+// norms + RoPE + f16 K/V store (even heads) + softmax over keys 0..pos + V sum.
+__device__ bool talker_attention(const Args &a, const LayerPtrs &L, int il, uint32_t tag_qkv, uint32_t tag_att, Smem &S) {
+    const int h = blk(), g = h / GRP, pos = a.n_past;
+    const uint16_t *Kc = a.kc[il] + g * HD;
+    uint16_t *Vc = a.vc[il] + g * HD;
+    if (!gather_head<1>(a, h, g, tag_qkv, S)) return false;
+    {
+        float *const vec[2] = {S.q[0], S.k[0]};
+        const float *const w[2] = {L.qn, L.kn};
+        head_norms(vec, w, 2, a.W->eps_t, S);
+    }
+    if (tid() < HD) {
+        const int i = tid() & (HD / 2 - 1);
+        float s, c;
+        sincosf(static_cast<float>(pos) * a.W->invf_t[i], &s, &c);
+        if (tid() < HD / 2) {
+            rope_pair(S.q[0], i, c, s);
+        } else {
+            rope_pair(S.k[0], i, c, s);
+            const float k0 = round_f16(S.k[0][i]), k1 = round_f16(S.k[0][i + HD / 2]);
+            S.k[0][i] = k0;
+            S.k[0][i + HD / 2] = k1;
+            if ((h & 1) == 0) {
+                uint16_t *kw = a.kc[il] + static_cast<size_t>(pos) * KVD + g * HD;
+                kw[i] = f2h(k0);
+                kw[i + HD / 2] = f2h(k1);
+            }
+        }
+    } else {
+        const int d = tid() - HD;
+        const float v = round_f16(S.v[0][d]);
+        S.v[0][d] = v;
+        if ((h & 1) == 0) Vc[static_cast<size_t>(pos) * KVD + d] = f2h(v);
+    }
+    __syncthreads();
+    // scores: one key per thread per sweep
+    for (int jb = 0; jb <= pos; jb += BT) {
+        const int j = jb + tid();
+        if (j <= pos) {
+            float acc = 0.f;
+            if (j == pos) {
+#pragma unroll 8
+                for (int d = 0; d < HD; ++d) acc = fmaf(S.q[0][d], S.k[0][d], acc);
+            } else {
+                uint4 kk[16];
+#pragma unroll
+                for (int i = 0; i < 16; ++i) kk[i] = ldg16(Kc + static_cast<size_t>(j) * KVD + i * 8);
+#pragma unroll
+                for (int i = 0; i < 16; ++i) acc = dot8(kk[i], &S.q[0][i * 8], acc);
+            }
+            S.sc[j] = acc * ATT_SCALE;
+        }
+    }
+    __syncthreads();
+    float m = -INFINITY;
+    for (int j = tid(); j <= pos; j += BT) m = fmaxf(m, S.sc[j]);
+    m = block_max(m, S);
+    float sum = 0.f;
+    for (int j = tid(); j <= pos; j += BT) {
+        const float e = expf(S.sc[j] - m);
+        S.sc[j] = e;
+        sum += e;
+    }
+    sum = block_sum(sum, S);
+    const float inv = 1.f / sum;
+    for (int j = tid(); j <= pos; j += BT) S.sc[j] *= inv;
+    __syncthreads();
+    // output: wave w sums keys j = w mod NW; lane owns dims 2l, 2l+1
+    float acc0 = 0.f, acc1 = 0.f;
+    for (int c0 = 0; c0 <= pos; c0 += VCH) {
+        const int n = min(VCH, pos + 1 - c0);
+        for (int i = tid(); i < n * (HD / 8); i += BT) {
+            const int r = i / (HD / 8), q8 = (i % (HD / 8)) * 8, j = c0 + r;
+            uint4 val;
+            if (j < pos) {
+                val = ldg16(Vc + static_cast<size_t>(j) * KVD + q8);
+            } else {
+                uint16_t hv[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) hv[e] = f2h(S.v[0][q8 + e]);
+                __builtin_memcpy(&val, hv, 16);
+            }
+            *reinterpret_cast<uint4 *>(&S.u.vch[r][q8]) = val;
+        }
+        __syncthreads();
+        for (int r = wave(); r < n; r += NW) {
+            const float p = S.sc[c0 + r];
+            half2_t hv;
+            __builtin_memcpy(&hv, &S.u.vch[r][2 * lane()], 4);
+            acc0 = fmaf(p, static_cast<float>(hv[0]), acc0);
+            acc1 = fmaf(p, static_cast<float>(hv[1]), acc1);
+        }
+        __syncthreads();
+    }
+    S.opart[wave()][2 * lane()] = acc0;
+    S.opart[wave()][2 * lane() + 1] = acc1;
+    __syncthreads();
+    if (tid() < HD) {
+        float o = 0.f;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) o += S.opart[w][tid()];
+        mb_put(a.mb + MB_ATT + h * HD + tid(), o, tag_att);
+    }
+    return true;
+}
+
+// Code-predictor attention for q head h = blockIdx over T rows at positions p0..p0+T-1;
+// K/V of this block's kv head live in S.ckv for the whole frame.
+template <int T>
+__device__ bool cp_attention(const Args &a, const LayerPtrs &L, int il, int p0, uint32_t tag_qkv, uint32_t tag_att, Smem &S) {
+    const int h = blk(), g = h / GRP;
+    if (!gather_head<T>(a, h, g, tag_qkv, S)) return false;
+    {
+        float *const vec[4] = {S.q[0], S.k[0], S.q[T - 1], S.k[T - 1]};
+        const float *const w[4] = {L.qn, L.kn, L.qn, L.kn};
+        head_norms(vec, w, 2 * T, a.W->eps_c, S);
+    }
+    for (int i = tid(); i < T * HD; i += BT) {          // q and k pairs of each row
+        const int t = i / HD, isk = (i / (HD / 2)) & 1, pr = i & (HD / 2 - 1);
+        float s, c;
+        sincosf(static_cast<float>(p0 + t) * a.W->invf_c[pr], &s, &c);
+        if (!isk) {
+            rope_pair(S.q[t], pr, c, s);
+        } else {
+            rope_pair(S.k[t], pr, c, s);
+            S.ckv[0][il][p0 + t][pr] = f2h(S.k[t][pr]);
+            S.ckv[0][il][p0 + t][pr + HD / 2] = f2h(S.k[t][pr + HD / 2]);
+        }
+    }
+    for (int i = tid(); i < T * HD; i += BT) S.ckv[1][il][p0 + i / HD][i % HD] = f2h(S.v[i / HD][i % HD]);
+    __syncthreads();
+    // scores: wave w takes (row, key) pairs w, w+NW, ...
+    for (int pr = wave(); pr < T * NCB; pr += NW) {
+        const int t = pr / NCB, j = pr % NCB;
+        if (j > p0 + t) continue;
+        half2_t kk;
+        __builtin_memcpy(&kk, &S.ckv[0][il][j][2 * lane()], 4);
+        const float d = wave_sum(fmaf(S.q[t][2 * lane()], static_cast<float>(kk[0]), S.q[t][2 * lane() + 1] * static_cast<float>(kk[1])));
+        if (lane() == 0) S.sc[t * NCB + j] = d * ATT_SCALE;
+    }
+    __syncthreads();
+    if (wave() < T) {
+        const int t = wave(), n = p0 + t + 1;
+        const float s = lane() < n ? S.sc[t * NCB + lane()] : -INFINITY;
+        const float m = wave_max(s);
+        const float e = lane() < n ? expf(s - m) : 0.f;
+        const float inv = 1.f / wave_sum(e);
+        if (lane() < n) S.sc[t * NCB + lane()] = e * inv;
+    }
+    __syncthreads();
+    for (int i = tid(); i < T * HD; i += BT) {
+        const int t = i / HD, d = i % HD, n = p0 + t + 1;
+        float o = 0.f;
+        for (int j = 0; j < n; ++j) o = fmaf(S.sc[t * NCB + j], h2f(S.ckv[1][il][j][d]), o);
+        mb_put(a.mb + MB_ATT + t * QD + h * HD + d, o, tag_att);
+    }
+    return true;
+}
+
+// ---- sampling (block-wide; identical result in every block) ------------------
+
+__device__ __forceinline__ unsigned float_key(float f) {
+    const unsigned u = __float_as_uint(f);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float key_float(unsigned u) {
+    return __uint_as_float((u & 0x80000000u) ? (u & 0x7FFFFFFFu) : ~u);
+}
+
+__device__ __forceinline__ uint32_t pcg32_next(uint64_t &s) {
+    const uint64_t old = s;
+    s = old * 6364136223846793005ull + 1442695040888963407ull;
+    const uint32_t xs = static_cast<uint32_t>(((old >> 18u) ^ old) >> 27u);
+    const uint32_t rot = static_cast<uint32_t>(old >> 59u);
+    return (xs >> rot) | (xs << ((0u - rot) & 31u));
+}
+
+// Exact k-th largest of the PER values each thread holds: 4 passes of 8-bit
+// radix select over monotone keys (the value block_kth_largest computes).
+template <int PER>
+__device__ __forceinline__ float kth_largest(const float (&x)[PER], int k, Smem &S) {
+    unsigned prefix = 0, mask = 0;
+    int need = k;
+    for (int pass = 3; pass >= 0; --pass) {
+        const int shift = pass * 8;
+        S.hist[tid()] = 0;
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const unsigned key = float_key(x[i]);
+            if ((key & mask) == prefix) atomicAdd(&S.hist[(key >> shift) & 0xFFu], 1u);
+        }
+        __syncthreads();
+        if (wave() == 0) {
+            // lane l owns digits 255-4l .. 252-4l (descending)
+            int c[4], tot = 0;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) { c[j] = static_cast<int>(S.hist[255 - 4 * lane() - j]); tot += c[j]; }
+            int incl = tot;
+#pragma unroll
+            for (int o = 1; o < WAVE; o <<= 1) {
+                const int v = __shfl_up(incl, o, WAVE);
+                if (lane() >= o) incl += v;
+            }
+            int above = incl - tot;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                if (above < need && above + c[j] >= need) { S.isel[0] = 255 - 4 * lane() - j; S.isel[1] = need - above; }
+                above += c[j];
+            }
+        }
+        __syncthreads();
+        need = S.isel[1];
+        prefix |= static_cast<unsigned>(S.isel[0]) << shift;
+        mask |= 0xFFu << shift;
+        __syncthreads();
+    }
+    return key_float(prefix);
+}
+
+// Chooses an index from the V values in S.u.samp.lg (already modified for the talker).
+// Greedy: argmax, lowest index on ties. Else: /temperature, exact top-k threshold
+// (values >= the k-th largest survive), e^(v - max), PCG32 draw over the survivors
+// in index order (frame.hip:258-296 semantics: f32 running sum, no contraction).
+template <int V>
+__device__ __forceinline__ int block_sample(float temperature, int top_k, uint64_t seed, Smem &S) {
+    constexpr int PER = V / BT;
+    float x[PER];
+    const int base = tid() * PER;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) x[i] = S.u.samp.lg[base + i];
+    __syncthreads();
+    if (temperature <= 0.f) {
+        float bv = -INFINITY;
+        int bi = 0;
+#pragma unroll
+        for (int i = 0; i < PER; ++i) if (x[i] > bv || (x[i] == bv && base + i < bi)) { bv = x[i]; bi = base + i; }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+            const float ov = __shfl_xor(bv, o, WAVE);
+            const int oi = __shfl_xor(bi, o, WAVE);
+            if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+        }
+        if (lane() == 0) { S.red[wave()] = bv; S.u.samp.idx[wave()] = bi; }
+        __syncthreads();
+        if (tid() == 0) {
+            float v = S.red[0];
+            int i0 = S.u.samp.idx[0];
+            for (int w = 1; w < NW; ++w)
+                if (S.red[w] > v || (S.red[w] == v && S.u.samp.idx[w] < i0)) { v = S.red[w]; i0 = S.u.samp.idx[w]; }
+            S.isel[2] = i0;
+        }
+        __syncthreads();
+        const int r = S.isel[2];
+        __syncthreads();
+        return r;
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) { x[i] = x[i] / temperature; mx = fmaxf(mx, x[i]); }
+    mx = block_max(mx, S);
+    const float thr = (top_k > 0 && top_k < V) ? kth_largest<PER>(x, top_k, S) : -INFINITY;
+    float ssum = 0.f;
+    int cnt = 0;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+        x[i] = x[i] >= thr ? expf(x[i] - mx) : 0.f;
+        ssum += x[i];
+        cnt += x[i] != 0.f;
+    }
+    ssum = block_sum(ssum, S);
+    // exclusive scan of the nonzero counts in thread order = index order
+    int incl = cnt;
+#pragma unroll
+    for (int o = 1; o < WAVE; o <<= 1) {
+        const int v = __shfl_up(incl, o, WAVE);
+        if (lane() >= o) incl += v;
+    }
+    if (lane() == WAVE - 1) S.hist[wave()] = static_cast<unsigned>(incl);
+    __syncthreads();
+    int off = incl - cnt;
+    for (int w = 0; w < wave(); ++w) off += static_cast<int>(S.hist[w]);
+    int n_nz = 0;
+    for (int w = 0; w < NW; ++w) n_nz += static_cast<int>(S.hist[w]);
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+        S.u.samp.lg[base + i] = x[i];
+        if (x[i] != 0.f) S.u.samp.idx[off++] = base + i;
+    }
+    __syncthreads();
+    if (tid() == 0) {
+        const float inv = 1.f / ssum;
+        uint64_t st = seed * 0x9E3779B97F4A7C15ull + 0xBF58476D1CE4E5B9ull + 1ull;
+        (void) pcg32_next(st); (void) pcg32_next(st); (void) pcg32_next(st);
+        const float u = static_cast<float>(pcg32_next(st) >> 8) * (1.0f / 16777216.0f);
+        int chosen = V - 1;
+        float cum = 0.f;
+        for (int j = 0; j < n_nz; ++j) {
+            const int i = S.u.samp.idx[j];
+            cum = __fadd_rn(cum, __fmul_rn(S.u.samp.lg[i], inv));
+            if (cum >= u) { chosen = i; break; }
+        }
+        S.isel[2] = chosen;
+    }
+    __syncthreads();
+    const int r = S.isel[2];
+    __syncthreads();
+    return r;
+}
+
+// ---- the frame ---------------------------------------------------------------
+
+struct Seq {           // tags: epoch + running phase number, identical in every block
+    uint32_t base, n;
+    __device__ uint32_t next() { return base + (++n); }
+};
+
+__device__ __forceinline__ const LayerPtrs &layer_at(const Args &a, int gi) {
+    return gi < a.n_tl ? a.W->tl[gi] : a.W->cp[(gi - a.n_tl) % a.n_cl];
+}
+
+// One decoder layer over T rows held in S.x (its input); leaves its output in S.x.
+// gi: global layer index (talker layers, then n_cl cp layers per cp pass).
+template <int T, bool TALKER>
+__device__ __forceinline__ bool run_layer(const Args &a, Regs &R, int gi, int p0, Seq &seq, Smem &S) {
+    const LayerPtrs &L = layer_at(a, gi);
+    const int n_total = a.n_tl + CPH * a.n_cl;
+    const bool has_next = gi + 1 < n_total;
+    const LayerPtrs &N = layer_at(a, has_next ? gi + 1 : gi);
+    const float eps = TALKER ? a.W->eps_t : a.W->eps_c;
+
+    rmsnorm_rows<T>(S.x, L.ln1, eps, S.xn, S);
+    const uint32_t t_qkv = seq.next();
+    qkv_phase<T>(a, R, S, t_qkv);
+    if (has_next) load_qkv(R, N);
+
+    const uint32_t t_att = seq.next();
+    if (blk() < NH) {
+        bool ok;
+        if constexpr (TALKER) ok = talker_attention(a, L, gi, t_qkv, t_att, S);
+        else ok = cp_attention<T>(a, L, (gi - a.n_tl) % a.n_cl, p0, t_qkv, t_att, S);
+        if (!ok) return false;
+    }
+    if (!gather_rows<T, QD>(a, MB_ATT, t_att, S.u.big, S)) return false;
+    const uint32_t t_x2 = seq.next();
+    o_phase<T>(a, R, S, t_x2);
+    if (has_next) load_o(R, N);
+
+    if (!gather_rows<T, H>(a, MB_X2, t_x2, &S.x[0][0], S)) return false;
+    rmsnorm_rows<T>(S.x, L.ln2, eps, S.xn, S);
+    const uint32_t t_h = seq.next();
+    gu_phase<T>(a, R, S, t_h);
+    if (has_next) load_gu(R, N);
+
+    if (!gather_rows<T, FF>(a, MB_H, t_h, S.u.big, S)) return false;
+    const uint32_t t_x = seq.next();
+    down_phase<T>(a, R, S, t_x);
+    if (has_next) load_dn(R, N);
+
+    return gather_rows<T, H>(a, MB_X, t_x, &S.x[0][0], S);
+}
+
+__device__ __forceinline__ void load_row_f16(const uint16_t *src, float *dst) {
+    for (int i = tid(); i < H; i += BT) dst[i] = h2f(src[i]);
+}
+
+__global__ void __launch_bounds__(BT, 1) k_frame(Args a) {
+    __shared__ Smem S;
+    if (tid() == 0) S.fail = 0;
+    Seq seq{a.epoch, 0};
+    Regs R;
+    const Weights &W = *a.W;
+    const int first = a.skip_talker ? a.n_tl : 0;
+    {
+        const LayerPtrs &L0 = layer_at(a, first);
+        load_qkv(R, L0); load_o(R, L0); load_gu(R, L0); load_dn(R, L0);
+    }
+    __syncthreads();
+
+    // ---- talker step (or frame 0's prefill outputs) ----
+    if (!a.skip_talker) {
+        for (int i = tid(); i < H; i += BT) S.x[0][i] = a.step_in[i];
+        __syncthreads();
+        for (int il = 0; il < a.n_tl; ++il) {
+            if (il == a.n_tl - 1) load_th(R, W.codec_head);
+            if (!run_layer<1, true>(a, R, il, a.n_past, seq, S)) return;
+        }
+        rmsnorm_rows<1>(S.x, W.tl_norm, W.eps_t, S.xn, S);
+        const uint32_t t_lg = seq.next();
+        {
+            float xf[2][8];
+            xfrag<2>(S.xn[0], 0, xf);
+#pragma unroll
+            for (int r = 0; r < 3; ++r) {
+                const float d = wave_sum(dot8(R.th[r][1], xf[1], dot8(R.th[r][0], xf[0], 0.f)));
+                if (lane() == r) mb_put(a.mb + MB_LG + blk() * (VT / NB) + wave() * 3 + r, d, t_lg);
+            }
+        }
+        load_lm(R, W.lm_head[0]);
+        if (!gather<VT>(a, MB_LG, t_lg, S.u.samp.lg, S)) return;
+    } else {
+        for (int i = tid(); i < H; i += BT) S.xn[0][i] = a.hidden_in[i];
+        for (int i = tid(); i < VT; i += BT) S.u.samp.lg[i] = a.logits_in[i];
+        load_lm(R, W.lm_head[0]);
+        __syncthreads();
+    }
+    if (a.tap_hidden && blk() == 0) {
+        for (int i = tid(); i < H; i += BT) a.tap_hidden[i] = S.xn[0][i];
+        for (int i = tid(); i < VT; i += BT) a.tap_logits[i] = S.u.samp.lg[i];
+    }
+
+    // ---- codebook 0: suppression, min-frames EOS, repetition penalty (frame.hip:413-419) ----
+    for (int i = tid(); i < VT; i += BT) {
+        float v = S.u.samp.lg[i];
+        if (i >= a.suppress_from && i != a.eos_id) v = -INFINITY;
+        else if (i == a.eos_id && a.frame_index < a.min_frames) v = -INFINITY;
+        else if (a.rep_penalty > 0.f && a.seen[i]) v = v > 0.f ? v / a.rep_penalty : v * a.rep_penalty;
+        S.u.samp.lg[i] = v;
+    }
+    __syncthreads();
+    const int cb0 = block_sample<VT>(a.temperature, a.top_k, a.talker_seed, S);
+    if (tid() == 0) S.codes[0] = cb0;
+
+    // ---- code predictor: positions {0,1} as one 2-row pass, then 2..15 ----
+    int gi = a.n_tl;
+    for (int i = tid(); i < H; i += BT) {
+        S.x[0][i] = S.xn[0][i];
+        S.x[1][i] = h2f(W.codec_emb[static_cast<size_t>(cb0) * H + i]);
+    }
+    __syncthreads();
+    for (int il = 0; il < a.n_cl; ++il, ++gi)
+        if (!run_layer<2, false>(a, R, gi, 0, seq, S)) return;
+    for (int pos = 1; pos < NCB; ++pos) {
+        if (pos > 1) {
+            for (int il = 0; il < a.n_cl; ++il, ++gi)
+                if (!run_layer<1, false>(a, R, gi, pos, seq, S)) return;
+        }
+        const int row = pos == 1 ? 1 : 0;
+        rmsnorm_rows<1>(reinterpret_cast<const float (*)[H]>(S.x[row]), W.cp_norm, W.eps_c, S.xn, S);
+        const uint32_t t_lg = seq.next();
+        {
+            float xf[2][8];
+            xfrag<2>(S.xn[0], 0, xf);
+#pragma unroll
+            for (int r = 0; r < 2; ++r) {
+                const float d = wave_sum(dot8(R.lm[r][1], xf[1], dot8(R.lm[r][0], xf[0], 0.f)));
+                if (lane() == r) mb_put(a.mb + MB_LG + blk() * (VC / NB) + wave() * 2 + r, d, t_lg);
+            }
+        }
+        if (pos + 1 < NCB) load_lm(R, W.lm_head[pos]);
+        if (!gather<VC>(a, MB_LG, t_lg, S.u.samp.lg, S)) return;
+        if (a.tap_cp_logits && blk() == 0) {
+            for (int i = tid(); i < VC; i += BT) a.tap_cp_logits[(pos - 1) * VC + i] = S.u.samp.lg[i];
+            __syncthreads();
+        }
+        const int code = block_sample<VC>(a.cp_temperature, a.cp_top_k, a.cp_seed + static_cast<uint64_t>(pos) * 0xD1B54A32D192ED03ull, S);
+        if (tid() == 0) S.codes[pos] = code;
+        if (pos + 1 < NCB) {
+            load_row_f16(W.cp_emb[pos - 1] + static_cast<size_t>(code) * H, S.x[0]);
+            __syncthreads();
+        }
+    }
+
+    // ---- next step embedding (frame.hip:503-513 order) and outputs ----
+    __syncthreads();
+    if (tid() < H / NB) {
+        const int i = blk() * (H / NB) + tid();
+        float v = h2f(W.codec_emb[static_cast<size_t>(S.codes[0]) * H + i]);
+        for (int cb = 0; cb < CPH; ++cb) v += h2f(W.cp_emb[cb][static_cast<size_t>(S.codes[cb + 1]) * H + i]);
+        a.step_out[i] = v + a.trailing[i];
+    }
+    if (blk() == 0 && tid() == 0) {
+        for (int c = 0; c < NCB; ++c) a.codes_out[c] = S.codes[c];
+        if (S.codes[0] != a.eos_id) a.seen[S.codes[0]] = 1u;
+    }
+}
+
+uint64_t splitmix64(uint64_t x) {
+    x += 0x9E3779B97F4A7C15ull;
+    x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ull;
+    x = (x ^ (x >> 27)) * 0x94D049BB133111EBull;
+    return x ^ (x >> 31);
+}
+
+} // namespace fk
+} // namespace navi_amd
+
+// ---------------------------------------------------------------------------
+// Host side (Frame::Impl, frame.hip:590-810)
+// ---------------------------------------------------------------------------
+
+using namespace navi_amd;
+using namespace navi_amd::fk;
+
+struct navi_frame {
+    navi_model_params p{};
+    navi_frame_options opt{};
+    Weights hw{};
+    Weights *dw = nullptr;
+    uint64_t *mb = nullptr;
+    uint32_t *ctl = nullptr;       // [0..15] codes, [16] abort epoch
+    float *step_out = nullptr;
+    uint8_t *seen = nullptr;
+    float *tap = nullptr;          // hidden | logits | cp logits
+    bool taps = false;
+    uint16_t **kv_dev = nullptr;   // [2][MAX_TL] per-layer K/V pointers as the kernel reads them
+    uint16_t *kv_host[2][MAX_TL] = {};
+    uint32_t epoch = 0;
+    int grid = NB, occ = 0;
+    hipEvent_t ev0 = nullptr, ev1 = nullptr;
+    std::vector<void *> owned;
+
+    ~navi_frame() {
+        if (ev0) (void) hipEventDestroy(ev0);
+        if (ev1) (void) hipEventDestroy(ev1);
+        for (void *q : owned) (void) hipFree(q);
+    }
+    template <class T> navi_status alloc(T *&ptr, size_t n, char *err, size_t errlen) {
+        void *q = nullptr;
+        NAVI_TRY_HIP(hipMalloc(&q, n * sizeof(T)), err, errlen);
+        owned.push_back(q);
+        NAVI_TRY_HIP(hipMemset(q, 0, n * sizeof(T)), err, errlen);
+        ptr = static_cast<T *>(q);
+        return NAVI_OK;
+    }
+};
+
+namespace {
+
+const navi_tensor_ref *find_tensor(const navi_tensor_ref *t, int n, const std::string &name) {
+    for (int i = 0; i < n; ++i) if (t[i].name && name == t[i].name) return &t[i];
+    return nullptr;
+}
+
+// Looks a weight up by name and checks its dtype and shape (Params::validate's contract).
+// d1 == 0: a 1-D tensor [d0]; else [d0, d1].
+template <class T>
+navi_status bind_tensor(const navi_tensor_ref *t, int n, const std::string &name, int dtype, uint64_t d0, uint64_t d1,
+                        const T *&out, char *err, size_t errlen) {
+    const navi_tensor_ref *r = find_tensor(t, n, name);
+    if (!r) { set_err(err, errlen, "frame: missing tensor '%s'", name.c_str()); return NAVI_ERR_INVALID; }
+    const int nd = d1 ? 2 : 1;
+    const bool ok = r->dtype == dtype && r->ndim == nd && r->dims[0] == d0 && (nd == 1 || r->dims[1] == d1);
+    if (!ok) { set_err(err, errlen, "frame: tensor '%s' has an unexpected dtype or shape", name.c_str()); return NAVI_ERR_INVALID; }
+    if (reinterpret_cast<uintptr_t>(r->ptr) & 15u) { set_err(err, errlen, "frame: tensor '%s' is not 16-byte aligned", name.c_str()); return NAVI_ERR_INVALID; }
+    out = static_cast<const T *>(r->ptr);
+    return NAVI_OK;
+}
+
+#define NAVI_BIND(T, name, dt, d0, d1, out)                                                       \
+    do {                                                                                          \
+        const navi_status s_ = bind_tensor<T>(tensors, n_tensors, (name), (dt), (d0), (d1), (out), err, errlen); \
+        if (s_ != NAVI_OK) return s_;                                                             \
+    } while (0)
+
+navi_status bind_layers(const navi_tensor_ref *tensors, int n_tensors, const std::string &prefix, int n, LayerPtrs *L,
+                        char *err, size_t errlen) {
+    for (int l = 0; l < n; ++l) {
+        const std::string p = prefix + ".layers." + std::to_string(l) + ".";
+        NAVI_BIND(float, p + "input_layernorm.weight", NAVI_DT_F32, H, 0, L[l].ln1);
+        NAVI_BIND(float, p + "post_attention_layernorm.weight", NAVI_DT_F32, H, 0, L[l].ln2);
+        NAVI_BIND(float, p + "self_attn.q_norm.weight", NAVI_DT_F32, HD, 0, L[l].qn);
+        NAVI_BIND(float, p + "self_attn.k_norm.weight", NAVI_DT_F32, HD, 0, L[l].kn);
+        NAVI_BIND(uint16_t, p + "self_attn.q_proj.weight", NAVI_DT_F16, QD, H, L[l].wq);
+        NAVI_BIND(uint16_t, p + "self_attn.k_proj.weight", NAVI_DT_F16, KVD, H, L[l].wk);
+        NAVI_BIND(uint16_t, p + "self_attn.v_proj.weight", NAVI_DT_F16, KVD, H, L[l].wv);
+        NAVI_BIND(uint16_t, p + "self_attn.o_proj.weight", NAVI_DT_F16, H, QD, L[l].wo);
+        NAVI_BIND(uint16_t, p + "mlp.gate_proj.weight", NAVI_DT_F16, FF, H, L[l].wg);
+        NAVI_BIND(uint16_t, p + "mlp.up_proj.weight", NAVI_DT_F16, FF, H, L[l].wu);
+        NAVI_BIND(uint16_t, p + "mlp.down_proj.weight", NAVI_DT_F16, H, FF, L[l].wd);
+    }
+    return NAVI_OK;
+}
+
+bool shape_is(const navi_xformer_params &x, int vocab) {
+    return x.hidden == H && x.n_head == NH && x.n_kv_head == NKV && x.head_dim == HD && x.ff == FF && x.vocab == vocab;
+}
+
+} // namespace
+
+extern "C" {
+
+navi_status navi_frame_create(const navi_model_params *p, const navi_tensor_ref *tensors, int32_t n_tensors,
+                              const navi_frame_options *opt, navi_frame **out, char *err, size_t errlen) {
+    if (!p || !tensors || !out) { set_err(err, errlen, "frame: null argument"); return NAVI_ERR_INVALID; }
+    *out = nullptr;
+    navi_status st = ensure_device(err, errlen);
+    if (st != NAVI_OK) return st;
+    if (!shape_is(p->talker, VT) || !shape_is(p->cp, VC) || p->n_code_groups != NCB) {
+        set_err(err, errlen, "frame: kernel is built for the Qwen3-TTS-0.6B shapes (hidden 1024, 16/8 heads x 128, ff 3072, vocab 3072/2048, 16 codebooks)");
+        return NAVI_ERR_UNSUPPORTED;
+    }
+    if (p->talker.n_layer < 1 || p->talker.n_layer > MAX_TL || p->cp.n_layer < 1 || p->cp.n_layer > MAX_CL) {
+        set_err(err, errlen, "frame: layer counts %d/%d exceed the kernel's %d/%d", p->talker.n_layer, p->cp.n_layer, MAX_TL, MAX_CL);
+        return NAVI_ERR_UNSUPPORTED;
+    }
+    navi_frame_options o{1, 0};
+    if (opt) o = *opt;
+    if (o.blocks_per_mp != 1) { set_err(err, errlen, "frame: blocks_per_mp must be 1 (one persistent block per CU)"); return NAVI_ERR_INVALID; }
+    if (o.spin_cap == 0) o.spin_cap = 2000000ull;   // ~1-2 s of polling at MALL latency
+
+    const DeviceState &ds = device_state();
+    if (ds.prop.multiProcessorCount < NB) {
+        set_err(err, errlen, "frame: needs %d co-resident blocks, device has %d CUs", NB, ds.prop.multiProcessorCount);
+        return NAVI_ERR_UNSUPPORTED;
+    }
+    int occ = 0;
+    NAVI_TRY_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, k_frame, BT, 0), err, errlen);
+    if (occ < 1) { set_err(err, errlen, "frame: k_frame cannot be resident"); return NAVI_ERR_UNSUPPORTED; }
+
+    auto *f = new navi_frame();
+    f->p = *p;
+    f->opt = o;
+    f->occ = occ;
+    Weights &w = f->hw;
+    auto fail = [&](navi_status s) { delete f; return s; };
+    if ((st = bind_layers(tensors, n_tensors, "talker.model", p->talker.n_layer, w.tl, err, errlen)) != NAVI_OK) return fail(st);
+    if ((st = bind_layers(tensors, n_tensors, "talker.code_predictor.model", p->cp.n_layer, w.cp, err, errlen)) != NAVI_OK) return fail(st);
+    {
+        const int n_tensors_ = n_tensors;
+        auto b16 = [&](const uint16_t *&dst, const std::string &name, uint64_t d0, uint64_t d1) {
+            return bind_tensor<uint16_t>(tensors, n_tensors_, name, NAVI_DT_F16, d0, d1, dst, err, errlen);
+        };
+        auto b32 = [&](const float *&dst, const std::string &name, uint64_t d0) {
+            return bind_tensor<float>(tensors, n_tensors_, name, NAVI_DT_F32, d0, 0, dst, err, errlen);
+        };
+        if ((st = b32(w.tl_norm, "talker.model.norm.weight", H)) != NAVI_OK) return fail(st);
+        if ((st = b32(w.cp_norm, "talker.code_predictor.model.norm.weight", H)) != NAVI_OK) return fail(st);
+        if ((st = b16(w.codec_head, "talker.codec_head.weight", VT, H)) != NAVI_OK) return fail(st);
+        if ((st = b16(w.codec_emb, "talker.model.codec_embedding.weight", VT, H)) != NAVI_OK) return fail(st);
+        for (int i = 0; i < CPH; ++i) {
+            if ((st = b16(w.cp_emb[i], "talker.code_predictor.model.codec_embedding." + std::to_string(i) + ".weight", VC, H)) != NAVI_OK) return fail(st);
+            if ((st = b16(w.lm_head[i], "talker.code_predictor.lm_head." + std::to_string(i) + ".weight", VC, H)) != NAVI_OK) return fail(st);
+        }
+    }
+    for (int i = 0; i < HD / 2; ++i) {
+        w.invf_t[i] = static_cast<float>(1.0 / std::pow(p->talker.rope_theta, 2.0 * i / HD));
+        w.invf_c[i] = static_cast<float>(1.0 / std::pow(p->cp.rope_theta, 2.0 * i / HD));
+    }
+    w.eps_t = p->talker.rms_eps;
+    w.eps_c = p->cp.rms_eps;
+
+    if ((st = f->alloc(f->dw, 1, err, errlen)) != NAVI_OK) return fail(st);
+    if ((st = f->alloc(f->mb, MB_WORDS, err, errlen)) != NAVI_OK) return fail(st);
+    if ((st = f->alloc(f->ctl, 32, err, errlen)) != NAVI_OK) return fail(st);
+    if ((st = f->alloc(f->step_out, H, err, errlen)) != NAVI_OK) return fail(st);
+    if ((st = f->alloc(f->seen, VT, err, errlen)) != NAVI_OK) return fail(st);
+    if ((st = f->alloc(f->tap, H + VT + CPH * VC, err, errlen)) != NAVI_OK) return fail(st);
+    if ((st = f->alloc(f->kv_dev, 2 * MAX_TL, err, errlen)) != NAVI_OK) return fail(st);
+    if (hipMemcpy(f->dw, &f->hw, sizeof(Weights), hipMemcpyHostToDevice) != hipSuccess) {
+        set_err(err, errlen, "frame: weight table upload failed");
+        return fail(NAVI_ERR_HIP);
+    }
+    if (hipEventCreate(&f->ev0) != hipSuccess || hipEventCreate(&f->ev1) != hipSuccess) {
+        set_err(err, errlen, "frame: hipEventCreate failed");
+        return fail(NAVI_ERR_HIP);
+    }
+    f->grid = NB;
+    *out = f;
+    return NAVI_OK;
+}
+
+void navi_frame_destroy(navi_frame *f) { delete f; }
+
+navi_status navi_frame_reset(navi_frame *f) {
+    if (!f) return NAVI_ERR_INVALID;
+    return hipMemsetAsync(f->seen, 0, VT, device_state().stream) == hipSuccess ? NAVI_OK : NAVI_ERR_HIP;
+}
+
+navi_status navi_frame_set_taps(navi_frame *f, int32_t enabled) {
+    if (!f) return NAVI_ERR_INVALID;
+    f->taps = enabled != 0;
+    return NAVI_OK;
+}
+
+const float *navi_frame_tap_hidden(const navi_frame *f) { return f ? f->tap : nullptr; }
+const float *navi_frame_tap_logits(const navi_frame *f) { return f ? f->tap + H : nullptr; }
+const float *navi_frame_tap_cp_logits(const navi_frame *f) { return f ? f->tap + H + VT : nullptr; }
+float *navi_frame_step_out(navi_frame *f) { return f ? f->step_out : nullptr; }
+int32_t navi_frame_grid_blocks(const navi_frame *f) { return f ? f->grid : 0; }
+int32_t navi_frame_occupancy_per_mp(const navi_frame *f) { return f ? f->occ : 0; }
+
+navi_status navi_frame_run(navi_frame *f, const navi_kv_view *kv, int32_t n_past, int32_t skip_talker,
+                           const float *d_hidden, const float *d_logits, const float *d_trailing,
+                           const navi_sampling *s, uint64_t seed, int32_t frame_index, navi_frame_result *out) {
+    if (!out) return NAVI_ERR_INVALID;
+    std::memset(out, 0, sizeof(*out));
+    auto fail = [&](navi_status st, const char *msg) {
+        out->ok = 0;
+        out->status = st;
+        std::snprintf(out->error, sizeof(out->error), "%s", msg);
+        return st;
+    };
+    if (!f || !s || !d_trailing) return fail(NAVI_ERR_INVALID, "frame: null argument");
+    Args a{};
+    if (skip_talker) {
+        if (!d_hidden || !d_logits) return fail(NAVI_ERR_INVALID, "frame: run_first needs the prefill's hidden and logits");
+        a.hidden_in = d_hidden;
+        a.logits_in = d_logits;
+    } else {
+        if (!kv || !kv->k || !kv->v) return fail(NAVI_ERR_INVALID, "frame: run needs a KV cache");
+        if (n_past >= kv->max_pos || n_past >= MAX_POS) return fail(NAVI_ERR_KV_FULL, "KV cache full");
+        if (n_past < 0) return fail(NAVI_ERR_INVALID, "frame: negative n_past");
+        if (kv->n_layer != f->p.talker.n_layer || kv->kv_dim != KVD) return fail(NAVI_ERR_INVALID, "KV cache layer count mismatch");
+        bool same = true;
+        for (int l = 0; l < kv->n_layer; ++l) same = same && f->kv_host[0][l] == kv->k[l] && f->kv_host[1][l] == kv->v[l];
+        if (!same) {
+            for (int l = 0; l < kv->n_layer; ++l) { f->kv_host[0][l] = kv->k[l]; f->kv_host[1][l] = kv->v[l]; }
+            if (hipMemcpyAsync(f->kv_dev, f->kv_host, sizeof(f->kv_host), hipMemcpyHostToDevice, device_state().stream) != hipSuccess)
+                return fail(NAVI_ERR_HIP, "frame: KV pointer upload failed");
+            if (hipStreamSynchronize(device_state().stream) != hipSuccess) return fail(NAVI_ERR_HIP, "frame: KV pointer upload failed");
+        }
+    }
+    a.kc = f->kv_dev;
+    a.vc = f->kv_dev + MAX_TL;
+    a.W = f->dw;
+    a.mb = f->mb;
+    a.abort_word = f->ctl + NCB;
+    a.codes_out = reinterpret_cast<int32_t *>(f->ctl);
+    a.n_tl = f->p.talker.n_layer;
+    a.n_cl = f->p.cp.n_layer;
+    a.n_past = n_past;
+    a.skip_talker = skip_talker ? 1 : 0;
+    a.step_in = f->step_out;
+    a.trailing = d_trailing;
+    a.step_out = f->step_out;
+    a.seen = f->seen;
+    a.temperature = s->temperature;
+    a.top_k = s->top_k;
+    a.rep_penalty = s->repetition_penalty;
+    a.cp_temperature = s->cp_temperature;
+    a.cp_top_k = s->cp_top_k;
+    a.min_frames = s->min_frames;
+    a.frame_index = frame_index;
+    a.eos_id = f->p.codec_eos_id;
+    a.suppress_from = VT - 1024;   // HF suppress_tokens = range(vocab - 1024, vocab) minus EOS
+    a.talker_seed = splitmix64(seed ^ (static_cast<uint64_t>(frame_index) * 0xA24BAED4963EE407ull));
+    a.cp_seed = splitmix64(a.talker_seed ^ 0x9FB21C651E98DF25ull);
+    a.spin_cap = f->opt.spin_cap;
+    f->epoch += EPOCH_STRIDE;
+    if (f->epoch == 0) f->epoch = EPOCH_STRIDE;
+    a.epoch = f->epoch;
+    if (f->taps) {
+        a.tap_hidden = f->tap;
+        a.tap_logits = f->tap + H;
+        a.tap_cp_logits = f->tap + H + VT;
+    }
+    hipStream_t st = device_state().stream;
+    if (hipEventRecord(f->ev0, st) != hipSuccess) return fail(NAVI_ERR_HIP, "frame: hipEventRecord failed");
+    void *args[] = {&a};
+    const hipError_t e = hipLaunchCooperativeKernel(reinterpret_cast<const void *>(k_frame), dim3(f->grid), dim3(BT), args, 0, st);
+    if (e != hipSuccess) {
+        std::string m = std::string("cooperative launch failed: ") + hipGetErrorString(e);
+        return fail(NAVI_ERR_LAUNCH, m.c_str());
+    }
+    uint32_t h[NCB + 1] = {};
+    if (hipEventRecord(f->ev1, st) != hipSuccess || hipMemcpyAsync(h, f->ctl, sizeof(h), hipMemcpyDeviceToHost, st) != hipSuccess ||
+        hipStreamSynchronize(st) != hipSuccess)
+        return fail(NAVI_ERR_HIP, "frame: launch or readback failed");
+    float ms = 0.f;
+    (void) hipEventElapsedTime(&ms, f->ev0, f->ev1);
+    out->us = ms * 1000.0;
+    if (h[NCB] == f->epoch) return fail(NAVI_ERR_TIMEOUT, "frame dataflow wait timed out: the persistent grid could not run to completion");
+    for (int c = 0; c < NCB; ++c) out->codes[c] = static_cast<int32_t>(h[c]);
+    out->eos = out->codes[0] == f->p.codec_eos_id;
+    out->ok = 1;
+    out->status = NAVI_OK;
+    return NAVI_OK;
+}
+
+} // extern "C"

@@ -1,0 +1,360 @@
+"""ctypes binding of include/navi_amd.h and the Python mirror of the host objects.
+
+This is plumbing: it loads the in-tree libnavi_amd.so (and fails loudly when it
+is missing), declares the C structs, and wraps the handles the way the
+reference's C++ classes wrap their Impl: `DeviceWeights` (one device arena per
+`.navi`, device_weights.cpp:245-299), `KvCache` (talker.h:20-24) and `Frame`
+(frame.h:46-71). Nothing here computes; every operation is a C ABI call.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from pathlib import Path
+
+import numpy as np
+
+from .navi_file import NaviFile
+
+LIB_PATH = Path(__file__).resolve().parent.parent / "lib" / "libnavi_amd.so"
+
+NAVI_OK, NAVI_ERR_TIMEOUT, NAVI_ERR_LAUNCH, NAVI_ERR_KV_FULL, NAVI_ERR_INVALID, NAVI_ERR_HIP, NAVI_ERR_UNSUPPORTED = range(7)
+
+# The exported entry points include/navi_amd.h declares (checked by the CPU tests).
+EXPORTS = [
+    "navi_device_open", "navi_device_stream", "navi_device_synchronize", "navi_build_arch",
+    "navi_mem_alloc", "navi_mem_free", "navi_mem_h2d", "navi_mem_d2h", "navi_mem_d2d", "navi_mem_zero",
+    "navi_frame_create", "navi_frame_destroy", "navi_frame_reset", "navi_frame_run", "navi_frame_step_out",
+    "navi_frame_grid_blocks", "navi_frame_occupancy_per_mp", "navi_frame_set_taps", "navi_frame_tap_hidden",
+    "navi_frame_tap_logits", "navi_frame_tap_cp_logits",
+]
+
+
+class NaviError(RuntimeError):
+    def __init__(self, status: int, msg: str):
+        super().__init__(f"[{status}] {msg}")
+        self.status = status
+
+
+class DeviceInfo(C.Structure):
+    _fields_ = [("index", C.c_int32), ("name", C.c_char * 64), ("arch", C.c_char * 32),
+                ("multiprocessors", C.c_int32), ("warp_size", C.c_int32), ("cooperative_launch", C.c_int32),
+                ("max_threads_per_block", C.c_int32), ("lds_per_block", C.c_uint64),
+                ("clock_khz", C.c_int32), ("mem_clock_khz", C.c_int32), ("mem_bus_width", C.c_int32),
+                ("vram_total", C.c_uint64), ("vram_free", C.c_uint64), ("l2_bytes", C.c_uint64),
+                ("hip_runtime_version", C.c_int32)]
+
+
+class XformerParams(C.Structure):
+    _fields_ = [("hidden", C.c_int32), ("n_layer", C.c_int32), ("n_head", C.c_int32), ("n_kv_head", C.c_int32),
+                ("head_dim", C.c_int32), ("ff", C.c_int32), ("vocab", C.c_int32), ("rms_eps", C.c_float),
+                ("rope_theta", C.c_double)]
+
+
+class ModelParams(C.Structure):
+    _fields_ = [("talker", XformerParams), ("cp", XformerParams), ("n_code_groups", C.c_int32),
+                ("codec_eos_id", C.c_int32), ("text_hidden", C.c_int32), ("text_vocab", C.c_int32),
+                ("tts_bos_id", C.c_int32), ("tts_eos_id", C.c_int32), ("tts_pad_id", C.c_int32),
+                ("codec_bos_id", C.c_int32), ("codec_pad_id", C.c_int32), ("codec_think_id", C.c_int32),
+                ("codec_nothink_id", C.c_int32), ("codec_think_bos_id", C.c_int32), ("codec_think_eos_id", C.c_int32)]
+
+
+class TensorRef(C.Structure):
+    _fields_ = [("name", C.c_char_p), ("ptr", C.c_void_p), ("dtype", C.c_int32), ("ndim", C.c_int32),
+                ("dims", C.c_uint64 * 4)]
+
+
+class KvView(C.Structure):
+    _fields_ = [("n_layer", C.c_int32), ("max_pos", C.c_int32), ("kv_dim", C.c_int32),
+                ("k", C.POINTER(C.c_void_p)), ("v", C.POINTER(C.c_void_p))]
+
+
+class Sampling(C.Structure):
+    _fields_ = [("temperature", C.c_float), ("top_k", C.c_int32), ("repetition_penalty", C.c_float),
+                ("cp_temperature", C.c_float), ("cp_top_k", C.c_int32), ("min_frames", C.c_int32)]
+
+    @staticmethod
+    def make(temperature=0.9, top_k=50, repetition_penalty=1.05, cp_temperature=0.9, cp_top_k=50, min_frames=2):
+        return Sampling(temperature, top_k, repetition_penalty, cp_temperature, cp_top_k, min_frames)
+
+    @staticmethod
+    def greedy(min_frames=2, repetition_penalty=1.05):
+        return Sampling(0.0, 50, repetition_penalty, 0.0, 50, min_frames)
+
+
+class FrameOptions(C.Structure):
+    _fields_ = [("blocks_per_mp", C.c_int32), ("spin_cap", C.c_uint64)]
+
+
+class FrameResult(C.Structure):
+    _fields_ = [("ok", C.c_int32), ("eos", C.c_int32), ("codes", C.c_int32 * 16), ("us", C.c_double),
+                ("status", C.c_int32), ("error", C.c_char * 160)]
+
+
+_lib = None
+
+
+def lib() -> C.CDLL:
+    """The loaded library; raises if it has not been built (there is no fallback)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        raise RuntimeError(f"{LIB_PATH} is missing: build it with __graft_entry__.build(); there is no CPU fallback")
+    L = C.CDLL(str(LIB_PATH))
+    E = C.c_char_p
+    L.navi_device_open.argtypes = [C.POINTER(DeviceInfo), E, C.c_size_t]
+    L.navi_device_stream.restype = C.c_void_p
+    L.navi_build_arch.restype = C.c_char_p
+    L.navi_mem_alloc.argtypes = [C.POINTER(C.c_void_p), C.c_size_t]
+    L.navi_mem_free.argtypes = [C.c_void_p]
+    for f in ("navi_mem_h2d", "navi_mem_d2h", "navi_mem_d2d"):
+        getattr(L, f).argtypes = [C.c_void_p, C.c_void_p, C.c_size_t]
+    L.navi_mem_zero.argtypes = [C.c_void_p, C.c_size_t]
+    L.navi_frame_create.argtypes = [C.POINTER(ModelParams), C.POINTER(TensorRef), C.c_int32, C.POINTER(FrameOptions),
+                                    C.POINTER(C.c_void_p), E, C.c_size_t]
+    L.navi_frame_destroy.argtypes = [C.c_void_p]
+    L.navi_frame_destroy.restype = None
+    L.navi_frame_reset.argtypes = [C.c_void_p]
+    L.navi_frame_run.argtypes = [C.c_void_p, C.POINTER(KvView), C.c_int32, C.c_int32, C.c_void_p, C.c_void_p, C.c_void_p,
+                                 C.POINTER(Sampling), C.c_uint64, C.c_int32, C.POINTER(FrameResult)]
+    L.navi_frame_step_out.argtypes = [C.c_void_p]
+    L.navi_frame_step_out.restype = C.c_void_p
+    for f in ("navi_frame_grid_blocks", "navi_frame_occupancy_per_mp"):
+        getattr(L, f).argtypes = [C.c_void_p]
+    L.navi_frame_set_taps.argtypes = [C.c_void_p, C.c_int32]
+    for f in ("navi_frame_tap_hidden", "navi_frame_tap_logits", "navi_frame_tap_cp_logits"):
+        getattr(L, f).argtypes = [C.c_void_p]
+        getattr(L, f).restype = C.c_void_p
+    _lib = L
+    return L
+
+
+def _check(st: int, err: C.Array | None = None, what: str = ""):
+    if st != NAVI_OK:
+        msg = err.value.decode(errors="replace") if err is not None else what
+        raise NaviError(st, msg or what)
+
+
+def device_open() -> DeviceInfo:
+    info = DeviceInfo()
+    err = C.create_string_buffer(256)
+    _check(lib().navi_device_open(C.byref(info), err, 256), err)
+    return info
+
+
+# ---- device memory -------------------------------------------------------------
+
+class DeviceBuffer:
+    def __init__(self, nbytes: int):
+        self.nbytes = int(nbytes)
+        p = C.c_void_p()
+        _check(lib().navi_mem_alloc(C.byref(p), self.nbytes), what="navi_mem_alloc")
+        self.ptr = p.value
+
+    def upload(self, arr: np.ndarray, offset: int = 0):
+        a = np.ascontiguousarray(arr)
+        assert offset + a.nbytes <= self.nbytes
+        _check(lib().navi_mem_h2d(self.ptr + offset, a.ctypes.data, a.nbytes), what="navi_mem_h2d")
+
+    def download(self, dtype, count: int, offset: int = 0) -> np.ndarray:
+        out = np.empty(count, dtype=dtype)
+        assert offset + out.nbytes <= self.nbytes
+        _check(lib().navi_mem_d2h(out.ctypes.data, self.ptr + offset, out.nbytes), what="navi_mem_d2h")
+        return out
+
+    def free(self):
+        if self.ptr:
+            lib().navi_mem_free(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+def download(ptr: int, dtype, count: int) -> np.ndarray:
+    out = np.empty(count, dtype=dtype)
+    _check(lib().navi_mem_d2h(out.ctypes.data, ptr, out.nbytes), what="navi_mem_d2h")
+    return out
+
+
+def upload(ptr: int, arr: np.ndarray):
+    a = np.ascontiguousarray(arr)
+    _check(lib().navi_mem_h2d(ptr, a.ctypes.data, a.nbytes), what="navi_mem_h2d")
+
+
+# ---- weights ---------------------------------------------------------------------
+
+ARENA_ALIGN = 256
+
+
+class DeviceWeights:
+    """One device arena holding every selected tensor of a `.navi`
+    (DeviceWeights::upload, device_weights.cpp:245-299: 256-byte aligned, file order,
+    `groups` placed adjacently)."""
+
+    def __init__(self, path, select=None, groups=()):
+        nf = NaviFile(path)
+        self.kv = dict(nf.kv)
+        chosen, seen_groups = [], set()
+        group_of = {n: gi for gi, g in enumerate(groups) for n in g}
+        take = (lambda t: select(t)) if select else (lambda t: t.dtype != 4)
+        for t in nf.tensors:
+            gi = group_of.get(t.name)
+            if gi is None:
+                if take(t):
+                    chosen.append(t)
+                continue
+            if gi in seen_groups:
+                continue
+            seen_groups.add(gi)
+            for n in groups[gi]:
+                m = nf.find(n)
+                if m is not None and take(m):
+                    chosen.append(m)
+        arena = sum((t.nbytes + ARENA_ALIGN - 1) // ARENA_ALIGN * ARENA_ALIGN for t in chosen)
+        self.buf = DeviceBuffer(max(arena, 1))
+        self.tensors = {}
+        off = 0
+        for t in chosen:
+            _check(lib().navi_mem_h2d(self.buf.ptr + off, C.addressof(C.c_char.from_buffer_copy(b"\0")) if t.nbytes == 0 else
+                                      np.frombuffer(nf.bytes_of(t), dtype=np.uint8).ctypes.data, t.nbytes), what=t.name)
+            self.tensors[t.name] = (self.buf.ptr + off, t.dtype, t.dims)
+            off += (t.nbytes + ARENA_ALIGN - 1) // ARENA_ALIGN * ARENA_ALIGN
+        self.bytes = arena
+        nf.close()
+
+    def ptr(self, name: str) -> int:
+        return self.tensors[name][0]
+
+    def refs(self):
+        """(TensorRef array, keepalive) for the ABI's create() calls."""
+        names = list(self.tensors)
+        arr = (TensorRef * len(names))()
+        keep = []
+        for i, n in enumerate(names):
+            p, dt, dims = self.tensors[n]
+            b = n.encode()
+            keep.append(b)
+            arr[i].name = b
+            arr[i].ptr = p
+            arr[i].dtype = dt
+            arr[i].ndim = len(dims)
+            for k, d in enumerate(dims[:4]):
+                arr[i].dims[k] = d
+        return arr, keep
+
+
+def model_params(kv: dict) -> ModelParams:
+    """read_params (params.cpp:59-130) for the fields the path uses."""
+    def xf(ns):
+        return XformerParams(kv[f"{ns}.hidden_size"], kv[f"{ns}.num_hidden_layers"], kv[f"{ns}.num_attention_heads"],
+                             kv[f"{ns}.num_key_value_heads"], kv[f"{ns}.head_dim"], kv[f"{ns}.intermediate_size"],
+                             kv.get(f"{ns}.vocab_size", 0), float(kv[f"{ns}.rms_norm_eps"]), float(kv[f"{ns}.rope_theta"]))
+    if kv.get("general.arch") != "qwen3-tts":
+        raise ValueError(f"architecture '{kv.get('general.arch')}' is not qwen3-tts")
+    return ModelParams(xf("talker"), xf("cp"), kv["talker.num_code_groups"], kv["talker.codec_eos_token_id"],
+                       kv["talker.text_hidden_size"], kv["talker.text_vocab_size"], kv["text.tts_bos_id"],
+                       kv["text.tts_eos_id"], kv["text.tts_pad_id"], kv["talker.codec_bos_id"], kv["talker.codec_pad_id"],
+                       kv["talker.codec_think_id"], kv["talker.codec_nothink_id"], kv["talker.codec_think_bos_id"],
+                       kv["talker.codec_think_eos_id"])
+
+
+# ---- KV cache ----------------------------------------------------------------------
+
+class KvCache:
+    """talker.h:20-24: per layer [max_pos][kv_dim] f16 K and V, device-resident."""
+
+    def __init__(self, n_layer: int, max_pos: int, kv_dim: int):
+        self.n_layer, self.max_pos, self.kv_dim = n_layer, max_pos, kv_dim
+        per = max_pos * kv_dim * 2
+        self.buf = DeviceBuffer(2 * n_layer * per)
+        self.k = [self.buf.ptr + l * per for l in range(n_layer)]
+        self.v = [self.buf.ptr + (n_layer + l) * per for l in range(n_layer)]
+        self.n_used = 0
+        self._kp = (C.c_void_p * n_layer)(*self.k)
+        self._vp = (C.c_void_p * n_layer)(*self.v)
+        self.view = KvView(n_layer, max_pos, kv_dim, C.cast(self._kp, C.POINTER(C.c_void_p)),
+                           C.cast(self._vp, C.POINTER(C.c_void_p)))
+
+    def fill(self, layer: int, k_rows: np.ndarray, v_rows: np.ndarray, pos0: int = 0):
+        """Writes f16 rows (uint16 bit patterns or float arrays) at positions pos0..."""
+        def bits(a):
+            a = np.asarray(a)
+            return a if a.dtype == np.uint16 else a.astype(np.float16).view(np.uint16)
+        kb, vb = bits(k_rows), bits(v_rows)
+        off = pos0 * self.kv_dim * 2
+        upload(self.k[layer] + off, kb)
+        upload(self.v[layer] + off, vb)
+
+    def read(self, layer: int, n: int):
+        k = download(self.k[layer], np.uint16, n * self.kv_dim).view(np.float16).astype(np.float32)
+        v = download(self.v[layer], np.uint16, n * self.kv_dim).view(np.float16).astype(np.float32)
+        return k.reshape(n, self.kv_dim), v.reshape(n, self.kv_dim)
+
+
+# ---- frame -------------------------------------------------------------------------
+
+class Frame:
+    """frame.h:46-71 over navi_frame_*."""
+
+    def __init__(self, weights: DeviceWeights, params: ModelParams | None = None, spin_cap: int = 0):
+        self.params = params or model_params(weights.kv)
+        refs, self._keep = weights.refs()
+        h = C.c_void_p()
+        err = C.create_string_buffer(256)
+        opt = FrameOptions(1, spin_cap)
+        _check(lib().navi_frame_create(C.byref(self.params), refs, len(refs), C.byref(opt), C.byref(h), err, 256), err)
+        self.h = h.value
+        self.hidden = self.params.talker.hidden
+
+    def close(self):
+        if self.h:
+            lib().navi_frame_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def reset(self):
+        _check(lib().navi_frame_reset(self.h), what="navi_frame_reset")
+
+    def set_taps(self, on: bool):
+        _check(lib().navi_frame_set_taps(self.h, 1 if on else 0), what="navi_frame_set_taps")
+
+    def _run(self, kv, n_past, skip, d_hidden, d_logits, d_trailing, s, seed, frame_index) -> FrameResult:
+        r = FrameResult()
+        lib().navi_frame_run(self.h, C.byref(kv.view) if kv is not None else None, n_past, skip, d_hidden, d_logits,
+                             d_trailing, C.byref(s), C.c_uint64(seed & ((1 << 64) - 1)), frame_index, C.byref(r))
+        return r
+
+    def run_first(self, d_hidden: int, d_logits: int, d_trailing: int, s: Sampling, seed: int, frame_index: int):
+        return self._run(None, 0, 1, d_hidden, d_logits, d_trailing, s, seed, frame_index)
+
+    def run(self, kv: KvCache, n_past: int, d_trailing: int, s: Sampling, seed: int, frame_index: int):
+        r = self._run(kv, n_past, 0, None, None, d_trailing, s, seed, frame_index)
+        if r.ok:
+            kv.n_used = n_past + 1
+        return r
+
+    @property
+    def d_step_out(self) -> int:
+        return lib().navi_frame_step_out(self.h)
+
+    def grid_blocks(self) -> int:
+        return lib().navi_frame_grid_blocks(self.h)
+
+    def taps(self):
+        L = lib()
+        hid = download(L.navi_frame_tap_hidden(self.h), np.float32, self.hidden)
+        lg = download(L.navi_frame_tap_logits(self.h), np.float32, self.params.talker.vocab)
+        cp = download(L.navi_frame_tap_cp_logits(self.h), np.float32, 15 * self.params.cp.vocab).reshape(15, -1)
+        return hid, lg, cp
+
+    def step_out(self) -> np.ndarray:
+        return download(self.d_step_out, np.float32, self.hidden)
