@@ -160,6 +160,12 @@ navi_status navi_frame_set_taps(navi_frame *f, int32_t enabled);
 const float *navi_frame_tap_hidden(const navi_frame *f);
 const float *navi_frame_tap_logits(const navi_frame *f);
 const float *navi_frame_tap_cp_logits(const navi_frame *f);
+/* Phase profile (the reference's NAVI_FRAME_PROFILE, frame.hip:71-73, as a runtime switch):
+ * with profiling on, thread 0 of every block stamps the 100 MHz real-time counter at the start
+ * and end of every wait of the next runs; navi_frame_profile copies the first n_slots stamps of
+ * blocks 0..n_blocks-1 (slots past a block's last stamp are 0 for a fresh buffer). */
+navi_status navi_frame_set_profile(navi_frame *f, int32_t enabled);
+navi_status navi_frame_profile(const navi_frame *f, uint64_t *out, int32_t n_blocks, int32_t n_slots);
 
 #ifdef __cplusplus
 }

@@ -25,7 +25,7 @@ EXPORTS = [
     "navi_mem_alloc", "navi_mem_free", "navi_mem_h2d", "navi_mem_d2h", "navi_mem_d2d", "navi_mem_zero",
     "navi_frame_create", "navi_frame_destroy", "navi_frame_reset", "navi_frame_run", "navi_frame_step_out",
     "navi_frame_grid_blocks", "navi_frame_occupancy_per_mp", "navi_frame_set_taps", "navi_frame_tap_hidden",
-    "navi_frame_tap_logits", "navi_frame_tap_cp_logits",
+    "navi_frame_tap_logits", "navi_frame_tap_cp_logits", "navi_frame_set_profile", "navi_frame_profile",
 ]
 
 
@@ -122,6 +122,8 @@ def lib() -> C.CDLL:
     for f in ("navi_frame_grid_blocks", "navi_frame_occupancy_per_mp"):
         getattr(L, f).argtypes = [C.c_void_p]
     L.navi_frame_set_taps.argtypes = [C.c_void_p, C.c_int32]
+    L.navi_frame_set_profile.argtypes = [C.c_void_p, C.c_int32]
+    L.navi_frame_profile.argtypes = [C.c_void_p, C.c_void_p, C.c_int32, C.c_int32]
     for f in ("navi_frame_tap_hidden", "navi_frame_tap_logits", "navi_frame_tap_cp_logits"):
         getattr(L, f).argtypes = [C.c_void_p]
         getattr(L, f).restype = C.c_void_p
@@ -355,6 +357,15 @@ class Frame:
         lg = download(L.navi_frame_tap_logits(self.h), np.float32, self.params.talker.vocab)
         cp = download(L.navi_frame_tap_cp_logits(self.h), np.float32, 15 * self.params.cp.vocab).reshape(15, -1)
         return hid, lg, cp
+
+    def set_profile(self, on: bool):
+        _check(lib().navi_frame_set_profile(self.h, 1 if on else 0), what="navi_frame_set_profile")
+
+    def profile(self, n_blocks: int = 256, n_slots: int = 4096) -> np.ndarray:
+        """[n_blocks][n_slots] 100 MHz stamps of the last run with profiling on."""
+        out = np.zeros((n_blocks, n_slots), dtype=np.uint64)
+        _check(lib().navi_frame_profile(self.h, out.ctypes.data, n_blocks, n_slots), what="navi_frame_profile")
+        return out
 
     def step_out(self) -> np.ndarray:
         return download(self.d_step_out, np.float32, self.hidden)
