@@ -49,7 +49,45 @@ __device__ __forceinline__ float dot8(const uint4 w, const float *x, float acc) 
     return acc;
 }
 
-__device__ __forceinline__ uint4 ldg16(const uint16_t *p) { return *reinterpret_cast<const uint4 *>(p); }
+// Global memory accessed through address space 1, so the compiler emits global_* (counted by
+// vmcnt only) instead of flat_* instructions, which also count in lgkmcnt and would make every
+// LDS wait also wait for the in-flight weight stream.
+#define NAVI_GLOBAL __attribute__((address_space(1)))
+template <class T>
+__device__ __forceinline__ T gld(const T *p) { return *(const NAVI_GLOBAL T *) p; }
+template <class T>
+__device__ __forceinline__ void gst(T *p, T v) { *(NAVI_GLOBAL T *) p = v; }
+
+typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+// 16-byte global load as a native vector (a HIP uint4 struct copy through an address-space-1
+// pointer still lowers to flat_load).
+__device__ __forceinline__ uint4 ldg16(const uint16_t *p) {
+    const u32x4_t v = *(const NAVI_GLOBAL u32x4_t *) p;
+    uint4 r;
+    __builtin_memcpy(&r, &v, 16);
+    return r;
+}
+
+// Streaming (non-temporal) 16-byte load for data read once per pass: the weight stream must
+// not evict the kernel's code and mailboxes from L2.
+__device__ __forceinline__ uint4 ldg16_stream(const uint16_t *p) {
+    const u32x4_t v = __builtin_nontemporal_load((const NAVI_GLOBAL u32x4_t *) p);
+    uint4 r;
+    __builtin_memcpy(&r, &v, 16);
+    return r;
+}
+
+// A wave-uniform pointer moved to SGPRs, so accesses address it as saddr + a shared
+// per-lane VGPR offset instead of one 64-bit VGPR pair per call site.
+template <class T>
+__device__ __forceinline__ T *sgpr_ptr(T *p) {
+    const uint64_t u = reinterpret_cast<uint64_t>(p);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(u));
+    const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(u >> 32));
+    return reinterpret_cast<T *>((static_cast<uint64_t>(hi) << 32) | lo);
+}
 
 // ---------------------------------------------------------------------------
 // Tagged mailboxes. A 64-bit word holds {f32 value (low), u32 tag (high)} and
@@ -62,19 +100,19 @@ __device__ __forceinline__ uint4 ldg16(const uint16_t *p) { return *reinterpret_
 
 __device__ __forceinline__ void mb_put(uint64_t *p, float v, uint32_t tag) {
     const uint64_t w = (static_cast<uint64_t>(tag) << 32) | __float_as_uint(v);
-    __hip_atomic_store(p, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store((NAVI_GLOBAL uint64_t *) p, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 __device__ __forceinline__ uint64_t mb_peek(uint64_t *p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return __hip_atomic_load((NAVI_GLOBAL uint64_t *) p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 __device__ __forceinline__ uint32_t ctl_peek(uint32_t *p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return __hip_atomic_load((NAVI_GLOBAL uint32_t *) p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 __device__ __forceinline__ void ctl_put(uint32_t *p, uint32_t v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store((NAVI_GLOBAL uint32_t *) p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 __device__ __forceinline__ uint32_t tag_of(uint64_t w) { return static_cast<uint32_t>(w >> 32); }

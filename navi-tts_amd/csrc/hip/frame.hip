@@ -38,8 +38,8 @@ constexpr int H = 1024, NH = 16, NKV = 8, HD = 128, FF = 3072, VT = 3072, VC = 2
 constexpr int QD = NH * HD, KVD = NKV * HD, QKV = QD + 2 * KVD;
 constexpr int NCB = 16, CPH = NCB - 1, GRP = NH / NKV;
 constexpr int MAX_TL = 32, MAX_CL = 5;
-constexpr int MAX_POS = 4096;          // talker KV positions the score buffer holds
-constexpr int VCH = 64;                // V rows staged in LDS per chunk
+constexpr int MAX_POS = 4096;          // talker KV positions a frame may attend over
+constexpr int KCH = 256;               // talker K/V rows staged in LDS per chunk
 constexpr float ATT_SCALE = 0.08838834764831845f;   // 1/sqrt(128)
 
 static_assert(QKV / NB == 4 * NW, "q/k/v: 4 rows per wave");
@@ -69,16 +69,14 @@ struct Weights {
 };
 
 struct Args {
-    const Weights *W;
     uint64_t *mb;
     uint32_t *abort_word;
     int32_t *codes_out;
-    uint16_t *const *kc, *const *vc;   // per talker layer, device arrays
     int n_tl, n_cl, n_past, skip_talker;
     const float *hidden_in, *logits_in, *step_in, *trailing;
     float *step_out;
     uint8_t *seen;
-    float temperature, rep_penalty, cp_temperature;
+    float temperature, rep_penalty, cp_temperature, eps_t, eps_c;
     int top_k, cp_top_k, min_frames, frame_index, eos_id, suppress_from;
     uint64_t talker_seed, cp_seed, spin_cap;
     uint32_t epoch;
@@ -95,22 +93,37 @@ struct Regs {
     uint4 dn[6];
     uint4 th[3][2];    // talker head rows
     uint4 lm[2][2];    // cp lm head rows
+    float ln1[H / BT];   // next input RMSNorm weights of this thread's elements
+    float ln2[H / BT];   // next post-attention RMSNorm weights
+    float qkw;           // q_norm (waves 0-1) or k_norm (waves 2-3) weight of dim tid % 128
+    float fn[H / BT];    // final RMSNorm weights (talker norm, then the cp norm)
 };
 
 struct Smem {
     float x[2][H];                  // residual stream rows
     float xn[2][H];                 // normed rows
     union {
-        float big[2 * FF];          // att [T][QD] | h [T][FF]
-        struct { float lg[VT]; int idx[VT]; } samp;
-        uint16_t vch[VCH][HD];      // V rows staged for the output sum
+        struct {                    // talker attention: one chunk of cached K/V rows, f16,
+            uint16_t k[KCH][HD];    // 16-byte chunk c of row j stored at slot c ^ (j & 15)
+            uint16_t v[KCH][HD];
+        } tkv;
+        struct {
+            union {
+                float big[2 * FF];  // att [T][QD] | h [T][FF]
+                struct { float lg[VT]; int idx[VT]; } samp;
+            };
+            uint16_t ckv[2][MAX_CL][NCB][HD];   // this block's cp K/V (kv head blockIdx/2), whole frame
+        } m;
     } u;
     float part[2][6 * NW];          // gate/up dots before SiLU(g)*u
+    float invf[2][HD / 2];          // RoPE inverse frequencies (talker, cp)
+    LayerPtrs lp[MAX_TL + MAX_CL];  // weight pointers, copied once: a scalar load of the table in
+    const uint16_t *emb[CPH];       // global memory misses the scalar cache under the weight stream
+    const uint16_t *lmh[CPH];
     float red[4 * NW];
     float q[2][HD], k[2][HD], v[2][HD];
-    float sc[MAX_POS];              // attention probabilities
+    float sc[KCH];                  // attention weights of one key chunk (cp: [T][NCB])
     float opart[NW][HD];
-    uint16_t ckv[2][MAX_CL][NCB][HD];   // this block's cp K/V (kv head blockIdx/2)
     unsigned hist[256];
     int isel[4];
     int codes[NCB];
@@ -124,8 +137,16 @@ constexpr int PROF_SLOTS = 4096;
 #define PROF_MARK(a, S)                                                                         \
     do {                                                                                        \
         if ((a).prof && threadIdx.x == 0 && (S).prof_i < PROF_SLOTS)                            \
-            (a).prof[static_cast<size_t>(blockIdx.x) * PROF_SLOTS + (S).prof_i++] = wall_clock64(); \
+            gst((a).prof + static_cast<size_t>(blockIdx.x) * PROF_SLOTS + (S).prof_i++, static_cast<uint64_t>(wall_clock64())); \
     } while (0)
+
+// The weight table and the per-layer KV pointers are separate `const __restrict__` kernel
+// arguments so their loads are scalar (s_load, counted by lgkmcnt): a vector load here would
+// wait behind every in-flight weight prefetch (vmcnt retires in order).
+struct Ctx {
+    const Weights *__restrict__ W;
+    uint16_t *const *__restrict__ kv;    // [0, MAX_TL): K per layer, [MAX_TL, 2 MAX_TL): V
+};
 
 __device__ __forceinline__ int tid() { return static_cast<int>(threadIdx.x); }
 __device__ __forceinline__ int lane() { return static_cast<int>(threadIdx.x) & (WAVE - 1); }
@@ -183,11 +204,12 @@ template <int N, int CH>
 __device__ __forceinline__ bool gather(const Args &a, int off, uint32_t tag, float *dst, Smem &S) {
     static_assert(N % BT == 0 && N % CH == 0, "gather size");
     constexpr int PER = N / BT, NPROD = N / CH;
+    uint64_t *const mb = sgpr_ptr(a.mb + off);
     PROF_MARK(a, S);
     if (wave() == 0) {
         bool ok = true;
         for (int q = lane(); q < NPROD && ok; q += WAVE) {
-            uint64_t *p = a.mb + off + q * CH + CH - 1;
+            uint64_t *p = mb + q * CH + CH - 1;
             uint64_t w = mb_peek(p);
             ok = poll_word(a, p, tag, w);
         }
@@ -197,12 +219,12 @@ __device__ __forceinline__ bool gather(const Args &a, int off, uint32_t tag, flo
     if (S.fail) return false;
     uint64_t w[PER];
 #pragma unroll
-    for (int k = 0; k < PER; ++k) w[k] = mb_peek(a.mb + off + tid() + k * BT);
+    for (int k = 0; k < PER; ++k) w[k] = mb_peek(mb + tid() + k * BT);
     bool ok = true;
 #pragma unroll
     for (int k = 0; k < PER; ++k) {
         const int i = tid() + k * BT;
-        if (ok) ok = poll_word(a, a.mb + off + i, tag, w[k]);
+        if (ok) ok = poll_word(a, mb + i, tag, w[k]);
         dst[i] = val_of(w[k]);
     }
     if (!ok) S.fail = 1;
@@ -223,7 +245,7 @@ __device__ __forceinline__ bool gather_rows(const Args &a, int off, uint32_t tag
 // ---- RMSNorm of T rows (every block, redundantly) ---------------------------
 
 template <int T>
-__device__ __forceinline__ void rmsnorm_rows(const float (*x)[H], const float *w, float eps, float (*out)[H], Smem &S) {
+__device__ __forceinline__ void rmsnorm_rows(const float (*x)[H], const float (&w)[H / BT], float eps, float (*out)[H], Smem &S) {
     constexpr int PER = H / BT;
 #pragma unroll
     for (int t = 0; t < T; ++t) {
@@ -233,9 +255,15 @@ __device__ __forceinline__ void rmsnorm_rows(const float (*x)[H], const float *w
         ss = block_sum(ss, S);
         const float sc = rsqrtf(ss / static_cast<float>(H) + eps);
 #pragma unroll
-        for (int k = 0; k < PER; ++k) out[t][tid() + k * BT] = e[k] * sc * w[tid() + k * BT];
+        for (int k = 0; k < PER; ++k) out[t][tid() + k * BT] = e[k] * sc * w[k];
     }
     __syncthreads();
+}
+
+// This thread's RMSNorm weights (elements tid + k * BT).
+__device__ __forceinline__ void load_norm(float (&w)[H / BT], const float *g) {
+#pragma unroll
+    for (int k = 0; k < H / BT; ++k) w[k] = gld(g + tid() + k * BT);
 }
 
 // x fragment a lane multiplies with 512-col chunks: cols base + c*512 + lane*8 .. +8
@@ -243,8 +271,8 @@ template <int NC>
 __device__ __forceinline__ void xfrag(const float *x, int base, float (&xf)[NC][8]) {
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
-        const float4 p = *reinterpret_cast<const float4 *>(x + base + c * 512 + lane() * 8);
-        const float4 q = *reinterpret_cast<const float4 *>(x + base + c * 512 + lane() * 8 + 4);
+        const f32x4_t p = *reinterpret_cast<const f32x4_t *>(x + base + c * 512 + lane() * 8);
+        const f32x4_t q = *reinterpret_cast<const f32x4_t *>(x + base + c * 512 + lane() * 8 + 4);
         xf[c][0] = p.x; xf[c][1] = p.y; xf[c][2] = p.z; xf[c][3] = p.w;
         xf[c][4] = q.x; xf[c][5] = q.y; xf[c][6] = q.z; xf[c][7] = q.w;
     }
@@ -259,18 +287,21 @@ __device__ __forceinline__ void load_qkv(Regs &R, const LayerPtrs &L) {
     if (rb < QD) { M = L.wq; base = rb; }
     else if (rb < QD + KVD) { M = L.wk; base = rb - QD; }
     else { M = L.wv; base = rb - QD - KVD; }
+    M = sgpr_ptr(M + static_cast<size_t>(base) * H);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-        const uint16_t *p = M + static_cast<size_t>(base + wave() * 4 + r) * H + lane() * 8;
-        R.qkv[r][0] = ldg16(p);
-        R.qkv[r][1] = ldg16(p + 512);
+        const uint16_t *p = M + static_cast<size_t>(wave() * 4 + r) * H + lane() * 8;
+        R.qkv[r][0] = ldg16_stream(p);
+        R.qkv[r][1] = ldg16_stream(p + 512);
     }
+    load_norm(R.ln1, L.ln1);
+    R.qkw = gld((wave() < 2 ? L.qn : L.kn) + (tid() & (HD - 1)));
 }
 
 __device__ __forceinline__ void load_o(Regs &R, const LayerPtrs &L) {
-    const uint16_t *p = L.wo + static_cast<size_t>(blk() * (H / NB) + wave()) * QD + lane() * 8;
+    const uint16_t *p = sgpr_ptr(L.wo + static_cast<size_t>(blk() * (H / NB)) * QD) + static_cast<size_t>(wave()) * QD + lane() * 8;
 #pragma unroll
-    for (int c = 0; c < 4; ++c) R.o[c] = ldg16(p + c * 512);
+    for (int c = 0; c < 4; ++c) R.o[c] = ldg16_stream(p + c * 512);
 }
 
 __device__ __forceinline__ void load_gu(Regs &R, const LayerPtrs &L) {
@@ -278,26 +309,26 @@ __device__ __forceinline__ void load_gu(Regs &R, const LayerPtrs &L) {
 #pragma unroll
     for (int r = 0; r < 6; ++r) {
         const int vr = wave() * 6 + r;
-        const uint16_t *M = vr < RB ? L.wg : L.wu;
-        const int row = blk() * RB + (vr < RB ? vr : vr - RB);
-        const uint16_t *p = M + static_cast<size_t>(row) * H + lane() * 8;
-        R.gu[r][0] = ldg16(p);
-        R.gu[r][1] = ldg16(p + 512);
+        const uint16_t *M = sgpr_ptr((vr < RB ? L.wg : L.wu) + static_cast<size_t>(blk() * RB) * H);
+        const uint16_t *p = M + static_cast<size_t>(vr < RB ? vr : vr - RB) * H + lane() * 8;
+        R.gu[r][0] = ldg16_stream(p);
+        R.gu[r][1] = ldg16_stream(p + 512);
     }
+    load_norm(R.ln2, L.ln2);
 }
 
 __device__ __forceinline__ void load_dn(Regs &R, const LayerPtrs &L) {
-    const uint16_t *p = L.wd + static_cast<size_t>(blk() * (H / NB) + wave()) * FF + lane() * 8;
+    const uint16_t *p = sgpr_ptr(L.wd + static_cast<size_t>(blk() * (H / NB)) * FF) + static_cast<size_t>(wave()) * FF + lane() * 8;
 #pragma unroll
-    for (int c = 0; c < 6; ++c) R.dn[c] = ldg16(p + c * 512);
+    for (int c = 0; c < 6; ++c) R.dn[c] = ldg16_stream(p + c * 512);
 }
 
 __device__ __forceinline__ void load_th(Regs &R, const uint16_t *head) {
 #pragma unroll
     for (int r = 0; r < 3; ++r) {
         const uint16_t *p = head + static_cast<size_t>(blk() * (VT / NB) + wave() * 3 + r) * H + lane() * 8;
-        R.th[r][0] = ldg16(p);
-        R.th[r][1] = ldg16(p + 512);
+        R.th[r][0] = ldg16_stream(p);
+        R.th[r][1] = ldg16_stream(p + 512);
     }
 }
 
@@ -305,8 +336,8 @@ __device__ __forceinline__ void load_lm(Regs &R, const uint16_t *head) {
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
         const uint16_t *p = head + static_cast<size_t>(blk() * (VC / NB) + wave() * 2 + r) * H + lane() * 8;
-        R.lm[r][0] = ldg16(p);
-        R.lm[r][1] = ldg16(p + 512);
+        R.lm[r][0] = ldg16_stream(p);
+        R.lm[r][1] = ldg16_stream(p + 512);
     }
 }
 
@@ -327,7 +358,7 @@ __device__ __forceinline__ void qkv_phase(const Args &a, const Regs &R, Smem &S,
     }
 }
 
-// x2[row] = x[row] + Wo . att  (att gathered into S.u.big as [T][QD])
+// x2[row] = x[row] + Wo . att  (att gathered into S.u.m.big as [T][QD])
 template <int T>
 __device__ __forceinline__ void o_phase(const Args &a, const Regs &R, Smem &S, uint32_t tag) {
     const int row = blk() * (H / NB) + wave();
@@ -337,7 +368,7 @@ __device__ __forceinline__ void o_phase(const Args &a, const Regs &R, Smem &S, u
 #pragma unroll
         for (int c2 = 0; c2 < 4; c2 += 2) {
             float xf[2][8];
-            xfrag<2>(S.u.big + t * QD, c2 * 512, xf);
+            xfrag<2>(S.u.m.big + t * QD, c2 * 512, xf);
             acc = dot8(R.o[c2 + 1], xf[1], dot8(R.o[c2], xf[0], acc));
         }
         const float d = wave_sum(acc);
@@ -367,7 +398,7 @@ __device__ __forceinline__ void gu_phase(const Args &a, const Regs &R, Smem &S, 
     }
 }
 
-// x[row] = x2[row] + Wd . h  (x2 in S.x, h gathered into S.u.big as [T][FF])
+// x[row] = x2[row] + Wd . h  (x2 in S.x, h gathered into S.u.m.big as [T][FF])
 template <int T>
 __device__ __forceinline__ void down_phase(const Args &a, const Regs &R, Smem &S, uint32_t tag) {
     const int row = blk() * (H / NB) + wave();
@@ -377,7 +408,7 @@ __device__ __forceinline__ void down_phase(const Args &a, const Regs &R, Smem &S
 #pragma unroll
         for (int c2 = 0; c2 < 6; c2 += 2) {
             float xf[2][8];
-            xfrag<2>(S.u.big + t * FF, c2 * 512, xf);
+            xfrag<2>(S.u.m.big + t * FF, c2 * 512, xf);
             acc = dot8(R.dn[c2 + 1], xf[1], dot8(R.dn[c2], xf[0], acc));
         }
         const float d = wave_sum(acc);
@@ -387,19 +418,22 @@ __device__ __forceinline__ void down_phase(const Args &a, const Regs &R, Smem &S
 
 // ---- attention --------------------------------------------------------------
 
-// q/k head RMSNorm over 128 dims for nvec vectors, two at a time (waves 0-1 and 2-3).
-__device__ __forceinline__ void head_norms(float *const *vec, const float *const *w, int nvec, float eps, Smem &S) {
-    for (int v0 = 0; v0 < nvec; v0 += 2) {
-        const int vi = v0 + (wave() >> 1), d = tid() & (HD - 1);
-        float e = 0.f;
-        if (vi < nvec) e = vec[vi][d];
+// q/k head RMSNorm over 128 dims of T rows' q and k vectors, one row at a time: waves
+// 0-1 normalise S.q[t], waves 2-3 S.k[t]; `w` is this thread's q_norm / k_norm weight.
+template <int T>
+__device__ __forceinline__ void head_norms(float w, float eps, Smem &S) {
+    const int d = tid() & (HD - 1);
+    const bool isk = wave() >= 2;
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+        const float e = isk ? S.k[t][d] : S.q[t][d];
         const float ps = wave_sum(e * e);
         if (lane() == 0) S.red[wave()] = ps;
         __syncthreads();
-        if (vi < nvec) {
-            const float ss = S.red[(wave() >> 1) * 2] + S.red[(wave() >> 1) * 2 + 1];
-            vec[vi][d] = e * rsqrtf(ss / static_cast<float>(HD) + eps) * w[vi][d];
-        }
+        const float ss = S.red[(wave() >> 1) * 2] + S.red[(wave() >> 1) * 2 + 1];
+        const float v = e * rsqrtf(ss / static_cast<float>(HD) + eps) * w;
+        if (isk) S.k[t][d] = v;
+        else S.q[t][d] = v;
         __syncthreads();
     }
 }
@@ -426,24 +460,44 @@ __device__ __forceinline__ bool gather_head(const Args &a, int h, int g, uint32_
     return S.fail == 0;
 }
 
-// Talker attention for q head h = blockIdx (one row at position pos):
-// norms + RoPE + f16 K/V store (even heads) + softmax over keys 0..pos + V sum.
-__device__ bool talker_attention(const Args &a, const LayerPtrs &L, int il, uint32_t tag_qkv, uint32_t tag_att, Smem &S) {
+typedef __attribute__((address_space(1))) void gmem_t;
+typedef __attribute__((address_space(3))) void lmem_t;
+
+__device__ __forceinline__ void wait_vm_all() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// LDS-DMA (global_load_lds_dwordx4) of cached K and V rows [j0, j0 + n), n <= KCH, of one kv head
+// into S.u.tkv. A wave instruction moves 1 KB = 4 rows; lane l fills LDS slot l % 16 of row l / 16
+// with the row's 16-byte chunk (l % 16) ^ (row & 15). No VGPRs; completion is the wave's vmcnt.
+__device__ __forceinline__ void stage_kv(const uint16_t *Kc, const uint16_t *Vc, int j0, int n, Smem &S) {
+    const int nblk = (n + 3) / 4;
+    for (int bi = wave(); bi < 2 * nblk; bi += NW) {
+        const bool isv = bi >= nblk;
+        const int r4 = (isv ? bi - nblk : bi) * 4, jj = r4 + (lane() >> 4), c = (lane() & 15) ^ (jj & 15);
+        const int jsrc = j0 + min(jj, n - 1);
+        const uint16_t *src = (isv ? Vc : Kc) + static_cast<size_t>(jsrc) * KVD + c * 8;
+        uint16_t *dst = isv ? &S.u.tkv.v[r4][0] : &S.u.tkv.k[r4][0];
+        __builtin_amdgcn_global_load_lds((gmem_t *) src, (lmem_t *) dst, 16, 0, 0);
+    }
+}
+
+// Talker attention for q head h = blockIdx (one row at position pos): q/k head norms, RoPE,
+// f16 K/V store at pos (even heads), softmax over keys 0..pos and the V sum. Cached keys are
+// staged in LDS by DMA in KCH-key chunks, the first chunk while this step's q/k/v are in
+// flight; chunks combine with the running-max softmax (one chunk up to pos = KCH).
+__device__ bool talker_attention(const Args &a, const Ctx &cx, float qkw, int il, uint32_t tag_qkv, uint32_t tag_att, Smem &S) {
     const int h = blk(), g = h / GRP, pos = a.n_past;
-    const uint16_t *Kc = a.kc[il] + g * HD;
-    uint16_t *Vc = a.vc[il] + g * HD;
+    uint16_t *const Kbase = cx.kv[il], *const Vbase = cx.kv[MAX_TL + il];
+    const uint16_t *Kc = Kbase + g * HD;
+    uint16_t *Vc = Vbase + g * HD;
+    if (pos > 0) stage_kv(Kc, Vc, 0, min(pos, KCH), S);
     PROF_MARK(a, S);
     if (!gather_head<1>(a, h, g, tag_qkv, S)) return false;
     PROF_MARK(a, S);
-    {
-        float *const vec[2] = {S.q[0], S.k[0]};
-        const float *const w[2] = {L.qn, L.kn};
-        head_norms(vec, w, 2, a.W->eps_t, S);
-    }
+    head_norms<1>(qkw, a.eps_t, S);
     if (tid() < HD) {
         const int i = tid() & (HD / 2 - 1);
         float s, c;
-        sincosf(static_cast<float>(pos) * a.W->invf_t[i], &s, &c);
+        sincosf(static_cast<float>(pos) * S.invf[0][i], &s, &c);
         if (tid() < HD / 2) {
             rope_pair(S.q[0], i, c, s);
         } else {
@@ -452,76 +506,73 @@ __device__ bool talker_attention(const Args &a, const LayerPtrs &L, int il, uint
             S.k[0][i] = k0;
             S.k[0][i + HD / 2] = k1;
             if ((h & 1) == 0) {
-                uint16_t *kw = a.kc[il] + static_cast<size_t>(pos) * KVD + g * HD;
-                kw[i] = f2h(k0);
-                kw[i + HD / 2] = f2h(k1);
+                uint16_t *kw = Kbase + static_cast<size_t>(pos) * KVD + g * HD;
+                gst(kw + i, f2h(k0));
+                gst(kw + i + HD / 2, f2h(k1));
             }
         }
     } else {
         const int d = tid() - HD;
         const float v = round_f16(S.v[0][d]);
         S.v[0][d] = v;
-        if ((h & 1) == 0) Vc[static_cast<size_t>(pos) * KVD + d] = f2h(v);
+        if ((h & 1) == 0) gst(Vc + static_cast<size_t>(pos) * KVD + d, f2h(v));
     }
-    __syncthreads();
-    // scores: one key per thread per sweep
-    for (int jb = 0; jb <= pos; jb += BT) {
-        const int j = jb + tid();
-        if (j <= pos) {
+    float m = -INFINITY, l = 0.f, acc0 = 0.f, acc1 = 0.f;
+    PROF_MARK(a, S);
+    for (int c0 = 0; c0 <= pos; c0 += KCH) {
+        const int n = min(KCH, pos + 1 - c0);
+        if (c0 > 0) {
+            __syncthreads();                               // previous chunk fully consumed
+            stage_kv(Kc, Vc, c0, min(KCH, pos - c0), S);
+        }
+        wait_vm_all();
+        __syncthreads();
+        PROF_MARK(a, S);
+        // scores: thread jj scores key c0 + jj
+        float sj = -INFINITY;
+        if (tid() < n) {
+            const int jj = tid();
             float acc = 0.f;
-            if (j == pos) {
+            if (c0 + jj == pos) {
 #pragma unroll 8
                 for (int d = 0; d < HD; ++d) acc = fmaf(S.q[0][d], S.k[0][d], acc);
             } else {
-                uint4 kk[16];
 #pragma unroll
-                for (int i = 0; i < 16; ++i) kk[i] = ldg16(Kc + static_cast<size_t>(j) * KVD + i * 8);
-#pragma unroll
-                for (int i = 0; i < 16; ++i) acc = dot8(kk[i], &S.q[0][i * 8], acc);
+                for (int c = 0; c < HD / 8; ++c) {
+                    const u32x4_t kv4 = *reinterpret_cast<const u32x4_t *>(&S.u.tkv.k[jj][(c ^ (jj & 15)) * 8]);
+                    uint4 kk;
+                    __builtin_memcpy(&kk, &kv4, 16);
+                    acc = dot8(kk, &S.q[0][c * 8], acc);
+                }
             }
-            S.sc[j] = acc * ATT_SCALE;
+            sj = acc * ATT_SCALE;
         }
-    }
-    __syncthreads();
-    float m = -INFINITY;
-    for (int j = tid(); j <= pos; j += BT) m = fmaxf(m, S.sc[j]);
-    m = block_max(m, S);
-    float sum = 0.f;
-    for (int j = tid(); j <= pos; j += BT) {
-        const float e = expf(S.sc[j] - m);
-        S.sc[j] = e;
-        sum += e;
-    }
-    sum = block_sum(sum, S);
-    const float inv = 1.f / sum;
-    for (int j = tid(); j <= pos; j += BT) S.sc[j] *= inv;
-    __syncthreads();
-    // output: wave w sums keys j = w mod NW; lane owns dims 2l, 2l+1
-    float acc0 = 0.f, acc1 = 0.f;
-    for (int c0 = 0; c0 <= pos; c0 += VCH) {
-        const int n = min(VCH, pos + 1 - c0);
-        for (int i = tid(); i < n * (HD / 8); i += BT) {
-            const int r = i / (HD / 8), q8 = (i % (HD / 8)) * 8, j = c0 + r;
-            uint4 val;
-            if (j < pos) {
-                val = ldg16(Vc + static_cast<size_t>(j) * KVD + q8);
+        const float mn = fmaxf(m, block_max(sj, S));
+        const float e = tid() < n ? expf(sj - mn) : 0.f;
+        S.sc[tid()] = e;
+        const float alpha = expf(m - mn);                  // 0 for the first chunk
+        l = l * alpha + block_sum(e, S);                   // block_sum's barriers publish S.sc
+        acc0 *= alpha;
+        acc1 *= alpha;
+        m = mn;
+        PROF_MARK(a, S);
+        // V sum: wave w takes keys w, w + NW, ...; lane owns dims 2 lane, 2 lane + 1
+        const int slot8 = 2 * (lane() & 3);
+        for (int jj = wave(); jj < n; jj += NW) {
+            const float p = S.sc[jj];
+            float v0, v1;
+            if (c0 + jj == pos) {
+                v0 = S.v[0][2 * lane()];
+                v1 = S.v[0][2 * lane() + 1];
             } else {
-                uint16_t hv[8];
-#pragma unroll
-                for (int e = 0; e < 8; ++e) hv[e] = f2h(S.v[0][q8 + e]);
-                __builtin_memcpy(&val, hv, 16);
+                half2_t hv;
+                __builtin_memcpy(&hv, &S.u.tkv.v[jj][((lane() >> 2) ^ (jj & 15)) * 8 + slot8], 4);
+                v0 = static_cast<float>(hv[0]);
+                v1 = static_cast<float>(hv[1]);
             }
-            *reinterpret_cast<uint4 *>(&S.u.vch[r][q8]) = val;
+            acc0 = fmaf(p, v0, acc0);
+            acc1 = fmaf(p, v1, acc1);
         }
-        __syncthreads();
-        for (int r = wave(); r < n; r += NW) {
-            const float p = S.sc[c0 + r];
-            half2_t hv;
-            __builtin_memcpy(&hv, &S.u.vch[r][2 * lane()], 4);
-            acc0 = fmaf(p, static_cast<float>(hv[0]), acc0);
-            acc1 = fmaf(p, static_cast<float>(hv[1]), acc1);
-        }
-        __syncthreads();
     }
     S.opart[wave()][2 * lane()] = acc0;
     S.opart[wave()][2 * lane() + 1] = acc1;
@@ -530,7 +581,7 @@ __device__ bool talker_attention(const Args &a, const LayerPtrs &L, int il, uint
         float o = 0.f;
 #pragma unroll
         for (int w = 0; w < NW; ++w) o += S.opart[w][tid()];
-        mb_put(a.mb + MB_ATT + h * HD + tid(), o, tag_att);
+        mb_put(a.mb + MB_ATT + h * HD + tid(), o * (1.f / l), tag_att);
     }
     PROF_MARK(a, S);
     return true;
@@ -539,36 +590,32 @@ __device__ bool talker_attention(const Args &a, const LayerPtrs &L, int il, uint
 // Code-predictor attention for q head h = blockIdx over T rows at positions p0..p0+T-1;
 // K/V of this block's kv head live in S.ckv for the whole frame.
 template <int T>
-__device__ bool cp_attention(const Args &a, const LayerPtrs &L, int il, int p0, uint32_t tag_qkv, uint32_t tag_att, Smem &S) {
+__device__ bool cp_attention(const Args &a, float qkw, int il, int p0, uint32_t tag_qkv, uint32_t tag_att, Smem &S) {
     const int h = blk(), g = h / GRP;
     PROF_MARK(a, S);
     if (!gather_head<T>(a, h, g, tag_qkv, S)) return false;
     PROF_MARK(a, S);
-    {
-        float *const vec[4] = {S.q[0], S.k[0], S.q[T - 1], S.k[T - 1]};
-        const float *const w[4] = {L.qn, L.kn, L.qn, L.kn};
-        head_norms(vec, w, 2 * T, a.W->eps_c, S);
-    }
+    head_norms<T>(qkw, a.eps_c, S);
     for (int i = tid(); i < T * HD; i += BT) {          // q and k pairs of each row
         const int t = i / HD, isk = (i / (HD / 2)) & 1, pr = i & (HD / 2 - 1);
         float s, c;
-        sincosf(static_cast<float>(p0 + t) * a.W->invf_c[pr], &s, &c);
+        sincosf(static_cast<float>(p0 + t) * S.invf[1][pr], &s, &c);
         if (!isk) {
             rope_pair(S.q[t], pr, c, s);
         } else {
             rope_pair(S.k[t], pr, c, s);
-            S.ckv[0][il][p0 + t][pr] = f2h(S.k[t][pr]);
-            S.ckv[0][il][p0 + t][pr + HD / 2] = f2h(S.k[t][pr + HD / 2]);
+            S.u.m.ckv[0][il][p0 + t][pr] = f2h(S.k[t][pr]);
+            S.u.m.ckv[0][il][p0 + t][pr + HD / 2] = f2h(S.k[t][pr + HD / 2]);
         }
     }
-    for (int i = tid(); i < T * HD; i += BT) S.ckv[1][il][p0 + i / HD][i % HD] = f2h(S.v[i / HD][i % HD]);
+    for (int i = tid(); i < T * HD; i += BT) S.u.m.ckv[1][il][p0 + i / HD][i % HD] = f2h(S.v[i / HD][i % HD]);
     __syncthreads();
     // scores: wave w takes (row, key) pairs w, w+NW, ...
     for (int pr = wave(); pr < T * NCB; pr += NW) {
         const int t = pr / NCB, j = pr % NCB;
         if (j > p0 + t) continue;
         half2_t kk;
-        __builtin_memcpy(&kk, &S.ckv[0][il][j][2 * lane()], 4);
+        __builtin_memcpy(&kk, &S.u.m.ckv[0][il][j][2 * lane()], 4);
         const float d = wave_sum(fmaf(S.q[t][2 * lane()], static_cast<float>(kk[0]), S.q[t][2 * lane() + 1] * static_cast<float>(kk[1])));
         if (lane() == 0) S.sc[t * NCB + j] = d * ATT_SCALE;
     }
@@ -585,7 +632,7 @@ __device__ bool cp_attention(const Args &a, const LayerPtrs &L, int il, int p0, 
     for (int i = tid(); i < T * HD; i += BT) {
         const int t = i / HD, d = i % HD, n = p0 + t + 1;
         float o = 0.f;
-        for (int j = 0; j < n; ++j) o = fmaf(S.sc[t * NCB + j], h2f(S.ckv[1][il][j][d]), o);
+        for (int j = 0; j < n; ++j) o = fmaf(S.sc[t * NCB + j], h2f(S.u.m.ckv[1][il][j][d]), o);
         mb_put(a.mb + MB_ATT + t * QD + h * HD + d, o, tag_att);
     }
     PROF_MARK(a, S);
@@ -653,7 +700,7 @@ __device__ __forceinline__ float kth_largest(const float (&x)[PER], int k, Smem 
     return key_float(prefix);
 }
 
-// Chooses an index from the V values in S.u.samp.lg (already modified for the talker).
+// Chooses an index from the V values in S.u.m.samp.lg (already modified for the talker).
 // Greedy: argmax, lowest index on ties. Else: /temperature, exact top-k threshold
 // (values >= the k-th largest survive), e^(v - max), PCG32 draw over the survivors
 // in index order (frame.hip:258-296 semantics: f32 running sum, no contraction).
@@ -663,7 +710,7 @@ __device__ __forceinline__ int block_sample(float temperature, int top_k, uint64
     float x[PER];
     const int base = tid() * PER;
 #pragma unroll
-    for (int i = 0; i < PER; ++i) x[i] = S.u.samp.lg[base + i];
+    for (int i = 0; i < PER; ++i) x[i] = S.u.m.samp.lg[base + i];
     __syncthreads();
     if (temperature <= 0.f) {
         float bv = -INFINITY;
@@ -676,13 +723,13 @@ __device__ __forceinline__ int block_sample(float temperature, int top_k, uint64
             const int oi = __shfl_xor(bi, o, WAVE);
             if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
         }
-        if (lane() == 0) { S.red[wave()] = bv; S.u.samp.idx[wave()] = bi; }
+        if (lane() == 0) { S.red[wave()] = bv; S.u.m.samp.idx[wave()] = bi; }
         __syncthreads();
         if (tid() == 0) {
             float v = S.red[0];
-            int i0 = S.u.samp.idx[0];
+            int i0 = S.u.m.samp.idx[0];
             for (int w = 1; w < NW; ++w)
-                if (S.red[w] > v || (S.red[w] == v && S.u.samp.idx[w] < i0)) { v = S.red[w]; i0 = S.u.samp.idx[w]; }
+                if (S.red[w] > v || (S.red[w] == v && S.u.m.samp.idx[w] < i0)) { v = S.red[w]; i0 = S.u.m.samp.idx[w]; }
             S.isel[2] = i0;
         }
         __syncthreads();
@@ -719,8 +766,8 @@ __device__ __forceinline__ int block_sample(float temperature, int top_k, uint64
     for (int w = 0; w < NW; ++w) n_nz += static_cast<int>(S.hist[w]);
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
-        S.u.samp.lg[base + i] = x[i];
-        if (x[i] != 0.f) S.u.samp.idx[off++] = base + i;
+        S.u.m.samp.lg[base + i] = x[i];
+        if (x[i] != 0.f) S.u.m.samp.idx[off++] = base + i;
     }
     __syncthreads();
     if (tid() == 0) {
@@ -731,8 +778,8 @@ __device__ __forceinline__ int block_sample(float temperature, int top_k, uint64
         int chosen = V - 1;
         float cum = 0.f;
         for (int j = 0; j < n_nz; ++j) {
-            const int i = S.u.samp.idx[j];
-            cum = __fadd_rn(cum, __fmul_rn(S.u.samp.lg[i], inv));
+            const int i = S.u.m.samp.idx[j];
+            cum = __fadd_rn(cum, __fmul_rn(S.u.m.samp.lg[i], inv));
             if (cum >= u) { chosen = i; break; }
         }
         S.isel[2] = chosen;
@@ -750,77 +797,98 @@ struct Seq {           // tags: epoch + running phase number, identical in every
     __device__ uint32_t next() { return base + (++n); }
 };
 
-__device__ __forceinline__ const LayerPtrs &layer_at(const Args &a, int gi) {
-    return gi < a.n_tl ? a.W->tl[gi] : a.W->cp[(gi - a.n_tl) % a.n_cl];
+__device__ __forceinline__ const LayerPtrs &layer_at(const Args &a, const Smem &S, int gi) {
+    return S.lp[gi < a.n_tl ? gi : MAX_TL + (gi - a.n_tl) % a.n_cl];
 }
 
 // One decoder layer over T rows held in S.x (its input); leaves its output in S.x.
 // gi: global layer index (talker layers, then n_cl cp layers per cp pass).
 template <int T, bool TALKER>
-__device__ __forceinline__ bool run_layer(const Args &a, Regs &R, int gi, int p0, Seq &seq, Smem &S) {
-    const LayerPtrs &L = layer_at(a, gi);
+__device__ __forceinline__ bool run_layer(const Args &a, const Ctx &cx, Regs &R, int gi, int p0, Seq &seq, Smem &S,
+                                          const uint16_t *head = nullptr) {
     const int n_total = a.n_tl + CPH * a.n_cl;
     const bool has_next = gi + 1 < n_total;
-    const LayerPtrs &N = layer_at(a, has_next ? gi + 1 : gi);
-    const float eps = TALKER ? a.W->eps_t : a.W->eps_c;
+    const LayerPtrs &N = layer_at(a, S, has_next ? gi + 1 : gi);
+    const float eps = TALKER ? a.eps_t : a.eps_c;
 
-    rmsnorm_rows<T>(S.x, L.ln1, eps, S.xn, S);
+    rmsnorm_rows<T>(S.x, R.ln1, eps, S.xn, S);
     const uint32_t t_qkv = seq.next();
     qkv_phase<T>(a, R, S, t_qkv);
+    const float qkw = R.qkw;     // this layer's q/k norm weight; the prefetch below replaces it
     if (has_next) load_qkv(R, N);
 
     const uint32_t t_att = seq.next();
     if (blk() < NH) {
         bool ok;
-        if constexpr (TALKER) ok = talker_attention(a, L, gi, t_qkv, t_att, S);
-        else ok = cp_attention<T>(a, L, (gi - a.n_tl) % a.n_cl, p0, t_qkv, t_att, S);
+        if constexpr (TALKER) ok = talker_attention(a, cx, qkw, gi, t_qkv, t_att, S);
+        else ok = cp_attention<T>(a, qkw, (gi - a.n_tl) % a.n_cl, p0, t_qkv, t_att, S);
         if (!ok) return false;
     }
-    if (!gather_rows<T, QD, HD>(a, MB_ATT, t_att, S.u.big, S)) return false;
+    if (!gather_rows<T, QD, HD>(a, MB_ATT, t_att, S.u.m.big, S)) return false;
     const uint32_t t_x2 = seq.next();
     o_phase<T>(a, R, S, t_x2);
     if (has_next) load_o(R, N);
 
     if (!gather_rows<T, H, H / NB>(a, MB_X2, t_x2, &S.x[0][0], S)) return false;
-    rmsnorm_rows<T>(S.x, L.ln2, eps, S.xn, S);
+    rmsnorm_rows<T>(S.x, R.ln2, eps, S.xn, S);
     const uint32_t t_h = seq.next();
     gu_phase<T>(a, R, S, t_h);
     if (has_next) load_gu(R, N);
 
-    if (!gather_rows<T, FF, FF / NB>(a, MB_H, t_h, S.u.big, S)) return false;
+    if (!gather_rows<T, FF, FF / NB>(a, MB_H, t_h, S.u.m.big, S)) return false;
     const uint32_t t_x = seq.next();
     down_phase<T>(a, R, S, t_x);
     if (has_next) load_dn(R, N);
+    if (head) {                  // the pass's head slice, issued one phase before it is needed
+        if constexpr (TALKER) load_th(R, head);
+        else load_lm(R, head);
+    }
 
     return gather_rows<T, H, H / NB>(a, MB_X, t_x, &S.x[0][0], S);
 }
 
 __device__ __forceinline__ void load_row_f16(const uint16_t *src, float *dst) {
-    for (int i = tid(); i < H; i += BT) dst[i] = h2f(src[i]);
+    for (int i = tid(); i < H; i += BT) dst[i] = h2f(gld(src + i));
 }
 
-__global__ void __launch_bounds__(BT, 1) k_frame(Args a) {
+__global__ void __launch_bounds__(BT, 1) k_frame(Args a, const Weights *__restrict__ Wp, uint16_t *const *__restrict__ kvp) {
     __shared__ Smem S;
     if (tid() == 0) { S.fail = 0; S.prof_i = 0; }
+    const Ctx cx{Wp, kvp};
+    const Weights &W = *Wp;
     Seq seq{a.epoch, 0};
     Regs R;
-    const Weights &W = *a.W;
+    // small per-thread state first: nothing is in flight yet, so these loads drain nothing
+    if (tid() < HD / 2) S.invf[0][tid()] = gld(W.invf_t + tid());
+    else if (tid() < HD) S.invf[1][tid() - HD / 2] = gld(W.invf_c + tid() - HD / 2);
+    {
+        constexpr int NP = static_cast<int>(sizeof(LayerPtrs) / sizeof(void *));
+        const void *const *src_t = reinterpret_cast<const void *const *>(W.tl);
+        const void *const *src_c = reinterpret_cast<const void *const *>(W.cp);
+        const void **dst = reinterpret_cast<const void **>(S.lp);
+        for (int i = tid(); i < (MAX_TL + MAX_CL) * NP; i += BT)
+            dst[i] = i < MAX_TL * NP ? gld(src_t + i) : gld(src_c + i - MAX_TL * NP);
+        if (tid() < CPH) { S.emb[tid()] = gld(W.cp_emb + tid()); S.lmh[tid()] = gld(W.lm_head + tid()); }
+    }
+    __syncthreads();
+    uint32_t seen_bits = 0;
+    for (int k = 0; k < VT / BT; ++k) seen_bits |= (gld(a.seen + tid() + k * BT) ? 1u : 0u) << k;
+    load_norm(R.fn, a.skip_talker ? W.cp_norm : W.tl_norm);
     const int first = a.skip_talker ? a.n_tl : 0;
     {
-        const LayerPtrs &L0 = layer_at(a, first);
+        const LayerPtrs &L0 = layer_at(a, S, first);
         load_qkv(R, L0); load_o(R, L0); load_gu(R, L0); load_dn(R, L0);
     }
     __syncthreads();
 
     // ---- talker step (or frame 0's prefill outputs) ----
     if (!a.skip_talker) {
-        for (int i = tid(); i < H; i += BT) S.x[0][i] = a.step_in[i];
+        for (int i = tid(); i < H; i += BT) S.x[0][i] = gld(a.step_in + i);
         __syncthreads();
-        for (int il = 0; il < a.n_tl; ++il) {
-            if (il == a.n_tl - 1) load_th(R, W.codec_head);
-            if (!run_layer<1, true>(a, R, il, a.n_past, seq, S)) return;
-        }
-        rmsnorm_rows<1>(S.x, W.tl_norm, W.eps_t, S.xn, S);
+        for (int il = 0; il < a.n_tl; ++il)
+            if (!run_layer<1, true>(a, cx, R, il, a.n_past, seq, S, il == a.n_tl - 1 ? W.codec_head : nullptr)) return;
+        rmsnorm_rows<1>(S.x, R.fn, a.eps_t, S.xn, S);
+        load_norm(R.fn, W.cp_norm);
         const uint32_t t_lg = seq.next();
         {
             float xf[2][8];
@@ -831,26 +899,26 @@ __global__ void __launch_bounds__(BT, 1) k_frame(Args a) {
                 if (lane() == r) mb_put(a.mb + MB_LG + blk() * (VT / NB) + wave() * 3 + r, d, t_lg);
             }
         }
-        load_lm(R, W.lm_head[0]);
-        if (!gather<VT, VT / NB>(a, MB_LG, t_lg, S.u.samp.lg, S)) return;
+        if (!gather<VT, VT / NB>(a, MB_LG, t_lg, S.u.m.samp.lg, S)) return;
     } else {
-        for (int i = tid(); i < H; i += BT) S.xn[0][i] = a.hidden_in[i];
-        for (int i = tid(); i < VT; i += BT) S.u.samp.lg[i] = a.logits_in[i];
-        load_lm(R, W.lm_head[0]);
+        for (int i = tid(); i < H; i += BT) S.xn[0][i] = gld(a.hidden_in + i);
+        for (int i = tid(); i < VT; i += BT) S.u.m.samp.lg[i] = gld(a.logits_in + i);
         __syncthreads();
     }
     if (a.tap_hidden && blk() == 0) {
-        for (int i = tid(); i < H; i += BT) a.tap_hidden[i] = S.xn[0][i];
-        for (int i = tid(); i < VT; i += BT) a.tap_logits[i] = S.u.samp.lg[i];
+        for (int i = tid(); i < H; i += BT) gst(a.tap_hidden + i, S.xn[0][i]);
+        for (int i = tid(); i < VT; i += BT) gst(a.tap_logits + i, S.u.m.samp.lg[i]);
     }
 
     // ---- codebook 0: suppression, min-frames EOS, repetition penalty (frame.hip:413-419) ----
-    for (int i = tid(); i < VT; i += BT) {
-        float v = S.u.samp.lg[i];
+#pragma unroll
+    for (int k = 0; k < VT / BT; ++k) {
+        const int i = tid() + k * BT;
+        float v = S.u.m.samp.lg[i];
         if (i >= a.suppress_from && i != a.eos_id) v = -INFINITY;
         else if (i == a.eos_id && a.frame_index < a.min_frames) v = -INFINITY;
-        else if (a.rep_penalty > 0.f && a.seen[i]) v = v > 0.f ? v / a.rep_penalty : v * a.rep_penalty;
-        S.u.samp.lg[i] = v;
+        else if (a.rep_penalty > 0.f && ((seen_bits >> k) & 1u)) v = v > 0.f ? v / a.rep_penalty : v * a.rep_penalty;
+        S.u.m.samp.lg[i] = v;
     }
     __syncthreads();
     PROF_MARK(a, S);
@@ -862,18 +930,18 @@ __global__ void __launch_bounds__(BT, 1) k_frame(Args a) {
     int gi = a.n_tl;
     for (int i = tid(); i < H; i += BT) {
         S.x[0][i] = S.xn[0][i];
-        S.x[1][i] = h2f(W.codec_emb[static_cast<size_t>(cb0) * H + i]);
+        S.x[1][i] = h2f(gld(W.codec_emb + static_cast<size_t>(cb0) * H + i));
     }
     __syncthreads();
     for (int il = 0; il < a.n_cl; ++il, ++gi)
-        if (!run_layer<2, false>(a, R, gi, 0, seq, S)) return;
+        if (!run_layer<2, false>(a, cx, R, gi, 0, seq, S, il == a.n_cl - 1 ? S.lmh[0] : nullptr)) return;
     for (int pos = 1; pos < NCB; ++pos) {
         if (pos > 1) {
             for (int il = 0; il < a.n_cl; ++il, ++gi)
-                if (!run_layer<1, false>(a, R, gi, pos, seq, S)) return;
+                if (!run_layer<1, false>(a, cx, R, gi, pos, seq, S, il == a.n_cl - 1 ? S.lmh[pos - 1] : nullptr)) return;
         }
         const int row = pos == 1 ? 1 : 0;
-        rmsnorm_rows<1>(reinterpret_cast<const float (*)[H]>(S.x[row]), W.cp_norm, W.eps_c, S.xn, S);
+        rmsnorm_rows<1>(reinterpret_cast<const float (*)[H]>(S.x[row]), R.fn, a.eps_c, S.xn, S);
         const uint32_t t_lg = seq.next();
         {
             float xf[2][8];
@@ -884,10 +952,9 @@ __global__ void __launch_bounds__(BT, 1) k_frame(Args a) {
                 if (lane() == r) mb_put(a.mb + MB_LG + blk() * (VC / NB) + wave() * 2 + r, d, t_lg);
             }
         }
-        if (pos + 1 < NCB) load_lm(R, W.lm_head[pos]);
-        if (!gather<VC, VC / NB>(a, MB_LG, t_lg, S.u.samp.lg, S)) return;
+        if (!gather<VC, VC / NB>(a, MB_LG, t_lg, S.u.m.samp.lg, S)) return;
         if (a.tap_cp_logits && blk() == 0) {
-            for (int i = tid(); i < VC; i += BT) a.tap_cp_logits[(pos - 1) * VC + i] = S.u.samp.lg[i];
+            for (int i = tid(); i < VC; i += BT) gst(a.tap_cp_logits + (pos - 1) * VC + i, S.u.m.samp.lg[i]);
             __syncthreads();
         }
         PROF_MARK(a, S);
@@ -895,7 +962,7 @@ __global__ void __launch_bounds__(BT, 1) k_frame(Args a) {
         PROF_MARK(a, S);
         if (tid() == 0) S.codes[pos] = code;
         if (pos + 1 < NCB) {
-            load_row_f16(W.cp_emb[pos - 1] + static_cast<size_t>(code) * H, S.x[0]);
+            load_row_f16(S.emb[pos - 1] + static_cast<size_t>(code) * H, S.x[0]);
             __syncthreads();
         }
     }
@@ -904,14 +971,14 @@ __global__ void __launch_bounds__(BT, 1) k_frame(Args a) {
     __syncthreads();
     if (tid() < H / NB) {
         const int i = blk() * (H / NB) + tid();
-        float v = h2f(W.codec_emb[static_cast<size_t>(S.codes[0]) * H + i]);
-        for (int cb = 0; cb < CPH; ++cb) v += h2f(W.cp_emb[cb][static_cast<size_t>(S.codes[cb + 1]) * H + i]);
-        a.step_out[i] = v + a.trailing[i];
+        float v = h2f(gld(W.codec_emb + static_cast<size_t>(S.codes[0]) * H + i));
+        for (int cb = 0; cb < CPH; ++cb) v += h2f(gld(S.emb[cb] + static_cast<size_t>(S.codes[cb + 1]) * H + i));
+        gst(a.step_out + i, v + gld(a.trailing + i));
     }
     PROF_MARK(a, S);
     if (blk() == 0 && tid() == 0) {
-        for (int c = 0; c < NCB; ++c) a.codes_out[c] = S.codes[c];
-        if (S.codes[0] != a.eos_id) a.seen[S.codes[0]] = 1u;
+        for (int c = 0; c < NCB; ++c) gst(a.codes_out + c, static_cast<int32_t>(S.codes[c]));
+        if (S.codes[0] != a.eos_id) gst(a.seen + S.codes[0], static_cast<uint8_t>(1u));
     }
 }
 
@@ -1174,10 +1241,10 @@ navi_status navi_frame_run(navi_frame *f, const navi_kv_view *kv, int32_t n_past
             if (hipStreamSynchronize(device_state().stream) != hipSuccess) return fail(NAVI_ERR_HIP, "frame: KV pointer upload failed");
         }
     }
-    a.kc = f->kv_dev;
-    a.vc = f->kv_dev + MAX_TL;
-    a.W = f->dw;
+
     a.mb = f->mb;
+    a.eps_t = f->p.talker.rms_eps;
+    a.eps_c = f->p.cp.rms_eps;
     a.abort_word = f->ctl + NCB;
     a.codes_out = reinterpret_cast<int32_t *>(f->ctl);
     a.n_tl = f->p.talker.n_layer;
@@ -1211,7 +1278,9 @@ navi_status navi_frame_run(navi_frame *f, const navi_kv_view *kv, int32_t n_past
     }
     hipStream_t st = device_state().stream;
     if (hipEventRecord(f->ev0, st) != hipSuccess) return fail(NAVI_ERR_HIP, "frame: hipEventRecord failed");
-    void *args[] = {&a};
+    const Weights *wp = f->dw;
+    uint16_t *const *kvp = f->kv_dev;
+    void *args[] = {&a, &wp, &kvp};
     const hipError_t e = hipLaunchCooperativeKernel(reinterpret_cast<const void *>(k_frame), dim3(f->grid), dim3(BT), args, 0, st);
     if (e != hipSuccess) {
         std::string m = std::string("cooperative launch failed: ") + hipGetErrorString(e);
