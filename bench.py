@@ -51,6 +51,30 @@ def algorithmic_bytes(kv: dict, n_past: int) -> dict:
     return {"talker": talker, "kv": kvb, "cp": cp, "cp_heads": heads, "total": talker + kvb + cp + heads}
 
 
+TRAFFIC_FILE = ROOT / "profiles" / "k_frame_n256_traffic.json"
+
+
+def copy_calibration(gib: float, reps: int):
+    """A plain copy kernel of known size (torch's elementwise `neg` over f32: reads and writes
+    exactly `gib` GiB once each) for scaling the FETCH_SIZE / WRITE_SIZE counters to bytes."""
+    import torch
+    n = int(gib * (1 << 30)) // 4
+    x = torch.ones(n, dtype=torch.float32, device="cuda")
+    y = torch.empty_like(x)
+    for _ in range(reps):
+        torch.neg(x, out=y)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration": {"bytes_read": 4 * n, "bytes_written": 4 * n, "dispatches": reps}}), flush=True)
+
+
+def measured_traffic():
+    """HBM bytes per k_frame launch from the committed counter runs (None when absent)."""
+    if not TRAFFIC_FILE.exists():
+        return None
+    t = json.loads(TRAFFIC_FILE.read_text())
+    return int(t["frame_bytes_per_launch"])
+
+
 def make_blob(path: Path):
     from navi_amd import blob
     if not path.exists():
@@ -90,10 +114,15 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--greedy", action="store_true", help="greedy sampling instead of the model defaults")
-    ap.add_argument("--cpu-frames", type=int, default=3, help="frames timed for the CPU baseline (0: skip)")
+    ap.add_argument("--cpu-frames", type=int, default=36, help="frames timed for the CPU baseline (0: skip)")
     ap.add_argument("--blob", default="", help="path for the random-init blob (default /dev/shm)")
     ap.add_argument("--keep-blob", action="store_true")
+    ap.add_argument("--copy-calibration", type=float, default=0.0, metavar="GIB",
+                    help="only run the counter-calibration copy kernel over GIB GiB and exit")
     args = ap.parse_args()
+    if args.copy_calibration > 0:
+        copy_calibration(args.copy_calibration, 4)
+        return
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
               "(the batch-1 frame is a chain of dependent phases; see DESIGN.md, 'More than one GPU')", file=sys.stderr)
@@ -155,7 +184,7 @@ def main():
                        "model": "Qwen3-TTS-12Hz-0.6B shapes", "global_batch": 1, "n_past": N_PAST,
                        "sampling": "greedy" if args.greedy else "top-k 50, T 0.9, rep 1.05", "parallelism": "none"},
             "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                         "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                         "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
                          "bytes_per_frame": b["total"], "kernel": "k_frame"},
             "cpu_baseline": cpu,
         }
