@@ -779,7 +779,9 @@ __device__ __forceinline__ int block_sample(float temperature, int top_k, uint64
         float cum = 0.f;
         for (int j = 0; j < n_nz; ++j) {
             const int i = S.u.m.samp.idx[j];
-            cum = __fadd_rn(cum, __fmul_rn(S.u.m.samp.lg[i], inv));
+            // Fused, as the reference's `cum += p[i] * inv_sum` compiles under hipcc's default
+            // contraction (frame.hip:290-292).
+            cum = fmaf(S.u.m.samp.lg[i], inv, cum);
             if (cum >= u) { chosen = i; break; }
         }
         S.isel[2] = chosen;

@@ -7,18 +7,26 @@ use it, and only as the checker or the reported CPU baseline.
 
 It restates, from the reference's own sources (cited per function):
 
-* `rng`      - splitmix64 seeding and the PCG32 draw (model/qwen3tts/frame.hip:169-175, 263-296, 581-586, 653-659);
-* `sampler`  - modified logits, exact top-k threshold, greedy/multinomial choice (frame.hip:178-296, 413-500);
-* `model`    - talker decode step, 16-position code-predictor pass, next-step assembly
-               (frame.hip:300-579), prompt assembly and prefill (model/qwen3tts/talker.hip:20-117, 283-399);
-* `vocoder`  - the codec decoder (model/qwen3tts/vocoder.hip:20-146, 261-385; kernels.h:72-350).
+* `rng`       - splitmix64 seeding and the PCG32 draw (model/qwen3tts/frame.hip:169-175, 263-296, 581-586, 653-659);
+* `sampler`   - modified logits, exact top-k threshold, greedy/multinomial choice (frame.hip:178-296, 413-500);
+* `model`     - talker decode step, 16-position code-predictor pass, next-step assembly
+                (frame.hip:300-579), prompt assembly and prefill (model/qwen3tts/talker.hip:20-117, 283-399);
+* `navi_read` - the `.navi` reader (docs/navi-format.md; runtime/weights/navi_file.cpp:79-148);
+* `csrc/sampler.c` + `csampler` - a second, C restatement of the seeding, the radix k-th-largest
+                select and the draw (the same frame.hip lines), used to cross-check `rng`/`sampler`.
 
 Precision policy (mirrors the engine's storage points, not its summation order):
 f16 weights exactly as stored in the blob, f32 activations and accumulation,
 K/V rounded to f16 where the engine stores them to its cache.
 
-Pinning: see tests/test_oracle_*.py. Every function is checked against a golden
-vector, a brute force, a textbook known answer or an independent library
-implementation (transformers' Qwen3 layer); DESIGN.md lists which check pins
-which function and names any function left "parity unpinned".
+Pinning (tests/test_oracle_*.py, tests/test_blob.py):
+* rng: SplitMix64 and PCG32 textbook known answers; Python == C on many seeds;
+* sampler: k-th largest three ways (sort, radix select in C, the definition) with ties, -inf and
+  signed zeros; fused sum vs libm fmaf; draw Python == C, hand cases, chi-square against the
+  softmax; suppression / EOS gate / penalty special cases;
+* model: decoder layer vs transformers' Qwen3DecoderLayer (random weights, non-unit norms), with a
+  planted-mistake control; prefill == sequential decode; RoPE and RMSNorm closed forms; the
+  assembly order; prompt layout vs the reference's fixtures (row counts, speaker row).
+Parity unpinned: none of the functions above. The per-frame composition (`Oracle.frame`) is the
+composition of pinned pieces.
 """

@@ -5,7 +5,7 @@ Follows model/qwen3tts/frame.hip:
 * `greedy`                 - block_argmax, frame.hip:178-203 (lowest index wins ties);
 * `kth_largest`            - block_kth_largest's result, frame.hip:221-256 (exact k-th largest,
                               duplicates counted); restated as a sort;
-* `draw`                   - block_draw, frame.hip:258-296 (f32 running sum over nonzero
+* `draw`                   - block_draw, frame.hip:258-296 (fused f32 running sum over nonzero
                               entries in index order, first cum >= u, else V-1);
 * `sample_talker` / `sample_cp` - tl_sample / cp_sample, frame.hip:421-500.
 
@@ -16,6 +16,7 @@ rounded, i.e. the correctly rounded values the device approximates.
 from __future__ import annotations
 
 from dataclasses import dataclass
+from fractions import Fraction
 
 import numpy as np
 
@@ -71,14 +72,33 @@ def softmax_weights(xs, top_k: int):
     return e, F32(F32(1.0) / ssum), thr
 
 
+def fma_f32(a, b, c) -> np.float32:
+    """f32(a*b + c) rounded once (round to nearest, ties to even), from the exact rational value."""
+    a, b, c = F32(a), F32(b), F32(c)
+    if not (np.isfinite(a) and np.isfinite(b) and np.isfinite(c)):
+        return F32(float(a) * float(b) + float(c))
+    exact = Fraction(float(a)) * Fraction(float(b)) + Fraction(float(c))
+    r = F32(float(exact))                     # within one f32 ulp of the exact value
+    best = None
+    for cand in (np.nextafter(r, F32(-np.inf)), r, np.nextafter(r, F32(np.inf))):
+        if not np.isfinite(cand):
+            continue
+        d = abs(Fraction(float(cand)) - exact)
+        if best is None or d < best[0] or (d == best[0] and (int(cand.view(np.uint32)) & 1) == 0):
+            best = (d, cand)
+    return F32(best[1])
+
+
 def draw(e, inv_sum, seed: int) -> tuple[int, float]:
-    """(index, margin): margin = |cum - u| at the decision (a near-tie indicator)."""
+    """(index, margin): margin = |cum - u| at the decision (a near-tie indicator). The running sum
+    is fused (cum = fma(p, inv_sum, cum)): the reference's `cum += p[i] * inv_sum` (frame.hip:290-292)
+    is contracted by hipcc's default -ffp-contract=fast-honor-pragmas."""
     u = F32(rng.draw_uniform(seed))
     cum = F32(0.0)
     inv_sum = F32(inv_sum)
     last_gap = np.inf
     for i in np.flatnonzero(np.asarray(e) != 0):
-        cum = F32(cum + F32(F32(e[i]) * inv_sum))
+        cum = fma_f32(e[i], inv_sum, cum)
         last_gap = min(last_gap, abs(float(cum) - float(u)))
         if cum >= u:
             return int(i), last_gap
