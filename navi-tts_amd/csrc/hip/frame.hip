@@ -5,7 +5,8 @@
 // Replaces k_frame and its phases (model/qwen3tts/frame.hip:85-579) and the
 // host side of Frame (frame.hip:590-810). MI355X design:
 //
-//  * Grid: one 512-thread block (8 wave64s) per CU, 256 blocks. Every matrix
+//  * Grid: one 256-thread block (4 wave64s, one per SIMD, so each wave may use
+//    the full 512 VGPR+AGPR budget) per CU, 256 blocks. Every matrix
 //    is partitioned into fixed per-block row slices (q/k/v 16 rows, o 4, gate+up
 //    12+12, down 4, talker head 12, cp lm_head 8) so each block streams the same
 //    slice of every layer, and the slice of the NEXT layer for a phase is loaded
