@@ -167,6 +167,54 @@ const float *navi_frame_tap_cp_logits(const navi_frame *f);
 navi_status navi_frame_set_profile(navi_frame *f, int32_t enabled);
 navi_status navi_frame_profile(const navi_frame *f, uint64_t *out, int32_t n_blocks, int32_t n_slots);
 
+/* ---- talker: prompt rows, prefill, KV cache (talker.h:34-67) ----------------- */
+
+typedef struct navi_talker navi_talker;
+
+typedef struct {                       /* talker.h:26-32 Prompt: device rows owned by the talker */
+    const float *prefill;              /* f32 [n_prefill][hidden] */
+    const float *trailing;             /* f32 [n_trailing][hidden] */
+    const float *tts_pad;              /* f32 [hidden] */
+    int32_t n_prefill, n_trailing;
+} navi_prompt;
+
+/* Talker::create (talker.hip:197-265): binds the talker's weights by name (text embedding,
+ * text projection, layers, final norm, codec head, codec embedding), allocates the KV cache
+ * (max_positions rows per layer, f16 [max_positions][kv_dim]) and the prompt/prefill work
+ * buffers for up to max_prompt_tokens rows. */
+navi_status navi_talker_create(const navi_model_params *p, const navi_tensor_ref *tensors, int32_t n_tensors,
+                               int32_t max_prompt_tokens, int32_t max_positions, navi_talker **out,
+                               char *err, size_t errlen);
+void navi_talker_destroy(navi_talker *t);
+/* Talker::build_prompt (talker.hip:283-352). ids: host i32[n_ids] = role header (3), text,
+ * trailer (5); language_id: the codec id of the language (the `talker.language.<name>` key),
+ * or < 0 for "auto" (no language row); speaker: host f32[hidden]. The returned rows stay
+ * valid until the next build_prompt. */
+navi_status navi_talker_build_prompt(navi_talker *t, const int32_t *ids, int32_t n_ids, int32_t language_id,
+                                     const float *speaker, navi_prompt *out, char *err, size_t errlen);
+/* Talker::prefill (talker.hip:354-399): d_rows f32 [n_rows][hidden] (device) at positions
+ * 0..n_rows-1; writes KV rows 0..n_rows-1, keeps the last row's post-norm hidden and its
+ * logits, and sets the cache's n_used to n_rows. */
+navi_status navi_talker_prefill(navi_talker *t, const float *d_rows, int32_t n_rows, char *err, size_t errlen);
+/* Talker::kv (talker.h:48): the cache as the view navi_frame_run takes; *n_used (may be NULL)
+ * is the number of rows the last prefill wrote. The pointer arrays live as long as t. */
+navi_status navi_talker_kv(navi_talker *t, navi_kv_view *out, int32_t *n_used);
+const float *navi_talker_hidden(const navi_talker *t);   /* Talker::d_hidden: f32[hidden] */
+const float *navi_talker_logits(const navi_talker *t);   /* Talker::d_logits: f32[vocab] */
+double navi_talker_last_ms(const navi_talker *t);         /* Talker::last_ms: device time of the last prefill */
+
+/* ---- linear layer (Talker::Impl::gemm, talker.hip:160-190; k_gemm_skinny / k_conv<K=1>,
+ * kernels.h:255-330) ---------------------------------------------------------------------
+ * d_y[m][n] = act(bias[n] + sum_k d_x[m][k] * w[n][k]) + residual[m][n] for m < M, n < N.
+ * d_x f32 rows with stride ldx, w f16 [N][K] row-major (nn.Linear layout), d_y f32 rows with
+ * stride ldy. bias, residual may be NULL; residual may alias d_y. act: 0 none, 1 SiLU.
+ * Requires K % 32 == 0, N % 64 == 0, ldx % 4 == 0, 16-byte aligned d_x and w, and
+ * |x| < 65504 (the activations travel as f16 hi + lo pairs through the matrix cores; a larger
+ * value fails with NAVI_ERR_INVALID). Runs on the library stream and returns when done. */
+navi_status navi_linear(const float *d_x, int32_t ldx, int32_t M, const uint16_t *w, int32_t K, int32_t N,
+                        const float *bias, const float *residual, int32_t act, float *d_y, int32_t ldy,
+                        char *err, size_t errlen);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1038,29 +1038,9 @@ struct navi_frame {
 
 namespace {
 
-const navi_tensor_ref *find_tensor(const navi_tensor_ref *t, int n, const std::string &name) {
-    for (int i = 0; i < n; ++i) if (t[i].name && name == t[i].name) return &t[i];
-    return nullptr;
-}
-
-// Looks a weight up by name and checks its dtype and shape (Params::validate's contract).
-// d1 == 0: a 1-D tensor [d0]; else [d0, d1].
-template <class T>
-navi_status bind_tensor(const navi_tensor_ref *t, int n, const std::string &name, int dtype, uint64_t d0, uint64_t d1,
-                        const T *&out, char *err, size_t errlen) {
-    const navi_tensor_ref *r = find_tensor(t, n, name);
-    if (!r) { set_err(err, errlen, "frame: missing tensor '%s'", name.c_str()); return NAVI_ERR_INVALID; }
-    const int nd = d1 ? 2 : 1;
-    const bool ok = r->dtype == dtype && r->ndim == nd && r->dims[0] == d0 && (nd == 1 || r->dims[1] == d1);
-    if (!ok) { set_err(err, errlen, "frame: tensor '%s' has an unexpected dtype or shape", name.c_str()); return NAVI_ERR_INVALID; }
-    if (reinterpret_cast<uintptr_t>(r->ptr) & 15u) { set_err(err, errlen, "frame: tensor '%s' is not 16-byte aligned", name.c_str()); return NAVI_ERR_INVALID; }
-    out = static_cast<const T *>(r->ptr);
-    return NAVI_OK;
-}
-
 #define NAVI_BIND(T, name, dt, d0, d1, out)                                                       \
     do {                                                                                          \
-        const navi_status s_ = bind_tensor<T>(tensors, n_tensors, (name), (dt), (d0), (d1), (out), err, errlen); \
+        const navi_status s_ = bind_tensor<T>("frame", tensors, n_tensors, (name), (dt), (d0), (d1), (out), err, errlen); \
         if (s_ != NAVI_OK) return s_;                                                             \
     } while (0)
 
@@ -1130,10 +1110,10 @@ navi_status navi_frame_create(const navi_model_params *p, const navi_tensor_ref 
     {
         const int n_tensors_ = n_tensors;
         auto b16 = [&](const uint16_t *&dst, const std::string &name, uint64_t d0, uint64_t d1) {
-            return bind_tensor<uint16_t>(tensors, n_tensors_, name, NAVI_DT_F16, d0, d1, dst, err, errlen);
+            return bind_tensor<uint16_t>("frame", tensors, n_tensors_, name, NAVI_DT_F16, d0, d1, dst, err, errlen);
         };
         auto b32 = [&](const float *&dst, const std::string &name, uint64_t d0) {
-            return bind_tensor<float>(tensors, n_tensors_, name, NAVI_DT_F32, d0, 0, dst, err, errlen);
+            return bind_tensor<float>("frame", tensors, n_tensors_, name, NAVI_DT_F32, d0, 0, dst, err, errlen);
         };
         if ((st = b32(w.tl_norm, "talker.model.norm.weight", H)) != NAVI_OK) return fail(st);
         if ((st = b32(w.cp_norm, "talker.code_predictor.model.norm.weight", H)) != NAVI_OK) return fail(st);

@@ -1,0 +1,725 @@
+// Prompt rows and the causal prefill of the talker on gfx950, plus the linear layer they are
+// built from (the C ABI's navi_talker_* and navi_linear).
+//
+// Replaces Talker (model/qwen3tts/talker.hip:20-399) and the GEMMs it runs through
+// Talker::Impl::gemm (k_gemm_skinny / k_conv<K=1>, kernels.h:72-330). MI355X design:
+//
+//  * Every projection is Y = X · W^T with f16 weights [N][K] and f32 activations, on the
+//    matrix cores (v_mfma_f32_16x16x32_f16). Each activation is split into an f16 pair
+//    x = hi + lo (hi = f16(x), lo = f16(x - hi)), so two MFMAs per weight fragment carry ~22
+//    bits of the activation: the products keep f32-level accuracy while the weights stream
+//    at the matrix cores' f16 rate. Activations must lie inside the f16 range; a device flag
+//    turns anything else into an error instead of an infinity.
+//  * A block owns 64 output columns (one 16-column MFMA tile per wave) and up to 64 rows;
+//    K is split across blocks so that even N = 1024 fills the 256 CUs. Split-K partials go to
+//    a workspace and are summed in a fixed order by the "finish" kernels, which also apply
+//    the epilogue (bias, SiLU, residual + the next RMSNorm, SwiGLU, q/k head norms + RoPE +
+//    the f16 K/V store): deterministic results and no extra pass for the epilogues.
+//  * Causal prefill attention: one block per (row, q head), scores over keys 0..row from the
+//    f16 cache, exactly as the frame's decode attention will later read them.
+#include "dev_common.h"
+#include "host_util.h"
+
+#include <algorithm>
+#include <cmath>
+#include <string>
+#include <vector>
+
+namespace navi_amd {
+namespace pf {
+
+constexpr int BT = 256;                 // 4 wave64s
+constexpr int KC = 256;                 // K elements staged in LDS per step
+constexpr int LDA = KC + 8;             // padded LDS row (halves): rotates banks between rows
+constexpr int HD = 128;                 // head dim the norm/rope/attention kernels are built for
+
+typedef _Float16 half8v __attribute__((ext_vector_type(8)));
+
+struct LinArgs {
+    const float *x;        // [M][ldx] f32
+    const uint16_t *w;     // [N][K] f16
+    float *part;           // [S][M][ldp] f32 partial sums (columns p_off .. p_off + N)
+    uint32_t *flag;        // set when an activation is outside the f16 range
+    int ldx, M, K, N, kps, ldp, p_off;
+};
+
+__device__ __forceinline__ void split_store(float v, _Float16 *hi, _Float16 *lo, bool &bad) {
+    bad |= !(fabsf(v) < 65504.f);
+    const _Float16 h = static_cast<_Float16>(v);
+    *hi = h;
+    *lo = static_cast<_Float16>(v - static_cast<float>(h));
+}
+
+// Partial Y for one (64-column tile, MT*16-row tile, K split). Output lane layout of
+// v_mfma_f32_16x16x32_f16: lane l holds column l % 16 of rows 4 * (l / 16) + r, r = 0..3.
+// A and B fragments use the same lane -> k mapping (k = 8 * (l / 16) + j within a 32-k step),
+// so every k of the step is summed exactly once whatever that mapping is inside the unit.
+template <int MT>
+__global__ void __launch_bounds__(BT) k_linear_partial(LinArgs a) {
+    __shared__ __align__(16) _Float16 ahi[MT * 16][LDA];
+    __shared__ __align__(16) _Float16 alo[MT * 16][LDA];
+    const int wv = threadIdx.x >> 6, l = threadIdx.x & 63;
+    const int n0 = blockIdx.x * 64 + wv * 16;
+    const int m0 = blockIdx.y * (MT * 16);
+    const int kb = blockIdx.z * a.kps, ke = kb + a.kps;
+    const NAVI_GLOBAL u32x4_t *wrow =
+        (const NAVI_GLOBAL u32x4_t *) (a.w + static_cast<size_t>(n0 + (l & 15)) * a.K + (l >> 4) * 8);
+    f32x4_t acc[MT];
+#pragma unroll
+    for (int i = 0; i < MT; ++i) acc[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    u32x4_t bcur[KC / 32], bnext[KC / 32];
+    auto load_b = [&](u32x4_t (&dst)[KC / 32], int k0) {
+        const int steps = min(KC, ke - k0) / 32;
+#pragma unroll
+        for (int c = 0; c < KC / 32; ++c)
+            if (c < steps) dst[c] = __builtin_nontemporal_load(wrow + (k0 >> 3) + c * 4);
+    };
+    load_b(bcur, kb);
+    bool bad = false;
+    for (int k0 = kb; k0 < ke; k0 += KC) {
+        const int kc = min(KC, ke - k0);
+        if (k0 + KC < ke) load_b(bnext, k0 + KC);
+        __syncthreads();                                   // previous step's readers are done
+        const int q4 = kc >> 2;
+        for (int i = threadIdx.x; i < MT * 16 * q4; i += BT) {
+            const int r = i / q4, c4 = (i - r * q4) * 4, m = m0 + r;
+            f32x4_t v = f32x4_t{0.f, 0.f, 0.f, 0.f};
+            if (m < a.M) v = *(const NAVI_GLOBAL f32x4_t *) (a.x + static_cast<size_t>(m) * a.ldx + k0 + c4);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) split_store(v[j], &ahi[r][c4 + j], &alo[r][c4 + j], bad);
+        }
+        __syncthreads();
+#pragma unroll
+        for (int c = 0; c < KC / 32; ++c) {
+            if (c < (kc >> 5)) {
+                half8v b;
+                __builtin_memcpy(&b, &bcur[c], 16);
+#pragma unroll
+                for (int i = 0; i < MT; ++i) {
+                    const half8v h = *reinterpret_cast<const half8v *>(&ahi[i * 16 + (l & 15)][c * 32 + (l >> 4) * 8]);
+                    const half8v o = *reinterpret_cast<const half8v *>(&alo[i * 16 + (l & 15)][c * 32 + (l >> 4) * 8]);
+                    acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(h, b, acc[i], 0, 0, 0);
+                    acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(o, b, acc[i], 0, 0, 0);
+                }
+            }
+        }
+#pragma unroll
+        for (int c = 0; c < KC / 32; ++c) bcur[c] = bnext[c];
+    }
+    if (bad) gst(a.flag, 1u);
+    float *p = a.part + static_cast<size_t>(blockIdx.z) * a.M * a.ldp + a.p_off + n0 + (l & 15);
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int m = m0 + i * 16 + (l >> 4) * 4 + r;
+            if (m < a.M) gst(p + static_cast<size_t>(m) * a.ldp, acc[i][r]);
+        }
+}
+
+__device__ __forceinline__ float block_sum256(float v, float *red) {
+    v = wave_sum(v);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    return red[0] + red[1] + red[2] + red[3];
+}
+
+__device__ __forceinline__ float sum_parts(const float *part, int S, size_t stride, size_t idx) {
+    float v = gld(part + idx);
+    for (int s = 1; s < S; ++s) v += gld(part + s * stride + idx);
+    return v;
+}
+
+__device__ __forceinline__ float silu(float g) { return g / (1.f + expf(-g)); }
+
+// y[m][n] = act(sum_s part + bias) + residual (Talker::Impl::gemm epilogues, kernels.h:315-321).
+__global__ void __launch_bounds__(BT) k_finish_linear(const float *part, int S, int M, int N, const float *bias,
+                                                      const float *residual, int act, float *y, int ldy) {
+    const int m = blockIdx.x;
+    for (int n = threadIdx.x; n < N; n += BT) {
+        float v = sum_parts(part, S, static_cast<size_t>(M) * N, static_cast<size_t>(m) * N + n);
+        if (bias) v += gld(bias + n);
+        if (act == 1) v = silu(v);
+        if (residual) v += gld(residual + static_cast<size_t>(m) * ldy + n);
+        gst(y + static_cast<size_t>(m) * ldy + n, v);
+    }
+}
+
+// x[m] = (S > 0 ? sum_s part + x[m] : src[m]); xn[m] = RMSNorm(x[m]) * w (k_rmsnorm, kernels.h:342-350,
+// fused with the residual epilogue of the o / down projections).
+__global__ void __launch_bounds__(BT) k_resid_norm(const float *part, int S, const float *src, float *x, const float *w,
+                                                   float eps, float *xn, int M, int H) {
+    __shared__ float red[4];
+    const int m = blockIdx.x;
+    float v[4], ss = 0.f;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int i = threadIdx.x + r * BT;
+        const size_t idx = static_cast<size_t>(m) * H + i;
+        v[r] = S > 0 ? sum_parts(part, S, static_cast<size_t>(M) * H, idx) + gld(x + idx) : gld(src + idx);
+        gst(x + idx, v[r]);
+        ss = fmaf(v[r], v[r], ss);
+    }
+    ss = block_sum256(ss, red);
+    const float scale = rsqrtf(ss / static_cast<float>(H) + eps);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int i = threadIdx.x + r * BT;
+        gst(xn + static_cast<size_t>(m) * H + i, v[r] * scale * gld(w + i));
+    }
+}
+
+// h[m][c] = SiLU(gate) * up from the [gate | up] partials (PRO_SILU_GATE / k_silu_gate, kernels.h:334-340).
+__global__ void __launch_bounds__(BT) k_swiglu(const float *part, int S, int M, int F, float *h) {
+    const int m = blockIdx.x;
+    const size_t stride = static_cast<size_t>(M) * 2 * F;
+    for (int c = threadIdx.x; c < F; c += BT) {
+        const float g = sum_parts(part, S, stride, static_cast<size_t>(m) * 2 * F + c);
+        const float u = sum_parts(part, S, stride, static_cast<size_t>(m) * 2 * F + F + c);
+        gst(h + static_cast<size_t>(m) * F + c, silu(g) * u);
+    }
+}
+
+// Row m of [q | k | v] (partials, ldp = nq + 2 nkv heads * 128): per-head RMSNorm of q and k,
+// rotate-half RoPE at position pos0 + m, q kept f32, k and v rounded to f16 into the cache
+// (k_qk_norm_rope, talker.hip:46-82).
+__global__ void __launch_bounds__(BT) k_qkv_finish(const float *part, int S, int M, int nq, int nkv, const float *qn,
+                                                   const float *kn, float eps, const float *invf, int pos0, float *q,
+                                                   uint16_t *kc, uint16_t *vc) {
+    extern __shared__ float row[];
+    const int m = blockIdx.x, pos = pos0 + m;
+    const int QD = nq * HD, KVD = nkv * HD, W = QD + 2 * KVD;
+    const size_t stride = static_cast<size_t>(M) * W;
+    for (int i = threadIdx.x; i < W; i += BT) row[i] = sum_parts(part, S, stride, static_cast<size_t>(m) * W + i);
+    __syncthreads();
+    const int wv = threadIdx.x >> 6, l = threadIdx.x & 63;
+    const float inv = gld(invf + l);
+    float sn, cs;
+    sincosf(static_cast<float>(pos) * inv, &sn, &cs);
+    for (int hh = wv; hh < nq + nkv; hh += BT / WAVE) {
+        float *hp = row + hh * HD;
+        const float *nw = hh < nq ? qn : kn;
+        const float a0 = hp[l], a1 = hp[l + HD / 2];
+        const float sc = rsqrtf(wave_sum(fmaf(a0, a0, a1 * a1)) / static_cast<float>(HD) + eps);
+        const float x0 = a0 * sc * gld(nw + l), x1 = a1 * sc * gld(nw + l + HD / 2);
+        hp[l] = x0 * cs - x1 * sn;
+        hp[l + HD / 2] = x1 * cs + x0 * sn;
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < QD; i += BT) gst(q + static_cast<size_t>(m) * QD + i, row[i]);
+    for (int i = threadIdx.x; i < KVD; i += BT) {
+        gst(kc + static_cast<size_t>(pos) * KVD + i, f2h(row[QD + i]));
+        gst(vc + static_cast<size_t>(pos) * KVD + i, f2h(row[QD + KVD + i]));
+    }
+}
+
+// Causal GQA attention of row m, head h over keys 0..pos0 + m of the f16 cache
+// (k_prefill_attention, talker.hip:88-117). 128 threads; scores in dynamic LDS.
+__global__ void __launch_bounds__(128) k_attn_prefill(const float *q, const uint16_t *kc, const uint16_t *vc, int nq,
+                                                      int nkv, int pos0, float scale, float *out) {
+    extern __shared__ float sc[];
+    __shared__ float qs[HD], red[2];
+    const int m = blockIdx.x, h = blockIdx.y, g = h / (nq / nkv), n = pos0 + m + 1;
+    const int QD = nq * HD, KVD = nkv * HD;
+    const int wv = threadIdx.x >> 6, l = threadIdx.x & 63;
+    qs[threadIdx.x] = gld(q + static_cast<size_t>(m) * QD + h * HD + threadIdx.x);
+    __syncthreads();
+    float mx = -INFINITY;
+    for (int j = wv; j < n; j += 2) {
+        const uint32_t kk = gld(reinterpret_cast<const uint32_t *>(kc + static_cast<size_t>(j) * KVD + g * HD) + l);
+        const float d = wave_sum(fmaf(qs[2 * l], h2f(static_cast<uint16_t>(kk)), qs[2 * l + 1] * h2f(static_cast<uint16_t>(kk >> 16))));
+        const float s = d * scale;
+        if (l == 0) sc[j] = s;
+        mx = fmaxf(mx, s);
+    }
+    if (l == 0) red[wv] = mx;
+    __syncthreads();
+    mx = fmaxf(red[0], red[1]);
+    __syncthreads();
+    float sum = 0.f;
+    for (int j = threadIdx.x; j < n; j += 128) {
+        const float e = expf(sc[j] - mx);
+        sc[j] = e;
+        sum += e;
+    }
+    sum = wave_sum(sum);
+    if (l == 0) red[wv] = sum;
+    __syncthreads();
+    sum = red[0] + red[1];
+    const int d = threadIdx.x;
+    float acc = 0.f;
+    const uint16_t *vp = vc + g * HD + d;
+    for (int j = 0; j < n; ++j) acc = fmaf(sc[j], h2f(gld(vp + static_cast<size_t>(j) * KVD)), acc);
+    gst(out + static_cast<size_t>(m) * QD + h * HD + d, acc / sum);
+}
+
+// rows[t] = table[ids[t]] (f16 -> f32), k_gather_rows (talker.hip:20-25).
+__global__ void __launch_bounds__(BT) k_gather_rows(const uint16_t *table, const int32_t *ids, int width, float *out) {
+    const uint16_t *src = table + static_cast<size_t>(gld(ids + blockIdx.x)) * width;
+    float *dst = out + static_cast<size_t>(blockIdx.x) * width;
+    for (int i = threadIdx.x; i < width; i += BT) gst(dst + i, h2f(gld(src + i)));
+}
+
+// out[t] = A[ia[t]] + B[ib[t]] (+ spk on spk_row), entries < 0 absent, k_assemble_rows (talker.hip:27-41).
+__global__ void __launch_bounds__(BT) k_assemble_rows(const float *A, const float *B, const float *spk, const int32_t *ia,
+                                                      const int32_t *ib, int spk_row, int width, float *out) {
+    const int t = blockIdx.x, a_i = gld(ia + t), b_i = gld(ib + t);
+    for (int i = threadIdx.x; i < width; i += BT) {
+        float v = 0.f;
+        if (a_i >= 0) v += gld(A + static_cast<size_t>(a_i) * width + i);
+        if (b_i >= 0) v += gld(B + static_cast<size_t>(b_i) * width + i);
+        if (t == spk_row) v += gld(spk + i);
+        gst(out + static_cast<size_t>(t) * width + i, v);
+    }
+}
+
+// ---- host: the split-K linear ------------------------------------------------------------
+
+int tiles_m(int M) { return M <= 16 ? 1 : M <= 32 ? 2 : M <= 48 ? 3 : 4; }
+
+// Number of K splits: enough blocks to cover the 256 CUs about twice, K / S a multiple of 32.
+int pick_splits(int M, int K, int N) {
+    const int mt = tiles_m(M);
+    const int blocks = (N / 64) * ((M + 16 * mt - 1) / (16 * mt));
+    int s = 1;
+    while (s * 2 * blocks <= 512 && (K / 32) % (s * 2) == 0 && K / (s * 2) >= 64) s *= 2;
+    return s;
+}
+
+size_t splits_floats(int M, int K, int N) { return static_cast<size_t>(pick_splits(M, K, N)) * M * N; }
+
+void launch_partial(const float *x, int ldx, int M, const uint16_t *w, int K, int N, int S, float *part, int ldp, int p_off,
+                    uint32_t *flag, hipStream_t st) {
+    LinArgs a{x, w, part, flag, ldx, M, K, N, K / S, ldp, p_off};
+    const int mt = tiles_m(M);
+    const dim3 grid(N / 64, (M + 16 * mt - 1) / (16 * mt), S);
+    switch (mt) {
+    case 1: hipLaunchKernelGGL(k_linear_partial<1>, grid, dim3(BT), 0, st, a); break;
+    case 2: hipLaunchKernelGGL(k_linear_partial<2>, grid, dim3(BT), 0, st, a); break;
+    case 3: hipLaunchKernelGGL(k_linear_partial<3>, grid, dim3(BT), 0, st, a); break;
+    default: hipLaunchKernelGGL(k_linear_partial<4>, grid, dim3(BT), 0, st, a); break;
+    }
+}
+
+bool linear_shape_ok(const float *x, int ldx, int M, const uint16_t *w, int K, int N) {
+    return M > 0 && K > 0 && N > 0 && K % 32 == 0 && N % 64 == 0 && ldx % 4 == 0 && ldx >= K &&
+           (reinterpret_cast<uintptr_t>(x) & 15u) == 0 && (reinterpret_cast<uintptr_t>(w) & 15u) == 0;
+}
+
+// Library workspace for navi_linear (grown on demand; entry points run on one host thread).
+struct LinearWs {
+    float *part = nullptr;
+    size_t floats = 0;
+    uint32_t *flag = nullptr;
+} g_ws;
+
+struct LayerW {
+    const float *ln1, *ln2, *qn, *kn;
+    const uint16_t *wq, *wk, *wv, *wo, *wg, *wu, *wd;
+};
+
+} // namespace pf
+} // namespace navi_amd
+
+using namespace navi_amd;
+using namespace navi_amd::pf;
+
+struct navi_talker {
+    // shapes
+    int H = 0, NQ = 0, NKV = 0, QD = 0, KVD = 0, F = 0, V = 0, L = 0, TH = 0, TV = 0;
+    float eps = 0.f;
+    int max_prompt = 0, max_pos = 0, mmax = 0;
+    int tts_bos = 0, tts_eos = 0, tts_pad = 0, codec_bos = 0, codec_pad = 0, think = 0, nothink = 0, think_bos = 0,
+        think_eos = 0, codec_vocab = 0;
+    // weights
+    const uint16_t *text_emb = nullptr, *codec_emb = nullptr, *fc1 = nullptr, *fc2 = nullptr, *head = nullptr;
+    const float *fc1_b = nullptr, *fc2_b = nullptr, *final_norm = nullptr;
+    std::vector<LayerW> layers;
+    // cache
+    std::vector<uint16_t *> kk, vv;
+    int n_used = 0;
+    // work buffers
+    float *x = nullptr, *xn = nullptr, *q = nullptr, *att = nullptr, *h = nullptr, *part = nullptr, *invf = nullptr;
+    size_t part_floats = 0;
+    uint32_t *flag = nullptr;
+    int32_t *d_ids = nullptr, *d_cids = nullptr, *d_ia = nullptr, *d_ib = nullptr, *d_ta = nullptr, *d_tb = nullptr;
+    float *text_rows = nullptr, *fc1_out = nullptr, *proj = nullptr, *codec_rows = nullptr, *spk = nullptr;
+    float *prefill = nullptr, *trailing = nullptr, *pad_row = nullptr, *hidden = nullptr, *logits = nullptr;
+    hipEvent_t ev0 = nullptr, ev1 = nullptr;
+    double last_ms = 0;
+    std::vector<void *> owned;
+
+    template <class T>
+    navi_status alloc(T *&p, size_t n, char *err, size_t errlen) {
+        void *ptr = nullptr;
+        NAVI_TRY_HIP(hipMalloc(&ptr, std::max<size_t>(n, 1) * sizeof(T)), err, errlen);
+        owned.push_back(ptr);
+        NAVI_TRY_HIP(hipMemsetAsync(ptr, 0, std::max<size_t>(n, 1) * sizeof(T), device_state().stream), err, errlen);
+        p = static_cast<T *>(ptr);
+        return NAVI_OK;
+    }
+
+    ~navi_talker() {
+        if (ev0) (void) hipEventDestroy(ev0);
+        if (ev1) (void) hipEventDestroy(ev1);
+        for (void *p : owned) (void) hipFree(p);
+    }
+};
+
+namespace {
+
+#define TALKER_BIND(T, name, dt, d0, d1, out)                                                                   \
+    do {                                                                                                        \
+        const navi_status s_ = bind_tensor<T>("talker", tensors, n_tensors, (name), (dt), (d0), (d1), (out), err, errlen); \
+        if (s_ != NAVI_OK) return s_;                                                                           \
+    } while (0)
+
+navi_status talker_bind(navi_talker &t, const navi_tensor_ref *tensors, int n_tensors, char *err, size_t errlen) {
+    TALKER_BIND(uint16_t, "talker.model.text_embedding.weight", NAVI_DT_F16, t.TV, t.TH, t.text_emb);
+    TALKER_BIND(uint16_t, "talker.model.codec_embedding.weight", NAVI_DT_F16, t.codec_vocab, t.H, t.codec_emb);
+    TALKER_BIND(uint16_t, "talker.text_projection.linear_fc1.weight", NAVI_DT_F16, t.TH, t.TH, t.fc1);
+    TALKER_BIND(float, "talker.text_projection.linear_fc1.bias", NAVI_DT_F32, t.TH, 0, t.fc1_b);
+    TALKER_BIND(uint16_t, "talker.text_projection.linear_fc2.weight", NAVI_DT_F16, t.H, t.TH, t.fc2);
+    TALKER_BIND(float, "talker.text_projection.linear_fc2.bias", NAVI_DT_F32, t.H, 0, t.fc2_b);
+    TALKER_BIND(uint16_t, "talker.codec_head.weight", NAVI_DT_F16, t.V, t.H, t.head);
+    TALKER_BIND(float, "talker.model.norm.weight", NAVI_DT_F32, t.H, 0, t.final_norm);
+    t.layers.resize(t.L);
+    for (int l = 0; l < t.L; ++l) {
+        const std::string p = "talker.model.layers." + std::to_string(l) + ".";
+        LayerW &w = t.layers[l];
+        TALKER_BIND(float, p + "input_layernorm.weight", NAVI_DT_F32, t.H, 0, w.ln1);
+        TALKER_BIND(float, p + "post_attention_layernorm.weight", NAVI_DT_F32, t.H, 0, w.ln2);
+        TALKER_BIND(float, p + "self_attn.q_norm.weight", NAVI_DT_F32, HD, 0, w.qn);
+        TALKER_BIND(float, p + "self_attn.k_norm.weight", NAVI_DT_F32, HD, 0, w.kn);
+        TALKER_BIND(uint16_t, p + "self_attn.q_proj.weight", NAVI_DT_F16, t.QD, t.H, w.wq);
+        TALKER_BIND(uint16_t, p + "self_attn.k_proj.weight", NAVI_DT_F16, t.KVD, t.H, w.wk);
+        TALKER_BIND(uint16_t, p + "self_attn.v_proj.weight", NAVI_DT_F16, t.KVD, t.H, w.wv);
+        TALKER_BIND(uint16_t, p + "self_attn.o_proj.weight", NAVI_DT_F16, t.H, t.QD, w.wo);
+        TALKER_BIND(uint16_t, p + "mlp.gate_proj.weight", NAVI_DT_F16, t.F, t.H, w.wg);
+        TALKER_BIND(uint16_t, p + "mlp.up_proj.weight", NAVI_DT_F16, t.F, t.H, w.wu);
+        TALKER_BIND(uint16_t, p + "mlp.down_proj.weight", NAVI_DT_F16, t.H, t.F, w.wd);
+    }
+    return NAVI_OK;
+}
+
+// The most partial floats any projection of a prefill (or prompt) of up to M rows needs.
+size_t talker_part_floats(const navi_talker &t) {
+    size_t best = 0;
+    const int shapes[][2] = {{t.H, t.QD + 2 * t.KVD}, {t.QD, t.H}, {t.H, 2 * t.F}, {t.F, t.H}, {t.H, t.V},
+                             {t.TH, t.TH}, {t.TH, t.H}};
+    for (int M = 1; M <= t.mmax; ++M)
+        for (const auto &s : shapes) {
+            // q/k/v and gate/up are split as one [q|k|v] / [gate|up] output
+            best = std::max(best, splits_floats(M, s[0], s[1]));
+        }
+    return best;
+}
+
+navi_status check_flag(navi_talker &t, const char *what, char *err, size_t errlen) {
+    uint32_t f = 0;
+    NAVI_TRY_HIP(hipMemcpyAsync(&f, t.flag, 4, hipMemcpyDeviceToHost, device_state().stream), err, errlen);
+    NAVI_TRY_HIP(hipStreamSynchronize(device_state().stream), err, errlen);
+    if (f) {
+        set_err(err, errlen, "talker: %s: an activation is outside the f16 range (|x| >= 65504 or NaN)", what);
+        return NAVI_ERR_INVALID;
+    }
+    return NAVI_OK;
+}
+
+} // namespace
+
+extern "C" {
+
+navi_status navi_talker_create(const navi_model_params *p, const navi_tensor_ref *tensors, int32_t n_tensors,
+                               int32_t max_prompt_tokens, int32_t max_positions, navi_talker **out, char *err,
+                               size_t errlen) {
+    if (!p || !tensors || !out) {
+        set_err(err, errlen, "talker: null argument");
+        return NAVI_ERR_INVALID;
+    }
+    *out = nullptr;
+    navi_status st = ensure_device(err, errlen);
+    if (st != NAVI_OK) return st;
+    const navi_xformer_params &x = p->talker;
+    if (x.head_dim != HD || x.hidden % 1024 != 0 || x.n_head % x.n_kv_head != 0 || x.ff % 64 != 0 || x.vocab % 64 != 0 ||
+        p->text_hidden % 64 != 0 || x.hidden != 1024) {
+        set_err(err, errlen, "talker: unsupported shape (hidden %d, head_dim %d, ff %d, vocab %d, text_hidden %d)", x.hidden,
+                x.head_dim, x.ff, x.vocab, p->text_hidden);
+        return NAVI_ERR_UNSUPPORTED;
+    }
+    if (max_prompt_tokens < 9 || max_prompt_tokens > 4096 || max_positions < max_prompt_tokens) {
+        set_err(err, errlen, "talker: max_prompt_tokens %d / max_positions %d out of range", max_prompt_tokens, max_positions);
+        return NAVI_ERR_INVALID;
+    }
+    auto t = new navi_talker();
+    t->H = x.hidden; t->NQ = x.n_head; t->NKV = x.n_kv_head; t->QD = x.n_head * HD; t->KVD = x.n_kv_head * HD;
+    t->F = x.ff; t->V = x.vocab; t->L = x.n_layer; t->TH = p->text_hidden; t->TV = p->text_vocab; t->eps = x.rms_eps;
+    t->codec_vocab = x.vocab;
+    t->max_prompt = max_prompt_tokens; t->max_pos = max_positions; t->mmax = max_prompt_tokens + 8;
+    t->tts_bos = p->tts_bos_id; t->tts_eos = p->tts_eos_id; t->tts_pad = p->tts_pad_id;
+    t->codec_bos = p->codec_bos_id; t->codec_pad = p->codec_pad_id; t->think = p->codec_think_id;
+    t->nothink = p->codec_nothink_id; t->think_bos = p->codec_think_bos_id; t->think_eos = p->codec_think_eos_id;
+    auto fail = [&](navi_status s) { delete t; return s; };
+    if ((st = talker_bind(*t, tensors, n_tensors, err, errlen)) != NAVI_OK) return fail(st);
+    const size_t M = t->mmax;
+    t->kk.resize(t->L);
+    t->vv.resize(t->L);
+    for (int l = 0; l < t->L; ++l) {
+        if ((st = t->alloc(t->kk[l], static_cast<size_t>(max_positions) * t->KVD, err, errlen)) != NAVI_OK) return fail(st);
+        if ((st = t->alloc(t->vv[l], static_cast<size_t>(max_positions) * t->KVD, err, errlen)) != NAVI_OK) return fail(st);
+    }
+    t->part_floats = talker_part_floats(*t);
+#define TALLOC(ptr, n)                                                           \
+    do {                                                                         \
+        if ((st = t->alloc(ptr, (n), err, errlen)) != NAVI_OK) return fail(st);  \
+    } while (0)
+    TALLOC(t->x, M * t->H);
+    TALLOC(t->xn, M * t->H);
+    TALLOC(t->q, M * t->QD);
+    TALLOC(t->att, M * t->QD);
+    TALLOC(t->h, M * t->F);
+    TALLOC(t->part, t->part_floats);
+    TALLOC(t->invf, HD / 2);
+    TALLOC(t->flag, 1);
+    TALLOC(t->d_ids, M);
+    TALLOC(t->d_cids, 16);
+    TALLOC(t->d_ia, M);
+    TALLOC(t->d_ib, M);
+    TALLOC(t->d_ta, M);
+    TALLOC(t->d_tb, M);
+    TALLOC(t->text_rows, M * t->TH);
+    TALLOC(t->fc1_out, M * t->TH);
+    TALLOC(t->proj, M * t->H);
+    TALLOC(t->codec_rows, 16 * t->H);
+    TALLOC(t->spk, t->H);
+    TALLOC(t->prefill, M * t->H);
+    TALLOC(t->trailing, M * t->H);
+    TALLOC(t->pad_row, t->H);
+    TALLOC(t->hidden, t->H);
+    TALLOC(t->logits, t->V);
+#undef TALLOC
+    float invf[HD / 2];
+    for (int i = 0; i < HD / 2; ++i) invf[i] = static_cast<float>(1.0 / std::pow(x.rope_theta, (2.0 * i) / HD));
+    hipStream_t s = device_state().stream;
+    if (hipMemcpyAsync(t->invf, invf, sizeof invf, hipMemcpyHostToDevice, s) != hipSuccess ||
+        hipEventCreate(&t->ev0) != hipSuccess || hipEventCreate(&t->ev1) != hipSuccess || hipStreamSynchronize(s) != hipSuccess) {
+        set_err(err, errlen, "talker: HIP setup failed");
+        return fail(NAVI_ERR_HIP);
+    }
+    *out = t;
+    return NAVI_OK;
+}
+
+void navi_talker_destroy(navi_talker *t) {
+    if (!t) return;
+    (void) hipStreamSynchronize(device_state().stream);
+    delete t;
+}
+
+navi_status navi_talker_build_prompt(navi_talker *t, const int32_t *ids, int32_t n_ids, int32_t language_id,
+                                     const float *speaker, navi_prompt *out, char *err, size_t errlen) {
+    if (!t || !ids || !speaker || !out) {
+        set_err(err, errlen, "talker: null argument");
+        return NAVI_ERR_INVALID;
+    }
+    if (n_ids < 9) {
+        set_err(err, errlen, "talker: prompt ids too short (need role header, text, and the trailer)");
+        return NAVI_ERR_INVALID;
+    }
+    if (n_ids > t->max_prompt) {
+        set_err(err, errlen, "talker: prompt longer than max_prompt_tokens");
+        return NAVI_ERR_INVALID;
+    }
+    for (int i = 0; i < n_ids; ++i)
+        if (ids[i] < 0 || ids[i] >= t->TV) {
+            set_err(err, errlen, "talker: token id %d at %d outside the text vocabulary", ids[i], i);
+            return NAVI_ERR_INVALID;
+        }
+    if (language_id >= t->codec_vocab) {
+        set_err(err, errlen, "talker: language id %d outside the codec vocabulary", language_id);
+        return NAVI_ERR_INVALID;
+    }
+    const int n_text = n_ids - 8;
+    // rows to project: role header (3), text ids[3:3+n_text], tts_bos, tts_eos, tts_pad
+    std::vector<int32_t> tids(ids, ids + 3 + n_text);
+    const int i_bos = static_cast<int>(tids.size());
+    tids.push_back(t->tts_bos);
+    const int i_eos = static_cast<int>(tids.size());
+    tids.push_back(t->tts_eos);
+    const int i_pad = static_cast<int>(tids.size());
+    tids.push_back(t->tts_pad);
+    const int n_rows = static_cast<int>(tids.size());
+    std::vector<int32_t> cids;
+    if (language_id < 0) cids = {t->nothink, t->think_bos, t->think_eos};
+    else cids = {t->think, t->think_bos, language_id, t->think_eos};
+    const int n_think = static_cast<int>(cids.size());
+    cids.push_back(t->codec_pad);
+    cids.push_back(t->codec_bos);
+    for (int32_t c : cids)
+        if (c < 0 || c >= t->codec_vocab) {
+            set_err(err, errlen, "talker: codec control id %d outside the codec vocabulary", c);
+            return NAVI_ERR_INVALID;
+        }
+    // prefill: role rows, think rows (+ tts_pad), speaker (+ tts_pad), tts_bos + codec_pad, text[0] + codec_bos
+    std::vector<int32_t> ia, ib;
+    for (int r = 0; r < 3; ++r) { ia.push_back(r); ib.push_back(-1); }
+    for (int r = 0; r < n_think; ++r) { ia.push_back(i_pad); ib.push_back(r); }
+    const int spk_row = static_cast<int>(ia.size());
+    ia.push_back(i_pad); ib.push_back(-1);
+    ia.push_back(i_bos); ib.push_back(n_think);
+    ia.push_back(3); ib.push_back(n_think + 1);
+    // trailing: text[1:] then tts_eos
+    std::vector<int32_t> ta, tb;
+    for (int r = 1; r < n_text; ++r) { ta.push_back(3 + r); tb.push_back(-1); }
+    ta.push_back(i_eos); tb.push_back(-1);
+    const int n_pre = static_cast<int>(ia.size()), n_trail = static_cast<int>(ta.size());
+
+    hipStream_t s = device_state().stream;
+    NAVI_TRY_HIP(hipMemsetAsync(t->flag, 0, 4, s), err, errlen);
+    NAVI_TRY_HIP(hipMemcpyAsync(t->d_ids, tids.data(), tids.size() * 4, hipMemcpyHostToDevice, s), err, errlen);
+    NAVI_TRY_HIP(hipMemcpyAsync(t->d_cids, cids.data(), cids.size() * 4, hipMemcpyHostToDevice, s), err, errlen);
+    NAVI_TRY_HIP(hipMemcpyAsync(t->spk, speaker, t->H * 4, hipMemcpyHostToDevice, s), err, errlen);
+    NAVI_TRY_HIP(hipMemcpyAsync(t->d_ia, ia.data(), ia.size() * 4, hipMemcpyHostToDevice, s), err, errlen);
+    NAVI_TRY_HIP(hipMemcpyAsync(t->d_ib, ib.data(), ib.size() * 4, hipMemcpyHostToDevice, s), err, errlen);
+    NAVI_TRY_HIP(hipMemcpyAsync(t->d_ta, ta.data(), ta.size() * 4, hipMemcpyHostToDevice, s), err, errlen);
+    NAVI_TRY_HIP(hipMemcpyAsync(t->d_tb, tb.data(), tb.size() * 4, hipMemcpyHostToDevice, s), err, errlen);
+    hipLaunchKernelGGL(k_gather_rows, dim3(n_rows), dim3(BT), 0, s, t->text_emb, t->d_ids, t->TH, t->text_rows);
+    int S = pick_splits(n_rows, t->TH, t->TH);
+    launch_partial(t->text_rows, t->TH, n_rows, t->fc1, t->TH, t->TH, S, t->part, t->TH, 0, t->flag, s);
+    hipLaunchKernelGGL(k_finish_linear, dim3(n_rows), dim3(BT), 0, s, t->part, S, n_rows, t->TH, t->fc1_b, nullptr, 1,
+                       t->fc1_out, t->TH);
+    S = pick_splits(n_rows, t->TH, t->H);
+    launch_partial(t->fc1_out, t->TH, n_rows, t->fc2, t->TH, t->H, S, t->part, t->H, 0, t->flag, s);
+    hipLaunchKernelGGL(k_finish_linear, dim3(n_rows), dim3(BT), 0, s, t->part, S, n_rows, t->H, t->fc2_b, nullptr, 0,
+                       t->proj, t->H);
+    hipLaunchKernelGGL(k_gather_rows, dim3(static_cast<unsigned>(cids.size())), dim3(BT), 0, s, t->codec_emb, t->d_cids,
+                       t->H, t->codec_rows);
+    hipLaunchKernelGGL(k_assemble_rows, dim3(n_pre), dim3(BT), 0, s, t->proj, t->codec_rows, t->spk, t->d_ia, t->d_ib,
+                       spk_row, t->H, t->prefill);
+    hipLaunchKernelGGL(k_assemble_rows, dim3(n_trail), dim3(BT), 0, s, t->proj, t->codec_rows, t->spk, t->d_ta, t->d_tb,
+                       -1, t->H, t->trailing);
+    NAVI_TRY_HIP(hipMemcpyAsync(t->pad_row, t->proj + static_cast<size_t>(i_pad) * t->H, t->H * 4,
+                                hipMemcpyDeviceToDevice, s), err, errlen);
+    NAVI_TRY_HIP(hipGetLastError(), err, errlen);
+    const navi_status st = check_flag(*t, "build_prompt", err, errlen);
+    if (st != NAVI_OK) return st;
+    out->prefill = t->prefill;
+    out->trailing = t->trailing;
+    out->tts_pad = t->pad_row;
+    out->n_prefill = n_pre;
+    out->n_trailing = n_trail;
+    return NAVI_OK;
+}
+
+navi_status navi_talker_prefill(navi_talker *t, const float *d_rows, int32_t n_rows, char *err, size_t errlen) {
+    if (!t || !d_rows) {
+        set_err(err, errlen, "talker: null argument");
+        return NAVI_ERR_INVALID;
+    }
+    if (n_rows < 1 || n_rows > t->mmax || n_rows > t->max_pos) {
+        set_err(err, errlen, "talker: prefill of %d rows exceeds the prompt buffers or the KV cache", n_rows);
+        return NAVI_ERR_INVALID;
+    }
+    const int T = n_rows, H = t->H, QKVW = t->QD + 2 * t->KVD;
+    hipStream_t s = device_state().stream;
+    NAVI_TRY_HIP(hipMemsetAsync(t->flag, 0, 4, s), err, errlen);
+    NAVI_TRY_HIP(hipEventRecord(t->ev0, s), err, errlen);
+    hipLaunchKernelGGL(k_resid_norm, dim3(T), dim3(BT), 0, s, nullptr, 0, d_rows, t->x, t->layers[0].ln1, t->eps, t->xn, T, H);
+    const float scale = 1.f / std::sqrt(static_cast<float>(HD));
+    const size_t att_lds = static_cast<size_t>(T) * sizeof(float);
+    for (int l = 0; l < t->L; ++l) {
+        const LayerW &w = t->layers[l];
+        int S = pick_splits(T, H, QKVW);
+        launch_partial(t->xn, H, T, w.wq, H, t->QD, S, t->part, QKVW, 0, t->flag, s);
+        launch_partial(t->xn, H, T, w.wk, H, t->KVD, S, t->part, QKVW, t->QD, t->flag, s);
+        launch_partial(t->xn, H, T, w.wv, H, t->KVD, S, t->part, QKVW, t->QD + t->KVD, t->flag, s);
+        hipLaunchKernelGGL(k_qkv_finish, dim3(T), dim3(BT), QKVW * sizeof(float), s, t->part, S, T, t->NQ, t->NKV, w.qn,
+                           w.kn, t->eps, t->invf, 0, t->q, t->kk[l], t->vv[l]);
+        hipLaunchKernelGGL(k_attn_prefill, dim3(T, t->NQ), dim3(128), att_lds, s, t->q, t->kk[l], t->vv[l], t->NQ, t->NKV, 0,
+                           scale, t->att);
+        S = pick_splits(T, t->QD, H);
+        launch_partial(t->att, t->QD, T, w.wo, t->QD, H, S, t->part, H, 0, t->flag, s);
+        hipLaunchKernelGGL(k_resid_norm, dim3(T), dim3(BT), 0, s, t->part, S, nullptr, t->x, w.ln2, t->eps, t->xn, T, H);
+        S = pick_splits(T, H, 2 * t->F);
+        launch_partial(t->xn, H, T, w.wg, H, t->F, S, t->part, 2 * t->F, 0, t->flag, s);
+        launch_partial(t->xn, H, T, w.wu, H, t->F, S, t->part, 2 * t->F, t->F, t->flag, s);
+        hipLaunchKernelGGL(k_swiglu, dim3(T), dim3(BT), 0, s, t->part, S, T, t->F, t->h);
+        S = pick_splits(T, t->F, H);
+        launch_partial(t->h, t->F, T, w.wd, t->F, H, S, t->part, H, 0, t->flag, s);
+        const float *next = l + 1 < t->L ? t->layers[l + 1].ln1 : t->final_norm;
+        hipLaunchKernelGGL(k_resid_norm, dim3(T), dim3(BT), 0, s, t->part, S, nullptr, t->x, next, t->eps, t->xn, T, H);
+    }
+    const float *last = t->xn + static_cast<size_t>(T - 1) * H;
+    NAVI_TRY_HIP(hipMemcpyAsync(t->hidden, last, H * 4, hipMemcpyDeviceToDevice, s), err, errlen);
+    const int S = pick_splits(1, H, t->V);
+    launch_partial(last, H, 1, t->head, H, t->V, S, t->part, t->V, 0, t->flag, s);
+    hipLaunchKernelGGL(k_finish_linear, dim3(1), dim3(BT), 0, s, t->part, S, 1, t->V, nullptr, nullptr, 0, t->logits, t->V);
+    NAVI_TRY_HIP(hipGetLastError(), err, errlen);
+    NAVI_TRY_HIP(hipEventRecord(t->ev1, s), err, errlen);
+    NAVI_TRY_HIP(hipEventSynchronize(t->ev1), err, errlen);
+    float ms = 0.f;
+    NAVI_TRY_HIP(hipEventElapsedTime(&ms, t->ev0, t->ev1), err, errlen);
+    t->last_ms = ms;
+    const navi_status st = check_flag(*t, "prefill", err, errlen);
+    if (st != NAVI_OK) return st;
+    t->n_used = T;
+    return NAVI_OK;
+}
+
+navi_status navi_talker_kv(navi_talker *t, navi_kv_view *out, int32_t *n_used) {
+    if (!t || !out) return NAVI_ERR_INVALID;
+    out->n_layer = t->L;
+    out->max_pos = t->max_pos;
+    out->kv_dim = t->KVD;
+    out->k = t->kk.data();
+    out->v = t->vv.data();
+    if (n_used) *n_used = t->n_used;
+    return NAVI_OK;
+}
+
+const float *navi_talker_hidden(const navi_talker *t) { return t ? t->hidden : nullptr; }
+const float *navi_talker_logits(const navi_talker *t) { return t ? t->logits : nullptr; }
+double navi_talker_last_ms(const navi_talker *t) { return t ? t->last_ms : 0.0; }
+
+navi_status navi_linear(const float *d_x, int32_t ldx, int32_t M, const uint16_t *w, int32_t K, int32_t N,
+                        const float *bias, const float *residual, int32_t act, float *d_y, int32_t ldy, char *err,
+                        size_t errlen) {
+    if (!d_x || !w || !d_y) {
+        set_err(err, errlen, "linear: null argument");
+        return NAVI_ERR_INVALID;
+    }
+    if (!linear_shape_ok(d_x, ldx, M, w, K, N) || ldy < N || (act != 0 && act != 1)) {
+        set_err(err, errlen, "linear: unsupported shape or alignment (M %d, K %d, N %d, ldx %d, ldy %d, act %d)", M, K, N,
+                ldx, ldy, act);
+        return NAVI_ERR_INVALID;
+    }
+    navi_status st = ensure_device(err, errlen);
+    if (st != NAVI_OK) return st;
+    hipStream_t s = device_state().stream;
+    const int S = pick_splits(M, K, N);
+    const size_t need = static_cast<size_t>(S) * M * N;
+    if (need > g_ws.floats) {
+        NAVI_TRY_HIP(hipStreamSynchronize(s), err, errlen);
+        if (g_ws.part) (void) hipFree(g_ws.part);
+        g_ws.part = nullptr;
+        g_ws.floats = 0;
+        NAVI_TRY_HIP(hipMalloc(&g_ws.part, need * sizeof(float)), err, errlen);
+        g_ws.floats = need;
+    }
+    if (!g_ws.flag) NAVI_TRY_HIP(hipMalloc(&g_ws.flag, 4), err, errlen);
+    NAVI_TRY_HIP(hipMemsetAsync(g_ws.flag, 0, 4, s), err, errlen);
+    launch_partial(d_x, ldx, M, w, K, N, S, g_ws.part, N, 0, g_ws.flag, s);
+    hipLaunchKernelGGL(k_finish_linear, dim3(M), dim3(BT), 0, s, g_ws.part, S, M, N, bias, residual, act, d_y, ldy);
+    NAVI_TRY_HIP(hipGetLastError(), err, errlen);
+    uint32_t f = 0;
+    NAVI_TRY_HIP(hipMemcpyAsync(&f, g_ws.flag, 4, hipMemcpyDeviceToHost, s), err, errlen);
+    NAVI_TRY_HIP(hipStreamSynchronize(s), err, errlen);
+    if (f) {
+        set_err(err, errlen, "linear: an activation is outside the f16 range (|x| >= 65504 or NaN)");
+        return NAVI_ERR_INVALID;
+    }
+    return NAVI_OK;
+}
+
+} // extern "C"

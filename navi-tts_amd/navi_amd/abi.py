@@ -26,6 +26,8 @@ EXPORTS = [
     "navi_frame_create", "navi_frame_destroy", "navi_frame_reset", "navi_frame_run", "navi_frame_step_out",
     "navi_frame_grid_blocks", "navi_frame_occupancy_per_mp", "navi_frame_set_taps", "navi_frame_tap_hidden",
     "navi_frame_tap_logits", "navi_frame_tap_cp_logits", "navi_frame_set_profile", "navi_frame_profile",
+    "navi_talker_create", "navi_talker_destroy", "navi_talker_build_prompt", "navi_talker_prefill", "navi_talker_kv",
+    "navi_talker_hidden", "navi_talker_logits", "navi_talker_last_ms", "navi_linear",
 ]
 
 
@@ -90,6 +92,11 @@ class FrameResult(C.Structure):
                 ("status", C.c_int32), ("error", C.c_char * 160)]
 
 
+class Prompt(C.Structure):
+    _fields_ = [("prefill", C.c_void_p), ("trailing", C.c_void_p), ("tts_pad", C.c_void_p),
+                ("n_prefill", C.c_int32), ("n_trailing", C.c_int32)]
+
+
 _lib = None
 
 
@@ -127,6 +134,21 @@ def lib() -> C.CDLL:
     for f in ("navi_frame_tap_hidden", "navi_frame_tap_logits", "navi_frame_tap_cp_logits"):
         getattr(L, f).argtypes = [C.c_void_p]
         getattr(L, f).restype = C.c_void_p
+    L.navi_talker_create.argtypes = [C.POINTER(ModelParams), C.POINTER(TensorRef), C.c_int32, C.c_int32, C.c_int32,
+                                     C.POINTER(C.c_void_p), E, C.c_size_t]
+    L.navi_talker_destroy.argtypes = [C.c_void_p]
+    L.navi_talker_destroy.restype = None
+    L.navi_talker_build_prompt.argtypes = [C.c_void_p, C.c_void_p, C.c_int32, C.c_int32, C.c_void_p, C.POINTER(Prompt),
+                                           E, C.c_size_t]
+    L.navi_talker_prefill.argtypes = [C.c_void_p, C.c_void_p, C.c_int32, E, C.c_size_t]
+    L.navi_talker_kv.argtypes = [C.c_void_p, C.POINTER(KvView), C.POINTER(C.c_int32)]
+    for f in ("navi_talker_hidden", "navi_talker_logits"):
+        getattr(L, f).argtypes = [C.c_void_p]
+        getattr(L, f).restype = C.c_void_p
+    L.navi_talker_last_ms.argtypes = [C.c_void_p]
+    L.navi_talker_last_ms.restype = C.c_double
+    L.navi_linear.argtypes = [C.c_void_p, C.c_int32, C.c_int32, C.c_void_p, C.c_int32, C.c_int32, C.c_void_p, C.c_void_p,
+                              C.c_int32, C.c_void_p, C.c_int32, E, C.c_size_t]
     _lib = L
     return L
 
@@ -369,3 +391,105 @@ class Frame:
 
     def step_out(self) -> np.ndarray:
         return download(self.d_step_out, np.float32, self.hidden)
+
+
+# ---- talker: prompt rows + prefill ----------------------------------------------------
+
+class TalkerKv:
+    """The talker-owned KV cache seen as the KvCache the frame takes (talker.h:20-24, 48)."""
+
+    def __init__(self, view: KvView, n_used: int):
+        self.view = view
+        self.n_layer, self.max_pos, self.kv_dim = view.n_layer, view.max_pos, view.kv_dim
+        self.k = [view.k[l] for l in range(view.n_layer)]
+        self.v = [view.v[l] for l in range(view.n_layer)]
+        self.n_used = n_used
+
+    def read(self, layer: int, n: int):
+        k = download(self.k[layer], np.uint16, n * self.kv_dim).view(np.float16).astype(np.float32)
+        v = download(self.v[layer], np.uint16, n * self.kv_dim).view(np.float16).astype(np.float32)
+        return k.reshape(n, self.kv_dim), v.reshape(n, self.kv_dim)
+
+    def fill(self, layer: int, k_rows: np.ndarray, v_rows: np.ndarray, pos0: int = 0):
+        KvCache.fill(self, layer, k_rows, v_rows, pos0)
+
+
+class Talker:
+    """talker.h:34-67 over navi_talker_*: prompt rows, the causal prefill, the KV cache."""
+
+    def __init__(self, weights: DeviceWeights, max_prompt_tokens: int = 1024, max_positions: int = 2048,
+                 params: ModelParams | None = None):
+        self.params = params or model_params(weights.kv)
+        self.kv_meta = weights.kv
+        refs, self._keep = weights.refs()
+        h = C.c_void_p()
+        err = C.create_string_buffer(256)
+        _check(lib().navi_talker_create(C.byref(self.params), refs, len(refs), max_prompt_tokens, max_positions,
+                                        C.byref(h), err, 256), err)
+        self.h = h.value
+        self.hidden = self.params.talker.hidden
+        v, n = KvView(), C.c_int32()
+        _check(lib().navi_talker_kv(self.h, C.byref(v), C.byref(n)), what="navi_talker_kv")
+        self.kv = TalkerKv(v, n.value)
+
+    def close(self):
+        if self.h:
+            lib().navi_talker_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def language_id(self, language: str) -> int:
+        if language in ("", "auto"):
+            return -1
+        key = f"talker.language.{language}"
+        if key not in self.kv_meta:
+            raise NaviError(NAVI_ERR_INVALID, f"talker: unknown language '{language}'")
+        return int(self.kv_meta[key])
+
+    def build_prompt(self, ids, language: str, speaker: np.ndarray) -> Prompt:
+        a = np.ascontiguousarray(ids, dtype=np.int32)
+        spk = np.ascontiguousarray(speaker, dtype=np.float32)
+        pr = Prompt()
+        err = C.create_string_buffer(256)
+        _check(lib().navi_talker_build_prompt(self.h, a.ctypes.data, a.size, self.language_id(language), spk.ctypes.data,
+                                              C.byref(pr), err, 256), err)
+        return pr
+
+    def prompt_arrays(self, pr: Prompt):
+        """(prefill rows, trailing rows, tts_pad row) downloaded as f32 arrays."""
+        H = self.hidden
+        return (download(pr.prefill, np.float32, pr.n_prefill * H).reshape(pr.n_prefill, H),
+                download(pr.trailing, np.float32, pr.n_trailing * H).reshape(pr.n_trailing, H),
+                download(pr.tts_pad, np.float32, H))
+
+    def prefill(self, d_rows: int, n_rows: int):
+        err = C.create_string_buffer(256)
+        _check(lib().navi_talker_prefill(self.h, d_rows, n_rows, err, 256), err)
+        self.kv.n_used = n_rows
+
+    @property
+    def d_hidden(self) -> int:
+        return lib().navi_talker_hidden(self.h)
+
+    @property
+    def d_logits(self) -> int:
+        return lib().navi_talker_logits(self.h)
+
+    def hidden_logits(self):
+        return (download(self.d_hidden, np.float32, self.hidden),
+                download(self.d_logits, np.float32, self.params.talker.vocab))
+
+    def last_ms(self) -> float:
+        return lib().navi_talker_last_ms(self.h)
+
+
+def linear(d_x: int, ldx: int, M: int, w: int, K: int, N: int, d_y: int, ldy: int, bias: int | None = None,
+           residual: int | None = None, act: int = 0):
+    """navi_linear: d_y = act(d_x . w^T + bias) + residual on the device."""
+    err = C.create_string_buffer(256)
+    _check(lib().navi_linear(d_x, ldx, M, w, K, N, bias, residual, act, d_y, ldy, err, 256), err)

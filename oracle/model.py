@@ -195,9 +195,11 @@ class Oracle:
             x = decoder_layer(self.cpp, w, x, ckv[l][0], ckv[l][1], pos0, self.invf_c)
         return x
 
-    def code_predictor(self, hidden: np.ndarray, cb0: int, s: sampler.Sampling, cp_seed: int, debug=None):
+    def code_predictor(self, hidden: np.ndarray, cb0: int, s: sampler.Sampling, cp_seed: int, debug=None, force=None):
         """codes[1..15] from the talker's post-norm hidden and cb0 (positions 0 and 1 run as one
-        2-row pass; causal, so identical to two single-row passes)."""
+        2-row pass; causal, so identical to two single-row passes). With `force` (16 codes), the
+        oracle records its own choice at each position in debug["cp_choice"] and continues with
+        the forced code (teacher forcing, so a comparison survives a near-tie flip)."""
         G = self.n_groups
         kvd = self.cpp.n_kv_head * self.cpp.head_dim
         ckv = [(torch.zeros(G, kvd), torch.zeros(G, kvd)) for _ in range(self.cpp.n_layer)]
@@ -211,7 +213,10 @@ class Oracle:
             lg = linear(h, self.lm_head[pos - 1])[0].numpy()
             if debug is not None:
                 debug.setdefault("cp_logits", []).append(lg)
-            codes.append(sampler.sample_cp(lg, s, cp_seed, pos))
+            c = sampler.sample_cp(lg, s, cp_seed, pos)
+            if debug is not None:
+                debug.setdefault("cp_choice", []).append(c)
+            codes.append(int(force[pos]) if force is not None else c)
         return codes
 
     def assemble_step(self, codes, trailing: np.ndarray) -> np.ndarray:
@@ -225,17 +230,26 @@ class Oracle:
         self.seen[:] = False
 
     def frame(self, s: sampler.Sampling, seed: int, frame_index: int, trailing: np.ndarray, *,
-              kv=None, n_past: int | None = None, step_in=None, hidden=None, logits=None, debug=None):
-        """run_first (hidden/logits given) or run (kv, n_past, step_in). Returns (codes, step_out)."""
+              kv=None, n_past: int | None = None, step_in=None, hidden=None, logits=None, debug=None, force=None):
+        """run_first (hidden/logits given) or run (kv, n_past, step_in). Returns (codes, step_out).
+        With `force` (16 codes): teacher forcing; the oracle's own choices go to debug["cb0_choice"]
+        and debug["cp_choice"], the forced codes drive the repetition set, the code predictor and
+        the next step. debug["cb0_scores"] holds the modified logits cb0 is chosen from."""
         if hidden is None:
             hidden, logits = self.talker_step(step_in, kv, n_past)
         if debug is not None:
             debug["hidden"], debug["logits"] = np.asarray(hidden, F32), np.asarray(logits, F32)
+            debug["cb0_scores"] = sampler.talker_modified_logits(logits, self.seen, self.eos_id, self.tp.vocab - 1024,
+                                                                 frame_index, s.min_frames, s.repetition_penalty)
         tseed, cseed = rng.frame_seeds(seed, frame_index)
         cb0 = sampler.sample_talker(logits, self.seen, s, tseed, frame_index, self.eos_id, self.tp.vocab - 1024)
+        if debug is not None:
+            debug["cb0_choice"] = cb0
+        if force is not None:
+            cb0 = int(force[0])
         if cb0 != self.eos_id:
             self.seen[cb0] = True
-        codes = self.code_predictor(hidden, cb0, s, cseed, debug)
+        codes = self.code_predictor(hidden, cb0, s, cseed, debug, force)
         return codes, self.assemble_step(codes, trailing)
 
     # -- prompt + prefill ----------------------------------------------------
