@@ -215,6 +215,42 @@ navi_status navi_linear(const float *d_x, int32_t ldx, int32_t M, const uint16_t
                         const float *bias, const float *residual, int32_t act, float *d_y, int32_t ldy,
                         char *err, size_t errlen);
 
+/* ---- vocoder: codes -> 24 kHz PCM (vocoder.h:27-55) -------------------------- */
+
+typedef struct navi_vocoder navi_vocoder;
+
+typedef struct {                       /* the codec decoder fields of params.h (params.cpp:106-117) */
+    navi_xformer_params xf;            /* pre-transformer: hidden 512, 8 layers, 16 x 64 heads, ff 1024,
+                                          rms eps 1e-5, rope theta 1e4 (vocab unused) */
+    int32_t latent_dim;                /* 1024 */
+    int32_t codebook_dim;              /* 512 (the RVQ works on codebook_dim / 2) */
+    int32_t codebook_size;             /* 2048 */
+    int32_t n_q, n_semantic;           /* 16, 1 */
+    int32_t decoder_dim;               /* 1536 */
+    int32_t sliding_window;            /* 72 */
+    int32_t upsampling_ratios[2];      /* 2, 2 */
+    int32_t upsample_rates[4];         /* 8, 5, 4, 3 */
+    int32_t samples_per_frame;         /* 1920 = the product of the ratios and rates */
+} navi_vocoder_params;
+
+/* Vocoder::create (vocoder.hip:465-600): binds the codec.decoder.* tensors by name, prepares
+ * the device-side copies the kernels read (concatenated projections and codebooks, tap-major
+ * conv weights, phase-split transposed convs, exp'd Snake parameters) and the streaming state
+ * for chunks of up to max_chunk_frames frames. */
+navi_status navi_vocoder_create(const navi_vocoder_params *p, const navi_tensor_ref *tensors, int32_t n_tensors,
+                                int32_t max_chunk_frames, navi_vocoder **out, char *err, size_t errlen);
+void navi_vocoder_destroy(navi_vocoder *v);
+/* Vocoder::reset (vocoder.hip:611-623): a new utterance (clears the causal histories, position 0). */
+navi_status navi_vocoder_reset(navi_vocoder *v);
+/* Vocoder::decode (vocoder.hip:625-643): codes host i32 [n_frames][n_q] in [0, codebook_size),
+ * continuing the utterance; writes n_frames * samples_per_frame samples to host pcm (where
+ * the reference appends to a vector). Decodes in chunks of max_chunk_frames; synchronous. */
+navi_status navi_vocoder_decode(navi_vocoder *v, const int32_t *codes, int32_t n_frames, float *pcm, char *err,
+                                size_t errlen);
+int32_t navi_vocoder_samples_per_frame(const navi_vocoder *v);   /* Vocoder::samples_per_frame */
+int32_t navi_vocoder_max_chunk_frames(const navi_vocoder *v);    /* Vocoder::max_chunk_frames */
+double navi_vocoder_last_ms(const navi_vocoder *v);              /* Vocoder::last_ms: device time of the last decode */
+
 #ifdef __cplusplus
 }
 #endif

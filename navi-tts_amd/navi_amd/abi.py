@@ -28,6 +28,8 @@ EXPORTS = [
     "navi_frame_tap_logits", "navi_frame_tap_cp_logits", "navi_frame_set_profile", "navi_frame_profile",
     "navi_talker_create", "navi_talker_destroy", "navi_talker_build_prompt", "navi_talker_prefill", "navi_talker_kv",
     "navi_talker_hidden", "navi_talker_logits", "navi_talker_last_ms", "navi_linear",
+    "navi_vocoder_create", "navi_vocoder_destroy", "navi_vocoder_reset", "navi_vocoder_decode",
+    "navi_vocoder_samples_per_frame", "navi_vocoder_max_chunk_frames", "navi_vocoder_last_ms",
 ]
 
 
@@ -92,6 +94,13 @@ class FrameResult(C.Structure):
                 ("status", C.c_int32), ("error", C.c_char * 160)]
 
 
+class VocoderParams(C.Structure):
+    _fields_ = [("xf", XformerParams), ("latent_dim", C.c_int32), ("codebook_dim", C.c_int32),
+                ("codebook_size", C.c_int32), ("n_q", C.c_int32), ("n_semantic", C.c_int32),
+                ("decoder_dim", C.c_int32), ("sliding_window", C.c_int32), ("upsampling_ratios", C.c_int32 * 2),
+                ("upsample_rates", C.c_int32 * 4), ("samples_per_frame", C.c_int32)]
+
+
 class Prompt(C.Structure):
     _fields_ = [("prefill", C.c_void_p), ("trailing", C.c_void_p), ("tts_pad", C.c_void_p),
                 ("n_prefill", C.c_int32), ("n_trailing", C.c_int32)]
@@ -147,6 +156,16 @@ def lib() -> C.CDLL:
         getattr(L, f).restype = C.c_void_p
     L.navi_talker_last_ms.argtypes = [C.c_void_p]
     L.navi_talker_last_ms.restype = C.c_double
+    L.navi_vocoder_create.argtypes = [C.POINTER(VocoderParams), C.POINTER(TensorRef), C.c_int32, C.c_int32,
+                                      C.POINTER(C.c_void_p), E, C.c_size_t]
+    L.navi_vocoder_destroy.argtypes = [C.c_void_p]
+    L.navi_vocoder_destroy.restype = None
+    L.navi_vocoder_reset.argtypes = [C.c_void_p]
+    L.navi_vocoder_decode.argtypes = [C.c_void_p, C.c_void_p, C.c_int32, C.c_void_p, E, C.c_size_t]
+    for f in ("navi_vocoder_samples_per_frame", "navi_vocoder_max_chunk_frames"):
+        getattr(L, f).argtypes = [C.c_void_p]
+    L.navi_vocoder_last_ms.argtypes = [C.c_void_p]
+    L.navi_vocoder_last_ms.restype = C.c_double
     L.navi_linear.argtypes = [C.c_void_p, C.c_int32, C.c_int32, C.c_void_p, C.c_int32, C.c_int32, C.c_void_p, C.c_void_p,
                               C.c_int32, C.c_void_p, C.c_int32, E, C.c_size_t]
     _lib = L
@@ -493,3 +512,63 @@ def linear(d_x: int, ldx: int, M: int, w: int, K: int, N: int, d_y: int, ldy: in
     """navi_linear: d_y = act(d_x . w^T + bias) + residual on the device."""
     err = C.create_string_buffer(256)
     _check(lib().navi_linear(d_x, ldx, M, w, K, N, bias, residual, act, d_y, ldy, err, 256), err)
+
+
+# ---- vocoder ---------------------------------------------------------------------------
+
+def vocoder_params(kv: dict) -> VocoderParams:
+    """The codec decoder fields of read_params (params.cpp:106-117)."""
+    ns = "codec.decoder"
+    xf = XformerParams(kv[f"{ns}.hidden_size"], kv[f"{ns}.num_hidden_layers"], kv[f"{ns}.num_attention_heads"],
+                       kv[f"{ns}.num_key_value_heads"], kv[f"{ns}.head_dim"], kv[f"{ns}.intermediate_size"], 0,
+                       float(kv[f"{ns}.rms_norm_eps"]), float(kv[f"{ns}.rope_theta"]))
+    p = VocoderParams()
+    p.xf = xf
+    p.latent_dim, p.codebook_dim = kv[f"{ns}.latent_dim"], kv[f"{ns}.codebook_dim"]
+    p.codebook_size, p.n_q = kv[f"{ns}.codebook_size"], kv[f"{ns}.num_quantizers"]
+    p.n_semantic, p.decoder_dim = kv[f"{ns}.num_semantic_quantizers"], kv[f"{ns}.decoder_dim"]
+    p.sliding_window = kv.get(f"{ns}.sliding_window", 0)
+    for i, r in enumerate(kv[f"{ns}.upsampling_ratios"]):
+        p.upsampling_ratios[i] = r
+    for i, r in enumerate(kv[f"{ns}.upsample_rates"]):
+        p.upsample_rates[i] = r
+    p.samples_per_frame = kv["codec.decode_upsample_rate"]
+    return p
+
+
+class Vocoder:
+    """vocoder.h:27-55 over navi_vocoder_*."""
+
+    def __init__(self, weights: DeviceWeights, max_chunk_frames: int = 32):
+        self.params = vocoder_params(weights.kv)
+        refs, self._keep = weights.refs()
+        h = C.c_void_p()
+        err = C.create_string_buffer(256)
+        _check(lib().navi_vocoder_create(C.byref(self.params), refs, len(refs), max_chunk_frames, C.byref(h), err, 256), err)
+        self.h = h.value
+        self.samples_per_frame = lib().navi_vocoder_samples_per_frame(self.h)
+        self.n_q = self.params.n_q
+
+    def close(self):
+        if self.h:
+            lib().navi_vocoder_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def reset(self):
+        _check(lib().navi_vocoder_reset(self.h), what="navi_vocoder_reset")
+
+    def decode(self, codes) -> np.ndarray:
+        c = np.ascontiguousarray(codes, dtype=np.int32).reshape(-1, self.n_q)
+        out = np.empty(c.shape[0] * self.samples_per_frame, np.float32)
+        err = C.create_string_buffer(256)
+        _check(lib().navi_vocoder_decode(self.h, c.ctypes.data, c.shape[0], out.ctypes.data, err, 256), err)
+        return out
+
+    def last_ms(self) -> float:
+        return lib().navi_vocoder_last_ms(self.h)
