@@ -251,6 +251,38 @@ int32_t navi_vocoder_samples_per_frame(const navi_vocoder *v);   /* Vocoder::sam
 int32_t navi_vocoder_max_chunk_frames(const navi_vocoder *v);    /* Vocoder::max_chunk_frames */
 double navi_vocoder_last_ms(const navi_vocoder *v);              /* Vocoder::last_ms: device time of the last decode */
 
+/* ---- one request end to end (Graph::synth, graph.cpp:52-111) ------------------------ */
+
+typedef struct {                       /* graph.h SynthRequest, with the text already tokenized */
+    const int32_t *ids;                /* host i32[n_ids]: role header, text, trailer (build_prompt's input) */
+    int32_t n_ids;
+    int32_t language_id;               /* codec language id, < 0 = auto */
+    const float *speaker;              /* host f32[hidden] */
+    /* Optional prompt given as device rows instead of ids (prefill, trailing, tts_pad): used when
+     * d_prefill != NULL, e.g. to prefill the text itself. */
+    const float *d_prefill, *d_trailing, *d_tts_pad;
+    int32_t n_prefill, n_trailing;
+    uint64_t seed;
+    int32_t max_frames;                /* cap (600 = 48 s at 12.5 Hz) */
+    navi_sampling sampling;
+    int32_t vocoder_batch;             /* frames per vocoder call; 0 = the vocoder's max chunk */
+    int32_t first_batch;               /* frames in the first call (time to first audio); 0 = vocoder_batch */
+} navi_synth_request;
+
+typedef struct {                       /* graph.h SynthStats */
+    int32_t n_tokens, n_frames, hit_cap, eos;
+    double prefill_ms, frames_ms, vocoder_ms, total_ms, ttfa_ms, audio_s, rtf;
+} navi_synth_stats;
+
+/* PCM of each vocoder batch, in order; n samples at 24 kHz. */
+typedef void (*navi_pcm_callback)(const float *pcm, int32_t n, void *user);
+
+/* Graph::synth: prompt -> prefill -> frames until EOS or max_frames -> vocoder in batches
+ * (first_batch frames first, then vocoder_batch), PCM handed to on_pcm per batch. Frame and
+ * vocoder are reset first; the frame runs on the talker's KV cache. Wall-clock stats. */
+navi_status navi_synth(navi_talker *t, navi_frame *f, navi_vocoder *v, const navi_synth_request *req,
+                       navi_pcm_callback on_pcm, void *user, navi_synth_stats *stats, char *err, size_t errlen);
+
 #ifdef __cplusplus
 }
 #endif

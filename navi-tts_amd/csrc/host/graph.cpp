@@ -1,0 +1,118 @@
+// One request end to end over the C ABI: prompt -> prefill -> frames -> vocoder batches
+// (Graph::synth, model/qwen3tts/graph.cpp:52-111), host code only.
+//
+// The request arrives tokenized (the tokenizer is not part of this library). Streaming
+// follows the reference: the vocoder runs as soon as first_batch frames (then vocoder_batch
+// frames) are pending, so time to first audio = prompt + prefill + first_batch frames + one
+// vocoder call; batching never changes the PCM (the vocoder is causal with carried state).
+#include "navi_amd.h"
+
+#include <algorithm>
+#include <chrono>
+#include <cstdio>
+#include <cstdarg>
+#include <vector>
+
+namespace {
+
+using clk = std::chrono::steady_clock;
+
+double ms_since(clk::time_point a) { return std::chrono::duration<double, std::milli>(clk::now() - a).count(); }
+
+void put_err(char *err, size_t errlen, const char *fmt, ...) {
+    if (!err || !errlen) return;
+    va_list ap;
+    va_start(ap, fmt);
+    std::vsnprintf(err, errlen, fmt, ap);
+    va_end(ap);
+}
+
+} // namespace
+
+extern "C" navi_status navi_synth(navi_talker *t, navi_frame *f, navi_vocoder *v, const navi_synth_request *req,
+                                  navi_pcm_callback on_pcm, void *user, navi_synth_stats *stats, char *err, size_t errlen) {
+    if (!t || !f || !v || !req || !stats) {
+        put_err(err, errlen, "synth: null argument");
+        return NAVI_ERR_INVALID;
+    }
+    *stats = navi_synth_stats{};
+    const auto t0 = clk::now();
+    navi_prompt pr{};
+    navi_status st;
+    if (req->d_prefill) {
+        if (!req->d_trailing || !req->d_tts_pad || req->n_prefill < 1 || req->n_trailing < 0) {
+            put_err(err, errlen, "synth: incomplete prompt rows");
+            return NAVI_ERR_INVALID;
+        }
+        pr.prefill = req->d_prefill;
+        pr.trailing = req->d_trailing;
+        pr.tts_pad = req->d_tts_pad;
+        pr.n_prefill = req->n_prefill;
+        pr.n_trailing = req->n_trailing;
+        stats->n_tokens = req->n_trailing;
+    } else {
+        if ((st = navi_talker_build_prompt(t, req->ids, req->n_ids, req->language_id, req->speaker, &pr, err, errlen)) != NAVI_OK)
+            return st;
+        stats->n_tokens = req->n_ids - 8;
+    }
+    if ((st = navi_talker_prefill(t, pr.prefill, pr.n_prefill, err, errlen)) != NAVI_OK) return st;
+    stats->prefill_ms = ms_since(t0);
+
+    navi_kv_view kv{};
+    if ((st = navi_talker_kv(t, &kv, nullptr)) != NAVI_OK) return st;
+    if ((st = navi_frame_reset(f)) != NAVI_OK || (st = navi_vocoder_reset(v)) != NAVI_OK) {
+        put_err(err, errlen, "synth: reset failed");
+        return st;
+    }
+    const int spf = navi_vocoder_samples_per_frame(v), cmax = navi_vocoder_max_chunk_frames(v);
+    const int batch = req->vocoder_batch > 0 ? std::min(req->vocoder_batch, cmax) : cmax;
+    const int first = req->first_batch > 0 ? std::min(req->first_batch, batch) : batch;
+    const size_t H = 1024;
+    std::vector<int32_t> codes;
+    std::vector<float> pcm;
+    int pending = 0;
+    bool first_audio = true;
+    auto flush = [&](bool final) -> navi_status {
+        if (pending == 0 || (!final && pending < (first_audio ? first : batch))) return NAVI_OK;
+        const auto tv = clk::now();
+        pcm.resize(static_cast<size_t>(pending) * spf);
+        const navi_status s = navi_vocoder_decode(v, codes.data() + codes.size() - static_cast<size_t>(pending) * 16, pending,
+                                                  pcm.data(), err, errlen);
+        if (s != NAVI_OK) return s;
+        stats->vocoder_ms += ms_since(tv);
+        pending = 0;
+        if (first_audio) {
+            stats->ttfa_ms = ms_since(t0);
+            first_audio = false;
+        }
+        if (on_pcm) on_pcm(pcm.data(), static_cast<int32_t>(pcm.size()), user);
+        return NAVI_OK;
+    };
+    for (int i = 0; i < req->max_frames; ++i) {
+        const float *trailing = i < pr.n_trailing ? pr.trailing + static_cast<size_t>(i) * H : pr.tts_pad;
+        navi_frame_result r{};
+        if (i == 0)
+            navi_frame_run(f, nullptr, 0, 1, navi_talker_hidden(t), navi_talker_logits(t), trailing, &req->sampling, req->seed, 0, &r);
+        else
+            navi_frame_run(f, &kv, pr.n_prefill + i - 1, 0, nullptr, nullptr, trailing, &req->sampling, req->seed, i, &r);
+        if (!r.ok) {
+            put_err(err, errlen, "frame %d: %s", i, r.error);
+            return r.status != NAVI_OK ? static_cast<navi_status>(r.status) : NAVI_ERR_HIP;
+        }
+        stats->frames_ms += r.us / 1000.0;
+        if (r.eos) {
+            stats->eos = 1;
+            break;
+        }
+        codes.insert(codes.end(), r.codes, r.codes + 16);
+        ++stats->n_frames;
+        ++pending;
+        if ((st = flush(false)) != NAVI_OK) return st;
+    }
+    stats->hit_cap = !stats->eos;
+    if ((st = flush(true)) != NAVI_OK) return st;
+    stats->total_ms = ms_since(t0);
+    stats->audio_s = static_cast<double>(stats->n_frames) * spf / 24000.0;
+    stats->rtf = stats->audio_s > 0 ? stats->total_ms / 1000.0 / stats->audio_s : 0.0;
+    return NAVI_OK;
+}

@@ -29,7 +29,7 @@ EXPORTS = [
     "navi_talker_create", "navi_talker_destroy", "navi_talker_build_prompt", "navi_talker_prefill", "navi_talker_kv",
     "navi_talker_hidden", "navi_talker_logits", "navi_talker_last_ms", "navi_linear",
     "navi_vocoder_create", "navi_vocoder_destroy", "navi_vocoder_reset", "navi_vocoder_decode",
-    "navi_vocoder_samples_per_frame", "navi_vocoder_max_chunk_frames", "navi_vocoder_last_ms",
+    "navi_vocoder_samples_per_frame", "navi_vocoder_max_chunk_frames", "navi_vocoder_last_ms", "navi_synth",
 ]
 
 
@@ -101,6 +101,25 @@ class VocoderParams(C.Structure):
                 ("upsample_rates", C.c_int32 * 4), ("samples_per_frame", C.c_int32)]
 
 
+class SynthRequest(C.Structure):
+    _fields_ = [("ids", C.c_void_p), ("n_ids", C.c_int32), ("language_id", C.c_int32), ("speaker", C.c_void_p),
+                ("d_prefill", C.c_void_p), ("d_trailing", C.c_void_p), ("d_tts_pad", C.c_void_p),
+                ("n_prefill", C.c_int32), ("n_trailing", C.c_int32), ("seed", C.c_uint64), ("max_frames", C.c_int32),
+                ("sampling", Sampling), ("vocoder_batch", C.c_int32), ("first_batch", C.c_int32)]
+
+
+class SynthStats(C.Structure):
+    _fields_ = [("n_tokens", C.c_int32), ("n_frames", C.c_int32), ("hit_cap", C.c_int32), ("eos", C.c_int32),
+                ("prefill_ms", C.c_double), ("frames_ms", C.c_double), ("vocoder_ms", C.c_double),
+                ("total_ms", C.c_double), ("ttfa_ms", C.c_double), ("audio_s", C.c_double), ("rtf", C.c_double)]
+
+    def as_dict(self) -> dict:
+        return {f: getattr(self, f) for f, _ in self._fields_}
+
+
+PCM_CALLBACK = C.CFUNCTYPE(None, C.POINTER(C.c_float), C.c_int32, C.c_void_p)
+
+
 class Prompt(C.Structure):
     _fields_ = [("prefill", C.c_void_p), ("trailing", C.c_void_p), ("tts_pad", C.c_void_p),
                 ("n_prefill", C.c_int32), ("n_trailing", C.c_int32)]
@@ -166,6 +185,8 @@ def lib() -> C.CDLL:
         getattr(L, f).argtypes = [C.c_void_p]
     L.navi_vocoder_last_ms.argtypes = [C.c_void_p]
     L.navi_vocoder_last_ms.restype = C.c_double
+    L.navi_synth.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.POINTER(SynthRequest), PCM_CALLBACK, C.c_void_p,
+                             C.POINTER(SynthStats), E, C.c_size_t]
     L.navi_linear.argtypes = [C.c_void_p, C.c_int32, C.c_int32, C.c_void_p, C.c_int32, C.c_int32, C.c_void_p, C.c_void_p,
                               C.c_int32, C.c_void_p, C.c_int32, E, C.c_size_t]
     _lib = L
@@ -572,3 +593,38 @@ class Vocoder:
 
     def last_ms(self) -> float:
         return lib().navi_vocoder_last_ms(self.h)
+
+
+# ---- one request end to end ------------------------------------------------------------
+
+def synth(talker: "Talker", frame: Frame, vocoder: "Vocoder", *, ids=None, language: str = "english", speaker=None,
+          prompt=None, seed: int = 0, max_frames: int = 600, sampling: Sampling | None = None, vocoder_batch: int = 0,
+          first_batch: int = 0):
+    """navi_synth (Graph::synth, graph.cpp:52-111). ids + speaker build the prompt; or `prompt` =
+    (d_prefill, n_prefill, d_trailing, n_trailing, d_tts_pad) gives the rows directly.
+    Returns (SynthStats, pcm f32 array, [samples per vocoder batch])."""
+    req = SynthRequest()
+    keep = []
+    if prompt is None:
+        a = np.ascontiguousarray(ids, dtype=np.int32)
+        spk = np.ascontiguousarray(speaker, dtype=np.float32)
+        keep += [a, spk]
+        req.ids, req.n_ids, req.speaker = a.ctypes.data, a.size, spk.ctypes.data
+        req.language_id = talker.language_id(language)
+    else:
+        req.d_prefill, req.n_prefill, req.d_trailing, req.n_trailing, req.d_tts_pad = prompt
+    req.seed = seed & ((1 << 64) - 1)
+    req.max_frames = max_frames
+    req.sampling = sampling or Sampling.make()
+    req.vocoder_batch, req.first_batch = vocoder_batch, first_batch
+    chunks = []
+
+    def on_pcm(ptr, n, _user):
+        chunks.append(np.ctypeslib.as_array(ptr, shape=(n,)).copy())
+
+    cb = PCM_CALLBACK(on_pcm)
+    st = SynthStats()
+    err = C.create_string_buffer(256)
+    _check(lib().navi_synth(talker.h, frame.h, vocoder.h, C.byref(req), cb, None, C.byref(st), err, 256), err)
+    pcm = np.concatenate(chunks) if chunks else np.zeros(0, np.float32)
+    return st, pcm, [c.size for c in chunks]

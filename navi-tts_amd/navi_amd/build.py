@@ -25,6 +25,8 @@ HIP_FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-Wall", "-
              "-I", str(ROOT / "include"), "-I", str(PKG / "csrc" / "hip")]
 
 HIP_SOURCES = ["device.hip", "frame.hip", "prefill.hip", "vocoder.hip"]
+HOST_SOURCES = ["graph.cpp"]          # csrc/host: C++ over the C ABI, no device code
+HOST_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-Wextra", "-I", str(ROOT / "include")]
 
 
 def _run(cmd: list[str]) -> None:
@@ -58,8 +60,15 @@ def build_hip(jobs: int = 8) -> Path:
         _run([HIPCC, *HIP_FLAGS, "-c", str(s), "-o", str(o)])
         return o
 
+    def compile_host(src: str) -> Path:
+        o = OBJ / (src + ".o")
+        _run(["g++", *HOST_FLAGS, "-c", str(PKG / "csrc" / "host" / src), "-o", str(o)])
+        return o
+
     with ThreadPoolExecutor(max_workers=jobs) as ex:
-        objs = list(ex.map(compile_one, HIP_SOURCES))
+        hip = ex.map(compile_one, HIP_SOURCES)
+        host = ex.map(compile_host, HOST_SOURCES)
+        objs = list(hip) + list(host)
     out = LIB / "libnavi_amd.so"
     _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(out), *map(str, objs)])
     return out

@@ -52,7 +52,8 @@ STRUCTS = {
     "navi_device_info": abi.DeviceInfo, "navi_xformer_params": abi.XformerParams, "navi_model_params": abi.ModelParams,
     "navi_tensor_ref": abi.TensorRef, "navi_kv_view": abi.KvView, "navi_sampling": abi.Sampling,
     "navi_frame_options": abi.FrameOptions, "navi_frame_result": abi.FrameResult, "navi_prompt": abi.Prompt,
-    "navi_vocoder_params": abi.VocoderParams,
+    "navi_vocoder_params": abi.VocoderParams, "navi_synth_request": abi.SynthRequest,
+    "navi_synth_stats": abi.SynthStats,
 }
 
 
