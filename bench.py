@@ -78,7 +78,94 @@ def measured_traffic():
 def make_blob(path: Path):
     from navi_amd import blob
     if not path.exists():
-        blob.write_random_blob(path, SEED, parts=("talker", "cp"))
+        blob.write_random_blob(path, SEED, parts=("talker", "cp", "codec"))
+
+
+def vocoder_flops_per_frame(kv: dict) -> float:
+    """Multiply-adds x 2 of one frame through the codec decoder (the convolutions and linears;
+    attention, norms and activations excluded): the work the matrix cores must do once."""
+    ns = "codec.decoder"
+    VH, FF = kv[f"{ns}.hidden_size"], kv[f"{ns}.intermediate_size"]
+    HDT = kv[f"{ns}.num_attention_heads"] * kv[f"{ns}.head_dim"]
+    L, CD, DD = kv[f"{ns}.latent_dim"], kv[f"{ns}.codebook_dim"], kv[f"{ns}.decoder_dim"]
+    mac = CD * CD + 3 * CD * L + L * VH + kv[f"{ns}.num_hidden_layers"] * (3 * HDT * VH + HDT * VH + 3 * FF * VH) + VH * L
+    rows = 1
+    for r in kv[f"{ns}.upsampling_ratios"]:
+        mac += rows * r * L * L                       # transposed conv, k = s
+        rows *= r
+        mac += rows * 8 * L * L                       # pwconv1 + pwconv2 (4L hidden)
+    mac += rows * 7 * L * DD
+    w = DD
+    for r in kv[f"{ns}.upsample_rates"]:
+        mac += rows * r * 2 * w * (w // 2)            # transposed conv: 2 taps per output phase
+        rows *= r
+        w //= 2
+        mac += rows * 3 * (7 * w * w + w * w)         # three residual units
+    mac += rows * 7 * w
+    return 2.0 * mac
+
+
+def streaming_and_vocoder(W, kv: dict, abi) -> dict:
+    """BASELINE configs[2] (streaming utterance) through navi_synth and configs[3] (vocoder),
+    plus the prefill times. The 128 text ids are prefilled with the prompt (130 rows: the
+    reference layout's 10 rows + the first 120 trailing text rows; the last 8 text rows and
+    tts_eos stream as trailing rows), so the context grows to ~370 as the config states."""
+    rng = np.random.default_rng(SEED)
+    talker = abi.Talker(W, max_prompt_tokens=256, max_positions=512)
+    frame = abi.Frame(W)
+    head = [kv["text.im_start_id"], kv["text.assistant_id"], 198]
+    tail = [kv["text.im_end_id"], 198, kv["text.im_start_id"], kv["text.assistant_id"], 198]
+    ids = head + rng.integers(0, 151643, 128).tolist() + tail
+    spk = rng.standard_normal(1024).astype(np.float32)
+    t0 = time.perf_counter()
+    pr = talker.build_prompt(ids, "english", spk)
+    build_ms = (time.perf_counter() - t0) * 1e3
+    n_pre = pr.n_prefill + 120
+    rows = abi.DeviceBuffer(4 * 1024 * n_pre)
+    abi.lib().navi_mem_d2d(rows.ptr, pr.prefill, 4 * 1024 * pr.n_prefill)
+    abi.lib().navi_mem_d2d(rows.ptr + 4 * 1024 * pr.n_prefill, pr.trailing, 4 * 1024 * 120)
+    trail = abi.DeviceBuffer(4 * 1024 * (pr.n_trailing - 120))
+    abi.lib().navi_mem_d2d(trail.ptr, pr.trailing + 4 * 1024 * 120, 4 * 1024 * (pr.n_trailing - 120))
+    pad = abi.DeviceBuffer(4 * 1024)
+    abi.lib().navi_mem_d2d(pad.ptr, pr.tts_pad, 4 * 1024)
+    pre_ms = {}
+    for n in (pr.n_prefill, n_pre):
+        t = []
+        for _ in range(5):
+            talker.prefill(rows.ptr, n)
+            t.append(talker.last_ms())
+        pre_ms[n] = float(np.median(t))
+    voc = abi.Vocoder(W, max_chunk_frames=32)
+    s = abi.Sampling.make(min_frames=240)
+    prompt = (rows.ptr, n_pre, trail.ptr, pr.n_trailing - 120, pad.ptr)
+    abi.synth(talker, frame, voc, prompt=prompt, seed=2, max_frames=16, sampling=s, vocoder_batch=16, first_batch=4)
+    st, pcm, _ = abi.synth(talker, frame, voc, prompt=prompt, seed=2, max_frames=240, sampling=s, vocoder_batch=16,
+                           first_batch=4)
+    codes = rng.integers(0, 2048, (240, 16))
+    v16 = abi.Vocoder(W, max_chunk_frames=16)
+    v240 = abi.Vocoder(W, max_chunk_frames=240)
+    v16.decode(codes[:16])
+    v240.decode(codes[:16])
+    v16.reset()
+    v240.reset()
+    v16.decode(codes)
+    ms16 = v16.last_ms() / 240
+    v240.decode(codes)
+    ms240 = v240.last_ms() / 240
+    fl = vocoder_flops_per_frame(kv)
+    return {
+        "prefill_ms": {"rows_10": round(pre_ms[pr.n_prefill], 3), "rows_130": round(pre_ms[n_pre], 3)},
+        "streaming": {"config": "configs[2]: 128 text ids prefilled (130 rows), speaker N(0,1), 240 frames, "
+                                "top-k 50, T 0.9, seed 2, first vocoder batch 4 then 16",
+                      "ttfa_ms": round(st.ttfa_ms, 2), "prompt_build_ms": round(build_ms, 2),
+                      "rtf": round(st.rtf, 4), "total_ms": round(st.total_ms, 1),
+                      "frames_ms_per_frame": round(st.frames_ms / max(st.n_frames, 1), 4),
+                      "vocoder_ms": round(st.vocoder_ms, 2), "n_frames": st.n_frames, "audio_s": round(st.audio_s, 2)},
+        "vocoder": {"config": "configs[3]: codes U[0,2048), 240 frames", "ms_per_frame_chunk16": round(ms16, 4),
+                    "ms_per_frame_block240": round(ms240, 4), "gflop_per_frame": round(fl / 1e9, 3),
+                    "tflops_block240": round(fl / (ms240 * 1e-3) / 1e12, 2),
+                    "mfma_frac_block240": round(fl / (ms240 * 1e-3) / 2.5e15, 5)},
+    }
 
 
 def cpu_baseline(path: Path, frames: int) -> dict:
@@ -117,6 +204,7 @@ def main():
     ap.add_argument("--cpu-frames", type=int, default=36, help="frames timed for the CPU baseline (0: skip)")
     ap.add_argument("--blob", default="", help="path for the random-init blob (default /dev/shm)")
     ap.add_argument("--keep-blob", action="store_true")
+    ap.add_argument("--no-streaming", action="store_true", help="skip the prefill / streaming / vocoder extras")
     ap.add_argument("--copy-calibration", type=float, default=0.0, metavar="GIB",
                     help="only run the counter-calibration copy kernel over GIB GiB and exit")
     args = ap.parse_args()
@@ -135,7 +223,7 @@ def main():
         print("[bench] writing random-init blob", flush=True, file=sys.stderr)
         make_blob(path)
         info = abi.device_open()
-        W = abi.DeviceWeights(path, select=lambda t: t.name.startswith("talker."))
+        W = abi.DeviceWeights(path, select=lambda t: t.dtype != 4)
         frame = abi.Frame(W)
         kvd = W.kv
         n_layer = kvd["talker.num_hidden_layers"]
@@ -169,6 +257,11 @@ def main():
         gbs = b["total"] / (dev_ms * 1e-3) / 1e9
         print(f"[bench] device ms/frame mean {dev_ms:.4f} median {np.median(dev)/1e3:.4f} min {dev.min()/1e3:.4f}; "
               f"wall {wall_ms:.4f} ms/frame; {gbs:.0f} GB/s over {b['total']/1e9:.4f} GB", flush=True, file=sys.stderr)
+        extra = None
+        if not args.no_streaming:
+            print("[bench] prefill, streaming utterance and vocoder", flush=True, file=sys.stderr)
+            extra = streaming_and_vocoder(W, kvd, abi)
+            print(f"[bench] {json.dumps(extra)}", flush=True, file=sys.stderr)
         del frame, W, kv
         cpu = None
         if args.cpu_frames > 0:
@@ -188,6 +281,8 @@ def main():
                          "bytes_per_frame": b["total"], "kernel": "k_frame"},
             "cpu_baseline": cpu,
         }
+        if extra:
+            line.update(extra)
         print(json.dumps(line), flush=True)
     finally:
         if not args.keep_blob and not args.blob and path.exists():
