@@ -52,6 +52,15 @@ static_assert(VC / NB == 2 * NW, "cp head: 2 rows per wave");
 // mailbox layout, in 64-bit words
 constexpr int MB_X = 0, MB_QKV = MB_X + 2 * H, MB_ATT = MB_QKV + 2 * QKV, MB_X2 = MB_ATT + 2 * QD,
               MB_H = MB_X2 + 2 * H, MB_LG = MB_H + 2 * FF, MB_WORDS = MB_LG + VT;
+// Every vector that all 256 blocks gather (att, x2, h, x, logits) is published in NREP copies,
+// MB_WORDS apart, and each block reads the copy of its XCD: the 32 CUs of an XCD then share one
+// copy's lines instead of all 256 CUs hammering the same few memory channels (all-to-all hop
+// of 1024 words on MI355X: 2.5 us with one copy, 1.6 us with one per XCD). q/k/v, read by the
+// 16 attention blocks only, stays in copy 0.
+constexpr int NREP = 8;
+
+// This wave's XCD (HW_REG_XCC_ID, a scalar register read): the mailbox copy it gathers from.
+__device__ __forceinline__ int xcc_copy() { return __builtin_amdgcn_s_getreg((3 << 11) | 20) & (NREP - 1); }
 constexpr uint32_t EPOCH_STRIDE = 4096;   // > tags used by one launch
 
 struct LayerPtrs {
@@ -205,14 +214,32 @@ template <int N, int CH>
 __device__ __forceinline__ bool gather(const Args &a, int off, uint32_t tag, float *dst, Smem &S) {
     static_assert(N % BT == 0 && N % CH == 0, "gather size");
     constexpr int PER = N / BT, NPROD = N / CH;
-    uint64_t *const mb = sgpr_ptr(a.mb + off);
+    uint64_t *const mb = sgpr_ptr(a.mb + xcc_copy() * MB_WORDS + off);
     PROF_MARK(a, S);
     if (wave() == 0) {
+        // every sentinel of this lane in flight at once; only the stale ones are read again
+        constexpr int NQ = (NPROD + WAVE - 1) / WAVE;
+        uint64_t sw[NQ];
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) {
+            const int pr = lane() + q * WAVE;
+            sw[q] = pr < NPROD ? mb_peek(mb + pr * CH + CH - 1) : static_cast<uint64_t>(tag) << 32;
+        }
+        uint64_t spins = 0;
         bool ok = true;
-        for (int q = lane(); q < NPROD && ok; q += WAVE) {
-            uint64_t *p = mb + q * CH + CH - 1;
-            uint64_t w = mb_peek(p);
-            ok = poll_word(a, p, tag, w);
+        for (;;) {
+            bool done = true;
+#pragma unroll
+            for (int q = 0; q < NQ; ++q) done &= tag_of(sw[q]) == tag;
+            if (done) break;
+            if (++spins >= a.spin_cap || ((spins & 63u) == 0 && aborted(a))) {
+                ctl_put(a.abort_word, a.epoch);
+                ok = false;
+                break;
+            }
+#pragma unroll
+            for (int q = 0; q < NQ; ++q)
+                if (tag_of(sw[q]) != tag) sw[q] = mb_peek(mb + (lane() + q * WAVE) * CH + CH - 1);
         }
         if (!ok) S.fail = 1;
     }
@@ -373,7 +400,7 @@ __device__ __forceinline__ void o_phase(const Args &a, const Regs &R, Smem &S, u
             acc = dot8(R.o[c2 + 1], xf[1], dot8(R.o[c2], xf[0], acc));
         }
         const float d = wave_sum(acc);
-        if (lane() == 0) mb_put(a.mb + MB_X2 + t * H + row, S.x[t][row] + d, tag);
+        if (lane() < NREP) mb_put(a.mb + lane() * MB_WORDS + MB_X2 + t * H + row, S.x[t][row] + d, tag);
     }
 }
 
@@ -392,10 +419,10 @@ __device__ __forceinline__ void gu_phase(const Args &a, const Regs &R, Smem &S, 
         }
     }
     __syncthreads();
-    if (tid() < RB * T) {
-        const int t = tid() / RB, j = tid() % RB;
+    if (tid() < RB * T * NREP) {                       // one (value, copy) per thread
+        const int v = tid() / NREP, r = tid() % NREP, t = v / RB, j = v % RB;
         const float g = S.part[t][j], u = S.part[t][RB + j];
-        mb_put(a.mb + MB_H + t * FF + blk() * RB + j, g / (1.f + expf(-g)) * u, tag);
+        mb_put(a.mb + r * MB_WORDS + MB_H + t * FF + blk() * RB + j, g / (1.f + expf(-g)) * u, tag);
     }
 }
 
@@ -413,7 +440,7 @@ __device__ __forceinline__ void down_phase(const Args &a, const Regs &R, Smem &S
             acc = dot8(R.dn[c2 + 1], xf[1], dot8(R.dn[c2], xf[0], acc));
         }
         const float d = wave_sum(acc);
-        if (lane() == 0) mb_put(a.mb + MB_X + t * H + row, S.x[t][row] + d, tag);
+        if (lane() < NREP) mb_put(a.mb + lane() * MB_WORDS + MB_X + t * H + row, S.x[t][row] + d, tag);
     }
 }
 
@@ -448,13 +475,24 @@ __device__ __forceinline__ void rope_pair(float *v, int i, float c, float s) {
 // Waits for q head h and kv head g of T rows: S.q/S.k/S.v[t].
 template <int T>
 __device__ __forceinline__ bool gather_head(const Args &a, int h, int g, uint32_t tag, Smem &S) {
-    bool ok = true;
-    for (int i = tid(); i < T * 3 * HD; i += BT) {
+    constexpr int PER = (T * 3 * HD + BT - 1) / BT;
+    int off[PER];
+    uint64_t w[PER];
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {                   // all of this thread's words in flight at once
+        const int i = tid() + k * BT;
         const int t = i / (3 * HD), seg = (i % (3 * HD)) / HD, d = i % HD;
-        const int off = MB_QKV + t * QKV + (seg == 0 ? h * HD : seg == 1 ? QD + g * HD : QD + KVD + g * HD) + d;
-        uint64_t w = mb_peek(a.mb + off);
-        if (ok) ok = poll_word(a, a.mb + off, tag, w);
-        (seg == 0 ? S.q[t] : seg == 1 ? S.k[t] : S.v[t])[d] = val_of(w);
+        off[k] = MB_QKV + t * QKV + (seg == 0 ? h * HD : seg == 1 ? QD + g * HD : QD + KVD + g * HD) + d;
+        if (i < T * 3 * HD) w[k] = mb_peek(a.mb + off[k]);
+    }
+    bool ok = true;
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+        const int i = tid() + k * BT;
+        if (i >= T * 3 * HD) continue;
+        if (ok) ok = poll_word(a, a.mb + off[k], tag, w[k]);
+        const int t = i / (3 * HD), seg = (i % (3 * HD)) / HD, d = i % HD;
+        (seg == 0 ? S.q[t] : seg == 1 ? S.k[t] : S.v[t])[d] = val_of(w[k]);
     }
     if (!ok) S.fail = 1;
     __syncthreads();
@@ -578,11 +616,12 @@ __device__ bool talker_attention(const Args &a, const Ctx &cx, float qkw, int il
     S.opart[wave()][2 * lane()] = acc0;
     S.opart[wave()][2 * lane() + 1] = acc1;
     __syncthreads();
-    if (tid() < HD) {
+    for (int i = tid(); i < HD * NREP; i += BT) {      // one (value, copy) per iteration
+        const int d = i % HD, r = i / HD;
         float o = 0.f;
 #pragma unroll
-        for (int w = 0; w < NW; ++w) o += S.opart[w][tid()];
-        mb_put(a.mb + MB_ATT + h * HD + tid(), o * (1.f / l), tag_att);
+        for (int w = 0; w < NW; ++w) o += S.opart[w][d];
+        mb_put(a.mb + r * MB_WORDS + MB_ATT + h * HD + d, o * (1.f / l), tag_att);
     }
     PROF_MARK(a, S);
     return true;
@@ -634,7 +673,12 @@ __device__ bool cp_attention(const Args &a, float qkw, int il, int p0, uint32_t 
         const int t = i / HD, d = i % HD, n = p0 + t + 1;
         float o = 0.f;
         for (int j = 0; j < n; ++j) o = fmaf(S.sc[t * NCB + j], h2f(S.u.m.ckv[1][il][j][d]), o);
-        mb_put(a.mb + MB_ATT + t * QD + h * HD + d, o, tag_att);
+        S.opart[t][d] = o;
+    }
+    __syncthreads();
+    for (int i = tid(); i < T * HD * NREP; i += BT) {  // one (value, copy) per iteration
+        const int r = i / (T * HD), v = i % (T * HD), t = v / HD, d = v % HD;
+        mb_put(a.mb + r * MB_WORDS + MB_ATT + t * QD + h * HD + d, S.opart[t][d], tag_att);
     }
     PROF_MARK(a, S);
     return true;
@@ -899,7 +943,7 @@ __global__ void __launch_bounds__(BT, 1) k_frame(Args a, const Weights *__restri
 #pragma unroll
             for (int r = 0; r < 3; ++r) {
                 const float d = wave_sum(dot8(R.th[r][1], xf[1], dot8(R.th[r][0], xf[0], 0.f)));
-                if (lane() == r) mb_put(a.mb + MB_LG + blk() * (VT / NB) + wave() * 3 + r, d, t_lg);
+                if (lane() < NREP) mb_put(a.mb + lane() * MB_WORDS + MB_LG + blk() * (VT / NB) + wave() * 3 + r, d, t_lg);
             }
         }
         if (!gather<VT, VT / NB>(a, MB_LG, t_lg, S.u.m.samp.lg, S)) return;
@@ -952,7 +996,7 @@ __global__ void __launch_bounds__(BT, 1) k_frame(Args a, const Weights *__restri
 #pragma unroll
             for (int r = 0; r < 2; ++r) {
                 const float d = wave_sum(dot8(R.lm[r][1], xf[1], dot8(R.lm[r][0], xf[0], 0.f)));
-                if (lane() == r) mb_put(a.mb + MB_LG + blk() * (VC / NB) + wave() * 2 + r, d, t_lg);
+                if (lane() < NREP) mb_put(a.mb + lane() * MB_WORDS + MB_LG + blk() * (VC / NB) + wave() * 2 + r, d, t_lg);
             }
         }
         if (!gather<VC, VC / NB>(a, MB_LG, t_lg, S.u.m.samp.lg, S)) return;
@@ -1132,7 +1176,7 @@ navi_status navi_frame_create(const navi_model_params *p, const navi_tensor_ref 
     w.eps_c = p->cp.rms_eps;
 
     if ((st = f->alloc(f->dw, 1, err, errlen)) != NAVI_OK) return fail(st);
-    if ((st = f->alloc(f->mb, MB_WORDS, err, errlen)) != NAVI_OK) return fail(st);
+    if ((st = f->alloc(f->mb, static_cast<size_t>(MB_WORDS) * NREP, err, errlen)) != NAVI_OK) return fail(st);
     if ((st = f->alloc(f->ctl, 32, err, errlen)) != NAVI_OK) return fail(st);
     if ((st = f->alloc(f->step_out, H, err, errlen)) != NAVI_OK) return fail(st);
     if ((st = f->alloc(f->seen, VT, err, errlen)) != NAVI_OK) return fail(st);
