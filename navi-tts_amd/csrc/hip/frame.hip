@@ -132,6 +132,7 @@ struct Smem {
     const uint16_t *lmh[CPH];
     float red[4 * NW];
     float q[2][HD], k[2][HD], v[2][HD];
+    float qw[NW][HD];               // talker attention: each wave's copy of the rotated q
     float sc[KCH];                  // attention weights of one key chunk (cp: [T][NCB])
     float opart[NW][HD];
     unsigned hist[256];
@@ -524,7 +525,7 @@ __device__ __forceinline__ void stage_kv(const uint16_t *Kc, const uint16_t *Vc,
 // staged in LDS by DMA in KCH-key chunks, the first chunk while this step's q/k/v are in
 // flight; chunks combine with the running-max softmax (one chunk up to pos = KCH).
 __device__ bool talker_attention(const Args &a, const Ctx &cx, float qkw, int il, uint32_t tag_qkv, uint32_t tag_att, Smem &S) {
-    const int h = blk(), g = h / GRP, pos = a.n_past;
+    const int h = blk(), g = h / GRP, pos = a.n_past;      // cached keys 0..pos-1, the current key at pos
     uint16_t *const Kbase = cx.kv[il], *const Vbase = cx.kv[MAX_TL + il];
     const uint16_t *Kc = Kbase + g * HD;
     uint16_t *Vc = Vbase + g * HD;
@@ -533,95 +534,123 @@ __device__ bool talker_attention(const Args &a, const Ctx &cx, float qkw, int il
     if (!gather_head<1>(a, h, g, tag_qkv, S)) return false;
     PROF_MARK(a, S);
     head_norms<1>(qkw, a.eps_t, S);
-    if (tid() < HD) {
-        const int i = tid() & (HD / 2 - 1);
-        float s, c;
-        sincosf(static_cast<float>(pos) * S.invf[0][i], &s, &c);
-        if (tid() < HD / 2) {
-            rope_pair(S.q[0], i, c, s);
-        } else {
-            rope_pair(S.k[0], i, c, s);
-            const float k0 = round_f16(S.k[0][i]), k1 = round_f16(S.k[0][i + HD / 2]);
-            S.k[0][i] = k0;
-            S.k[0][i + HD / 2] = k1;
-            if ((h & 1) == 0) {
-                uint16_t *kw = Kbase + static_cast<size_t>(pos) * KVD + g * HD;
-                gst(kw + i, f2h(k0));
-                gst(kw + i + HD / 2, f2h(k1));
-            }
-        }
-    } else {
-        const int d = tid() - HD;
-        const float v = round_f16(S.v[0][d]);
-        S.v[0][d] = v;
-        if ((h & 1) == 0) gst(Vc + static_cast<size_t>(pos) * KVD + d, f2h(v));
+    // Every wave, redundantly (no barrier): RoPE of q and of the current k with the pair (l, l + 64)
+    // in lane l, q copied to the wave's own LDS row for the score loop, the current key's score and
+    // value in registers; wave 0 of the even block of the kv group writes the new K/V row.
+    const int L = lane(), w = wave();
+    float sn, cs;
+    sincosf(static_cast<float>(pos) * S.invf[0][L], &sn, &cs);
+    {
+        const float qa = S.q[0][L], qb = S.q[0][L + HD / 2];
+        S.qw[w][L] = qa * cs - qb * sn;
+        S.qw[w][L + HD / 2] = qa * sn + qb * cs;
     }
-    float m = -INFINITY, l = 0.f, acc0 = 0.f, acc1 = 0.f;
+    const float ka = S.k[0][L], kb = S.k[0][L + HD / 2];
+    const float kra = round_f16(ka * cs - kb * sn), krb = round_f16(ka * sn + kb * cs);
+    const float s_cur = wave_sum(fmaf(S.qw[w][L], kra, S.qw[w][L + HD / 2] * krb)) * ATT_SCALE;
+    const float vc0 = round_f16(S.v[0][2 * L]), vc1 = round_f16(S.v[0][2 * L + 1]);
+    if (w == 0 && (h & 1) == 0) {
+        uint16_t *kw = Kbase + static_cast<size_t>(pos) * KVD + g * HD;
+        gst(kw + L, f2h(kra));
+        gst(kw + L + HD / 2, f2h(krb));
+        uint16_t *vw = Vc + static_cast<size_t>(pos) * KVD;
+        gst(vw + 2 * L, f2h(vc0));
+        gst(vw + 2 * L + 1, f2h(vc1));
+    }
     PROF_MARK(a, S);
-    for (int c0 = 0; c0 <= pos; c0 += KCH) {
-        const int n = min(KCH, pos + 1 - c0);
+    // Per-wave online softmax over the wave's keys of each chunk (wave w: chunk rows w*64 .. w*64+63);
+    // wave 0 also takes the current key in the last chunk. Lane L owns value dims 2L, 2L + 1.
+    float mw = -INFINITY, lw = 0.f, acc0 = 0.f, acc1 = 0.f;
+    const int slot8 = 2 * (L & 3);
+    for (int c0 = 0; c0 < max(pos, 1); c0 += KCH) {
+        const int n = min(KCH, pos - c0);                  // cached keys in this chunk (may be 0)
+        const bool last = c0 + KCH >= pos;
         if (c0 > 0) {
             __syncthreads();                               // previous chunk fully consumed
-            stage_kv(Kc, Vc, c0, min(KCH, pos - c0), S);
+            stage_kv(Kc, Vc, c0, n, S);
         }
         wait_vm_all();
-        __syncthreads();
+        __syncthreads();                                   // every wave's part of the chunk has landed
         PROF_MARK(a, S);
-        // scores: thread jj scores key c0 + jj
+        const int j0 = w * WAVE, cnt = max(0, min(WAVE, n - j0));
         float sj = -INFINITY;
-        if (tid() < n) {
-            const int jj = tid();
+        if (L < cnt) {
+            const int jj = j0 + L;
             float acc = 0.f;
-            if (c0 + jj == pos) {
-#pragma unroll 8
-                for (int d = 0; d < HD; ++d) acc = fmaf(S.q[0][d], S.k[0][d], acc);
-            } else {
 #pragma unroll
-                for (int c = 0; c < HD / 8; ++c) {
-                    const u32x4_t kv4 = *reinterpret_cast<const u32x4_t *>(&S.u.tkv.k[jj][(c ^ (jj & 15)) * 8]);
-                    uint4 kk;
-                    __builtin_memcpy(&kk, &kv4, 16);
-                    acc = dot8(kk, &S.q[0][c * 8], acc);
-                }
+            for (int c = 0; c < HD / 8; ++c) {
+                const u32x4_t kv4 = *reinterpret_cast<const u32x4_t *>(&S.u.tkv.k[jj][(c ^ (jj & 15)) * 8]);
+                uint4 kk;
+                __builtin_memcpy(&kk, &kv4, 16);
+                acc = dot8(kk, &S.qw[w][c * 8], acc);
             }
             sj = acc * ATT_SCALE;
         }
-        const float mn = fmaxf(m, block_max(sj, S));
-        const float e = tid() < n ? expf(sj - mn) : 0.f;
-        S.sc[tid()] = e;
-        const float alpha = expf(m - mn);                  // 0 for the first chunk
-        l = l * alpha + block_sum(e, S);                   // block_sum's barriers publish S.sc
-        acc0 *= alpha;
-        acc1 *= alpha;
-        m = mn;
-        PROF_MARK(a, S);
-        // V sum: wave w takes keys w, w + NW, ...; lane owns dims 2 lane, 2 lane + 1
-        const int slot8 = 2 * (lane() & 3);
-        for (int jj = wave(); jj < n; jj += NW) {
-            const float p = S.sc[jj];
-            float v0, v1;
-            if (c0 + jj == pos) {
-                v0 = S.v[0][2 * lane()];
-                v1 = S.v[0][2 * lane() + 1];
-            } else {
-                half2_t hv;
-                __builtin_memcpy(&hv, &S.u.tkv.v[jj][((lane() >> 2) ^ (jj & 15)) * 8 + slot8], 4);
-                v0 = static_cast<float>(hv[0]);
-                v1 = static_cast<float>(hv[1]);
+        const bool cur = last && w == 0;
+        float mn = fmaxf(mw, wave_max(sj));
+        if (cur) mn = fmaxf(mn, s_cur);
+        if (mn == -INFINITY) continue;                     // this wave has no key yet
+        const float e = L < cnt ? expf(sj - mn) : 0.f;
+        const float alpha = expf(mw - mn);                 // 0 while the wave had no key
+        const float ec = cur ? expf(s_cur - mn) : 0.f;
+        lw = lw * alpha + wave_sum(e) + ec;
+        acc0 = acc0 * alpha + ec * vc0;
+        acc1 = acc1 * alpha + ec * vc1;
+        mw = mn;
+        // V sum in groups of 8 keys: the 8 LDS reads are issued before the first FMA, and 2
+        // independent accumulator pairs halve the FMA chains (key j's weight: lane j's e)
+        float b0[2] = {acc0, 0.f}, b1[2] = {acc1, 0.f};
+        int j = 0;
+        for (; j + 8 <= cnt; j += 8) {
+            half2_t hv[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int jj = j0 + j + u;
+                __builtin_memcpy(&hv[u], &S.u.tkv.v[jj][((L >> 2) ^ (jj & 15)) * 8 + slot8], 4);
             }
-            acc0 = fmaf(p, v0, acc0);
-            acc1 = fmaf(p, v1, acc1);
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const float p = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), j + u));
+                b0[u & 1] = fmaf(p, static_cast<float>(hv[u][0]), b0[u & 1]);
+                b1[u & 1] = fmaf(p, static_cast<float>(hv[u][1]), b1[u & 1]);
+            }
         }
+        for (; j < cnt; ++j) {
+            const int jj = j0 + j;
+            const float p = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), j));
+            half2_t hv;
+            __builtin_memcpy(&hv, &S.u.tkv.v[jj][((L >> 2) ^ (jj & 15)) * 8 + slot8], 4);
+            b0[0] = fmaf(p, static_cast<float>(hv[0]), b0[0]);
+            b1[0] = fmaf(p, static_cast<float>(hv[1]), b1[0]);
+        }
+        acc0 = b0[0] + b0[1];
+        acc1 = b1[0] + b1[1];
     }
-    S.opart[wave()][2 * lane()] = acc0;
-    S.opart[wave()][2 * lane() + 1] = acc1;
+    PROF_MARK(a, S);
+    // combine the four waves' (max, sum, accumulator) and publish o / l
+    if (L == 0) {
+        S.red[w] = mw;
+        S.red[NW + w] = lw;
+    }
+    S.opart[w][2 * L] = acc0;
+    S.opart[w][2 * L + 1] = acc1;
     __syncthreads();
+    float M = S.red[0];
+#pragma unroll
+    for (int i = 1; i < NW; ++i) M = fmaxf(M, S.red[i]);
+    float sc[NW], den = 0.f;
+#pragma unroll
+    for (int i = 0; i < NW; ++i) {
+        sc[i] = S.red[i] == -INFINITY ? 0.f : expf(S.red[i] - M);
+        den = fmaf(S.red[NW + i], sc[i], den);
+    }
+    const float inv = 1.f / den;
     for (int i = tid(); i < HD * NREP; i += BT) {      // one (value, copy) per iteration
         const int d = i % HD, r = i / HD;
         float o = 0.f;
 #pragma unroll
-        for (int w = 0; w < NW; ++w) o += S.opart[w][d];
-        mb_put(a.mb + r * MB_WORDS + MB_ATT + h * HD + d, o * (1.f / l), tag_att);
+        for (int k = 0; k < NW; ++k) o = fmaf(S.opart[k][d], sc[k], o);
+        mb_put(a.mb + r * MB_WORDS + MB_ATT + h * HD + d, o * inv, tag_att);
     }
     PROF_MARK(a, S);
     return true;
