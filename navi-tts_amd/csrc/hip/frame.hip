@@ -133,6 +133,7 @@ struct Smem {
     float red[4 * NW];
     float q[2][HD], k[2][HD], v[2][HD];
     float qw[NW][HD];               // talker attention: each wave's copy of the rotated q
+    float nw[2 * HD];               // attention: q_norm (0..127) and k_norm (128..255) weights
     float sc[KCH];                  // attention weights of one key chunk (cp: [T][NCB])
     float opart[NW][HD];
     unsigned hist[256];
@@ -447,24 +448,13 @@ __device__ __forceinline__ void down_phase(const Args &a, const Regs &R, Smem &S
 
 // ---- attention --------------------------------------------------------------
 
-// q/k head RMSNorm over 128 dims of T rows' q and k vectors, one row at a time: waves
-// 0-1 normalise S.q[t], waves 2-3 S.k[t]; `w` is this thread's q_norm / k_norm weight.
-template <int T>
-__device__ __forceinline__ void head_norms(float w, float eps, Smem &S) {
-    const int d = tid() & (HD - 1);
-    const bool isk = wave() >= 2;
-#pragma unroll
-    for (int t = 0; t < T; ++t) {
-        const float e = isk ? S.k[t][d] : S.q[t][d];
-        const float ps = wave_sum(e * e);
-        if (lane() == 0) S.red[wave()] = ps;
-        __syncthreads();
-        const float ss = S.red[(wave() >> 1) * 2] + S.red[(wave() >> 1) * 2 + 1];
-        const float v = e * rsqrtf(ss / static_cast<float>(HD) + eps) * w;
-        if (isk) S.k[t][d] = v;
-        else S.q[t][d] = v;
-        __syncthreads();
-    }
+// RMSNorm of one 128-dim head row with weights nw, lane l's elements (l, l + 64) into (x0, x1).
+__device__ __forceinline__ void head_norm_pair(const float *row, const float *nw, float eps, float &x0, float &x1) {
+    const int l = lane();
+    const float a0 = row[l], a1 = row[l + HD / 2];
+    const float sc = rsqrtf(wave_sum(fmaf(a0, a0, a1 * a1)) / static_cast<float>(HD) + eps);
+    x0 = a0 * sc * nw[l];
+    x1 = a1 * sc * nw[l + HD / 2];
 }
 
 __device__ __forceinline__ void rope_pair(float *v, int i, float c, float s) {
@@ -531,21 +521,21 @@ __device__ bool talker_attention(const Args &a, const Ctx &cx, float qkw, int il
     uint16_t *Vc = Vbase + g * HD;
     if (pos > 0) stage_kv(Kc, Vc, 0, min(pos, KCH), S);
     PROF_MARK(a, S);
+    S.nw[tid()] = qkw;                                     // published by gather_head's barrier
     if (!gather_head<1>(a, h, g, tag_qkv, S)) return false;
     PROF_MARK(a, S);
-    head_norms<1>(qkw, a.eps_t, S);
-    // Every wave, redundantly (no barrier): RoPE of q and of the current k with the pair (l, l + 64)
-    // in lane l, q copied to the wave's own LDS row for the score loop, the current key's score and
-    // value in registers; wave 0 of the even block of the kv group writes the new K/V row.
+    // Every wave, redundantly (no barrier): head RMSNorm and RoPE of q and of the current k with
+    // the pair (l, l + 64) in lane l, q copied to the wave's own LDS row for the score loop, the
+    // current key's score and value in registers; wave 0 of the even block of the kv group writes
+    // the new K/V row.
     const int L = lane(), w = wave();
     float sn, cs;
     sincosf(static_cast<float>(pos) * S.invf[0][L], &sn, &cs);
-    {
-        const float qa = S.q[0][L], qb = S.q[0][L + HD / 2];
-        S.qw[w][L] = qa * cs - qb * sn;
-        S.qw[w][L + HD / 2] = qa * sn + qb * cs;
-    }
-    const float ka = S.k[0][L], kb = S.k[0][L + HD / 2];
+    float qa, qb, ka, kb;
+    head_norm_pair(S.q[0], S.nw, a.eps_t, qa, qb);
+    head_norm_pair(S.k[0], S.nw + HD, a.eps_t, ka, kb);
+    S.qw[w][L] = qa * cs - qb * sn;
+    S.qw[w][L + HD / 2] = qa * sn + qb * cs;
     const float kra = round_f16(ka * cs - kb * sn), krb = round_f16(ka * sn + kb * cs);
     const float s_cur = wave_sum(fmaf(S.qw[w][L], kra, S.qw[w][L + HD / 2] * krb)) * ATT_SCALE;
     const float vc0 = round_f16(S.v[0][2 * L]), vc1 = round_f16(S.v[0][2 * L + 1]);
@@ -662,52 +652,78 @@ template <int T>
 __device__ bool cp_attention(const Args &a, float qkw, int il, int p0, uint32_t tag_qkv, uint32_t tag_att, Smem &S) {
     const int h = blk(), g = h / GRP;
     PROF_MARK(a, S);
+    S.nw[tid()] = qkw;                                     // published by gather_head's barrier
     if (!gather_head<T>(a, h, g, tag_qkv, S)) return false;
     PROF_MARK(a, S);
-    head_norms<T>(qkw, a.eps_c, S);
-    for (int i = tid(); i < T * HD; i += BT) {          // q and k pairs of each row
-        const int t = i / HD, isk = (i / (HD / 2)) & 1, pr = i & (HD / 2 - 1);
-        float s, c;
-        sincosf(static_cast<float>(p0 + t) * S.invf[1][pr], &s, &c);
-        if (!isk) {
-            rope_pair(S.q[t], pr, c, s);
-        } else {
-            rope_pair(S.k[t], pr, c, s);
-            S.u.m.ckv[0][il][p0 + t][pr] = f2h(S.k[t][pr]);
-            S.u.m.ckv[0][il][p0 + t][pr + HD / 2] = f2h(S.k[t][pr + HD / 2]);
+    // Wave t computes row t (position p0 + t) alone: head norms and RoPE of q (into the wave's
+    // own LDS row) and of the new keys 0..T-1, written with the new values into S.ckv (every
+    // computing wave writes the same values, so each reads back what it wrote itself; later
+    // positions' passes read them after many barriers); then lane j scores key j against the
+    // whole q row (no cross-lane reduction per key), the softmax, the value sum (lane l: dims
+    // 2l, 2l + 1) and the publication.
+    const int L = lane(), w = wave();
+    if (w >= T) return true;
+    const int t = w, pos = p0 + t, n = pos + 1;
+    {
+        float sn, cs;
+        sincosf(static_cast<float>(pos) * S.invf[1][L], &sn, &cs);
+        float x0, x1;
+        head_norm_pair(S.q[t], S.nw, a.eps_c, x0, x1);
+        S.qw[w][L] = x0 * cs - x1 * sn;
+        S.qw[w][L + HD / 2] = x0 * sn + x1 * cs;
+    }
+#pragma unroll
+    for (int u = 0; u < T; ++u) {
+        float sn, cs;
+        sincosf(static_cast<float>(p0 + u) * S.invf[1][L], &sn, &cs);
+        float x0, x1;
+        head_norm_pair(S.k[u], S.nw + HD, a.eps_c, x0, x1);
+        S.u.m.ckv[0][il][p0 + u][L] = f2h(x0 * cs - x1 * sn);
+        S.u.m.ckv[0][il][p0 + u][L + HD / 2] = f2h(x0 * sn + x1 * cs);
+        S.u.m.ckv[1][il][p0 + u][2 * L] = f2h(S.v[u][2 * L]);
+        S.u.m.ckv[1][il][p0 + u][2 * L + 1] = f2h(S.v[u][2 * L + 1]);
+    }
+    float sl = -INFINITY;
+    if (L < n) {
+        float acc = 0.f;
+#pragma unroll
+        for (int c = 0; c < HD / 8; ++c) {
+            uint4 kk;
+            __builtin_memcpy(&kk, &S.u.m.ckv[0][il][L][c * 8], 16);
+            acc = dot8(kk, &S.qw[w][c * 8], acc);
         }
+        sl = acc * ATT_SCALE;
     }
-    for (int i = tid(); i < T * HD; i += BT) S.u.m.ckv[1][il][p0 + i / HD][i % HD] = f2h(S.v[i / HD][i % HD]);
-    __syncthreads();
-    // scores: wave w takes (row, key) pairs w, w+NW, ...
-    for (int pr = wave(); pr < T * NCB; pr += NW) {
-        const int t = pr / NCB, j = pr % NCB;
-        if (j > p0 + t) continue;
-        half2_t kk;
-        __builtin_memcpy(&kk, &S.u.m.ckv[0][il][j][2 * lane()], 4);
-        const float d = wave_sum(fmaf(S.q[t][2 * lane()], static_cast<float>(kk[0]), S.q[t][2 * lane() + 1] * static_cast<float>(kk[1])));
-        if (lane() == 0) S.sc[t * NCB + j] = d * ATT_SCALE;
+    const float m = wave_max(sl);
+    const float e = L < n ? expf(sl - m) : 0.f;
+    const float inv = 1.f / wave_sum(e);
+    float o0 = 0.f, o1 = 0.f, p0a = 0.f, p1a = 0.f;
+    int j = 0;
+    for (; j + 2 <= n; j += 2) {
+        const float pa = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), j));
+        const float pb = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), j + 1));
+        half2_t ha, hb;
+        __builtin_memcpy(&ha, &S.u.m.ckv[1][il][j][2 * L], 4);
+        __builtin_memcpy(&hb, &S.u.m.ckv[1][il][j + 1][2 * L], 4);
+        o0 = fmaf(pa, static_cast<float>(ha[0]), o0);
+        o1 = fmaf(pa, static_cast<float>(ha[1]), o1);
+        p0a = fmaf(pb, static_cast<float>(hb[0]), p0a);
+        p1a = fmaf(pb, static_cast<float>(hb[1]), p1a);
     }
-    __syncthreads();
-    if (wave() < T) {
-        const int t = wave(), n = p0 + t + 1;
-        const float s = lane() < n ? S.sc[t * NCB + lane()] : -INFINITY;
-        const float m = wave_max(s);
-        const float e = lane() < n ? expf(s - m) : 0.f;
-        const float inv = 1.f / wave_sum(e);
-        if (lane() < n) S.sc[t * NCB + lane()] = e * inv;
+    if (j < n) {
+        const float pa = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), j));
+        half2_t ha;
+        __builtin_memcpy(&ha, &S.u.m.ckv[1][il][j][2 * L], 4);
+        o0 = fmaf(pa, static_cast<float>(ha[0]), o0);
+        o1 = fmaf(pa, static_cast<float>(ha[1]), o1);
     }
-    __syncthreads();
-    for (int i = tid(); i < T * HD; i += BT) {
-        const int t = i / HD, d = i % HD, n = p0 + t + 1;
-        float o = 0.f;
-        for (int j = 0; j < n; ++j) o = fmaf(S.sc[t * NCB + j], h2f(S.u.m.ckv[1][il][j][d]), o);
-        S.opart[t][d] = o;
-    }
-    __syncthreads();
-    for (int i = tid(); i < T * HD * NREP; i += BT) {  // one (value, copy) per iteration
-        const int r = i / (T * HD), v = i % (T * HD), t = v / HD, d = v % HD;
-        mb_put(a.mb + r * MB_WORDS + MB_ATT + t * QD + h * HD + d, S.opart[t][d], tag_att);
+    o0 = (o0 + p0a) * inv;
+    o1 = (o1 + p1a) * inv;
+#pragma unroll
+    for (int r = 0; r < NREP; ++r) {
+        uint64_t *dst = a.mb + r * MB_WORDS + MB_ATT + t * QD + h * HD + 2 * L;
+        mb_put(dst, o0, tag_att);
+        mb_put(dst + 1, o1, tag_att);
     }
     PROF_MARK(a, S);
     return true;
