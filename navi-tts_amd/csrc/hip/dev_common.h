@@ -41,6 +41,29 @@ __device__ __forceinline__ float wave_max(float v) {
     return fmaxf(fmaxf(lane_value(v, 0), lane_value(v, 16)), fmaxf(lane_value(v, 32), lane_value(v, 48)));
 }
 
+// Inclusive prefix sum over the 64 lanes: row_shr 1/2/4/8 within each 16-lane row, then
+// row_bcast:15 into rows 1 and 3 and row_bcast:31 into rows 2 and 3. All lanes active.
+template <int CTRL, int ROWS>
+__device__ __forceinline__ int dpp_shift(int v) { return __builtin_amdgcn_update_dpp(0, v, CTRL, ROWS, 0xF, false); }
+__device__ __forceinline__ int wave_incl_scan(int v) {
+    v += dpp_shift<0x111, 0xF>(v);
+    v += dpp_shift<0x112, 0xF>(v);
+    v += dpp_shift<0x114, 0xF>(v);
+    v += dpp_shift<0x118, 0xF>(v);
+    v += dpp_shift<0x142, 0xA>(v);
+    v += dpp_shift<0x143, 0xC>(v);
+    return v;
+}
+
+__device__ __forceinline__ int wave_min_int(int v) {
+    v = min(v, __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false));
+    v = min(v, __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, false));
+    v = min(v, __builtin_amdgcn_mov_dpp(v, 0x141, 0xF, 0xF, false));
+    v = min(v, __builtin_amdgcn_mov_dpp(v, 0x140, 0xF, 0xF, false));
+    return min(min(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16)),
+               min(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
+}
+
 __device__ __forceinline__ float h2f(uint16_t h) {
     _Float16 f;
     __builtin_memcpy(&f, &h, 2);

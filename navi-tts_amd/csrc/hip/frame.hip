@@ -138,6 +138,8 @@ struct Smem {
     float opart[NW][HD];
     unsigned hist[256];
     int isel[4];
+    float sred[2 * NW];             // sampling: per-wave maxima / sums
+    int sidx[NW];                   // sampling: per-wave argmax
     int codes[NCB];
     int fail;
     int prof_i;
@@ -747,139 +749,124 @@ __device__ __forceinline__ uint32_t pcg32_next(uint64_t &s) {
     return (xs >> rot) | (xs << ((0u - rot) & 31u));
 }
 
-// Exact k-th largest of the PER values each thread holds: 4 passes of 8-bit
-// radix select over monotone keys (the value block_kth_largest computes).
-template <int PER>
-__device__ __forceinline__ float kth_largest(const float (&x)[PER], int k, Smem &S) {
-    unsigned prefix = 0, mask = 0;
-    int need = k;
-    for (int pass = 3; pass >= 0; --pass) {
-        const int shift = pass * 8;
-        S.hist[tid()] = 0;
-        __syncthreads();
-#pragma unroll
-        for (int i = 0; i < PER; ++i) {
-            const unsigned key = float_key(x[i]);
-            if ((key & mask) == prefix) atomicAdd(&S.hist[(key >> shift) & 0xFFu], 1u);
-        }
-        __syncthreads();
-        if (wave() == 0) {
-            // lane l owns digits 255-4l .. 252-4l (descending)
-            int c[4], tot = 0;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) { c[j] = static_cast<int>(S.hist[255 - 4 * lane() - j]); tot += c[j]; }
-            int incl = tot;
-#pragma unroll
-            for (int o = 1; o < WAVE; o <<= 1) {
-                const int v = __shfl_up(incl, o, WAVE);
-                if (lane() >= o) incl += v;
-            }
-            int above = incl - tot;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                if (above < need && above + c[j] >= need) { S.isel[0] = 255 - 4 * lane() - j; S.isel[1] = need - above; }
-                above += c[j];
-            }
-        }
-        __syncthreads();
-        need = S.isel[1];
-        prefix |= static_cast<unsigned>(S.isel[0]) << shift;
-        mask |= 0xFFu << shift;
-        __syncthreads();
-    }
-    return key_float(prefix);
-}
-
-// Chooses an index from the V values in S.u.m.samp.lg (already modified for the talker).
-// Greedy: argmax, lowest index on ties. Else: /temperature, exact top-k threshold
-// (values >= the k-th largest survive), e^(v - max), PCG32 draw over the survivors
-// in index order (frame.hip:258-296 semantics: f32 running sum, no contraction).
+// Sampling of one index from the V values in S.u.m.samp.lg (already modified for the talker),
+// identical in every block. Thread layout: element i = k * BT + tid, so index order is (k, wave,
+// lane). Greedy: argmax, lowest index on ties (frame.hip:178-203). Else (frame.hip:421-454,
+// 212-296): /temperature, exact top-k threshold (the k-th largest by a 4-pass 8-bit radix
+// select over monotone keys, values >= it survive), e^(v - max), and wave 0 draws with the
+// PCG32 u over the survivors in index order with the fused running sum of the reference
+// (`cum += p * inv_sum` compiles to an FMA under hipcc's default contraction). Each radix pass
+// costs one barrier: the four histograms are cleared up front, and every wave finds the digit
+// itself from the shared histogram with a DPP prefix sum.
 template <int V>
 __device__ __forceinline__ int block_sample(float temperature, int top_k, uint64_t seed, Smem &S) {
     constexpr int PER = V / BT;
     float x[PER];
-    const int base = tid() * PER;
 #pragma unroll
-    for (int i = 0; i < PER; ++i) x[i] = S.u.m.samp.lg[base + i];
-    __syncthreads();
+    for (int k = 0; k < PER; ++k) x[k] = S.u.m.samp.lg[k * BT + tid()];
     if (temperature <= 0.f) {
-        float bv = -INFINITY;
-        int bi = 0;
+        float bv = x[0];
+        int bi = tid();
 #pragma unroll
-        for (int i = 0; i < PER; ++i) if (x[i] > bv || (x[i] == bv && base + i < bi)) { bv = x[i]; bi = base + i; }
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) {
-            const float ov = __shfl_xor(bv, o, WAVE);
-            const int oi = __shfl_xor(bi, o, WAVE);
-            if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
-        }
-        if (lane() == 0) { S.red[wave()] = bv; S.u.m.samp.idx[wave()] = bi; }
+        for (int k = 1; k < PER; ++k)
+            if (x[k] > bv) { bv = x[k]; bi = k * BT + tid(); }   // k ascending: the first maximum of this thread
+        const float m = wave_max(bv);
+        const int wi = wave_min_int(bv == m ? bi : V);
+        if (lane() == 0) { S.sred[wave()] = m; S.sidx[wave()] = wi; }
         __syncthreads();
-        if (tid() == 0) {
-            float v = S.red[0];
-            int i0 = S.u.m.samp.idx[0];
-            for (int w = 1; w < NW; ++w)
-                if (S.red[w] > v || (S.red[w] == v && S.u.m.samp.idx[w] < i0)) { v = S.red[w]; i0 = S.u.m.samp.idx[w]; }
-            S.isel[2] = i0;
-        }
-        __syncthreads();
-        const int r = S.isel[2];
-        __syncthreads();
-        return r;
-    }
-    float mx = -INFINITY;
+        float v = S.sred[0];
+        int i0 = S.sidx[0];
 #pragma unroll
-    for (int i = 0; i < PER; ++i) { x[i] = x[i] / temperature; mx = fmaxf(mx, x[i]); }
-    mx = block_max(mx, S);
-    const float thr = (top_k > 0 && top_k < V) ? kth_largest<PER>(x, top_k, S) : -INFINITY;
-    float ssum = 0.f;
-    int cnt = 0;
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-        x[i] = x[i] >= thr ? expf(x[i] - mx) : 0.f;
-        ssum += x[i];
-        cnt += x[i] != 0.f;
+        for (int w = 1; w < NW; ++w)
+            if (S.sred[w] > v || (S.sred[w] == v && S.sidx[w] < i0)) { v = S.sred[w]; i0 = S.sidx[w]; }
+        return i0;
     }
-    ssum = block_sum(ssum, S);
-    // exclusive scan of the nonzero counts in thread order = index order
-    int incl = cnt;
+    unsigned (*hist)[256] = reinterpret_cast<unsigned (*)[256]>(S.u.m.samp.idx);
+    const bool topk = top_k > 0 && top_k < V;
+    if (topk) {
 #pragma unroll
-    for (int o = 1; o < WAVE; o <<= 1) {
-        const int v = __shfl_up(incl, o, WAVE);
-        if (lane() >= o) incl += v;
+        for (int p = 0; p < 4; ++p) hist[p][tid()] = 0u;
     }
-    if (lane() == WAVE - 1) S.hist[wave()] = static_cast<unsigned>(incl);
+    float lmx = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < PER; ++k) { x[k] = x[k] / temperature; lmx = fmaxf(lmx, x[k]); }
+    lmx = wave_max(lmx);
+    if (lane() == 0) S.sred[wave()] = lmx;
     __syncthreads();
-    int off = incl - cnt;
-    for (int w = 0; w < wave(); ++w) off += static_cast<int>(S.hist[w]);
-    int n_nz = 0;
-    for (int w = 0; w < NW; ++w) n_nz += static_cast<int>(S.hist[w]);
+    float mx = S.sred[0];
 #pragma unroll
-    for (int i = 0; i < PER; ++i) {
-        S.u.m.samp.lg[base + i] = x[i];
-        if (x[i] != 0.f) S.u.m.samp.idx[off++] = base + i;
+    for (int w = 1; w < NW; ++w) mx = fmaxf(mx, S.sred[w]);
+    float thr = -INFINITY;
+    if (topk) {
+        unsigned prefix = 0, mask = 0;
+        int need = top_k;
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            const int shift = 24 - 8 * p;
+#pragma unroll
+            for (int k = 0; k < PER; ++k) {
+                const unsigned key = float_key(x[k]);
+                if ((key & mask) == prefix) atomicAdd(&hist[p][(key >> shift) & 0xFFu], 1u);
+            }
+            __syncthreads();
+            // lane l owns digits 255-4l .. 252-4l (descending); every wave finds the digit itself
+            int c[4], tot = 0;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) { c[j] = static_cast<int>(hist[p][255 - 4 * lane() - j]); tot += c[j]; }
+            int above = wave_incl_scan(tot) - tot;
+            int dsel = -1, nsel = 0;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                if (dsel < 0 && above < need && above + c[j] >= need) { dsel = 255 - 4 * lane() - j; nsel = need - above; }
+                above += c[j];
+            }
+            const uint64_t hit = __ballot(dsel >= 0);
+            const int src = hit ? static_cast<int>(__builtin_ctzll(hit)) : 0;   // exactly one lane finds it
+            const int digit = __builtin_amdgcn_readlane(dsel, src);
+            need = __builtin_amdgcn_readlane(nsel, src);
+            prefix |= static_cast<unsigned>(digit) << shift;
+            mask |= 0xFFu << shift;
+        }
+        thr = key_float(prefix);
     }
+    float ls = 0.f;
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+        const float e = x[k] >= thr ? expf(x[k] - mx) : 0.f;
+        S.u.m.samp.lg[k * BT + tid()] = e;
+        ls += e;
+    }
+    ls = wave_sum(ls);
+    if (lane() == 0) S.sred[NW + wave()] = ls;
     __syncthreads();
-    if (tid() == 0) {
+    if (wave() == 0) {
+        float ssum = 0.f;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) ssum += S.sred[NW + w];
         const float inv = 1.f / ssum;
         uint64_t st = seed * 0x9E3779B97F4A7C15ull + 0xBF58476D1CE4E5B9ull + 1ull;
         (void) pcg32_next(st); (void) pcg32_next(st); (void) pcg32_next(st);
         const float u = static_cast<float>(pcg32_next(st) >> 8) * (1.0f / 16777216.0f);
         int chosen = V - 1;
         float cum = 0.f;
-        for (int j = 0; j < n_nz; ++j) {
-            const int i = S.u.m.samp.idx[j];
-            // Fused, as the reference's `cum += p[i] * inv_sum` compiles under hipcc's default
-            // contraction (frame.hip:290-292).
-            cum = fmaf(S.u.m.samp.lg[i], inv, cum);
-            if (cum >= u) { chosen = i; break; }
+        bool found = false;
+        for (int k = 0; k < PER && !found; ++k) {
+            for (int w = 0; w < NW && !found; ++w) {
+                const int base = k * BT + w * WAVE;
+                const float ev = S.u.m.samp.lg[base + lane()];
+                uint64_t nz = __ballot(ev != 0.f);
+                while (nz && !found) {
+                    const int b = static_cast<int>(__builtin_ctzll(nz));
+                    nz &= nz - 1;
+                    cum = fmaf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(ev), b)), inv, cum);
+                    if (cum >= u) { chosen = base + b; found = true; }
+                }
+            }
         }
-        S.isel[2] = chosen;
+        if (lane() == 0) S.isel[2] = chosen;
     }
     __syncthreads();
-    const int r = S.isel[2];
-    __syncthreads();
-    return r;
+    return S.isel[2];
 }
 
 // ---- the frame ---------------------------------------------------------------
