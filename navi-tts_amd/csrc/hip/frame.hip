@@ -125,7 +125,6 @@ struct Smem {
             uint16_t ckv[2][MAX_CL][NCB][HD];   // this block's cp K/V (kv head blockIdx/2), whole frame
         } m;
     } u;
-    float part[2][6 * NW];          // gate/up dots before SiLU(g)*u
     float invf[2][HD / 2];          // RoPE inverse frequencies (talker, cp)
     LayerPtrs lp[MAX_TL + MAX_CL];  // weight pointers, copied once: a scalar load of the table in
     const uint16_t *emb[CPH];       // global memory misses the scalar cache under the weight stream
@@ -276,20 +275,36 @@ __device__ __forceinline__ bool gather_rows(const Args &a, int off, uint32_t tag
 
 // ---- RMSNorm of T rows (every block, redundantly) ---------------------------
 
+// RMSNorm, split (every block, redundantly): out[t] = x[t] * w elementwise and this wave's partial
+// sum of x[t]^2 in S.red, published by one barrier; the scalar rsqrt(mean(x^2) + eps) (norm_scale)
+// multiplies the matvec results instead of every element (block_rmsnorm, frame.hip:107-114).
 template <int T>
-__device__ __forceinline__ void rmsnorm_rows(const float (*x)[H], const float (&w)[H / BT], float eps, float (*out)[H], Smem &S) {
+__device__ __forceinline__ void norm_prep(const float (*x)[H], const float (&w)[H / BT], float (*out)[H], Smem &S) {
     constexpr int PER = H / BT;
 #pragma unroll
     for (int t = 0; t < T; ++t) {
-        float e[PER], ss = 0.f;
+        float ss = 0.f;
 #pragma unroll
-        for (int k = 0; k < PER; ++k) { e[k] = x[t][tid() + k * BT]; ss = fmaf(e[k], e[k], ss); }
-        ss = block_sum(ss, S);
-        const float sc = rsqrtf(ss / static_cast<float>(H) + eps);
-#pragma unroll
-        for (int k = 0; k < PER; ++k) out[t][tid() + k * BT] = e[k] * sc * w[k];
+        for (int k = 0; k < PER; ++k) {
+            const float e = x[t][tid() + k * BT];
+            ss = fmaf(e, e, ss);
+            out[t][tid() + k * BT] = e * w[k];
+        }
+        ss = wave_sum(ss);
+        if (lane() == 0) S.red[t * NW + wave()] = ss;
     }
     __syncthreads();
+}
+
+template <int T>
+__device__ __forceinline__ void norm_scale(float eps, float (&sc)[T], const Smem &S) {
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+        float ss = 0.f;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) ss += S.red[t * NW + w];
+        sc[t] = rsqrtf(ss / static_cast<float>(H) + eps);
+    }
 }
 
 // This thread's RMSNorm weights (elements tid + k * BT).
@@ -340,9 +355,9 @@ __device__ __forceinline__ void load_gu(Regs &R, const LayerPtrs &L) {
     constexpr int RB = FF / NB;   // 12 gate + 12 up rows per block
 #pragma unroll
     for (int r = 0; r < 6; ++r) {
-        const int vr = wave() * 6 + r;
-        const uint16_t *M = sgpr_ptr((vr < RB ? L.wg : L.wu) + static_cast<size_t>(blk() * RB) * H);
-        const uint16_t *p = M + static_cast<size_t>(vr < RB ? vr : vr - RB) * H + lane() * 8;
+        const int vr = wave() * 3 + (r % 3);               // r < 3: gate row vr, r >= 3: up row vr
+        const uint16_t *M = sgpr_ptr((r < 3 ? L.wg : L.wu) + static_cast<size_t>(blk() * RB) * H);
+        const uint16_t *p = M + static_cast<size_t>(vr) * H + lane() * 8;
         R.gu[r][0] = ldg16_stream(p);
         R.gu[r][1] = ldg16_stream(p + 512);
     }
@@ -376,7 +391,7 @@ __device__ __forceinline__ void load_lm(Regs &R, const uint16_t *head) {
 // ---- matvec phases --------------------------------------------------------
 
 template <int T>
-__device__ __forceinline__ void qkv_phase(const Args &a, const Regs &R, Smem &S, uint32_t tag) {
+__device__ __forceinline__ void qkv_phase(const Args &a, const Regs &R, Smem &S, uint32_t tag, const float (&sc)[T]) {
     const int row0 = blk() * (QKV / NB) + wave() * 4;
 #pragma unroll
     for (int t = 0; t < T; ++t) {
@@ -384,7 +399,7 @@ __device__ __forceinline__ void qkv_phase(const Args &a, const Regs &R, Smem &S,
         xfrag<2>(S.xn[t], 0, xf);
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const float d = wave_sum(dot8(R.qkv[r][1], xf[1], dot8(R.qkv[r][0], xf[0], 0.f)));
+            const float d = wave_sum(dot8(R.qkv[r][1], xf[1], dot8(R.qkv[r][0], xf[0], 0.f))) * sc[t];
             if (lane() == r) mb_put(a.mb + MB_QKV + t * QKV + row0 + r, d, tag);
         }
     }
@@ -410,23 +425,22 @@ __device__ __forceinline__ void o_phase(const Args &a, const Regs &R, Smem &S, u
 
 // h[row] = silu(Wg . xn) * (Wu . xn)
 template <int T>
-__device__ __forceinline__ void gu_phase(const Args &a, const Regs &R, Smem &S, uint32_t tag) {
-    constexpr int RB = FF / NB;
+__device__ __forceinline__ void gu_phase(const Args &a, const Regs &R, Smem &S, uint32_t tag, const float (&sc)[T]) {
+    constexpr int RB = FF / NB;   // wave w holds gate rows 3w..3w+2 (r < 3) and the matching up rows (r >= 3)
 #pragma unroll
     for (int t = 0; t < T; ++t) {
         float xf[2][8];
         xfrag<2>(S.xn[t], 0, xf);
+        float d[6];
 #pragma unroll
-        for (int r = 0; r < 6; ++r) {
-            const float d = wave_sum(dot8(R.gu[r][1], xf[1], dot8(R.gu[r][0], xf[0], 0.f)));
-            if (lane() == 0) S.part[t][wave() * 6 + r] = d;
+        for (int r = 0; r < 6; ++r) d[r] = wave_sum(dot8(R.gu[r][1], xf[1], dot8(R.gu[r][0], xf[0], 0.f))) * sc[t];
+        // lane 8r + c publishes h row 3w + r to copy c
+        const int r = lane() >> 3, c = lane() & 7;
+        if (r < 3) {
+            const float g = r == 0 ? d[0] : r == 1 ? d[1] : d[2];
+            const float u = r == 0 ? d[3] : r == 1 ? d[4] : d[5];
+            mb_put(a.mb + c * MB_WORDS + MB_H + t * FF + blk() * RB + wave() * 3 + r, g / (1.f + expf(-g)) * u, tag);
         }
-    }
-    __syncthreads();
-    if (tid() < RB * T * NREP) {                       // one (value, copy) per thread
-        const int v = tid() / NREP, r = tid() % NREP, t = v / RB, j = v % RB;
-        const float g = S.part[t][j], u = S.part[t][RB + j];
-        mb_put(a.mb + r * MB_WORDS + MB_H + t * FF + blk() * RB + j, g / (1.f + expf(-g)) * u, tag);
     }
 }
 
@@ -890,9 +904,11 @@ __device__ __forceinline__ bool run_layer(const Args &a, const Ctx &cx, Regs &R,
     const LayerPtrs &N = layer_at(a, S, has_next ? gi + 1 : gi);
     const float eps = TALKER ? a.eps_t : a.eps_c;
 
-    rmsnorm_rows<T>(S.x, R.ln1, eps, S.xn, S);
+    norm_prep<T>(S.x, R.ln1, S.xn, S);
+    float sc[T];
+    norm_scale<T>(eps, sc, S);
     const uint32_t t_qkv = seq.next();
-    qkv_phase<T>(a, R, S, t_qkv);
+    qkv_phase<T>(a, R, S, t_qkv, sc);
     const float qkw = R.qkw;     // this layer's q/k norm weight; the prefetch below replaces it
     if (has_next) load_qkv(R, N);
 
@@ -909,9 +925,10 @@ __device__ __forceinline__ bool run_layer(const Args &a, const Ctx &cx, Regs &R,
     if (has_next) load_o(R, N);
 
     if (!gather_rows<T, H, H / NB>(a, MB_X2, t_x2, &S.x[0][0], S)) return false;
-    rmsnorm_rows<T>(S.x, R.ln2, eps, S.xn, S);
+    norm_prep<T>(S.x, R.ln2, S.xn, S);
+    norm_scale<T>(eps, sc, S);
     const uint32_t t_h = seq.next();
-    gu_phase<T>(a, R, S, t_h);
+    gu_phase<T>(a, R, S, t_h, sc);
     if (has_next) load_gu(R, N);
 
     if (!gather_rows<T, FF, FF / NB>(a, MB_H, t_h, S.u.m.big, S)) return false;
@@ -966,7 +983,9 @@ __global__ void __launch_bounds__(BT, 1) k_frame(Args a, const Weights *__restri
         __syncthreads();
         for (int il = 0; il < a.n_tl; ++il)
             if (!run_layer<1, true>(a, cx, R, il, a.n_past, seq, S, il == a.n_tl - 1 ? W.codec_head : nullptr)) return;
-        rmsnorm_rows<1>(S.x, R.fn, a.eps_t, S.xn, S);
+        norm_prep<1>(S.x, R.fn, S.xn, S);
+        float hsc[1];
+        norm_scale<1>(a.eps_t, hsc, S);
         load_norm(R.fn, W.cp_norm);
         const uint32_t t_lg = seq.next();
         {
@@ -974,11 +993,14 @@ __global__ void __launch_bounds__(BT, 1) k_frame(Args a, const Weights *__restri
             xfrag<2>(S.xn[0], 0, xf);
 #pragma unroll
             for (int r = 0; r < 3; ++r) {
-                const float d = wave_sum(dot8(R.th[r][1], xf[1], dot8(R.th[r][0], xf[0], 0.f)));
+                const float d = wave_sum(dot8(R.th[r][1], xf[1], dot8(R.th[r][0], xf[0], 0.f))) * hsc[0];
                 if (lane() < NREP) mb_put(a.mb + lane() * MB_WORDS + MB_LG + blk() * (VT / NB) + wave() * 3 + r, d, t_lg);
             }
         }
         if (!gather<VT, VT / NB>(a, MB_LG, t_lg, S.u.m.samp.lg, S)) return;
+        // the post-norm hidden the code predictor takes: each thread scales the elements it wrote
+        // (and is the only one to read below), after the gather's barriers ended the head's reads
+        for (int i = tid(); i < H; i += BT) S.xn[0][i] *= hsc[0];
     } else {
         for (int i = tid(); i < H; i += BT) S.xn[0][i] = gld(a.hidden_in + i);
         for (int i = tid(); i < VT; i += BT) S.u.m.samp.lg[i] = gld(a.logits_in + i);
@@ -1020,14 +1042,16 @@ __global__ void __launch_bounds__(BT, 1) k_frame(Args a, const Weights *__restri
                 if (!run_layer<1, false>(a, cx, R, gi, pos, seq, S, il == a.n_cl - 1 ? S.lmh[pos - 1] : nullptr)) return;
         }
         const int row = pos == 1 ? 1 : 0;
-        rmsnorm_rows<1>(reinterpret_cast<const float (*)[H]>(S.x[row]), R.fn, a.eps_c, S.xn, S);
+        norm_prep<1>(reinterpret_cast<const float (*)[H]>(S.x[row]), R.fn, S.xn, S);
+        float hsc[1];
+        norm_scale<1>(a.eps_c, hsc, S);
         const uint32_t t_lg = seq.next();
         {
             float xf[2][8];
             xfrag<2>(S.xn[0], 0, xf);
 #pragma unroll
             for (int r = 0; r < 2; ++r) {
-                const float d = wave_sum(dot8(R.lm[r][1], xf[1], dot8(R.lm[r][0], xf[0], 0.f)));
+                const float d = wave_sum(dot8(R.lm[r][1], xf[1], dot8(R.lm[r][0], xf[0], 0.f))) * hsc[0];
                 if (lane() < NREP) mb_put(a.mb + lane() * MB_WORDS + MB_LG + blk() * (VC / NB) + wave() * 2 + r, d, t_lg);
             }
         }
