@@ -35,7 +35,7 @@ constexpr int LDW = CCH + 8;             // padded LDS row (halves)
 typedef _Float16 half8v __attribute__((ext_vector_type(8)));
 
 enum Pro { PRO_NONE = 0, PRO_SNAKE = 1, PRO_SILU_GATE = 2 };
-enum Epi { EPI_BIAS = 0, EPI_GELU = 1, EPI_RESIDUAL = 2, EPI_SCALE_RESIDUAL = 3 };
+enum Epi { EPI_BIAS = 0, EPI_GELU = 1, EPI_RESIDUAL = 2, EPI_SCALE_RESIDUAL = 3, EPI_CLAMP = 4 };
 
 struct ConvArgs {
     const float *x;        // input rows [T][ldx]; PRO_SILU_GATE: gate at [ci], up at [Cin + ci]
@@ -153,6 +153,7 @@ __global__ void __launch_bounds__(BT) k_conv_mfma(ConvArgs a) {
             if (EPI == EPI_GELU) v = 0.5f * v * (1.f + erff(v * 0.70710678118654752f));
             else if (EPI == EPI_RESIDUAL) v += gld(a.res + o);
             else if (EPI == EPI_SCALE_RESIDUAL) v = v * sc + gld(a.res + o);
+            else if (EPI == EPI_CLAMP) v = fminf(fmaxf(v, -1.f), 1.f);
             gst(a.y + o, v);
         }
 }
@@ -296,23 +297,11 @@ __global__ void __launch_bounds__(128) k_window_attn(const float *qkv, int nh, i
     }
 }
 
-// The last conv (Cin -> 1, k7, Snake prologue) and the clamp: one thread per sample.
-__global__ void __launch_bounds__(BT) k_final_conv(const float *x, const float *hist, int T, int Cin, const uint16_t *w,
-                                                   const float *bias, const float *sa, const float *sb, float *pcm) {
+// pcm[t] = y[t][0]: the last conv runs on the matrix cores with its one output channel padded to
+// a 16-column tile (15 zero weight rows); this keeps column 0.
+__global__ void __launch_bounds__(BT) k_take_col0(const float *y, int T, int ld, float *pcm) {
     const int t = blockIdx.x * BT + threadIdx.x;
-    if (t >= T) return;
-    float acc = gld(bias);
-    for (int ci = 0; ci < Cin; ++ci) {
-        const float a = gld(sa + ci), b = gld(sb + ci);
-        for (int j = 0; j < 7; ++j) {
-            const int tt = t - 6 + j;
-            float v = tt >= 0 ? gld(x + static_cast<size_t>(tt) * Cin + ci) : gld(hist + static_cast<size_t>(6 + tt) * Cin + ci);
-            const float s = sinf(v * a);
-            v += s * s * b;
-            acc = fmaf(h2f(gld(w + ci * 7 + j)), v, acc);
-        }
-    }
-    gst(pcm + t, fminf(fmaxf(acc, -1.f), 1.f));
+    if (t < T) gst(pcm + t, gld(y + static_cast<size_t>(t) * ld));
 }
 
 // ---- weight preparation (vocoder.hip:350-420, done here on the device) ----------------
@@ -389,10 +378,8 @@ struct navi_vocoder {
     Conv up_conv[2];
     ConvNeXt cnx[2];
     Block blocks[4];
-    // final conv
-    const uint16_t *fw = nullptr;
-    const float *fb = nullptr, *fsa = nullptr, *fsb = nullptr;
-    float *fhist = nullptr, *fhist2 = nullptr;
+    Conv final_conv;                   // Cin -> 1 padded to 16 output channels
+    float *pcm16 = nullptr;            // [rows][16] output of the padded final conv
     float *invf = nullptr;
     uint32_t *flag = nullptr;
     // buffers
@@ -436,6 +423,7 @@ void launch_k(const ConvArgs &a, int pro, int epi, dim3 grid, hipStream_t s) {
     NAVI_CONV(PRO_SNAKE, EPI_BIAS)
     NAVI_CONV(PRO_SNAKE, EPI_RESIDUAL)
     NAVI_CONV(PRO_SILU_GATE, EPI_SCALE_RESIDUAL)
+    NAVI_CONV(PRO_SNAKE, EPI_CLAMP)
 #undef NAVI_CONV
 }
 
@@ -531,12 +519,8 @@ navi_status decode_chunk(navi_vocoder &v, int T, char *err, size_t errlen) {
         }
         in = v.P[b];
     }
-    hipLaunchKernelGGL(k_final_conv, dim3((R + BT - 1) / BT), dim3(BT), 0, s, in, v.fhist, R, width, v.fw, v.fb, v.fsa, v.fsb,
-                       v.pcm);
-    const size_t nh = static_cast<size_t>(6) * width;
-    hipLaunchKernelGGL(k_hist_update, dim3(static_cast<unsigned>((nh + BT - 1) / BT)), dim3(BT), 0, s, v.fhist, in, R, 6, width,
-                       width, v.fhist2);
-    std::swap(v.fhist, v.fhist2);
+    VOC_TRY(run_conv(v, v.final_conv, PRO_SNAKE, EPI_CLAMP, in, R, width, v.pcm16, 16, nullptr, nullptr, err, errlen));
+    hipLaunchKernelGGL(k_take_col0, dim3((R + BT - 1) / BT), dim3(BT), 0, s, v.pcm16, R, 16, v.pcm);
     v.pos0 += T;
     NAVI_TRY_HIP(hipGetLastError(), err, errlen);
     return NAVI_OK;
@@ -808,11 +792,28 @@ navi_status navi_vocoder_create(const navi_vocoder_params *p, const navi_tensor_
         VA(v->Q[b], rows * C * bk.Cout);
         width = bk.Cout;
     }
-    VB(uint16_t, DEC + "decoder.6.conv.weight", NAVI_DT_F16, 1, width, 7, v->fw);
-    VB(float, DEC + "decoder.6.conv.bias", NAVI_DT_F32, 1, 0, 0, v->fb);
-    if ((st = snake(DEC + "decoder.5", width, v->fsa, v->fsb)) != NAVI_OK) return fail(st);
-    VA(v->fhist, static_cast<size_t>(6) * width);
-    VA(v->fhist2, static_cast<size_t>(6) * width);
+    {
+        const uint16_t *w = nullptr, *w1 = nullptr;
+        const float *b = nullptr;
+        VB(uint16_t, DEC + "decoder.6.conv.weight", NAVI_DT_F16, 1, width, 7, w);
+        VB(float, DEC + "decoder.6.conv.bias", NAVI_DT_F32, 1, 0, 0, b);
+        Conv &c = v->final_conv;
+        c.Cin = width; c.Cout = 16; c.K = 7;
+        // tap-major [1][7][Cin] into row 0 of a zeroed [16][7][Cin]; bias 0 for the padding columns
+        if ((st = relayout(w, 1, width, 7, w1)) != NAVI_OK) return fail(st);
+        uint16_t *wp = nullptr;
+        float *bp = nullptr;
+        VA(wp, static_cast<size_t>(16) * 7 * width);
+        VA(bp, 16);
+        if (hipMemcpyAsync(wp, w1, static_cast<size_t>(7) * width * 2, hipMemcpyDeviceToDevice, s) != hipSuccess ||
+            hipMemcpyAsync(bp, b, 4, hipMemcpyDeviceToDevice, s) != hipSuccess) {
+            set_err(err, errlen, "vocoder: final conv copy failed");
+            return fail(NAVI_ERR_HIP);
+        }
+        c.w = wp;
+        c.bias = bp;
+        if ((st = hist(c)) != NAVI_OK || (st = snake(DEC + "decoder.5", width, c.sa, c.sb)) != NAVI_OK) return fail(st);
+    }
     float invf[64] = {};
     for (int i = 0; i < xf.head_dim / 2; ++i) invf[i] = static_cast<float>(1.0 / std::pow(xf.rope_theta, (2.0 * i) / xf.head_dim));
     VA(v->invf, 64);
@@ -833,6 +834,7 @@ navi_status navi_vocoder_create(const navi_vocoder_params *p, const navi_tensor_
     VA(v->G, up_rows * 4 * L);
     VA(v->d, up_rows * DD);
     VA(v->pcm, C * p->samples_per_frame);
+    VA(v->pcm16, C * p->samples_per_frame * 16);
 #undef VB
 #undef VA
     if (hipMemcpyAsync(v->invf, invf, sizeof invf, hipMemcpyHostToDevice, s) != hipSuccess || hipEventCreate(&v->ev0) != hipSuccess ||
@@ -856,8 +858,7 @@ navi_status navi_vocoder_reset(navi_vocoder *v) {
     v->pos0 = 0;
     auto zero = [&](float *ptr, size_t n) { return !ptr || hipMemsetAsync(ptr, 0, n * sizeof(float), s) == hipSuccess; };
     auto zc = [&](Conv &c) { return zero(c.hist, static_cast<size_t>(c.H) * c.Cin) && zero(c.hist2, static_cast<size_t>(c.H) * c.Cin); };
-    bool ok = zc(v->pre_conv) && zc(v->dec0) && zero(v->fhist, 6 * static_cast<size_t>(v->blocks[3].Cout)) &&
-              zero(v->fhist2, 6 * static_cast<size_t>(v->blocks[3].Cout));
+    bool ok = zc(v->pre_conv) && zc(v->dec0) && zc(v->final_conv);
     for (int j = 0; j < 2; ++j) ok = ok && zero(v->cnx[j].hist, 6 * static_cast<size_t>(v->L)) && zero(v->cnx[j].hist2, 6 * static_cast<size_t>(v->L));
     for (Block &b : v->blocks) {
         ok = ok && zc(b.up);
