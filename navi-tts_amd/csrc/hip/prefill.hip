@@ -74,21 +74,39 @@ __global__ void __launch_bounds__(BT) k_linear_partial(LinArgs a) {
         for (int c = 0; c < KC / 32; ++c)
             if (c < steps) dst[c] = __builtin_nontemporal_load(wrow + (k0 >> 3) + c * 4);
     };
+    // A staging: every thread owns IT float4s of the MT*16 x kc step tile; the step's loads are
+    // all issued at once (and the next step's before this step's MFMAs), never one by one.
+    constexpr int IT = MT * 16 * (KC / 4) / BT;
+    f32x4_t av[IT];
+    auto load_a = [&](int k0) {
+        const int q4 = min(KC, ke - k0) >> 2;
+#pragma unroll
+        for (int it = 0; it < IT; ++it) {
+            const int i = threadIdx.x + it * BT, r = i / q4, c4 = (i - r * q4) * 4, m = m0 + r;
+            av[it] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+            if (r < MT * 16 && m < a.M) av[it] = *(const NAVI_GLOBAL f32x4_t *) (a.x + static_cast<size_t>(m) * a.ldx + k0 + c4);
+        }
+    };
     load_b(bcur, kb);
+    load_a(kb);
     bool bad = false;
     for (int k0 = kb; k0 < ke; k0 += KC) {
         const int kc = min(KC, ke - k0);
         if (k0 + KC < ke) load_b(bnext, k0 + KC);
         __syncthreads();                                   // previous step's readers are done
-        const int q4 = kc >> 2;
-        for (int i = threadIdx.x; i < MT * 16 * q4; i += BT) {
-            const int r = i / q4, c4 = (i - r * q4) * 4, m = m0 + r;
-            f32x4_t v = f32x4_t{0.f, 0.f, 0.f, 0.f};
-            if (m < a.M) v = *(const NAVI_GLOBAL f32x4_t *) (a.x + static_cast<size_t>(m) * a.ldx + k0 + c4);
+        {
+            const int q4 = kc >> 2;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) split_store(v[j], &ahi[r][c4 + j], &alo[r][c4 + j], bad);
+            for (int it = 0; it < IT; ++it) {
+                const int i = threadIdx.x + it * BT, r = i / q4, c4 = (i - r * q4) * 4;
+                if (r < MT * 16) {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) split_store(av[it][j], &ahi[r][c4 + j], &alo[r][c4 + j], bad);
+                }
+            }
         }
         __syncthreads();
+        if (k0 + KC < ke) load_a(k0 + KC);
 #pragma unroll
         for (int c = 0; c < KC / 32; ++c) {
             if (c < (kc >> 5)) {
@@ -125,11 +143,24 @@ __device__ __forceinline__ float block_sum256(float v, float *red) {
     return red[0] + red[1] + red[2] + red[3];
 }
 
-__device__ __forceinline__ float sum_parts(const float *part, int S, size_t stride, size_t idx) {
-    float v = gld(part + idx);
-    for (int s = 1; s < S; ++s) v += gld(part + s * stride + idx);
+// part[0] + part[1] + ... + part[S-1] at four consecutive columns, in that order (deterministic);
+// the loads go out eight partials at a time instead of one after another.
+__device__ __forceinline__ f32x4_t sum_parts4(const float *part, int S, size_t stride, size_t idx) {
+    f32x4_t v = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int s0 = 0; s0 < S; s0 += 8) {
+        f32x4_t t[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            if (s0 + j < S) t[j] = *(const NAVI_GLOBAL f32x4_t *) (part + (s0 + j) * stride + idx);
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            if (s0 + j < S) v = s0 + j == 0 ? t[j] : v + t[j];
+    }
     return v;
 }
+
+__device__ __forceinline__ f32x4_t ld4(const float *p) { return *(const NAVI_GLOBAL f32x4_t *) p; }
+__device__ __forceinline__ void st4(float *p, f32x4_t v) { *(NAVI_GLOBAL f32x4_t *) p = v; }
 
 __device__ __forceinline__ float silu(float g) { return g / (1.f + expf(-g)); }
 
@@ -137,12 +168,14 @@ __device__ __forceinline__ float silu(float g) { return g / (1.f + expf(-g)); }
 __global__ void __launch_bounds__(BT) k_finish_linear(const float *part, int S, int M, int N, const float *bias,
                                                       const float *residual, int act, float *y, int ldy) {
     const int m = blockIdx.x;
-    for (int n = threadIdx.x; n < N; n += BT) {
-        float v = sum_parts(part, S, static_cast<size_t>(M) * N, static_cast<size_t>(m) * N + n);
-        if (bias) v += gld(bias + n);
-        if (act == 1) v = silu(v);
-        if (residual) v += gld(residual + static_cast<size_t>(m) * ldy + n);
-        gst(y + static_cast<size_t>(m) * ldy + n, v);
+    for (int n = threadIdx.x * 4; n < N; n += BT * 4) {
+        f32x4_t v = sum_parts4(part, S, static_cast<size_t>(M) * N, static_cast<size_t>(m) * N + n);
+        if (bias) v += ld4(bias + n);
+        if (act == 1)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) v[j] = silu(v[j]);
+        if (residual) v += ld4(residual + static_cast<size_t>(m) * ldy + n);
+        st4(y + static_cast<size_t>(m) * ldy + n, v);
     }
 }
 
@@ -151,33 +184,33 @@ __global__ void __launch_bounds__(BT) k_finish_linear(const float *part, int S, 
 __global__ void __launch_bounds__(BT) k_resid_norm(const float *part, int S, const float *src, float *x, const float *w,
                                                    float eps, float *xn, int M, int H) {
     __shared__ float red[4];
-    const int m = blockIdx.x;
-    float v[4], ss = 0.f;
+    const int m = blockIdx.x, i = threadIdx.x * 4;            // H == 4 * BT
+    const size_t idx = static_cast<size_t>(m) * H + i;
+    const f32x4_t v = S > 0 ? sum_parts4(part, S, static_cast<size_t>(M) * H, idx) + ld4(x + idx) : ld4(src + idx);
+    const f32x4_t wv = ld4(w + i);
+    st4(x + idx, v);
+    float ss = 0.f;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        const int i = threadIdx.x + r * BT;
-        const size_t idx = static_cast<size_t>(m) * H + i;
-        v[r] = S > 0 ? sum_parts(part, S, static_cast<size_t>(M) * H, idx) + gld(x + idx) : gld(src + idx);
-        gst(x + idx, v[r]);
-        ss = fmaf(v[r], v[r], ss);
-    }
+    for (int j = 0; j < 4; ++j) ss = fmaf(v[j], v[j], ss);
     ss = block_sum256(ss, red);
     const float scale = rsqrtf(ss / static_cast<float>(H) + eps);
+    f32x4_t o;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        const int i = threadIdx.x + r * BT;
-        gst(xn + static_cast<size_t>(m) * H + i, v[r] * scale * gld(w + i));
-    }
+    for (int j = 0; j < 4; ++j) o[j] = v[j] * scale * wv[j];
+    st4(xn + idx, o);
 }
 
 // h[m][c] = SiLU(gate) * up from the [gate | up] partials (PRO_SILU_GATE / k_silu_gate, kernels.h:334-340).
 __global__ void __launch_bounds__(BT) k_swiglu(const float *part, int S, int M, int F, float *h) {
     const int m = blockIdx.x;
     const size_t stride = static_cast<size_t>(M) * 2 * F;
-    for (int c = threadIdx.x; c < F; c += BT) {
-        const float g = sum_parts(part, S, stride, static_cast<size_t>(m) * 2 * F + c);
-        const float u = sum_parts(part, S, stride, static_cast<size_t>(m) * 2 * F + F + c);
-        gst(h + static_cast<size_t>(m) * F + c, silu(g) * u);
+    for (int c = threadIdx.x * 4; c < F; c += BT * 4) {
+        const f32x4_t g = sum_parts4(part, S, stride, static_cast<size_t>(m) * 2 * F + c);
+        const f32x4_t u = sum_parts4(part, S, stride, static_cast<size_t>(m) * 2 * F + F + c);
+        f32x4_t o;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) o[j] = silu(g[j]) * u[j];
+        st4(h + static_cast<size_t>(m) * F + c, o);
     }
 }
 
@@ -191,7 +224,11 @@ __global__ void __launch_bounds__(BT) k_qkv_finish(const float *part, int S, int
     const int m = blockIdx.x, pos = pos0 + m;
     const int QD = nq * HD, KVD = nkv * HD, W = QD + 2 * KVD;
     const size_t stride = static_cast<size_t>(M) * W;
-    for (int i = threadIdx.x; i < W; i += BT) row[i] = sum_parts(part, S, stride, static_cast<size_t>(m) * W + i);
+    for (int i = threadIdx.x * 4; i < W; i += BT * 4) {
+        const f32x4_t v = sum_parts4(part, S, stride, static_cast<size_t>(m) * W + i);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) row[i + j] = v[j];
+    }
     __syncthreads();
     const int wv = threadIdx.x >> 6, l = threadIdx.x & 63;
     const float inv = gld(invf + l);
@@ -214,44 +251,94 @@ __global__ void __launch_bounds__(BT) k_qkv_finish(const float *part, int S, int
     }
 }
 
-// Causal GQA attention of row m, head h over keys 0..pos0 + m of the f16 cache
-// (k_prefill_attention, talker.hip:88-117). 128 threads; scores in dynamic LDS.
-__global__ void __launch_bounds__(128) k_attn_prefill(const float *q, const uint16_t *kc, const uint16_t *vc, int nq,
-                                                      int nkv, int pos0, float scale, float *out) {
-    extern __shared__ float sc[];
-    __shared__ float qs[HD], red[2];
-    const int m = blockIdx.x, h = blockIdx.y, g = h / (nq / nkv), n = pos0 + m + 1;
+// Causal GQA attention of row m for the two q heads of kv group g over keys 0..pos0 + m of the
+// f16 cache (k_prefill_attention, talker.hip:88-117). 256 threads. Scores: one key per thread
+// (its 256-byte K row loaded at once, dotted with both q heads). V: each wave sums every 4th key
+// for both heads (a lane owns 2 dims), eight keys' loads in flight, then the four waves'
+// partial sums are added in wave order.
+__global__ void __launch_bounds__(BT) k_attn_prefill(const float *q, const uint16_t *kc, const uint16_t *vc, int nq,
+                                                     int nkv, int pos0, float scale, float *out) {
+    extern __shared__ float sc[];                        // [2][n] scores, then probabilities
+    __shared__ float qs[2][HD], red[2][4], part[4][2][HD];
+    const int m = blockIdx.x, g = blockIdx.y, n = pos0 + m + 1;
     const int QD = nq * HD, KVD = nkv * HD;
     const int wv = threadIdx.x >> 6, l = threadIdx.x & 63;
-    qs[threadIdx.x] = gld(q + static_cast<size_t>(m) * QD + h * HD + threadIdx.x);
+    qs[threadIdx.x >> 7][threadIdx.x & (HD - 1)] = gld(q + static_cast<size_t>(m) * QD + g * 2 * HD + threadIdx.x);
     __syncthreads();
-    float mx = -INFINITY;
-    for (int j = wv; j < n; j += 2) {
-        const uint32_t kk = gld(reinterpret_cast<const uint32_t *>(kc + static_cast<size_t>(j) * KVD + g * HD) + l);
-        const float d = wave_sum(fmaf(qs[2 * l], h2f(static_cast<uint16_t>(kk)), qs[2 * l + 1] * h2f(static_cast<uint16_t>(kk >> 16))));
-        const float s = d * scale;
-        if (l == 0) sc[j] = s;
-        mx = fmaxf(mx, s);
+    float mx0 = -INFINITY, mx1 = -INFINITY;
+    for (int j = threadIdx.x; j < n; j += BT) {
+        const NAVI_GLOBAL u32x4_t *kp = (const NAVI_GLOBAL u32x4_t *) (kc + static_cast<size_t>(j) * KVD + g * HD);
+        u32x4_t kr[HD / 8];
+#pragma unroll
+        for (int c = 0; c < HD / 8; ++c) kr[c] = kp[c];
+        float d0 = 0.f, d1 = 0.f;
+#pragma unroll
+        for (int c = 0; c < HD / 8; ++c)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int i = c * 8 + e * 2;
+                const float k0 = h2f(static_cast<uint16_t>(kr[c][e])), k1 = h2f(static_cast<uint16_t>(kr[c][e] >> 16));
+                d0 = fmaf(qs[0][i + 1], k1, fmaf(qs[0][i], k0, d0));
+                d1 = fmaf(qs[1][i + 1], k1, fmaf(qs[1][i], k0, d1));
+            }
+        d0 *= scale;
+        d1 *= scale;
+        sc[j] = d0;
+        sc[n + j] = d1;
+        mx0 = fmaxf(mx0, d0);
+        mx1 = fmaxf(mx1, d1);
     }
-    if (l == 0) red[wv] = mx;
+    mx0 = wave_max(mx0);
+    mx1 = wave_max(mx1);
+    if (l == 0) { red[0][wv] = mx0; red[1][wv] = mx1; }
     __syncthreads();
-    mx = fmaxf(red[0], red[1]);
+    mx0 = fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3]));
+    mx1 = fmaxf(fmaxf(red[1][0], red[1][1]), fmaxf(red[1][2], red[1][3]));
     __syncthreads();
-    float sum = 0.f;
-    for (int j = threadIdx.x; j < n; j += 128) {
-        const float e = expf(sc[j] - mx);
-        sc[j] = e;
-        sum += e;
+    float s0 = 0.f, s1 = 0.f;
+    for (int j = threadIdx.x; j < n; j += BT) {
+        const float e0 = expf(sc[j] - mx0), e1 = expf(sc[n + j] - mx1);
+        sc[j] = e0;
+        sc[n + j] = e1;
+        s0 += e0;
+        s1 += e1;
     }
-    sum = wave_sum(sum);
-    if (l == 0) red[wv] = sum;
+    s0 = wave_sum(s0);
+    s1 = wave_sum(s1);
+    if (l == 0) { red[0][wv] = s0; red[1][wv] = s1; }
+    __syncthreads();                                      // also publishes the probabilities
+    s0 = red[0][0] + red[0][1] + red[0][2] + red[0][3];
+    s1 = red[1][0] + red[1][1] + red[1][2] + red[1][3];
+    const uint16_t *vp = vc + g * HD + 2 * l;
+    float a00 = 0.f, a01 = 0.f, a10 = 0.f, a11 = 0.f;
+    for (int j0 = wv; j0 < n; j0 += 4 * 8) {
+        uint32_t vv[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int j = j0 + 4 * u;
+            vv[u] = j < n ? gld(reinterpret_cast<const uint32_t *>(vp + static_cast<size_t>(j) * KVD)) : 0u;
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int j = j0 + 4 * u;
+            if (j < n) {
+                const float p0 = sc[j], p1 = sc[n + j];
+                const float v0 = h2f(static_cast<uint16_t>(vv[u])), v1 = h2f(static_cast<uint16_t>(vv[u] >> 16));
+                a00 = fmaf(p0, v0, a00);
+                a01 = fmaf(p0, v1, a01);
+                a10 = fmaf(p1, v0, a10);
+                a11 = fmaf(p1, v1, a11);
+            }
+        }
+    }
+    part[wv][0][2 * l] = a00;
+    part[wv][0][2 * l + 1] = a01;
+    part[wv][1][2 * l] = a10;
+    part[wv][1][2 * l + 1] = a11;
     __syncthreads();
-    sum = red[0] + red[1];
-    const int d = threadIdx.x;
-    float acc = 0.f;
-    const uint16_t *vp = vc + g * HD + d;
-    for (int j = 0; j < n; ++j) acc = fmaf(sc[j], h2f(gld(vp + static_cast<size_t>(j) * KVD)), acc);
-    gst(out + static_cast<size_t>(m) * QD + h * HD + d, acc / sum);
+    const int hh = threadIdx.x >> 7, d = threadIdx.x & (HD - 1);
+    const float acc = part[0][hh][d] + part[1][hh][d] + part[2][hh][d] + part[3][hh][d];
+    gst(out + static_cast<size_t>(m) * QD + (g * 2 + hh) * HD + d, acc / (hh ? s1 : s0));
 }
 
 // rows[t] = table[ids[t]] (f16 -> f32), k_gather_rows (talker.hip:20-25).
@@ -442,7 +529,7 @@ navi_status navi_talker_create(const navi_model_params *p, const navi_tensor_ref
     navi_status st = ensure_device(err, errlen);
     if (st != NAVI_OK) return st;
     const navi_xformer_params &x = p->talker;
-    if (x.head_dim != HD || x.hidden % 1024 != 0 || x.n_head % x.n_kv_head != 0 || x.ff % 64 != 0 || x.vocab % 64 != 0 ||
+    if (x.head_dim != HD || x.hidden % 1024 != 0 || x.n_head != 2 * x.n_kv_head || x.ff % 64 != 0 || x.vocab % 64 != 0 ||
         p->text_hidden % 64 != 0 || x.hidden != 1024) {
         set_err(err, errlen, "talker: unsupported shape (hidden %d, head_dim %d, ff %d, vocab %d, text_hidden %d)", x.hidden,
                 x.head_dim, x.ff, x.vocab, p->text_hidden);
@@ -627,7 +714,7 @@ navi_status navi_talker_prefill(navi_talker *t, const float *d_rows, int32_t n_r
     NAVI_TRY_HIP(hipEventRecord(t->ev0, s), err, errlen);
     hipLaunchKernelGGL(k_resid_norm, dim3(T), dim3(BT), 0, s, nullptr, 0, d_rows, t->x, t->layers[0].ln1, t->eps, t->xn, T, H);
     const float scale = 1.f / std::sqrt(static_cast<float>(HD));
-    const size_t att_lds = static_cast<size_t>(T) * sizeof(float);
+    const size_t att_lds = static_cast<size_t>(2) * T * sizeof(float);
     for (int l = 0; l < t->L; ++l) {
         const LayerW &w = t->layers[l];
         int S = pick_splits(T, H, QKVW);
@@ -636,7 +723,7 @@ navi_status navi_talker_prefill(navi_talker *t, const float *d_rows, int32_t n_r
         launch_partial(t->xn, H, T, w.wv, H, t->KVD, S, t->part, QKVW, t->QD + t->KVD, t->flag, s);
         hipLaunchKernelGGL(k_qkv_finish, dim3(T), dim3(BT), QKVW * sizeof(float), s, t->part, S, T, t->NQ, t->NKV, w.qn,
                            w.kn, t->eps, t->invf, 0, t->q, t->kk[l], t->vv[l]);
-        hipLaunchKernelGGL(k_attn_prefill, dim3(T, t->NQ), dim3(128), att_lds, s, t->q, t->kk[l], t->vv[l], t->NQ, t->NKV, 0,
+        hipLaunchKernelGGL(k_attn_prefill, dim3(T, t->NKV), dim3(BT), att_lds, s, t->q, t->kk[l], t->vv[l], t->NQ, t->NKV, 0,
                            scale, t->att);
         S = pick_splits(T, t->QD, H);
         launch_partial(t->att, t->QD, T, w.wo, t->QD, H, S, t->part, H, 0, t->flag, s);

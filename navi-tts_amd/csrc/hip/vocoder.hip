@@ -70,52 +70,81 @@ __global__ void __launch_bounds__(BT) k_conv_mfma(ConvArgs a) {
     f32x4_t acc[MT];
 #pragma unroll
     for (int i = 0; i < MT; ++i) acc[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    // Staging of the time window of one channel chunk: a thread owns IT float4s of it, always
+    // the same 4 channels (BT is a multiple of the chunk's float4 count, 8 or 16). A chunk's
+    // loads (inputs, weights) are all issued at once, and the next chunk's go out before this
+    // chunk's MFMAs, so no load waits on another.
+    constexpr int IT = (WROWS * (CCH / 4) + BT - 1) / BT;
+    f32x4_t av[IT], au[PRO == PRO_SILU_GATE ? IT : 1], sa4 = f32x4_t{0.f, 0.f, 0.f, 0.f}, sb4 = sa4;
+    u32x4_t bq[K][CCH / 32];
+    auto load_tap = [&](int j, int ci0) {
+        const int cc = min(CCH, a.Cin - ci0);
+#pragma unroll
+        for (int s = 0; s < CCH / 32; ++s)
+            if (s * 32 < cc)
+                bq[j][s] = __builtin_nontemporal_load((const NAVI_GLOBAL u32x4_t *) (wbase + static_cast<size_t>(j) * a.Cin + ci0 + s * 32));
+    };
+    auto load_a = [&](int ci0) {
+        const int q4 = min(CCH, a.Cin - ci0) >> 2;
+        const int ci = ci0 + (threadIdx.x % q4) * 4;
+        if (PRO == PRO_SNAKE) {
+            sa4 = *(const NAVI_GLOBAL f32x4_t *) (a.sa + ci);
+            sb4 = *(const NAVI_GLOBAL f32x4_t *) (a.sb + ci);
+        }
+#pragma unroll
+        for (int it = 0; it < IT; ++it) {
+            const int r = (threadIdx.x + it * BT) / q4, t = t0 - H + r;
+            av[it] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+            if (PRO == PRO_SILU_GATE) au[it] = av[it];
+            if (r < rows) {
+                if (t >= 0 && t < a.T) {
+                    const float *row = a.x + static_cast<size_t>(t) * a.ldx;
+                    av[it] = *(const NAVI_GLOBAL f32x4_t *) (row + ci);
+                    if (PRO == PRO_SILU_GATE) au[it] = *(const NAVI_GLOBAL f32x4_t *) (row + a.Cin + ci);
+                } else if (t < 0 && a.hist) {
+                    av[it] = *(const NAVI_GLOBAL f32x4_t *) (a.hist + static_cast<size_t>(H + t) * a.Cin + ci);
+                }
+            }
+        }
+    };
     bool bad = false;
+    if (live)
+#pragma unroll
+        for (int j = 0; j < K; ++j) load_tap(j, 0);
+    load_a(0);
     for (int ci0 = 0; ci0 < a.Cin; ci0 += CCH) {
         const int cc = min(CCH, a.Cin - ci0);               // multiple of 32
-        u32x4_t bq[K][CCH / 32];
-        if (live) {
+        const bool more = ci0 + CCH < a.Cin;
+        __syncthreads();                                    // the previous chunk's readers are done
+        {
+            const int q4 = cc >> 2, c = (threadIdx.x % q4) * 4;
 #pragma unroll
-            for (int j = 0; j < K; ++j)
+            for (int it = 0; it < IT; ++it) {
+                const int r = (threadIdx.x + it * BT) / q4, t = t0 - H + r;
+                if (r >= rows) continue;
+                f32x4_t v = av[it];
+                if (PRO == PRO_SILU_GATE && t >= 0 && t < a.T) {
 #pragma unroll
-                for (int s = 0; s < CCH / 32; ++s)
-                    if (s * 32 < cc)
-                        bq[j][s] = __builtin_nontemporal_load((const NAVI_GLOBAL u32x4_t *) (wbase + static_cast<size_t>(j) * a.Cin + ci0 + s * 32));
-        }
-        __syncthreads();
-        const int q4 = cc >> 2;
-        for (int i = threadIdx.x; i < rows * q4; i += BT) {
-            const int r = i / q4, c = (i - r * q4) * 4, ci = ci0 + c, t = t0 - H + r;
-            f32x4_t v = f32x4_t{0.f, 0.f, 0.f, 0.f};
-            if (t >= 0 && t < a.T) {
-                const float *row = a.x + static_cast<size_t>(t) * a.ldx;
-                if (PRO == PRO_SILU_GATE) {
-                    const f32x4_t g = *(const NAVI_GLOBAL f32x4_t *) (row + ci);
-                    const f32x4_t u = *(const NAVI_GLOBAL f32x4_t *) (row + a.Cin + ci);
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) v[e] = silu(g[e]) * u[e];
-                } else {
-                    v = *(const NAVI_GLOBAL f32x4_t *) (row + ci);
+                    for (int e = 0; e < 4; ++e) v[e] = silu(v[e]) * au[it][e];
                 }
-            } else if (t < 0 && a.hist) {
-                v = *(const NAVI_GLOBAL f32x4_t *) (a.hist + static_cast<size_t>(H + t) * a.Cin + ci);
-            }
-            if (PRO == PRO_SNAKE && t < a.T) {
+                if (PRO == PRO_SNAKE && t < a.T) {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const float sn = sinf(v[e] * sa4[e]);
+                        v[e] += sn * sn * sb4[e];
+                    }
+                }
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    const float s = sinf(v[e] * gld(a.sa + ci + e));
-                    v[e] += s * s * gld(a.sb + ci + e);
+                    bad |= !(fabsf(v[e]) < 65504.f);
+                    const _Float16 h = static_cast<_Float16>(v[e]);
+                    whi[r][c + e] = h;
+                    wlo[r][c + e] = static_cast<_Float16>(v[e] - static_cast<float>(h));
                 }
-            }
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                bad |= !(fabsf(v[e]) < 65504.f);
-                const _Float16 h = static_cast<_Float16>(v[e]);
-                whi[r][c + e] = h;
-                wlo[r][c + e] = static_cast<_Float16>(v[e] - static_cast<float>(h));
             }
         }
         __syncthreads();
+        if (more) load_a(ci0 + CCH);
         if (live) {
 #pragma unroll
             for (int j = 0; j < K; ++j) {
@@ -134,6 +163,7 @@ __global__ void __launch_bounds__(BT) k_conv_mfma(ConvArgs a) {
                         }
                     }
                 }
+                if (more) load_tap(j, ci0 + CCH);           // tap j's registers are free again
             }
         }
     }
