@@ -12,8 +12,13 @@
 //    that window. Activations travel as f16 hi + lo pairs (f32-level products, as in the
 //    prefill); weights stream as f16.
 //  * Transposed convolutions (stride s, kernel s or 2s) are s phases of a causal conv with
-//    k / s taps writing every s-th output row; Snake, SiLU-gate prologues and bias, GELU,
-//    residual, layer-scale epilogues are fused into the same kernel.
+//    k / s taps writing every s-th output row. The SiLU-gate prologue and bias, GELU,
+//    residual, layer-scale and clamp epilogues are fused into the same kernel; the Snake that
+//    starts every decoder-block conv is applied once per element by the conv producing its
+//    input (a second, Snake'd output), not once per consuming block.
+//  * Few output tiles (short chunks, narrow layers): the input channels are split over up to
+//    S blocks per tile and the partial sums added in split order by a finish kernel, so a
+//    16-frame chunk still spreads over the 256 CUs.
 //  * Streaming state: each causal conv keeps its last (K-1)*dil input rows (the history the
 //    next chunk's first rows read), the ConvNeXt depthwise conv its last 6, the attention its
 //    K/V in a ring of >= window + chunk positions: chunked decoding equals one-shot decoding.
@@ -34,26 +39,48 @@ constexpr int LDW = CCH + 8;             // padded LDS row (halves)
 
 typedef _Float16 half8v __attribute__((ext_vector_type(8)));
 
-enum Pro { PRO_NONE = 0, PRO_SNAKE = 1, PRO_SILU_GATE = 2 };
-enum Epi { EPI_BIAS = 0, EPI_GELU = 1, EPI_RESIDUAL = 2, EPI_SCALE_RESIDUAL = 3, EPI_CLAMP = 4 };
+enum Pro { PRO_NONE = 0, PRO_SILU_GATE = 2 };
+enum Epi { EPI_BIAS = 0, EPI_GELU = 1, EPI_RESIDUAL = 2, EPI_SCALE_RESIDUAL = 3, EPI_CLAMP = 4, EPI_PARTIAL = 5 };
 
 struct ConvArgs {
     const float *x;        // input rows [T][ldx]; PRO_SILU_GATE: gate at [ci], up at [Cin + ci]
     const float *hist;     // [(K-1)*dil][Cin] rows before t = 0, or null (zeros)
     const uint16_t *w;     // [phases][Cout][K][Cin] f16
     const float *bias;     // [Cout] or null
-    const float *sa, *sb;  // Snake: exp(alpha), 1 / (exp(beta) + 1e-9) per input channel
     const float *res;      // EPI_RESIDUAL / EPI_SCALE_RESIDUAL: rows like y (stride ldy)
     const float *scale;    // EPI_SCALE_RESIDUAL: [Cout]
-    float *y;              // output row t * phases + phase, stride ldy
+    float *y;              // output row t * phases + phase, stride ldy (may be null when z is set)
+    // Optional second output z = Snake(y) = y + sin^2(y * za) * zb per output channel (za = exp(alpha),
+    // zb = 1 / (exp(beta) + 1e-9)): the prologue of the conv that consumes y, applied once per
+    // element by its producer. Same layout as y.
+    float *z;
+    const float *za, *zb;
+    float *part;           // EPI_PARTIAL: [splits][T * phases][Cout] partial sums, no bias
     uint32_t *flag;        // set when a (prologue-applied) activation is outside the f16 range
-    int ldx, ldy, T, Cin, Cout, dil, phases;
+    int ldx, ldy, T, Cin, Cout, dil, phases, cps;   // cps: input channels per K split
 };
 
 __device__ __forceinline__ float silu(float g) { return g / (1.f + expf(-g)); }
 
+__device__ __forceinline__ float snake(float v, float za, float zb) {
+    const float sn = sinf(v * za);
+    return v + sn * sn * zb;
+}
+
+// y (and z) at output (row, co) from the accumulated sum (EPI_PARTIAL excluded).
+__device__ __forceinline__ void conv_epilogue(const ConvArgs &a, int epi, size_t o, int co, float v) {
+    if (a.bias) v += gld(a.bias + co);
+    if (epi == EPI_GELU) v = 0.5f * v * (1.f + erff(v * 0.70710678118654752f));
+    else if (epi == EPI_RESIDUAL) v += gld(a.res + o);
+    else if (epi == EPI_SCALE_RESIDUAL) v = v * gld(a.scale + co) + gld(a.res + o);
+    else if (epi == EPI_CLAMP) v = fminf(fmaxf(v, -1.f), 1.f);
+    if (a.y) gst(a.y + o, v);
+    if (a.z) gst(a.z + o, snake(v, gld(a.za + co), gld(a.zb + co)));
+}
+
 // Output lane layout of v_mfma_f32_16x16x32_f16: lane l holds column l % 16 of rows
-// 4 * (l / 16) + r, r = 0..3; A and B use the same lane -> k mapping.
+// 4 * (l / 16) + r, r = 0..3; A and B use the same lane -> k mapping. blockIdx.z = split *
+// phases + phase: a block reduces input channels [split * cps, (split + 1) * cps).
 template <int MT, int K, int PRO, int EPI>
 __global__ void __launch_bounds__(BT) k_conv_mfma(ConvArgs a) {
     constexpr int MAXH = (K - 1) * 9;                       // dilation <= 9
@@ -63,7 +90,8 @@ __global__ void __launch_bounds__(BT) k_conv_mfma(ConvArgs a) {
     const int wv = threadIdx.x >> 6, l = threadIdx.x & 63;
     const int n0 = blockIdx.x * 64 + wv * 16;
     const int t0 = blockIdx.y * (MT * 16);
-    const int phase = blockIdx.z;
+    const int phase = blockIdx.z % a.phases, split = blockIdx.z / a.phases;
+    const int cb = split * a.cps, ce = min(a.Cin, cb + a.cps);
     const int H = (K - 1) * a.dil, rows = MT * 16 + H;
     const bool live = n0 < a.Cout;                          // Cout % 16 == 0: whole waves are in or out
     const uint16_t *wbase = a.w + (static_cast<size_t>(phase) * a.Cout + (live ? n0 + (l & 15) : 0)) * K * a.Cin + (l >> 4) * 8;
@@ -75,22 +103,18 @@ __global__ void __launch_bounds__(BT) k_conv_mfma(ConvArgs a) {
     // loads (inputs, weights) are all issued at once, and the next chunk's go out before this
     // chunk's MFMAs, so no load waits on another.
     constexpr int IT = (WROWS * (CCH / 4) + BT - 1) / BT;
-    f32x4_t av[IT], au[PRO == PRO_SILU_GATE ? IT : 1], sa4 = f32x4_t{0.f, 0.f, 0.f, 0.f}, sb4 = sa4;
+    f32x4_t av[IT], au[PRO == PRO_SILU_GATE ? IT : 1];
     u32x4_t bq[K][CCH / 32];
     auto load_tap = [&](int j, int ci0) {
-        const int cc = min(CCH, a.Cin - ci0);
+        const int cc = min(CCH, ce - ci0);
 #pragma unroll
         for (int s = 0; s < CCH / 32; ++s)
             if (s * 32 < cc)
                 bq[j][s] = __builtin_nontemporal_load((const NAVI_GLOBAL u32x4_t *) (wbase + static_cast<size_t>(j) * a.Cin + ci0 + s * 32));
     };
     auto load_a = [&](int ci0) {
-        const int q4 = min(CCH, a.Cin - ci0) >> 2;
+        const int q4 = min(CCH, ce - ci0) >> 2;
         const int ci = ci0 + (threadIdx.x % q4) * 4;
-        if (PRO == PRO_SNAKE) {
-            sa4 = *(const NAVI_GLOBAL f32x4_t *) (a.sa + ci);
-            sb4 = *(const NAVI_GLOBAL f32x4_t *) (a.sb + ci);
-        }
 #pragma unroll
         for (int it = 0; it < IT; ++it) {
             const int r = (threadIdx.x + it * BT) / q4, t = t0 - H + r;
@@ -108,13 +132,15 @@ __global__ void __launch_bounds__(BT) k_conv_mfma(ConvArgs a) {
         }
     };
     bool bad = false;
-    if (live)
+    if (cb < ce) {
+        if (live)
 #pragma unroll
-        for (int j = 0; j < K; ++j) load_tap(j, 0);
-    load_a(0);
-    for (int ci0 = 0; ci0 < a.Cin; ci0 += CCH) {
-        const int cc = min(CCH, a.Cin - ci0);               // multiple of 32
-        const bool more = ci0 + CCH < a.Cin;
+            for (int j = 0; j < K; ++j) load_tap(j, cb);
+        load_a(cb);
+    }
+    for (int ci0 = cb; ci0 < ce; ci0 += CCH) {
+        const int cc = min(CCH, ce - ci0);                  // multiple of 32
+        const bool more = ci0 + CCH < ce;
         __syncthreads();                                    // the previous chunk's readers are done
         {
             const int q4 = cc >> 2, c = (threadIdx.x % q4) * 4;
@@ -126,13 +152,6 @@ __global__ void __launch_bounds__(BT) k_conv_mfma(ConvArgs a) {
                 if (PRO == PRO_SILU_GATE && t >= 0 && t < a.T) {
 #pragma unroll
                     for (int e = 0; e < 4; ++e) v[e] = silu(v[e]) * au[it][e];
-                }
-                if (PRO == PRO_SNAKE && t < a.T) {
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const float sn = sinf(v[e] * sa4[e]);
-                        v[e] += sn * sn * sb4[e];
-                    }
                 }
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
@@ -170,22 +189,37 @@ __global__ void __launch_bounds__(BT) k_conv_mfma(ConvArgs a) {
     if (bad) gst(a.flag, 1u);
     if (!live) return;
     const int co = n0 + (l & 15);
-    const float bv = a.bias ? gld(a.bias + co) : 0.f;
-    const float sc = EPI == EPI_SCALE_RESIDUAL ? gld(a.scale + co) : 0.f;
+    float *part = a.part + static_cast<size_t>(split) * a.T * a.phases * a.Cout;
 #pragma unroll
     for (int i = 0; i < MT; ++i)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int t = t0 + i * 16 + (l >> 4) * 4 + r;
             if (t >= a.T) continue;
-            const size_t o = (static_cast<size_t>(t) * a.phases + phase) * a.ldy + co;
-            float v = acc[i][r] + bv;
-            if (EPI == EPI_GELU) v = 0.5f * v * (1.f + erff(v * 0.70710678118654752f));
-            else if (EPI == EPI_RESIDUAL) v += gld(a.res + o);
-            else if (EPI == EPI_SCALE_RESIDUAL) v = v * sc + gld(a.res + o);
-            else if (EPI == EPI_CLAMP) v = fminf(fmaxf(v, -1.f), 1.f);
-            gst(a.y + o, v);
+            const size_t row = static_cast<size_t>(t) * a.phases + phase;
+            if (EPI == EPI_PARTIAL) gst(part + row * a.Cout + co, acc[i][r]);
+            else conv_epilogue(a, EPI, row * a.ldy + co, co, acc[i][r]);
         }
+}
+
+// Sum of the K-split partials in split order, then the epilogue (EPI_PARTIAL's second half).
+__global__ void __launch_bounds__(BT) k_conv_finish(ConvArgs a, int splits, int epi) {
+    const size_t rows = static_cast<size_t>(a.T) * a.phases, n = rows * a.Cout;
+    const size_t i = static_cast<size_t>(blockIdx.x) * BT + threadIdx.x;
+    if (i >= n) return;
+    const size_t row = i / a.Cout;
+    const int co = static_cast<int>(i - row * a.Cout);
+    float v = 0.f;
+    for (int s0 = 0; s0 < splits; s0 += 8) {
+        float t[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            if (s0 + j < splits) t[j] = gld(a.part + (s0 + j) * n + i);
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            if (s0 + j < splits) v = s0 + j == 0 ? t[j] : v + t[j];
+    }
+    conv_epilogue(a, epi, row * a.ldy + co, co, v);
 }
 
 // new[r] = row r of the last H rows of [old ; x] (the causal history for the next chunk).
@@ -370,8 +404,11 @@ __global__ void k_snake_prep(const float *alpha, const float *beta, int n, float
 struct Conv {
     const uint16_t *w = nullptr;       // [phases][Cout][K][Cin]
     const float *bias = nullptr;
+    // The Snake on this conv's input (exp(alpha), 1 / (exp(beta) + 1e-9)); applied by the conv
+    // that produces the input, as its z output.
     const float *sa = nullptr, *sb = nullptr;
     int Cin = 0, Cout = 0, K = 1, dil = 1, phases = 1, H = 0;
+    int S = 1;                         // input-channel splits (fixed at create: conv_splits)
     float *hist = nullptr, *hist2 = nullptr;
 };
 
@@ -416,7 +453,9 @@ struct navi_vocoder {
     int32_t *d_codes = nullptr;
     float *e = nullptr, *h = nullptr, *a = nullptr, *x = nullptr, *n = nullptr, *qkv = nullptr, *att = nullptr,
           *gu = nullptr, *u = nullptr, *A = nullptr, *B = nullptr, *G = nullptr, *d = nullptr, *pcm = nullptr;
-    float *P[4] = {}, *Q[4] = {};
+    float *P[4] = {}, *Q[4] = {}, *ZP[4] = {};
+    float *part = nullptr;             // K-split partial sums (conv_splits)
+    size_t part_floats = 0;
     hipEvent_t ev0 = nullptr, ev1 = nullptr;
     double last_ms = 0;
     std::vector<void *> owned;
@@ -449,36 +488,76 @@ void launch_k(const ConvArgs &a, int pro, int epi, dim3 grid, hipStream_t s) {
     }
     NAVI_CONV(PRO_NONE, EPI_BIAS)
     NAVI_CONV(PRO_NONE, EPI_GELU)
+    NAVI_CONV(PRO_NONE, EPI_RESIDUAL)
     NAVI_CONV(PRO_NONE, EPI_SCALE_RESIDUAL)
-    NAVI_CONV(PRO_SNAKE, EPI_BIAS)
-    NAVI_CONV(PRO_SNAKE, EPI_RESIDUAL)
+    NAVI_CONV(PRO_NONE, EPI_CLAMP)
+    NAVI_CONV(PRO_NONE, EPI_PARTIAL)
     NAVI_CONV(PRO_SILU_GATE, EPI_SCALE_RESIDUAL)
-    NAVI_CONV(PRO_SNAKE, EPI_CLAMP)
+    NAVI_CONV(PRO_SILU_GATE, EPI_PARTIAL)
 #undef NAVI_CONV
 }
 
-// Runs one conv over T input rows; updates its history afterwards.
+int conv_mt(int T) { return T <= 16 ? 1 : 4; }
+
+// Input-channel splits of a conv over T rows: when the output tiles alone would leave most of the
+// 256 CUs idle, the channel chunks are spread over up to S blocks per tile (at least 2 chunks each)
+// and summed by k_conv_finish.
+//
+// The count is fixed per conv when the vocoder is created (from the rows of a 16-frame chunk, or
+// of the largest chunk if smaller): the summation order, and so the PCM, then does not depend on
+// how the codes are batched.
+int conv_splits(const Conv &c, int T) {
+    const int mt = conv_mt(T);
+    const int blocks = ((c.Cout + 63) / 64) * ((T + 16 * mt - 1) / (16 * mt)) * c.phases;
+    const int chunks = (c.Cin + CCH - 1) / CCH;
+    int S = 1;
+    while (blocks * S * 2 <= 384 && chunks >= S * 4) S *= 2;
+    return S;
+}
+
+
+// Runs one conv over T input rows; updates its history afterwards. z (optional): also write
+// Snake(y) with the Snake parameters of zc, the conv that consumes this output.
 navi_status run_conv(navi_vocoder &v, Conv &c, int pro, int epi, const float *x, int T, int ldx, float *y, int ldy,
-                     const float *res, const float *scale, char *err, size_t errlen) {
+                     const float *res, const float *scale, char *err, size_t errlen, float *z = nullptr,
+                     const Conv *zc = nullptr) {
     hipStream_t s = device_state().stream;
     ConvArgs a{};
-    a.x = x; a.hist = c.hist; a.w = c.w; a.bias = c.bias; a.sa = c.sa; a.sb = c.sb; a.res = res; a.scale = scale;
-    a.y = y; a.flag = v.flag; a.ldx = ldx; a.ldy = ldy; a.T = T; a.Cin = c.Cin; a.Cout = c.Cout; a.dil = c.dil;
-    a.phases = c.phases;
-    const int mt = T <= 16 ? 1 : 4;
-    const dim3 grid((c.Cout + 63) / 64, (T + 16 * mt - 1) / (16 * mt), c.phases);
+    a.x = x; a.hist = c.hist; a.w = c.w; a.bias = c.bias; a.res = res; a.scale = scale;
+    a.y = y; a.z = z; a.flag = v.flag; a.ldx = ldx; a.ldy = ldy; a.T = T; a.Cin = c.Cin; a.Cout = c.Cout;
+    a.dil = c.dil; a.phases = c.phases;
+    if (z) {
+        a.za = zc->sa;
+        a.zb = zc->sb;
+    }
+    const int mt = conv_mt(T), S = c.S;
+    const int chunks = (c.Cin + CCH - 1) / CCH;
+    a.cps = (chunks + S - 1) / S * CCH;
+    if (S > 1) {
+        if (static_cast<size_t>(S) * T * c.phases * c.Cout > v.part_floats) {
+            set_err(err, errlen, "vocoder: split workspace too small");
+            return NAVI_ERR_INVALID;
+        }
+        a.part = v.part;
+    }
+    const int kepi = S > 1 ? static_cast<int>(EPI_PARTIAL) : epi;
+    const dim3 grid((c.Cout + 63) / 64, (T + 16 * mt - 1) / (16 * mt), c.phases * S);
     switch (c.K * 10 + (mt == 1 ? 1 : 4)) {
-    case 11: launch_k<1, 1>(a, pro, epi, grid, s); break;
-    case 14: launch_k<4, 1>(a, pro, epi, grid, s); break;
-    case 21: launch_k<1, 2>(a, pro, epi, grid, s); break;
-    case 24: launch_k<4, 2>(a, pro, epi, grid, s); break;
-    case 31: launch_k<1, 3>(a, pro, epi, grid, s); break;
-    case 34: launch_k<4, 3>(a, pro, epi, grid, s); break;
-    case 71: launch_k<1, 7>(a, pro, epi, grid, s); break;
-    case 74: launch_k<4, 7>(a, pro, epi, grid, s); break;
+    case 11: launch_k<1, 1>(a, pro, kepi, grid, s); break;
+    case 14: launch_k<4, 1>(a, pro, kepi, grid, s); break;
+    case 21: launch_k<1, 2>(a, pro, kepi, grid, s); break;
+    case 24: launch_k<4, 2>(a, pro, kepi, grid, s); break;
+    case 31: launch_k<1, 3>(a, pro, kepi, grid, s); break;
+    case 34: launch_k<4, 3>(a, pro, kepi, grid, s); break;
+    case 71: launch_k<1, 7>(a, pro, kepi, grid, s); break;
+    case 74: launch_k<4, 7>(a, pro, kepi, grid, s); break;
     default:
         set_err(err, errlen, "vocoder: no conv kernel for K=%d", c.K);
         return NAVI_ERR_UNSUPPORTED;
+    }
+    if (S > 1) {
+        const size_t n = static_cast<size_t>(T) * c.phases * c.Cout;
+        hipLaunchKernelGGL(k_conv_finish, dim3(static_cast<unsigned>((n + BT - 1) / BT)), dim3(BT), 0, s, a, S, epi);
     }
     if (c.H > 0) {
         const size_t nh = static_cast<size_t>(c.H) * c.Cin;
@@ -534,22 +613,31 @@ navi_status decode_chunk(navi_vocoder &v, int T, char *err, size_t errlen) {
         VOC_TRY(run_conv(v, cx.pw2, PRO_NONE, EPI_SCALE_RESIDUAL, v.G, R, 4 * L, dst, L, dst, cx.gamma, err, errlen));
         src = dst;
     }
-    VOC_TRY(run_conv(v, v.dec0, PRO_NONE, EPI_BIAS, src, R, L, v.d, v.DD, nullptr, nullptr, err, errlen));
+    // The Snake that starts every conv of the decoder blocks is applied once per element by the
+    // conv that produces its input (z output): dec0 -> block 0 up, up -> unit 0 conv1, conv1 ->
+    // conv2, conv2 -> next conv1 / next block's up / the final conv. P holds the residual stream,
+    // ZP its Snake for the next consumer, Q the Snake of conv1's output (conv1's raw output is not
+    // needed).
+    VOC_TRY(run_conv(v, v.dec0, PRO_NONE, EPI_BIAS, src, R, L, nullptr, v.DD, nullptr, nullptr, err, errlen, v.d,
+                     &v.blocks[0].up));
     const float *in = v.d;
     int width = v.DD;
     for (int b = 0; b < 4; ++b) {
         Block &bk = v.blocks[b];
-        VOC_TRY(run_conv(v, bk.up, PRO_SNAKE, EPI_BIAS, in, R, width, v.P[b], bk.Cout, nullptr, nullptr, err, errlen));
+        VOC_TRY(run_conv(v, bk.up, PRO_NONE, EPI_BIAS, in, R, width, v.P[b], bk.Cout, nullptr, nullptr, err, errlen, v.ZP[b],
+                         &bk.u[0].c1));
         R *= bk.rate;
         width = bk.Cout;
         for (int k = 0; k < 3; ++k) {
-            VOC_TRY(run_conv(v, bk.u[k].c1, PRO_SNAKE, EPI_BIAS, v.P[b], R, width, v.Q[b], width, nullptr, nullptr, err, errlen));
-            VOC_TRY(run_conv(v, bk.u[k].c2, PRO_SNAKE, EPI_RESIDUAL, v.Q[b], R, width, v.P[b], width, v.P[b], nullptr, err,
-                             errlen));
+            const Conv *next = k < 2 ? &bk.u[k + 1].c1 : b < 3 ? &v.blocks[b + 1].up : &v.final_conv;
+            VOC_TRY(run_conv(v, bk.u[k].c1, PRO_NONE, EPI_BIAS, v.ZP[b], R, width, nullptr, width, nullptr, nullptr, err,
+                             errlen, v.Q[b], &bk.u[k].c2));
+            VOC_TRY(run_conv(v, bk.u[k].c2, PRO_NONE, EPI_RESIDUAL, v.Q[b], R, width, v.P[b], width, v.P[b], nullptr, err,
+                             errlen, v.ZP[b], next));
         }
-        in = v.P[b];
+        in = v.ZP[b];
     }
-    VOC_TRY(run_conv(v, v.final_conv, PRO_SNAKE, EPI_CLAMP, in, R, width, v.pcm16, 16, nullptr, nullptr, err, errlen));
+    VOC_TRY(run_conv(v, v.final_conv, PRO_NONE, EPI_CLAMP, in, R, width, v.pcm16, 16, nullptr, nullptr, err, errlen));
     hipLaunchKernelGGL(k_take_col0, dim3((R + BT - 1) / BT), dim3(BT), 0, s, v.pcm16, R, 16, v.pcm);
     v.pos0 += T;
     NAVI_TRY_HIP(hipGetLastError(), err, errlen);
@@ -820,6 +908,7 @@ navi_status navi_vocoder_create(const navi_vocoder_params *p, const navi_tensor_
         rows *= bk.rate;
         VA(v->P[b], rows * C * bk.Cout);
         VA(v->Q[b], rows * C * bk.Cout);
+        VA(v->ZP[b], rows * C * bk.Cout);
         width = bk.Cout;
     }
     {
@@ -865,6 +954,33 @@ navi_status navi_vocoder_create(const navi_vocoder_params *p, const navi_tensor_
     VA(v->d, up_rows * DD);
     VA(v->pcm, C * p->samples_per_frame);
     VA(v->pcm16, C * p->samples_per_frame * 16);
+    {
+        // split counts from the rows of a 16-frame chunk (or the largest chunk if smaller), and
+        // the workspace the largest chunk then needs
+        size_t need = 0;
+        const int Cn = static_cast<int>(std::min<size_t>(C, 16)), Cf = static_cast<int>(C);
+        auto upd = [&](Conv &c, int rows_per_frame) {
+            c.S = conv_splits(c, Cn * rows_per_frame);
+            if (c.S > 1) need = std::max(need, static_cast<size_t>(c.S) * Cf * rows_per_frame * c.phases * c.Cout);
+        };
+        upd(v->rvq_proj, 1); upd(v->pre_conv, 1); upd(v->in_proj, 1); upd(v->out_proj, 1);
+        for (TLayer &ly : v->layers) { upd(ly.qkv, 1); upd(ly.o, 1); upd(ly.gu, 1); upd(ly.down, 1); }
+        int R = 1;
+        for (int j = 0; j < 2; ++j) {
+            upd(v->up_conv[j], R);
+            R *= p->upsampling_ratios[j];
+            upd(v->cnx[j].pw1, R); upd(v->cnx[j].pw2, R);
+        }
+        upd(v->dec0, R);
+        for (Block &bk : v->blocks) {
+            upd(bk.up, R);
+            R *= bk.rate;
+            for (Unit &u : bk.u) { upd(u.c1, R); upd(u.c2, R); }
+        }
+        upd(v->final_conv, R);
+        v->part_floats = need;
+        VA(v->part, need);
+    }
 #undef VB
 #undef VA
     if (hipMemcpyAsync(v->invf, invf, sizeof invf, hipMemcpyHostToDevice, s) != hipSuccess || hipEventCreate(&v->ev0) != hipSuccess ||
