@@ -283,6 +283,41 @@ typedef void (*navi_pcm_callback)(const float *pcm, int32_t n, void *user);
 navi_status navi_synth(navi_talker *t, navi_frame *f, navi_vocoder *v, const navi_synth_request *req,
                        navi_pcm_callback on_pcm, void *user, navi_synth_stats *stats, char *err, size_t errlen);
 
+/* ---- multi-stream batched decode -------------------------------------
+ * No counterpart in the reference, which decodes one request at a time: this is the batch-1
+ * frame (navi_frame_run; k_frame, frame.hip:517-579) applied to n independent streams at once,
+ * for servers that hold many requests. Stream i computes the frame navi_frame_run computes for
+ * it alone (same seeds, sampling rules and step assembly), up to the summation order of the
+ * projections, which run as GEMMs over the streams on the matrix cores. */
+
+typedef struct navi_streams navi_streams;
+
+/* Binds the talker and code-predictor weights by name (the names navi_frame_create binds) and
+ * allocates the work buffers for up to max_streams streams whose contexts reach max_positions. */
+navi_status navi_streams_create(const navi_model_params *p, const navi_tensor_ref *tensors, int32_t n_tensors,
+                                int32_t max_streams, int32_t max_positions, navi_streams **out, char *err, size_t errlen);
+void navi_streams_destroy(navi_streams *h);
+/* Clears the repetition set of one stream (stream >= 0) or of all (stream < 0): Frame::reset. */
+navi_status navi_streams_reset(navi_streams *h, int32_t stream);
+/* One frame for streams 0..n-1. Host arrays of n: kv (each stream's cache, borrowed; row n_past[i]
+ * is written), n_past, seeds, frame_index. d_step_in: device f32 [n][hidden] step inputs, or NULL
+ * to continue from this handle's step_out rows; d_trailing: device f32 [n][hidden] (each stream's
+ * trailing text row). codes_out: host i32 [n][16]; stream i ended when codes_out[i][0] is the EOS
+ * id. Errors as navi_frame_run's: NAVI_ERR_KV_FULL names the stream. Synchronous. */
+navi_status navi_streams_run(navi_streams *h, int32_t n, const navi_kv_view *kv, const int32_t *n_past, const float *d_step_in,
+                             const float *d_trailing, const navi_sampling *s, const uint64_t *seeds,
+                             const int32_t *frame_index, int32_t *codes_out, char *err, size_t errlen);
+float *navi_streams_step_out(navi_streams *h);           /* device f32 [max_streams][hidden]: the next step inputs */
+/* Diagnostics (as navi_frame_set_taps): when on, each run copies the talker's post-norm hidden
+ * [max_streams][hidden], raw codec logits [max_streams][talker vocab] and the 15 cp logit rows
+ * [max_streams][15][cp vocab] to device buffers. */
+navi_status navi_streams_set_taps(navi_streams *h, int32_t on);
+const float *navi_streams_tap_hidden(const navi_streams *h);
+const float *navi_streams_tap_logits(const navi_streams *h);
+const float *navi_streams_tap_cp_logits(const navi_streams *h);
+int32_t navi_streams_max_streams(const navi_streams *h);
+double navi_streams_last_ms(const navi_streams *h);      /* device time of the last navi_streams_run */
+
 #ifdef __cplusplus
 }
 #endif

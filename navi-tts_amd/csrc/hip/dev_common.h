@@ -158,4 +158,23 @@ __device__ __forceinline__ void ctl_put(uint32_t *p, uint32_t v) {
 __device__ __forceinline__ uint32_t tag_of(uint64_t w) { return static_cast<uint32_t>(w >> 32); }
 __device__ __forceinline__ float val_of(uint64_t w) { return __uint_as_float(static_cast<uint32_t>(w)); }
 
+// part[0] + part[1] + ... + part[S-1] at four consecutive columns, in that order (deterministic);
+// the loads go out eight partials at a time instead of one after another.
+__device__ __forceinline__ f32x4_t sum_parts4(const float *part, int S, size_t stride, size_t idx) {
+    f32x4_t v = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int s0 = 0; s0 < S; s0 += 8) {
+        f32x4_t t[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            if (s0 + j < S) t[j] = *(const NAVI_GLOBAL f32x4_t *) (part + (s0 + j) * stride + idx);
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            if (s0 + j < S) v = s0 + j == 0 ? t[j] : v + t[j];
+    }
+    return v;
+}
+
+__device__ __forceinline__ f32x4_t ld4(const float *p) { return *(const NAVI_GLOBAL f32x4_t *) p; }
+__device__ __forceinline__ void st4(float *p, f32x4_t v) { *(NAVI_GLOBAL f32x4_t *) p = v; }
+
 } // namespace navi_amd

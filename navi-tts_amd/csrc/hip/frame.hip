@@ -24,6 +24,7 @@
 //    frame fails with "timed out" instead of hanging (frame.hip:78-99 contract).
 #include "dev_common.h"
 #include "host_util.h"
+#include "sampler.h"
 
 #include <algorithm>
 #include <cmath>
@@ -745,142 +746,10 @@ __device__ bool cp_attention(const Args &a, float qkw, int il, int p0, uint32_t 
     return true;
 }
 
-// ---- sampling (block-wide; identical result in every block) ------------------
+// ---- sampling: block_sample (sampler.h) on this block's LDS ----------------------
 
-__device__ __forceinline__ unsigned float_key(float f) {
-    const unsigned u = __float_as_uint(f);
-    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-}
-__device__ __forceinline__ float key_float(unsigned u) {
-    return __uint_as_float((u & 0x80000000u) ? (u & 0x7FFFFFFFu) : ~u);
-}
-
-__device__ __forceinline__ uint32_t pcg32_next(uint64_t &s) {
-    const uint64_t old = s;
-    s = old * 6364136223846793005ull + 1442695040888963407ull;
-    const uint32_t xs = static_cast<uint32_t>(((old >> 18u) ^ old) >> 27u);
-    const uint32_t rot = static_cast<uint32_t>(old >> 59u);
-    return (xs >> rot) | (xs << ((0u - rot) & 31u));
-}
-
-// Sampling of one index from the V values in S.u.m.samp.lg (already modified for the talker),
-// identical in every block. Thread layout: element i = k * BT + tid, so index order is (k, wave,
-// lane). Greedy: argmax, lowest index on ties (frame.hip:178-203). Else (frame.hip:421-454,
-// 212-296): /temperature, exact top-k threshold (the k-th largest by a 4-pass 8-bit radix
-// select over monotone keys, values >= it survive), e^(v - max), and wave 0 draws with the
-// PCG32 u over the survivors in index order with the fused running sum of the reference
-// (`cum += p * inv_sum` compiles to an FMA under hipcc's default contraction). Each radix pass
-// costs one barrier: the four histograms are cleared up front, and every wave finds the digit
-// itself from the shared histogram with a DPP prefix sum.
-template <int V>
-__device__ __forceinline__ int block_sample(float temperature, int top_k, uint64_t seed, Smem &S) {
-    constexpr int PER = V / BT;
-    float x[PER];
-#pragma unroll
-    for (int k = 0; k < PER; ++k) x[k] = S.u.m.samp.lg[k * BT + tid()];
-    if (temperature <= 0.f) {
-        float bv = x[0];
-        int bi = tid();
-#pragma unroll
-        for (int k = 1; k < PER; ++k)
-            if (x[k] > bv) { bv = x[k]; bi = k * BT + tid(); }   // k ascending: the first maximum of this thread
-        const float m = wave_max(bv);
-        const int wi = wave_min_int(bv == m ? bi : V);
-        if (lane() == 0) { S.sred[wave()] = m; S.sidx[wave()] = wi; }
-        __syncthreads();
-        float v = S.sred[0];
-        int i0 = S.sidx[0];
-#pragma unroll
-        for (int w = 1; w < NW; ++w)
-            if (S.sred[w] > v || (S.sred[w] == v && S.sidx[w] < i0)) { v = S.sred[w]; i0 = S.sidx[w]; }
-        return i0;
-    }
-    unsigned (*hist)[256] = reinterpret_cast<unsigned (*)[256]>(S.u.m.samp.idx);
-    const bool topk = top_k > 0 && top_k < V;
-    if (topk) {
-#pragma unroll
-        for (int p = 0; p < 4; ++p) hist[p][tid()] = 0u;
-    }
-    float lmx = -INFINITY;
-#pragma unroll
-    for (int k = 0; k < PER; ++k) { x[k] = x[k] / temperature; lmx = fmaxf(lmx, x[k]); }
-    lmx = wave_max(lmx);
-    if (lane() == 0) S.sred[wave()] = lmx;
-    __syncthreads();
-    float mx = S.sred[0];
-#pragma unroll
-    for (int w = 1; w < NW; ++w) mx = fmaxf(mx, S.sred[w]);
-    float thr = -INFINITY;
-    if (topk) {
-        unsigned prefix = 0, mask = 0;
-        int need = top_k;
-#pragma unroll
-        for (int p = 0; p < 4; ++p) {
-            const int shift = 24 - 8 * p;
-#pragma unroll
-            for (int k = 0; k < PER; ++k) {
-                const unsigned key = float_key(x[k]);
-                if ((key & mask) == prefix) atomicAdd(&hist[p][(key >> shift) & 0xFFu], 1u);
-            }
-            __syncthreads();
-            // lane l owns digits 255-4l .. 252-4l (descending); every wave finds the digit itself
-            int c[4], tot = 0;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) { c[j] = static_cast<int>(hist[p][255 - 4 * lane() - j]); tot += c[j]; }
-            int above = wave_incl_scan(tot) - tot;
-            int dsel = -1, nsel = 0;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                if (dsel < 0 && above < need && above + c[j] >= need) { dsel = 255 - 4 * lane() - j; nsel = need - above; }
-                above += c[j];
-            }
-            const uint64_t hit = __ballot(dsel >= 0);
-            const int src = hit ? static_cast<int>(__builtin_ctzll(hit)) : 0;   // exactly one lane finds it
-            const int digit = __builtin_amdgcn_readlane(dsel, src);
-            need = __builtin_amdgcn_readlane(nsel, src);
-            prefix |= static_cast<unsigned>(digit) << shift;
-            mask |= 0xFFu << shift;
-        }
-        thr = key_float(prefix);
-    }
-    float ls = 0.f;
-#pragma unroll
-    for (int k = 0; k < PER; ++k) {
-        const float e = x[k] >= thr ? expf(x[k] - mx) : 0.f;
-        S.u.m.samp.lg[k * BT + tid()] = e;
-        ls += e;
-    }
-    ls = wave_sum(ls);
-    if (lane() == 0) S.sred[NW + wave()] = ls;
-    __syncthreads();
-    if (wave() == 0) {
-        float ssum = 0.f;
-#pragma unroll
-        for (int w = 0; w < NW; ++w) ssum += S.sred[NW + w];
-        const float inv = 1.f / ssum;
-        uint64_t st = seed * 0x9E3779B97F4A7C15ull + 0xBF58476D1CE4E5B9ull + 1ull;
-        (void) pcg32_next(st); (void) pcg32_next(st); (void) pcg32_next(st);
-        const float u = static_cast<float>(pcg32_next(st) >> 8) * (1.0f / 16777216.0f);
-        int chosen = V - 1;
-        float cum = 0.f;
-        bool found = false;
-        for (int k = 0; k < PER && !found; ++k) {
-            for (int w = 0; w < NW && !found; ++w) {
-                const int base = k * BT + w * WAVE;
-                const float ev = S.u.m.samp.lg[base + lane()];
-                uint64_t nz = __ballot(ev != 0.f);
-                while (nz && !found) {
-                    const int b = static_cast<int>(__builtin_ctzll(nz));
-                    nz &= nz - 1;
-                    cum = fmaf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(ev), b)), inv, cum);
-                    if (cum >= u) { chosen = base + b; found = true; }
-                }
-            }
-        }
-        if (lane() == 0) S.isel[2] = chosen;
-    }
-    __syncthreads();
-    return S.isel[2];
+__device__ __forceinline__ SampleLds sample_lds(Smem &S) {
+    return SampleLds{S.u.m.samp.lg, reinterpret_cast<unsigned (*)[256]>(S.u.m.samp.idx), S.sred, S.sidx, &S.isel[2]};
 }
 
 // ---- the frame ---------------------------------------------------------------
@@ -1023,7 +892,7 @@ __global__ void __launch_bounds__(BT, 1) k_frame(Args a, const Weights *__restri
     }
     __syncthreads();
     PROF_MARK(a, S);
-    const int cb0 = block_sample<VT>(a.temperature, a.top_k, a.talker_seed, S);
+    const int cb0 = block_sample<VT, BT>(a.temperature, a.top_k, a.talker_seed, sample_lds(S));
     PROF_MARK(a, S);
     if (tid() == 0) S.codes[0] = cb0;
 
@@ -1061,7 +930,7 @@ __global__ void __launch_bounds__(BT, 1) k_frame(Args a, const Weights *__restri
             __syncthreads();
         }
         PROF_MARK(a, S);
-        const int code = block_sample<VC>(a.cp_temperature, a.cp_top_k, a.cp_seed + static_cast<uint64_t>(pos) * 0xD1B54A32D192ED03ull, S);
+        const int code = block_sample<VC, BT>(a.cp_temperature, a.cp_top_k, a.cp_seed + static_cast<uint64_t>(pos) * 0xD1B54A32D192ED03ull, sample_lds(S));
         PROF_MARK(a, S);
         if (tid() == 0) S.codes[pos] = code;
         if (pos + 1 < NCB) {

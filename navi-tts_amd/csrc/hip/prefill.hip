@@ -19,6 +19,7 @@
 //    f16 cache, exactly as the frame's decode attention will later read them.
 #include "dev_common.h"
 #include "host_util.h"
+#include "linear.h"
 
 #include <algorithm>
 #include <cmath>
@@ -37,10 +38,12 @@ typedef _Float16 half8v __attribute__((ext_vector_type(8)));
 
 struct LinArgs {
     const float *x;        // [M][ldx] f32
-    const uint16_t *w;     // [N][K] f16
+    // W as up to three row blocks (q | k | v, gate | up): output columns [0, n1) are rows of w,
+    // [n1, n2) rows of w1, [n2, N) rows of w2, each [rows][K] f16
+    const uint16_t *w, *w1, *w2;
     float *part;           // [S][M][ldp] f32 partial sums (columns p_off .. p_off + N)
     uint32_t *flag;        // set when an activation is outside the f16 range
-    int ldx, M, K, N, kps, ldp, p_off;
+    int ldx, M, K, N, kps, ldp, p_off, n1, n2;
 };
 
 __device__ __forceinline__ void split_store(float v, _Float16 *hi, _Float16 *lo, bool &bad) {
@@ -62,8 +65,10 @@ __global__ void __launch_bounds__(BT) k_linear_partial(LinArgs a) {
     const int n0 = blockIdx.x * 64 + wv * 16;
     const int m0 = blockIdx.y * (MT * 16);
     const int kb = blockIdx.z * a.kps, ke = kb + a.kps;
-    const NAVI_GLOBAL u32x4_t *wrow =
-        (const NAVI_GLOBAL u32x4_t *) (a.w + static_cast<size_t>(n0 + (l & 15)) * a.K + (l >> 4) * 8);
+    const int nc = n0 + (l & 15);
+    const uint16_t *wr = nc < a.n1 ? a.w + static_cast<size_t>(nc) * a.K
+                       : nc < a.n2 ? a.w1 + static_cast<size_t>(nc - a.n1) * a.K : a.w2 + static_cast<size_t>(nc - a.n2) * a.K;
+    const NAVI_GLOBAL u32x4_t *wrow = (const NAVI_GLOBAL u32x4_t *) (wr + (l >> 4) * 8);
     f32x4_t acc[MT];
 #pragma unroll
     for (int i = 0; i < MT; ++i) acc[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
@@ -143,24 +148,7 @@ __device__ __forceinline__ float block_sum256(float v, float *red) {
     return red[0] + red[1] + red[2] + red[3];
 }
 
-// part[0] + part[1] + ... + part[S-1] at four consecutive columns, in that order (deterministic);
-// the loads go out eight partials at a time instead of one after another.
-__device__ __forceinline__ f32x4_t sum_parts4(const float *part, int S, size_t stride, size_t idx) {
-    f32x4_t v = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    for (int s0 = 0; s0 < S; s0 += 8) {
-        f32x4_t t[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j)
-            if (s0 + j < S) t[j] = *(const NAVI_GLOBAL f32x4_t *) (part + (s0 + j) * stride + idx);
-#pragma unroll
-        for (int j = 0; j < 8; ++j)
-            if (s0 + j < S) v = s0 + j == 0 ? t[j] : v + t[j];
-    }
-    return v;
-}
 
-__device__ __forceinline__ f32x4_t ld4(const float *p) { return *(const NAVI_GLOBAL f32x4_t *) p; }
-__device__ __forceinline__ void st4(float *p, f32x4_t v) { *(NAVI_GLOBAL f32x4_t *) p = v; }
 
 __device__ __forceinline__ float silu(float g) { return g / (1.f + expf(-g)); }
 
@@ -376,9 +364,10 @@ int pick_splits(int M, int K, int N) {
 
 size_t splits_floats(int M, int K, int N) { return static_cast<size_t>(pick_splits(M, K, N)) * M * N; }
 
-void launch_partial(const float *x, int ldx, int M, const uint16_t *w, int K, int N, int S, float *part, int ldp, int p_off,
-                    uint32_t *flag, hipStream_t st) {
-    LinArgs a{x, w, part, flag, ldx, M, K, N, K / S, ldp, p_off};
+void launch_partial3(const float *x, int ldx, int M, const uint16_t *w0, int n0, const uint16_t *w1, int n1, const uint16_t *w2,
+                     int n2, int K, int S, float *part, int ldp, int p_off, uint32_t *flag, hipStream_t st) {
+    const int N = n0 + n1 + n2;
+    LinArgs a{x, w0, w1, w2, part, flag, ldx, M, K, N, K / S, ldp, p_off, n0, n0 + n1};
     const int mt = tiles_m(M);
     const dim3 grid(N / 64, (M + 16 * mt - 1) / (16 * mt), S);
     switch (mt) {
@@ -387,6 +376,25 @@ void launch_partial(const float *x, int ldx, int M, const uint16_t *w, int K, in
     case 3: hipLaunchKernelGGL(k_linear_partial<3>, grid, dim3(BT), 0, st, a); break;
     default: hipLaunchKernelGGL(k_linear_partial<4>, grid, dim3(BT), 0, st, a); break;
     }
+}
+
+void launch_partial(const float *x, int ldx, int M, const uint16_t *w, int K, int N, int S, float *part, int ldp, int p_off,
+                    uint32_t *flag, hipStream_t st) {
+    launch_partial3(x, ldx, M, w, N, nullptr, 0, nullptr, 0, K, S, part, ldp, p_off, flag, st);
+}
+
+void launch_resid_norm(const float *part, int S, const float *src, float *x, const float *w, float eps, float *xn, int M,
+                       int H, hipStream_t st) {
+    hipLaunchKernelGGL(k_resid_norm, dim3(M), dim3(BT), 0, st, part, S, src, x, w, eps, xn, M, H);
+}
+
+void launch_swiglu(const float *part, int S, int M, int F, float *h, hipStream_t st) {
+    hipLaunchKernelGGL(k_swiglu, dim3(M), dim3(BT), 0, st, part, S, M, F, h);
+}
+
+void launch_finish_linear(const float *part, int S, int M, int N, const float *bias, const float *residual, int act, float *y,
+                          int ldy, hipStream_t st) {
+    hipLaunchKernelGGL(k_finish_linear, dim3(M), dim3(BT), 0, st, part, S, M, N, bias, residual, act, y, ldy);
 }
 
 bool linear_shape_ok(const float *x, int ldx, int M, const uint16_t *w, int K, int N) {
@@ -718,9 +726,7 @@ navi_status navi_talker_prefill(navi_talker *t, const float *d_rows, int32_t n_r
     for (int l = 0; l < t->L; ++l) {
         const LayerW &w = t->layers[l];
         int S = pick_splits(T, H, QKVW);
-        launch_partial(t->xn, H, T, w.wq, H, t->QD, S, t->part, QKVW, 0, t->flag, s);
-        launch_partial(t->xn, H, T, w.wk, H, t->KVD, S, t->part, QKVW, t->QD, t->flag, s);
-        launch_partial(t->xn, H, T, w.wv, H, t->KVD, S, t->part, QKVW, t->QD + t->KVD, t->flag, s);
+        launch_partial3(t->xn, H, T, w.wq, t->QD, w.wk, t->KVD, w.wv, t->KVD, H, S, t->part, QKVW, 0, t->flag, s);
         hipLaunchKernelGGL(k_qkv_finish, dim3(T), dim3(BT), QKVW * sizeof(float), s, t->part, S, T, t->NQ, t->NKV, w.qn,
                            w.kn, t->eps, t->invf, 0, t->q, t->kk[l], t->vv[l]);
         hipLaunchKernelGGL(k_attn_prefill, dim3(T, t->NKV), dim3(BT), att_lds, s, t->q, t->kk[l], t->vv[l], t->NQ, t->NKV, 0,
@@ -729,8 +735,7 @@ navi_status navi_talker_prefill(navi_talker *t, const float *d_rows, int32_t n_r
         launch_partial(t->att, t->QD, T, w.wo, t->QD, H, S, t->part, H, 0, t->flag, s);
         hipLaunchKernelGGL(k_resid_norm, dim3(T), dim3(BT), 0, s, t->part, S, nullptr, t->x, w.ln2, t->eps, t->xn, T, H);
         S = pick_splits(T, H, 2 * t->F);
-        launch_partial(t->xn, H, T, w.wg, H, t->F, S, t->part, 2 * t->F, 0, t->flag, s);
-        launch_partial(t->xn, H, T, w.wu, H, t->F, S, t->part, 2 * t->F, t->F, t->flag, s);
+        launch_partial3(t->xn, H, T, w.wg, t->F, w.wu, t->F, nullptr, 0, H, S, t->part, 2 * t->F, 0, t->flag, s);
         hipLaunchKernelGGL(k_swiglu, dim3(T), dim3(BT), 0, s, t->part, S, T, t->F, t->h);
         S = pick_splits(T, t->F, H);
         launch_partial(t->h, t->F, T, w.wd, t->F, H, S, t->part, H, 0, t->flag, s);

@@ -1,0 +1,716 @@
+// Multi-stream batched decode on gfx950 (the C ABI's navi_streams_*): n independent requests
+// ("streams"), each with its own KV cache, repetition set and seeds, advanced by one frame per
+// call, with the talker and the code predictor run as GEMMs over the streams on the matrix cores.
+//
+// The reference has no batched decode. Each stream's frame follows the batch-1 frame row by row
+// (k_frame, model/qwen3tts/frame.hip:517-579, and the host side of Frame, frame.hip:653-810):
+// same seeds, same sampling rules, same step assembly, so stream i computes what navi_frame_run
+// computes for it alone, up to the summation order of the projections. MI355X design:
+//
+//  * Projections: the prefill's split-K MFMA linear (activations as f16 hi + lo pairs, f16
+//    weights) with M = n streams (code-predictor positions 0 and 1: 2n rows). Every weight byte
+//    streams from HBM once per step for all streams, so the weights cost 3.3 GB per step whatever n.
+//  * Talker attention: split-KV decode attention, one block per (stream, kv head, key range); the
+//    two q heads of a GQA group share the K/V loads (one key per thread for the scores, eight
+//    keys' V rows in flight per wave); a combine kernel merges the ranges' (max, sum, vector).
+//  * Code-predictor attention: one block per (stream, kv head) fuses the q/k head norms, RoPE, the
+//    f16 K/V store into the stream's cp cache and the attention over its <= 16 positions.
+//  * Sampling: block_sample (sampler.h, the frame kernel's sampler) with one block per stream.
+#include "dev_common.h"
+#include "host_util.h"
+#include "linear.h"
+#include "sampler.h"
+
+#include <algorithm>
+#include <cmath>
+#include <string>
+#include <vector>
+
+namespace navi_amd {
+namespace ms {
+
+constexpr int BT = 256, NW = BT / WAVE;
+constexpr int HD = 128, NCB = 16, CPH = NCB - 1;
+constexpr int MAX_TL = 32, MAX_CL = 8;
+constexpr int KPS = 256;               // keys per attention split (one per thread)
+constexpr float ATT_SCALE = 0.08838834764831845f;   // 1/sqrt(128)
+
+// Per-stream state the kernels read: position, frame index, seeds, cache pointers.
+struct StreamMeta {
+    int n_past, frame_index;
+    uint64_t talker_seed, cp_seed;
+};
+
+// ---- talker: q/k norms + RoPE + K/V store, per stream -----------------------------------
+
+// Row m of the [q | k | v] partials: per-head RMSNorm of q and k, RoPE at the stream's position,
+// q kept f32, k and v rounded to f16 into the stream's cache (norm_rope_store, frame.hip:311-346).
+__global__ void __launch_bounds__(BT) k_st_qkv_finish(const float *part, int S, int M, int nq, int nkv, const float *qn,
+                                                      const float *kn, float eps, const float *invf, const StreamMeta *meta,
+                                                      uint16_t *const *kcache, uint16_t *const *vcache, float *q) {
+    extern __shared__ float row[];
+    const int m = blockIdx.x, pos = meta[m].n_past;
+    const int QD = nq * HD, KVD = nkv * HD, W = QD + 2 * KVD;
+    const size_t stride = static_cast<size_t>(M) * W;
+    for (int i = threadIdx.x * 4; i < W; i += BT * 4) {
+        const f32x4_t v = sum_parts4(part, S, stride, static_cast<size_t>(m) * W + i);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) row[i + j] = v[j];
+    }
+    __syncthreads();
+    const int wv = threadIdx.x >> 6, l = threadIdx.x & 63;
+    float sn, cs;
+    sincosf(static_cast<float>(pos) * gld(invf + l), &sn, &cs);
+    for (int hh = wv; hh < nq + nkv; hh += NW) {
+        float *hp = row + hh * HD;
+        const float *nw = hh < nq ? qn : kn;
+        const float a0 = hp[l], a1 = hp[l + HD / 2];
+        const float sc = rsqrtf(wave_sum(fmaf(a0, a0, a1 * a1)) / static_cast<float>(HD) + eps);
+        const float x0 = a0 * sc * gld(nw + l), x1 = a1 * sc * gld(nw + l + HD / 2);
+        hp[l] = x0 * cs - x1 * sn;
+        hp[l + HD / 2] = x0 * sn + x1 * cs;
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < QD; i += BT) gst(q + static_cast<size_t>(m) * QD + i, row[i]);
+    uint16_t *kc = kcache[m] + static_cast<size_t>(pos) * KVD, *vc = vcache[m] + static_cast<size_t>(pos) * KVD;
+    for (int i = threadIdx.x; i < KVD; i += BT) {
+        gst(kc + i, f2h(row[QD + i]));
+        gst(vc + i, f2h(row[QD + KVD + i]));
+    }
+}
+
+// ---- talker: split-KV decode attention ----------------------------------------------------
+
+// Block (m, g, s): keys [s * KPS, min(n, (s + 1) * KPS)) of stream m's cache, n = n_past + 1, for
+// the two q heads of kv group g. Writes per head (max, sum of e^(score - max), unnormalised
+// vector) to part[m][g][s][h] = {m, l, o[HD]}.
+__global__ void __launch_bounds__(BT) k_st_attn(const float *q, const StreamMeta *meta, uint16_t *const *kcache,
+                                                uint16_t *const *vcache, int nq, int nkv, int splits, float *part) {
+    __shared__ float qs[2][HD], sc[2][KPS], red[2][NW], opart[NW][2][HD];
+    const int m = blockIdx.x, g = blockIdx.y, s = blockIdx.z;
+    const int n = meta[m].n_past + 1, j0 = s * KPS, j1 = min(n, j0 + KPS), cnt = max(0, j1 - j0);
+    const int QD = nq * HD, KVD = nkv * HD;
+    const int wv = threadIdx.x >> 6, l = threadIdx.x & 63;
+    float *out = part + ((static_cast<size_t>(m) * nkv + g) * splits + s) * 2 * (HD + 2);
+    qs[threadIdx.x >> 7][threadIdx.x & (HD - 1)] = gld(q + static_cast<size_t>(m) * QD + g * 2 * HD + threadIdx.x);
+    __syncthreads();
+    const uint16_t *kb = kcache[m] + g * HD, *vb = vcache[m] + g * HD;
+    float d0 = -INFINITY, d1 = -INFINITY;
+    if (static_cast<int>(threadIdx.x) < cnt) {
+        const NAVI_GLOBAL u32x4_t *kp = (const NAVI_GLOBAL u32x4_t *) (kb + static_cast<size_t>(j0 + threadIdx.x) * KVD);
+        u32x4_t kr[HD / 8];
+#pragma unroll
+        for (int c = 0; c < HD / 8; ++c) kr[c] = kp[c];
+        float a0 = 0.f, a1 = 0.f;
+#pragma unroll
+        for (int c = 0; c < HD / 8; ++c)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int i = c * 8 + e * 2;
+                const float k0 = h2f(static_cast<uint16_t>(kr[c][e])), k1 = h2f(static_cast<uint16_t>(kr[c][e] >> 16));
+                a0 = fmaf(qs[0][i + 1], k1, fmaf(qs[0][i], k0, a0));
+                a1 = fmaf(qs[1][i + 1], k1, fmaf(qs[1][i], k0, a1));
+            }
+        d0 = a0 * ATT_SCALE;
+        d1 = a1 * ATT_SCALE;
+    }
+    float mx0 = wave_max(d0), mx1 = wave_max(d1);
+    if (l == 0) { red[0][wv] = mx0; red[1][wv] = mx1; }
+    __syncthreads();
+    mx0 = fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3]));
+    mx1 = fmaxf(fmaxf(red[1][0], red[1][1]), fmaxf(red[1][2], red[1][3]));
+    const float e0 = static_cast<int>(threadIdx.x) < cnt ? expf(d0 - mx0) : 0.f;
+    const float e1 = static_cast<int>(threadIdx.x) < cnt ? expf(d1 - mx1) : 0.f;
+    sc[0][threadIdx.x] = e0;
+    sc[1][threadIdx.x] = e1;
+    const float s0 = wave_sum(e0), s1 = wave_sum(e1);
+    __syncthreads();                                      // red reads done, probabilities published
+    if (l == 0) { red[0][wv] = s0; red[1][wv] = s1; }
+    // V: wave w sums keys j = w, w + 4, ...; lane l owns dims 2l, 2l + 1 of both heads
+    float a00 = 0.f, a01 = 0.f, a10 = 0.f, a11 = 0.f;
+    const uint16_t *vp = vb + static_cast<size_t>(j0) * KVD + 2 * l;
+    for (int jb = wv; jb < cnt; jb += NW * 8) {
+        uint32_t vv[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int j = jb + NW * u;
+            vv[u] = j < cnt ? gld(reinterpret_cast<const uint32_t *>(vp + static_cast<size_t>(j) * KVD)) : 0u;
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int j = jb + NW * u;
+            if (j < cnt) {
+                const float p0 = sc[0][j], p1 = sc[1][j];
+                const float v0 = h2f(static_cast<uint16_t>(vv[u])), v1 = h2f(static_cast<uint16_t>(vv[u] >> 16));
+                a00 = fmaf(p0, v0, a00);
+                a01 = fmaf(p0, v1, a01);
+                a10 = fmaf(p1, v0, a10);
+                a11 = fmaf(p1, v1, a11);
+            }
+        }
+    }
+    opart[wv][0][2 * l] = a00;
+    opart[wv][0][2 * l + 1] = a01;
+    opart[wv][1][2 * l] = a10;
+    opart[wv][1][2 * l + 1] = a11;
+    __syncthreads();
+    const int hh = threadIdx.x >> 7, d = threadIdx.x & (HD - 1);
+    float *o = out + hh * (HD + 2);
+    gst(o + 2 + d, opart[0][hh][d] + opart[1][hh][d] + opart[2][hh][d] + opart[3][hh][d]);
+    if (d == 0) {
+        gst(o, hh ? mx1 : mx0);
+        gst(o + 1, red[hh][0] + red[hh][1] + red[hh][2] + red[hh][3]);
+    }
+}
+
+// att[m][(2g + h) * HD + d] = sum_s o_s e^(m_s - M) / sum_s l_s e^(m_s - M) over the key ranges.
+__global__ void __launch_bounds__(BT) k_st_attn_combine(const float *part, const StreamMeta *meta, int nq, int nkv, int splits,
+                                                        float *att) {
+    const int m = blockIdx.x, g = blockIdx.y, hh = threadIdx.x >> 7, d = threadIdx.x & (HD - 1);
+    const int used = (meta[m].n_past + 1 + KPS - 1) / KPS;
+    const float *p = part + (static_cast<size_t>(m) * nkv + g) * splits * 2 * (HD + 2) + hh * (HD + 2);
+    float M = -INFINITY;
+    for (int s = 0; s < used; ++s) M = fmaxf(M, gld(p + s * 2 * (HD + 2)));
+    float num = 0.f, den = 0.f;
+    for (int s = 0; s < used; ++s) {
+        const float *ps = p + s * 2 * (HD + 2);
+        const float w = expf(gld(ps) - M);
+        den = fmaf(gld(ps + 1), w, den);
+        num = fmaf(gld(ps + 2 + d), w, num);
+    }
+    gst(att + static_cast<size_t>(m) * nq * HD + (g * 2 + hh) * HD + d, num / den);
+}
+
+// ---- code predictor: norms + RoPE + K/V store + attention, per (stream, kv head) -----------
+
+// Rows m * T + t (t < T) at cp positions p0 + t of stream m. The block sums the partials of its
+// group's columns (q heads 2g, 2g + 1, k and v of head g), normalises q and k per head, applies
+// RoPE, stores K/V in f16 into cpk/cpv [stream][layer][pos][kvd], then attends each row over
+// positions 0..p0 + t with the f16-rounded keys (the frame kernel's cp attention reads the same
+// f16 values from LDS).
+__global__ void __launch_bounds__(BT) k_st_cp_attn(const float *part, int S, int rows, int T, int p0, int nq, int nkv,
+                                                   const float *qn, const float *kn, float eps, const float *invf, int layer,
+                                                   int n_layer, uint16_t *cpk, uint16_t *cpv, float *att) {
+    __shared__ float vec[2][4][HD];          // [t][q0, q1, k, v]
+    __shared__ float kf[NCB][HD], vf[NCB][HD];
+    const int m = blockIdx.x, g = blockIdx.y;
+    const int QD = nq * HD, KVD = nkv * HD, W = QD + 2 * KVD;
+    const size_t stride = static_cast<size_t>(rows) * W;
+    const int wv = threadIdx.x >> 6, l = threadIdx.x & 63;
+    // partial sums: (t, vector, dim) with 4 dims per thread
+    for (int i = threadIdx.x; i < T * 4 * (HD / 4); i += BT) {
+        const int t = i / (4 * (HD / 4)), r = i % (4 * (HD / 4)), vi = r / (HD / 4), d = (r % (HD / 4)) * 4;
+        const int col = vi < 2 ? (g * 2 + vi) * HD + d : vi == 2 ? QD + g * HD + d : QD + KVD + g * HD + d;
+        const f32x4_t v = sum_parts4(part, S, stride, static_cast<size_t>(m * T + t) * W + col);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) vec[t][vi][d + e] = v[e];
+    }
+    const size_t base = (static_cast<size_t>(m) * n_layer + layer) * NCB * KVD + g * HD;
+    // earlier positions of this stream's cp cache (written by earlier launches)
+    for (int i = threadIdx.x; i < p0 * HD; i += BT) {
+        const int j = i / HD, d = i % HD;
+        kf[j][d] = h2f(gld(cpk + base + static_cast<size_t>(j) * KVD + d));
+        vf[j][d] = h2f(gld(cpv + base + static_cast<size_t>(j) * KVD + d));
+    }
+    __syncthreads();
+    // head norms + RoPE: one wave per (t, vector) of q0, q1, k
+    for (int task = wv; task < T * 3; task += NW) {
+        const int t = task / 3, vi = task % 3;
+        float *hp = vec[t][vi];
+        const float *nw = vi < 2 ? qn : kn;
+        float sn, cs;
+        sincosf(static_cast<float>(p0 + t) * gld(invf + l), &sn, &cs);
+        const float a0 = hp[l], a1 = hp[l + HD / 2];
+        const float scl = rsqrtf(wave_sum(fmaf(a0, a0, a1 * a1)) / static_cast<float>(HD) + eps);
+        const float x0 = a0 * scl * gld(nw + l), x1 = a1 * scl * gld(nw + l + HD / 2);
+        hp[l] = x0 * cs - x1 * sn;
+        hp[l + HD / 2] = x0 * sn + x1 * cs;
+    }
+    __syncthreads();
+    // the new keys/values: f16 into the cache and (f16-rounded) into LDS
+    for (int i = threadIdx.x; i < T * HD; i += BT) {
+        const int t = i / HD, d = i % HD;
+        const uint16_t kh = f2h(vec[t][2][d]), vh = f2h(vec[t][3][d]);
+        gst(cpk + base + static_cast<size_t>(p0 + t) * KVD + d, kh);
+        gst(cpv + base + static_cast<size_t>(p0 + t) * KVD + d, vh);
+        kf[p0 + t][d] = h2f(kh);
+        vf[p0 + t][d] = h2f(vh);
+    }
+    __syncthreads();
+    // attention: one wave per (t, head), lane j scores key j
+    for (int task = wv; task < T * 2; task += NW) {
+        const int t = task / 2, hh = task % 2, n = p0 + t + 1;
+        float sl = -INFINITY;
+        if (l < n) {
+            float acc = 0.f;
+#pragma unroll 8
+            for (int d = 0; d < HD; ++d) acc = fmaf(kf[l][d], vec[t][hh][d], acc);
+            sl = acc * ATT_SCALE;
+        }
+        const float mx = wave_max(sl);
+        const float e = l < n ? expf(sl - mx) : 0.f;
+        const float inv = 1.f / wave_sum(e);
+        float o0 = 0.f, o1 = 0.f;
+        for (int j = 0; j < n; ++j) {
+            const float p = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), j));
+            o0 = fmaf(p, vf[j][2 * l], o0);
+            o1 = fmaf(p, vf[j][2 * l + 1], o1);
+        }
+        float *dst = att + static_cast<size_t>(m * T + t) * QD + (g * 2 + hh) * HD + 2 * l;
+        gst(dst, o0 * inv);
+        gst(dst + 1, o1 * inv);
+    }
+}
+
+// ---- sampling, one block per stream --------------------------------------------------------
+
+struct SampleArgs {
+    float temperature, rep_penalty, cp_temperature;
+    int top_k, cp_top_k, min_frames, eos_id, suppress_from;
+};
+
+// Talker codebook 0 of stream m (tl_modified_logit + tl_sample, frame.hip:413-454): control range
+// suppressed except EOS, EOS suppressed before min_frames, repetition penalty over the stream's
+// set; then the cp input rows of the stream: x[2m] = post-norm hidden, x[2m + 1] = codec_emb[cb0].
+__global__ void __launch_bounds__(BT) k_st_talker_sample(const float *logits, int V, const StreamMeta *meta, uint8_t *seen,
+                                                         SampleArgs sa, const float *hidden, const uint16_t *codec_emb, int H,
+                                                         float *cp_x, int32_t *codes) {
+    constexpr int VT = 3072;
+    __shared__ float lg[VT];
+    __shared__ unsigned hist[4][256];
+    __shared__ float sred[2 * NW];
+    __shared__ int sidx[NW], sel;
+    const int m = blockIdx.x;
+    const StreamMeta me = meta[m];
+    const float *lp = logits + static_cast<size_t>(m) * V;
+    uint8_t *sn = seen + static_cast<size_t>(m) * V;
+    for (int i = threadIdx.x; i < VT; i += BT) {
+        float v = gld(lp + i);
+        if (i >= sa.suppress_from && i != sa.eos_id) v = -INFINITY;
+        else if (i == sa.eos_id && me.frame_index < sa.min_frames) v = -INFINITY;
+        else if (sa.rep_penalty > 0.f && gld(sn + i)) v = v > 0.f ? v / sa.rep_penalty : v * sa.rep_penalty;
+        lg[i] = v;
+    }
+    __syncthreads();
+    const int cb0 = block_sample<VT, BT>(sa.temperature, sa.top_k, me.talker_seed, SampleLds{lg, hist, sred, sidx, &sel});
+    if (threadIdx.x == 0) {
+        gst(codes + static_cast<size_t>(m) * NCB, cb0);
+        if (cb0 != sa.eos_id) gst(sn + cb0, static_cast<uint8_t>(1u));
+    }
+    const float *hr = hidden + static_cast<size_t>(m) * H;
+    const uint16_t *er = codec_emb + static_cast<size_t>(cb0) * H;
+    for (int i = threadIdx.x; i < H; i += BT) {
+        gst(cp_x + static_cast<size_t>(2 * m) * H + i, gld(hr + i));
+        gst(cp_x + static_cast<size_t>(2 * m + 1) * H + i, h2f(gld(er + i)));
+    }
+}
+
+// Code pos of stream m from lm_head[pos - 1]'s logits (cp_sample, frame.hip:483-500: no
+// suppression, penalty or EOS gate; seed cp_seed + pos * 0xD1B54A32D192ED03); then, if next_emb,
+// the next cp input row x[m] = next_emb[code].
+__global__ void __launch_bounds__(BT) k_st_cp_sample(const float *logits, const StreamMeta *meta, SampleArgs sa, int pos,
+                                                     const uint16_t *next_emb, int H, float *x, int32_t *codes) {
+    constexpr int VC = 2048;
+    __shared__ float lg[VC];
+    __shared__ unsigned hist[4][256];
+    __shared__ float sred[2 * NW];
+    __shared__ int sidx[NW], sel;
+    const int m = blockIdx.x;
+    const float *lp = logits + static_cast<size_t>(m) * VC;
+    for (int i = threadIdx.x; i < VC; i += BT) lg[i] = gld(lp + i);
+    __syncthreads();
+    const uint64_t seed = meta[m].cp_seed + static_cast<uint64_t>(pos) * 0xD1B54A32D192ED03ull;
+    const int code = block_sample<VC, BT>(sa.cp_temperature, sa.cp_top_k, seed, SampleLds{lg, hist, sred, sidx, &sel});
+    if (threadIdx.x == 0) gst(codes + static_cast<size_t>(m) * NCB + pos, code);
+    if (next_emb) {
+        const uint16_t *er = next_emb + static_cast<size_t>(code) * H;
+        for (int i = threadIdx.x; i < H; i += BT) gst(x + static_cast<size_t>(m) * H + i, h2f(gld(er + i)));
+    }
+}
+
+struct EmbTable {
+    const uint16_t *cp_emb[CPH];
+};
+
+// step_out[m] = codec_emb[c0] + sum_cb cp_emb[cb][c_{cb+1}] + trailing[m], f32 adds in that order
+// (assemble_step, frame.hip:504-513).
+__global__ void __launch_bounds__(BT) k_st_assemble(const int32_t *codes, const uint16_t *codec_emb, EmbTable et,
+                                                    const float *trailing, int H, float *step_out) {
+    const int m = blockIdx.x;
+    const int32_t *c = codes + static_cast<size_t>(m) * NCB;
+    int cs[NCB];
+#pragma unroll
+    for (int k = 0; k < NCB; ++k) cs[k] = gld(c + k);
+    for (int i = threadIdx.x; i < H; i += BT) {
+        float v = h2f(gld(codec_emb + static_cast<size_t>(cs[0]) * H + i));
+#pragma unroll
+        for (int cb = 0; cb < CPH; ++cb) v += h2f(gld(et.cp_emb[cb] + static_cast<size_t>(cs[cb + 1]) * H + i));
+        gst(step_out + static_cast<size_t>(m) * H + i, v + gld(trailing + static_cast<size_t>(m) * H + i));
+    }
+}
+
+struct LayerW {
+    const float *ln1, *ln2, *qn, *kn;
+    const uint16_t *wq, *wk, *wv, *wo, *wg, *wu, *wd;
+};
+
+} // namespace ms
+} // namespace navi_amd
+
+using namespace navi_amd;
+using namespace navi_amd::ms;
+
+struct navi_streams {
+    navi_model_params p{};
+    int H = 0, NQ = 0, NKV = 0, QD = 0, KVD = 0, F = 0, VT = 0, VC = 0, TL = 0, CL = 0;
+    int ms = 0, max_pos = 0, splits = 0;
+    // weights
+    std::vector<LayerW> tl, cl;
+    const float *tl_norm = nullptr, *cp_norm = nullptr;
+    const uint16_t *codec_head = nullptr, *codec_emb = nullptr;
+    EmbTable cp_emb{};
+    const uint16_t *lm_head[CPH] = {};
+    // work buffers
+    float *x = nullptr, *xn = nullptr, *q = nullptr, *att = nullptr, *h = nullptr, *part = nullptr, *apart = nullptr;
+    float *lg = nullptr, *step = nullptr, *invf_t = nullptr, *invf_c = nullptr;
+    size_t part_floats = 0;
+    uint16_t *cpk = nullptr, *cpv = nullptr;
+    uint8_t *seen = nullptr;
+    int32_t *codes = nullptr;
+    uint32_t *flag = nullptr;
+    StreamMeta *meta = nullptr;
+    uint16_t **ktab = nullptr, **vtab = nullptr;   // device [TL][ms]: stream caches per layer
+    std::vector<uint16_t *> kh, vh;                 // host copy of the tables
+    std::vector<StreamMeta> hmeta;
+    float *tap = nullptr;                           // taps: hidden [ms][H] | logits [ms][VT] | cp logits [ms][15][VC]
+    hipEvent_t ev0 = nullptr, ev1 = nullptr;
+    double last_ms = 0;
+    std::vector<void *> owned;
+
+    float *tap_hidden() const { return tap; }
+    float *tap_logits() const { return tap ? tap + static_cast<size_t>(ms) * H : nullptr; }
+    float *tap_cp() const { return tap ? tap + static_cast<size_t>(ms) * (H + VT) : nullptr; }
+
+    template <class T>
+    navi_status alloc(T *&ptr, size_t n, char *err, size_t errlen) {
+        void *v = nullptr;
+        NAVI_TRY_HIP(hipMalloc(&v, std::max<size_t>(n, 1) * sizeof(T)), err, errlen);
+        owned.push_back(v);
+        NAVI_TRY_HIP(hipMemsetAsync(v, 0, std::max<size_t>(n, 1) * sizeof(T), device_state().stream), err, errlen);
+        ptr = static_cast<T *>(v);
+        return NAVI_OK;
+    }
+
+    ~navi_streams() {
+        if (ev0) (void) hipEventDestroy(ev0);
+        if (ev1) (void) hipEventDestroy(ev1);
+        for (void *v : owned) (void) hipFree(v);
+    }
+};
+
+namespace {
+
+uint64_t splitmix64(uint64_t z) {
+    z += 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+navi_status bind_layers(const char *who, const navi_tensor_ref *t, int n, const std::string &prefix, int L, int H, int QD,
+                        int KVD, int F, std::vector<LayerW> &out, char *err, size_t errlen) {
+    out.resize(L);
+    for (int l = 0; l < L; ++l) {
+        const std::string p = prefix + ".layers." + std::to_string(l) + ".";
+        LayerW &w = out[l];
+        navi_status st;
+#define SB(T, name, dt, d0, d1, dst) \
+        if ((st = bind_tensor<T>(who, t, n, p + name, dt, d0, d1, dst, err, errlen)) != NAVI_OK) return st
+        SB(float, "input_layernorm.weight", NAVI_DT_F32, H, 0, w.ln1);
+        SB(float, "post_attention_layernorm.weight", NAVI_DT_F32, H, 0, w.ln2);
+        SB(float, "self_attn.q_norm.weight", NAVI_DT_F32, HD, 0, w.qn);
+        SB(float, "self_attn.k_norm.weight", NAVI_DT_F32, HD, 0, w.kn);
+        SB(uint16_t, "self_attn.q_proj.weight", NAVI_DT_F16, QD, H, w.wq);
+        SB(uint16_t, "self_attn.k_proj.weight", NAVI_DT_F16, KVD, H, w.wk);
+        SB(uint16_t, "self_attn.v_proj.weight", NAVI_DT_F16, KVD, H, w.wv);
+        SB(uint16_t, "self_attn.o_proj.weight", NAVI_DT_F16, H, QD, w.wo);
+        SB(uint16_t, "mlp.gate_proj.weight", NAVI_DT_F16, F, H, w.wg);
+        SB(uint16_t, "mlp.up_proj.weight", NAVI_DT_F16, F, H, w.wu);
+        SB(uint16_t, "mlp.down_proj.weight", NAVI_DT_F16, H, F, w.wd);
+#undef SB
+    }
+    return NAVI_OK;
+}
+
+// One decoder layer over `rows` rows (x: residual in/out, xn: its RMSNorm with ln1 on entry, the
+// next norm's output on exit). attend(part, S) consumes the q|k|v partials and writes h.att.
+template <class Attend>
+void layer(navi_streams &h, const LayerW &w, const float *next_norm, float eps, int rows, Attend attend, hipStream_t s) {
+    const int H = h.H, QKVW = h.QD + 2 * h.KVD;
+    int S = pf::pick_splits(rows, H, QKVW);
+    pf::launch_partial3(h.xn, H, rows, w.wq, h.QD, w.wk, h.KVD, w.wv, h.KVD, H, S, h.part, QKVW, 0, h.flag, s);
+    attend(S);
+    S = pf::pick_splits(rows, h.QD, H);
+    pf::launch_partial(h.att, h.QD, rows, w.wo, h.QD, H, S, h.part, H, 0, h.flag, s);
+    pf::launch_resid_norm(h.part, S, nullptr, h.x, w.ln2, eps, h.xn, rows, H, s);
+    S = pf::pick_splits(rows, H, 2 * h.F);
+    pf::launch_partial3(h.xn, H, rows, w.wg, h.F, w.wu, h.F, nullptr, 0, H, S, h.part, 2 * h.F, 0, h.flag, s);
+    pf::launch_swiglu(h.part, S, rows, h.F, h.h, s);
+    S = pf::pick_splits(rows, h.F, H);
+    pf::launch_partial(h.h, h.F, rows, w.wd, h.F, H, S, h.part, H, 0, h.flag, s);
+    pf::launch_resid_norm(h.part, S, nullptr, h.x, next_norm, eps, h.xn, rows, H, s);
+}
+
+} // namespace
+
+extern "C" {
+
+navi_status navi_streams_create(const navi_model_params *p, const navi_tensor_ref *tensors, int32_t n_tensors,
+                                int32_t max_streams, int32_t max_positions, navi_streams **out, char *err, size_t errlen) {
+    if (!p || !tensors || !out) {
+        set_err(err, errlen, "streams: null argument");
+        return NAVI_ERR_INVALID;
+    }
+    *out = nullptr;
+    navi_status st = ensure_device(err, errlen);
+    if (st != NAVI_OK) return st;
+    const navi_xformer_params &t = p->talker, &c = p->cp;
+    if (t.hidden != 1024 || c.hidden != t.hidden || t.head_dim != HD || c.head_dim != HD || t.n_head != 2 * t.n_kv_head ||
+        c.n_head != t.n_head || c.n_kv_head != t.n_kv_head || t.ff % 64 != 0 || c.ff != t.ff || t.vocab != 3072 ||
+        c.vocab != 2048 || p->n_code_groups != NCB || t.n_layer < 1 || t.n_layer > MAX_TL || c.n_layer < 1 ||
+        c.n_layer > MAX_CL) {
+        set_err(err, errlen, "streams: unsupported shape");
+        return NAVI_ERR_UNSUPPORTED;
+    }
+    if (max_streams < 1 || max_streams > 64 || max_positions < 1 || max_positions > 32768) {
+        set_err(err, errlen, "streams: max_streams %d / max_positions %d out of range (1..64 / 1..32768)", max_streams,
+                max_positions);
+        return NAVI_ERR_INVALID;
+    }
+    auto h = new navi_streams();
+    auto fail = [&](navi_status s_) { delete h; return s_; };
+    h->p = *p;
+    h->H = t.hidden; h->NQ = t.n_head; h->NKV = t.n_kv_head; h->QD = t.n_head * HD; h->KVD = t.n_kv_head * HD;
+    h->F = t.ff; h->VT = t.vocab; h->VC = c.vocab; h->TL = t.n_layer; h->CL = c.n_layer;
+    h->ms = max_streams;
+    h->max_pos = max_positions;
+    h->splits = (max_positions + KPS - 1) / KPS;
+    const int H = h->H;
+    if ((st = bind_layers("streams", tensors, n_tensors, "talker.model", h->TL, H, h->QD, h->KVD, h->F, h->tl, err, errlen)) != NAVI_OK ||
+        (st = bind_layers("streams", tensors, n_tensors, "talker.code_predictor.model", h->CL, H, h->QD, h->KVD, h->F, h->cl, err,
+                          errlen)) != NAVI_OK ||
+        (st = bind_tensor<float>("streams", tensors, n_tensors, "talker.model.norm.weight", NAVI_DT_F32, H, 0, h->tl_norm, err,
+                                 errlen)) != NAVI_OK ||
+        (st = bind_tensor<float>("streams", tensors, n_tensors, "talker.code_predictor.model.norm.weight", NAVI_DT_F32, H, 0,
+                                 h->cp_norm, err, errlen)) != NAVI_OK ||
+        (st = bind_tensor<uint16_t>("streams", tensors, n_tensors, "talker.codec_head.weight", NAVI_DT_F16, h->VT, H,
+                                    h->codec_head, err, errlen)) != NAVI_OK ||
+        (st = bind_tensor<uint16_t>("streams", tensors, n_tensors, "talker.model.codec_embedding.weight", NAVI_DT_F16, h->VT, H,
+                                    h->codec_emb, err, errlen)) != NAVI_OK)
+        return fail(st);
+    for (int i = 0; i < CPH; ++i) {
+        if ((st = bind_tensor<uint16_t>("streams", tensors, n_tensors,
+                                        "talker.code_predictor.model.codec_embedding." + std::to_string(i) + ".weight",
+                                        NAVI_DT_F16, h->VC, H, h->cp_emb.cp_emb[i], err, errlen)) != NAVI_OK ||
+            (st = bind_tensor<uint16_t>("streams", tensors, n_tensors, "talker.code_predictor.lm_head." + std::to_string(i) + ".weight",
+                                        NAVI_DT_F16, h->VC, H, h->lm_head[i], err, errlen)) != NAVI_OK)
+            return fail(st);
+    }
+    const size_t R = static_cast<size_t>(2) * max_streams;   // rows of the first cp pass
+    const int QKVW = h->QD + 2 * h->KVD;
+    size_t pf_need = 0;
+    for (int M = 1; M <= static_cast<int>(R); ++M) {
+        const int shapes[][2] = {{H, QKVW}, {h->QD, H}, {H, 2 * h->F}, {h->F, H}, {H, h->VT}, {H, h->VC}};
+        for (const auto &s : shapes) pf_need = std::max(pf_need, pf::splits_floats(M, s[0], s[1]));
+    }
+    h->part_floats = pf_need;
+#define SA(ptr, n_) \
+    if ((st = h->alloc(ptr, (n_), err, errlen)) != NAVI_OK) return fail(st)
+    SA(h->x, R * H);
+    SA(h->xn, R * H);
+    SA(h->q, static_cast<size_t>(max_streams) * h->QD);
+    SA(h->att, R * h->QD);
+    SA(h->h, R * h->F);
+    SA(h->part, pf_need);
+    SA(h->apart, static_cast<size_t>(max_streams) * h->NKV * h->splits * 2 * (HD + 2));
+    SA(h->lg, static_cast<size_t>(max_streams) * h->VT);
+    SA(h->step, static_cast<size_t>(max_streams) * H);
+    SA(h->invf_t, HD / 2);
+    SA(h->invf_c, HD / 2);
+    SA(h->cpk, static_cast<size_t>(max_streams) * h->CL * NCB * h->KVD);
+    SA(h->cpv, static_cast<size_t>(max_streams) * h->CL * NCB * h->KVD);
+    SA(h->seen, static_cast<size_t>(max_streams) * h->VT);
+    SA(h->codes, static_cast<size_t>(max_streams) * NCB);
+    SA(h->flag, 1);
+    SA(h->meta, max_streams);
+    SA(h->ktab, static_cast<size_t>(MAX_TL) * max_streams);
+    SA(h->vtab, static_cast<size_t>(MAX_TL) * max_streams);
+#undef SA
+    h->kh.assign(static_cast<size_t>(MAX_TL) * max_streams, nullptr);
+    h->vh.assign(static_cast<size_t>(MAX_TL) * max_streams, nullptr);
+    h->hmeta.resize(max_streams);
+    float it[HD / 2], ic[HD / 2];
+    for (int i = 0; i < HD / 2; ++i) {
+        it[i] = static_cast<float>(1.0 / std::pow(t.rope_theta, 2.0 * i / HD));
+        ic[i] = static_cast<float>(1.0 / std::pow(c.rope_theta, 2.0 * i / HD));
+    }
+    hipStream_t s = device_state().stream;
+    if (hipMemcpyAsync(h->invf_t, it, sizeof it, hipMemcpyHostToDevice, s) != hipSuccess ||
+        hipMemcpyAsync(h->invf_c, ic, sizeof ic, hipMemcpyHostToDevice, s) != hipSuccess || hipEventCreate(&h->ev0) != hipSuccess ||
+        hipEventCreate(&h->ev1) != hipSuccess || hipStreamSynchronize(s) != hipSuccess) {
+        set_err(err, errlen, "streams: HIP setup failed");
+        return fail(NAVI_ERR_HIP);
+    }
+    *out = h;
+    return NAVI_OK;
+}
+
+void navi_streams_destroy(navi_streams *h) {
+    if (!h) return;
+    (void) hipStreamSynchronize(device_state().stream);
+    delete h;
+}
+
+navi_status navi_streams_reset(navi_streams *h, int32_t stream) {
+    if (!h || stream >= h->ms) return NAVI_ERR_INVALID;
+    hipStream_t s = device_state().stream;
+    const size_t off = stream < 0 ? 0 : static_cast<size_t>(stream) * h->VT;
+    const size_t n = stream < 0 ? static_cast<size_t>(h->ms) * h->VT : h->VT;
+    return hipMemsetAsync(h->seen + off, 0, n, s) == hipSuccess && hipStreamSynchronize(s) == hipSuccess ? NAVI_OK : NAVI_ERR_HIP;
+}
+
+navi_status navi_streams_set_taps(navi_streams *h, int32_t on) {
+    if (!h) return NAVI_ERR_INVALID;
+    if (!on || h->tap) return NAVI_OK;
+    char err[8];
+    return h->alloc(h->tap, static_cast<size_t>(h->ms) * (h->H + h->VT + CPH * h->VC), err, sizeof err);
+}
+
+const float *navi_streams_tap_hidden(const navi_streams *h) { return h ? h->tap_hidden() : nullptr; }
+const float *navi_streams_tap_logits(const navi_streams *h) { return h ? h->tap_logits() : nullptr; }
+const float *navi_streams_tap_cp_logits(const navi_streams *h) { return h ? h->tap_cp() : nullptr; }
+
+float *navi_streams_step_out(navi_streams *h) { return h ? h->step : nullptr; }
+int32_t navi_streams_max_streams(const navi_streams *h) { return h ? h->ms : 0; }
+double navi_streams_last_ms(const navi_streams *h) { return h ? h->last_ms : 0.0; }
+
+navi_status navi_streams_run(navi_streams *h, int32_t n, const navi_kv_view *kv, const int32_t *n_past, const float *d_step_in,
+                             const float *d_trailing, const navi_sampling *smp, const uint64_t *seeds,
+                             const int32_t *frame_index, int32_t *codes_out, char *err, size_t errlen) {
+    if (!h || !kv || !n_past || !d_trailing || !smp || !seeds || !frame_index || !codes_out) {
+        set_err(err, errlen, "streams: null argument");
+        return NAVI_ERR_INVALID;
+    }
+    if (n < 1 || n > h->ms) {
+        set_err(err, errlen, "streams: %d streams, this handle takes 1..%d", n, h->ms);
+        return NAVI_ERR_INVALID;
+    }
+    bool tab_changed = false;
+    int zsplits = 1;                                        // key ranges of the longest context
+    for (int i = 0; i < n; ++i) {
+        if (kv[i].n_layer != h->TL || kv[i].kv_dim != h->KVD || !kv[i].k || !kv[i].v) {
+            set_err(err, errlen, "streams: stream %d: KV cache layer count or width mismatch", i);
+            return NAVI_ERR_INVALID;
+        }
+        if (n_past[i] < 0 || n_past[i] >= kv[i].max_pos || n_past[i] >= h->max_pos) {
+            set_err(err, errlen, "stream %d: KV cache full", i);
+            return NAVI_ERR_KV_FULL;
+        }
+        for (int l = 0; l < h->TL; ++l) {
+            uint16_t *&kd = h->kh[static_cast<size_t>(l) * h->ms + i], *&vd = h->vh[static_cast<size_t>(l) * h->ms + i];
+            if (kd != kv[i].k[l] || vd != kv[i].v[l]) {
+                kd = kv[i].k[l];
+                vd = kv[i].v[l];
+                tab_changed = true;
+            }
+        }
+        zsplits = std::max(zsplits, (n_past[i] + 1 + KPS - 1) / KPS);
+        StreamMeta &m = h->hmeta[i];
+        m.n_past = n_past[i];
+        m.frame_index = frame_index[i];
+        m.talker_seed = splitmix64(seeds[i] ^ (static_cast<uint64_t>(frame_index[i]) * 0xA24BAED4963EE407ull));
+        m.cp_seed = splitmix64(m.talker_seed ^ 0x9FB21C651E98DF25ull);
+    }
+    hipStream_t s = device_state().stream;
+    const int H = h->H, QKVW = h->QD + 2 * h->KVD;
+    if (tab_changed) {
+        NAVI_TRY_HIP(hipMemcpyAsync(h->ktab, h->kh.data(), h->kh.size() * sizeof(uint16_t *), hipMemcpyHostToDevice, s), err, errlen);
+        NAVI_TRY_HIP(hipMemcpyAsync(h->vtab, h->vh.data(), h->vh.size() * sizeof(uint16_t *), hipMemcpyHostToDevice, s), err, errlen);
+    }
+    NAVI_TRY_HIP(hipMemcpyAsync(h->meta, h->hmeta.data(), n * sizeof(StreamMeta), hipMemcpyHostToDevice, s), err, errlen);
+    NAVI_TRY_HIP(hipMemsetAsync(h->flag, 0, 4, s), err, errlen);
+    NAVI_TRY_HIP(hipEventRecord(h->ev0, s), err, errlen);
+    SampleArgs sa{smp->temperature, smp->repetition_penalty, smp->cp_temperature, smp->top_k, smp->cp_top_k, smp->min_frames,
+                  h->p.codec_eos_id, h->VT - 1024};
+    const float et = h->p.talker.rms_eps, ec = h->p.cp.rms_eps;
+
+    // talker step over the n streams
+    pf::launch_resid_norm(nullptr, 0, d_step_in ? d_step_in : h->step, h->x, h->tl[0].ln1, et, h->xn, n, H, s);
+    for (int l = 0; l < h->TL; ++l) {
+        const float *next = l + 1 < h->TL ? h->tl[l + 1].ln1 : h->tl_norm;
+        layer(*h, h->tl[l], next, et, n, [&](int S) {
+            hipLaunchKernelGGL(k_st_qkv_finish, dim3(n), dim3(BT), QKVW * sizeof(float), s, h->part, S, n, h->NQ, h->NKV,
+                               h->tl[l].qn, h->tl[l].kn, et, h->invf_t, h->meta, h->ktab + static_cast<size_t>(l) * h->ms,
+                               h->vtab + static_cast<size_t>(l) * h->ms, h->q);
+            hipLaunchKernelGGL(k_st_attn, dim3(n, h->NKV, zsplits), dim3(BT), 0, s, h->q, h->meta,
+                               h->ktab + static_cast<size_t>(l) * h->ms, h->vtab + static_cast<size_t>(l) * h->ms, h->NQ,
+                               h->NKV, h->splits, h->apart);
+            hipLaunchKernelGGL(k_st_attn_combine, dim3(n, h->NKV), dim3(BT), 0, s, h->apart, h->meta, h->NQ, h->NKV, h->splits,
+                               h->att);
+        }, s);
+    }
+    // head + codebook 0; the cp input rows (hidden, codec_emb[cb0]) per stream
+    int S = pf::pick_splits(n, H, h->VT);
+    pf::launch_partial(h->xn, H, n, h->codec_head, H, h->VT, S, h->part, h->VT, 0, h->flag, s);
+    pf::launch_finish_linear(h->part, S, n, h->VT, nullptr, nullptr, 0, h->lg, h->VT, s);
+    if (h->tap) {
+        NAVI_TRY_HIP(hipMemcpyAsync(h->tap_hidden(), h->xn, static_cast<size_t>(n) * H * 4, hipMemcpyDeviceToDevice, s), err, errlen);
+        NAVI_TRY_HIP(hipMemcpyAsync(h->tap_logits(), h->lg, static_cast<size_t>(n) * h->VT * 4, hipMemcpyDeviceToDevice, s), err,
+                     errlen);
+    }
+    hipLaunchKernelGGL(k_st_talker_sample, dim3(n), dim3(BT), 0, s, h->lg, h->VT, h->meta, h->seen, sa, h->xn, h->codec_emb, H,
+                       h->x, h->codes);
+
+    // code predictor: positions 0 and 1 as one 2-row pass per stream, then one row per position
+    for (int pos = 1; pos < NCB; ++pos) {
+        const int T = pos == 1 ? 2 : 1, p0 = pos == 1 ? 0 : pos, rows = n * T;
+        pf::launch_resid_norm(nullptr, 0, h->x, h->x, h->cl[0].ln1, ec, h->xn, rows, H, s);
+        for (int l = 0; l < h->CL; ++l) {
+            const float *next = l + 1 < h->CL ? h->cl[l + 1].ln1 : h->cp_norm;
+            layer(*h, h->cl[l], next, ec, rows, [&](int S2) {
+                hipLaunchKernelGGL(k_st_cp_attn, dim3(n, h->NKV), dim3(BT), 0, s, h->part, S2, rows, T, p0, h->NQ, h->NKV,
+                                   h->cl[l].qn, h->cl[l].kn, ec, h->invf_c, l, h->CL, h->cpk, h->cpv, h->att);
+            }, s);
+        }
+        // lm_head[pos - 1] on the last row of each stream
+        S = pf::pick_splits(n, H, h->VC);
+        pf::launch_partial(h->xn + static_cast<size_t>(T - 1) * H, T * H, n, h->lm_head[pos - 1], H, h->VC, S, h->part, h->VC, 0,
+                           h->flag, s);
+        pf::launch_finish_linear(h->part, S, n, h->VC, nullptr, nullptr, 0, h->lg, h->VC, s);
+        if (h->tap)
+            NAVI_TRY_HIP(hipMemcpy2DAsync(h->tap_cp() + static_cast<size_t>(pos - 1) * h->VC, static_cast<size_t>(CPH) * h->VC * 4,
+                                          h->lg, static_cast<size_t>(h->VC) * 4, static_cast<size_t>(h->VC) * 4, n,
+                                          hipMemcpyDeviceToDevice, s),
+                         err, errlen);
+        hipLaunchKernelGGL(k_st_cp_sample, dim3(n), dim3(BT), 0, s, h->lg, h->meta, sa, pos,
+                           pos < CPH ? h->cp_emb.cp_emb[pos - 1] : nullptr, H, h->x, h->codes);
+    }
+    hipLaunchKernelGGL(k_st_assemble, dim3(n), dim3(BT), 0, s, h->codes, h->codec_emb, h->cp_emb, d_trailing, H, h->step);
+    NAVI_TRY_HIP(hipGetLastError(), err, errlen);
+    NAVI_TRY_HIP(hipEventRecord(h->ev1, s), err, errlen);
+    uint32_t bad = 0;
+    NAVI_TRY_HIP(hipMemcpyAsync(codes_out, h->codes, static_cast<size_t>(n) * NCB * sizeof(int32_t), hipMemcpyDeviceToHost, s), err,
+                 errlen);
+    NAVI_TRY_HIP(hipMemcpyAsync(&bad, h->flag, 4, hipMemcpyDeviceToHost, s), err, errlen);
+    NAVI_TRY_HIP(hipStreamSynchronize(s), err, errlen);
+    float ms_ = 0.f;
+    (void) hipEventElapsedTime(&ms_, h->ev0, h->ev1);
+    h->last_ms = ms_;
+    if (bad) {
+        set_err(err, errlen, "streams: an activation is outside the f16 range (|x| >= 65504 or NaN)");
+        return NAVI_ERR_INVALID;
+    }
+    return NAVI_OK;
+}
+
+} // extern "C"

@@ -30,6 +30,9 @@ EXPORTS = [
     "navi_talker_hidden", "navi_talker_logits", "navi_talker_last_ms", "navi_linear",
     "navi_vocoder_create", "navi_vocoder_destroy", "navi_vocoder_reset", "navi_vocoder_decode",
     "navi_vocoder_samples_per_frame", "navi_vocoder_max_chunk_frames", "navi_vocoder_last_ms", "navi_synth",
+    "navi_streams_create", "navi_streams_destroy", "navi_streams_reset", "navi_streams_run", "navi_streams_step_out",
+    "navi_streams_max_streams", "navi_streams_last_ms", "navi_streams_set_taps", "navi_streams_tap_hidden",
+    "navi_streams_tap_logits", "navi_streams_tap_cp_logits",
 ]
 
 
@@ -189,6 +192,20 @@ def lib() -> C.CDLL:
                              C.POINTER(SynthStats), E, C.c_size_t]
     L.navi_linear.argtypes = [C.c_void_p, C.c_int32, C.c_int32, C.c_void_p, C.c_int32, C.c_int32, C.c_void_p, C.c_void_p,
                               C.c_int32, C.c_void_p, C.c_int32, E, C.c_size_t]
+    L.navi_streams_create.argtypes = [C.POINTER(ModelParams), C.POINTER(TensorRef), C.c_int32, C.c_int32, C.c_int32,
+                                      C.POINTER(C.c_void_p), E, C.c_size_t]
+    L.navi_streams_destroy.argtypes = [C.c_void_p]
+    L.navi_streams_destroy.restype = None
+    L.navi_streams_reset.argtypes = [C.c_void_p, C.c_int32]
+    L.navi_streams_run.argtypes = [C.c_void_p, C.c_int32, C.POINTER(KvView), C.c_void_p, C.c_void_p, C.c_void_p,
+                                   C.POINTER(Sampling), C.c_void_p, C.c_void_p, C.c_void_p, E, C.c_size_t]
+    L.navi_streams_set_taps.argtypes = [C.c_void_p, C.c_int32]
+    for f in ("navi_streams_step_out", "navi_streams_tap_hidden", "navi_streams_tap_logits", "navi_streams_tap_cp_logits"):
+        getattr(L, f).argtypes = [C.c_void_p]
+        getattr(L, f).restype = C.c_void_p
+    L.navi_streams_max_streams.argtypes = [C.c_void_p]
+    L.navi_streams_last_ms.argtypes = [C.c_void_p]
+    L.navi_streams_last_ms.restype = C.c_double
     _lib = L
     return L
 
@@ -431,6 +448,74 @@ class Frame:
 
     def step_out(self) -> np.ndarray:
         return download(self.d_step_out, np.float32, self.hidden)
+
+
+# ---- multi-stream decode ---------------------------------------------------------------
+
+class Streams:
+    """navi_streams_*: one frame for each of n independent streams per call."""
+
+    def __init__(self, weights: DeviceWeights, max_streams: int, max_positions: int, params: ModelParams | None = None):
+        self.params = params or model_params(weights.kv)
+        refs, self._keep = weights.refs()
+        h = C.c_void_p()
+        err = C.create_string_buffer(256)
+        _check(lib().navi_streams_create(C.byref(self.params), refs, len(refs), max_streams, max_positions, C.byref(h),
+                                         err, 256), err)
+        self.h = h.value
+        self.max_streams = max_streams
+        self.hidden = self.params.talker.hidden
+
+    def close(self):
+        if self.h:
+            lib().navi_streams_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def reset(self, stream: int = -1):
+        _check(lib().navi_streams_reset(self.h, stream), what="navi_streams_reset")
+
+    def set_taps(self, on: bool):
+        _check(lib().navi_streams_set_taps(self.h, 1 if on else 0), what="navi_streams_set_taps")
+
+    def run(self, kvs, n_past, d_trailing: int, s: Sampling, seeds, frame_index, d_step_in: int | None = None):
+        """codes [n][16] (int32) for streams 0..n-1; kvs: one KvCache (or TalkerKv) per stream."""
+        n = len(kvs)
+        views = (KvView * n)(*[k.view for k in kvs])
+        npast = np.ascontiguousarray(n_past, dtype=np.int32)
+        sd = np.ascontiguousarray([x & ((1 << 64) - 1) for x in seeds], dtype=np.uint64)
+        fi = np.ascontiguousarray(frame_index, dtype=np.int32)
+        codes = np.zeros((n, 16), dtype=np.int32)
+        err = C.create_string_buffer(256)
+        _check(lib().navi_streams_run(self.h, n, views, npast.ctypes.data, d_step_in, d_trailing, C.byref(s),
+                                      sd.ctypes.data, fi.ctypes.data, codes.ctypes.data, err, 256), err)
+        for i, k in enumerate(kvs):
+            k.n_used = int(npast[i]) + 1
+        return codes
+
+    @property
+    def d_step_out(self) -> int:
+        return lib().navi_streams_step_out(self.h)
+
+    def step_out(self, n: int) -> np.ndarray:
+        return download(self.d_step_out, np.float32, n * self.hidden).reshape(n, self.hidden)
+
+    def taps(self, n: int):
+        """(post-norm hidden [n][H], raw logits [n][VT], cp logits [n][15][VC]) of the last run."""
+        L, p = lib(), self.params
+        ms, H, VT, VC = self.max_streams, self.hidden, p.talker.vocab, p.cp.vocab
+        hid = download(L.navi_streams_tap_hidden(self.h), np.float32, ms * H).reshape(ms, H)[:n]
+        lg = download(L.navi_streams_tap_logits(self.h), np.float32, ms * VT).reshape(ms, VT)[:n]
+        cp = download(L.navi_streams_tap_cp_logits(self.h), np.float32, ms * 15 * VC).reshape(ms, 15, VC)[:n]
+        return hid, lg, cp
+
+    def last_ms(self) -> float:
+        return lib().navi_streams_last_ms(self.h)
 
 
 # ---- talker: prompt rows + prefill ----------------------------------------------------
