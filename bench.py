@@ -105,6 +105,50 @@ def vocoder_flops_per_frame(kv: dict) -> float:
     return 2.0 * mac
 
 
+def multistream(W, kv: dict, abi, steps: int = 12, warmup: int = 3, n_streams: int = 32, ctx: int = 1024) -> dict:
+    """32 independent streams, each with its own f16 N(0,1) KV cache at
+    context 1024, advanced one frame per navi_streams_run (talker + code predictor as MFMA GEMMs
+    over the streams), top-k 50 with per-stream seeds 0..31. Every step reads the weights once and
+    every stream's KV once: bytes = weights + 32 x KV(1025 positions)."""
+    from navi_amd import blob
+    n_layer = kv["talker.num_hidden_layers"]
+    kvs = []
+    host = np.empty((ctx, 1024), np.uint16)
+    ri = blob._randinit()
+    for i in range(n_streams):
+        c = abi.KvCache(n_layer, ctx + 8, 1024)
+        for l in range(n_layer):
+            for which, dst in (("k", c.k[l]), ("v", c.v[l])):
+                ri.navi_fill_normal_f16(SEED, f"bench.kv.{i}.{l}.{which}".encode(), 1.0, host.ctypes.data, host.size)
+                abi.upload(dst, host)
+        kvs.append(c)
+    st = abi.Streams(W, max_streams=n_streams, max_positions=ctx + 8)
+    rng = np.random.default_rng(SEED)
+    step_in = abi.DeviceBuffer(4 * 1024 * n_streams)
+    step_in.upload(rng.standard_normal((n_streams, 1024)).astype(np.float32))
+    trail = abi.DeviceBuffer(4 * 1024 * n_streams)
+    trail.upload(np.zeros((n_streams, 1024), np.float32))
+    s = abi.Sampling.make(min_frames=10 ** 6)
+    seeds = list(range(n_streams))
+    n_past = [ctx] * n_streams
+    for i in range(warmup):
+        st.run(kvs, n_past, trail.ptr, s, seeds, [i] * n_streams, d_step_in=step_in.ptr if i == 0 else None)
+    dev, t0 = [], time.perf_counter()
+    for i in range(steps):
+        st.run(kvs, n_past, trail.ptr, s, seeds, [warmup + i] * n_streams)
+        dev.append(st.last_ms())
+    wall = (time.perf_counter() - t0) * 1e3 / steps
+    ms = float(np.mean(dev))
+    b = algorithmic_bytes(kv, ctx)
+    total = b["total"] - b["kv"] + n_streams * b["kv"]
+    gbs = total / (ms * 1e-3) / 1e9
+    return {"multistream": {"config": f"configs[4]: {n_streams} streams, KV f16 N(0,1) at context {ctx} each, "
+                                      "top-k 50, T 0.9, seeds 0..31",
+                            "streams": n_streams, "ms_per_step": round(ms, 3), "wall_ms_per_step": round(wall, 3),
+                            "frames_per_s": round(n_streams / (ms * 1e-3), 1), "bytes_per_step": int(total),
+                            "achieved_gbs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}}
+
+
 def streaming_and_vocoder(W, kv: dict, abi) -> dict:
     """BASELINE configs[2] (streaming utterance) through navi_synth and configs[3] (vocoder),
     plus the prefill times. The 128 text ids are prefilled with the prompt (130 rows: the
@@ -262,6 +306,10 @@ def main():
             print("[bench] prefill, streaming utterance and vocoder", flush=True, file=sys.stderr)
             extra = streaming_and_vocoder(W, kvd, abi)
             print(f"[bench] {json.dumps(extra)}", flush=True, file=sys.stderr)
+            print("[bench] multi-stream decode", flush=True, file=sys.stderr)
+            ms_ = multistream(W, kvd, abi)
+            print(f"[bench] {json.dumps(ms_)}", flush=True, file=sys.stderr)
+            extra.update(ms_)
         del frame, W, kv
         cpu = None
         if args.cpu_frames > 0:
