@@ -59,6 +59,10 @@ constexpr int MB_X = 0, MB_QKV = MB_X + 2 * H, MB_ATT = MB_QKV + 2 * QKV, MB_X2 
 // of 1024 words on MI355X: 2.5 us with one copy, 1.6 us with one per XCD). q/k/v, read by the
 // 16 attention blocks only, stays in copy 0.
 constexpr int NREP = 8;
+// Talker attention partials: NR key ranges per head, one AP_W-word chunk each ({o[128], max, sum,
+// padding}), single copy after the replicated mailboxes.
+constexpr int NR = NB / NH, AP_W = 144, MB_AP = NREP * MB_WORDS, MB_TOTAL = MB_AP + NH * NR * AP_W;
+static_assert(NR * AP_W % BT == 0 && AP_W > HD + 1, "partial chunk layout");
 
 // This wave's XCD (HW_REG_XCC_ID, a scalar register read): the mailbox copy it gathers from.
 __device__ __forceinline__ int xcc_copy() { return __builtin_amdgcn_s_getreg((3 << 11) | 20) & (NREP - 1); }
@@ -214,11 +218,11 @@ __device__ __forceinline__ bool poll_word(const Args &a, uint64_t *p, uint32_t t
 // the barrier; then every thread reads the whole vector once, re-polling only the
 // rare word whose tag is not yet visible. Polling N words from every thread instead
 // floods the coherent path: 4.9 us vs 2.8 us for N = 3072 on MI355X.
-template <int N, int CH>
+template <int N, int CH, bool REPL = true>
 __device__ __forceinline__ bool gather(const Args &a, int off, uint32_t tag, float *dst, Smem &S) {
     static_assert(N % BT == 0 && N % CH == 0, "gather size");
     constexpr int PER = N / BT, NPROD = N / CH;
-    uint64_t *const mb = sgpr_ptr(a.mb + xcc_copy() * MB_WORDS + off);
+    uint64_t *const mb = sgpr_ptr(a.mb + (REPL ? xcc_copy() * MB_WORDS : 0) + off);
     PROF_MARK(a, S);
     if (wave() == 0) {
         // every sentinel of this lane in flight at once; only the stale ones are read again
@@ -527,62 +531,66 @@ __device__ __forceinline__ void stage_kv(const uint16_t *Kc, const uint16_t *Vc,
     }
 }
 
-// Talker attention for q head h = blockIdx (one row at position pos): q/k head norms, RoPE,
-// f16 K/V store at pos (even heads), softmax over keys 0..pos and the V sum. Cached keys are
-// staged in LDS by DMA in KCH-key chunks, the first chunk while this step's q/k/v are in
-// flight; chunks combine with the running-max softmax (one chunk up to pos = KCH).
-__device__ bool talker_attention(const Args &a, const Ctx &cx, float qkw, int il, uint32_t tag_qkv, uint32_t tag_att, Smem &S) {
-    const int h = blk(), g = h / GRP, pos = a.n_past;      // cached keys 0..pos-1, the current key at pos
+// Talker attention, spread over all 256 blocks: block b takes q head h = b % NH and range
+// r = b / NH of the cached keys (NR ranges of ceil(pos / NR) keys; the current key at pos goes
+// to the last range, whose even-head block also writes the new f16 K/V row). A block stages its
+// range's K/V rows in LDS by DMA while this step's q/k/v are in flight, normalises and rotates
+// q (and the current k), runs a per-wave online softmax over its keys and publishes the range's
+// partial (max, sum, unnormalised V sum) as one AP_W-word chunk. Block h (range 0) gathers the NR
+// partials of head h, combines them in range order and publishes the head's output. The ranges
+// of a head sit on one XCD (block h + NH r), so the partial hop stays within its L2.
+__device__ bool talker_attention(const Args &a, const Ctx &cx, float qkw, int il, uint32_t tag_qkv, uint32_t tag_ap,
+                                 uint32_t tag_att, Smem &S) {
+    const int h = blk() % NH, r = blk() / NH, g = h / GRP, pos = a.n_past;
+    const int R = (pos + NR - 1) / NR, j0 = min(pos, r * R), n = max(0, min(pos, j0 + R) - j0);   // n <= KCH
+    const bool last = r == NR - 1;
     uint16_t *const Kbase = cx.kv[il], *const Vbase = cx.kv[MAX_TL + il];
     const uint16_t *Kc = Kbase + g * HD;
     uint16_t *Vc = Vbase + g * HD;
-    if (pos > 0) stage_kv(Kc, Vc, 0, min(pos, KCH), S);
+    if (n > 0) stage_kv(Kc, Vc, j0, n, S);
     PROF_MARK(a, S);
     S.nw[tid()] = qkw;                                     // published by gather_head's barrier
     if (!gather_head<1>(a, h, g, tag_qkv, S)) return false;
     PROF_MARK(a, S);
-    // Every wave, redundantly (no barrier): head RMSNorm and RoPE of q and of the current k with
-    // the pair (l, l + 64) in lane l, q copied to the wave's own LDS row for the score loop, the
-    // current key's score and value in registers; wave 0 of the even block of the kv group writes
-    // the new K/V row.
+    // Every wave, redundantly (no barrier): head RMSNorm and RoPE of q (and, in the last range, of
+    // the current k) with the pair (l, l + 64) in lane l, q copied to the wave's own LDS row for
+    // the score loop, the current key's score and value in registers.
     const int L = lane(), w = wave();
     float sn, cs;
     sincosf(static_cast<float>(pos) * S.invf[0][L], &sn, &cs);
-    float qa, qb, ka, kb;
+    float qa, qb;
     head_norm_pair(S.q[0], S.nw, a.eps_t, qa, qb);
-    head_norm_pair(S.k[0], S.nw + HD, a.eps_t, ka, kb);
     S.qw[w][L] = qa * cs - qb * sn;
     S.qw[w][L + HD / 2] = qa * sn + qb * cs;
-    const float kra = round_f16(ka * cs - kb * sn), krb = round_f16(ka * sn + kb * cs);
-    const float s_cur = wave_sum(fmaf(S.qw[w][L], kra, S.qw[w][L + HD / 2] * krb)) * ATT_SCALE;
-    const float vc0 = round_f16(S.v[0][2 * L]), vc1 = round_f16(S.v[0][2 * L + 1]);
-    if (w == 0 && (h & 1) == 0) {
-        uint16_t *kw = Kbase + static_cast<size_t>(pos) * KVD + g * HD;
-        gst(kw + L, f2h(kra));
-        gst(kw + L + HD / 2, f2h(krb));
-        uint16_t *vw = Vc + static_cast<size_t>(pos) * KVD;
-        gst(vw + 2 * L, f2h(vc0));
-        gst(vw + 2 * L + 1, f2h(vc1));
+    float s_cur = -INFINITY, vc0 = 0.f, vc1 = 0.f;
+    if (last) {
+        float ka, kb;
+        head_norm_pair(S.k[0], S.nw + HD, a.eps_t, ka, kb);
+        const float kra = round_f16(ka * cs - kb * sn), krb = round_f16(ka * sn + kb * cs);
+        s_cur = wave_sum(fmaf(S.qw[w][L], kra, S.qw[w][L + HD / 2] * krb)) * ATT_SCALE;
+        vc0 = round_f16(S.v[0][2 * L]);
+        vc1 = round_f16(S.v[0][2 * L + 1]);
+        if (w == 0 && (h & 1) == 0) {
+            uint16_t *kw = Kbase + static_cast<size_t>(pos) * KVD + g * HD;
+            gst(kw + L, f2h(kra));
+            gst(kw + L + HD / 2, f2h(krb));
+            uint16_t *vw = Vc + static_cast<size_t>(pos) * KVD;
+            gst(vw + 2 * L, f2h(vc0));
+            gst(vw + 2 * L + 1, f2h(vc1));
+        }
     }
+    wait_vm_all();
+    __syncthreads();                                       // every wave's part of the range has landed
     PROF_MARK(a, S);
-    // Per-wave online softmax over the wave's keys of each chunk (wave w: chunk rows w*64 .. w*64+63);
-    // wave 0 also takes the current key in the last chunk. Lane L owns value dims 2L, 2L + 1.
+    // Per-wave online softmax over the wave's keys (wave w: range rows w*64 .. w*64+63); wave 0 of
+    // the last range also takes the current key. Lane L owns value dims 2L, 2L + 1.
     float mw = -INFINITY, lw = 0.f, acc0 = 0.f, acc1 = 0.f;
     const int slot8 = 2 * (L & 3);
-    for (int c0 = 0; c0 < max(pos, 1); c0 += KCH) {
-        const int n = min(KCH, pos - c0);                  // cached keys in this chunk (may be 0)
-        const bool last = c0 + KCH >= pos;
-        if (c0 > 0) {
-            __syncthreads();                               // previous chunk fully consumed
-            stage_kv(Kc, Vc, c0, n, S);
-        }
-        wait_vm_all();
-        __syncthreads();                                   // every wave's part of the chunk has landed
-        PROF_MARK(a, S);
-        const int j0 = w * WAVE, cnt = max(0, min(WAVE, n - j0));
+    {
+        const int jw = w * WAVE, cnt = max(0, min(WAVE, n - jw));
         float sj = -INFINITY;
         if (L < cnt) {
-            const int jj = j0 + L;
+            const int jj = jw + L;
             float acc = 0.f;
 #pragma unroll
             for (int c = 0; c < HD / 8; ++c) {
@@ -594,47 +602,45 @@ __device__ bool talker_attention(const Args &a, const Ctx &cx, float qkw, int il
             sj = acc * ATT_SCALE;
         }
         const bool cur = last && w == 0;
-        float mn = fmaxf(mw, wave_max(sj));
+        float mn = wave_max(sj);
         if (cur) mn = fmaxf(mn, s_cur);
-        if (mn == -INFINITY) continue;                     // this wave has no key yet
-        const float e = L < cnt ? expf(sj - mn) : 0.f;
-        const float alpha = expf(mw - mn);                 // 0 while the wave had no key
-        const float ec = cur ? expf(s_cur - mn) : 0.f;
-        lw = lw * alpha + wave_sum(e) + ec;
-        acc0 = acc0 * alpha + ec * vc0;
-        acc1 = acc1 * alpha + ec * vc1;
-        mw = mn;
-        // V sum in groups of 8 keys: the 8 LDS reads are issued before the first FMA, and 2
-        // independent accumulator pairs halve the FMA chains (key j's weight: lane j's e)
-        float b0[2] = {acc0, 0.f}, b1[2] = {acc1, 0.f};
-        int j = 0;
-        for (; j + 8 <= cnt; j += 8) {
-            half2_t hv[8];
+        if (mn != -INFINITY) {
+            const float e = L < cnt ? expf(sj - mn) : 0.f;
+            const float ec = cur ? expf(s_cur - mn) : 0.f;
+            lw = wave_sum(e) + ec;
+            mw = mn;
+            // V sum in groups of 8 keys: the 8 LDS reads are issued before the first FMA, and 2
+            // independent accumulator pairs halve the FMA chains (key j's weight: lane j's e)
+            float b0[2] = {ec * vc0, 0.f}, b1[2] = {ec * vc1, 0.f};
+            int j = 0;
+            for (; j + 8 <= cnt; j += 8) {
+                half2_t hv[8];
 #pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                const int jj = j0 + j + u;
-                __builtin_memcpy(&hv[u], &S.u.tkv.v[jj][((L >> 2) ^ (jj & 15)) * 8 + slot8], 4);
-            }
+                for (int u = 0; u < 8; ++u) {
+                    const int jj = jw + j + u;
+                    __builtin_memcpy(&hv[u], &S.u.tkv.v[jj][((L >> 2) ^ (jj & 15)) * 8 + slot8], 4);
+                }
 #pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                const float p = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), j + u));
-                b0[u & 1] = fmaf(p, static_cast<float>(hv[u][0]), b0[u & 1]);
-                b1[u & 1] = fmaf(p, static_cast<float>(hv[u][1]), b1[u & 1]);
+                for (int u = 0; u < 8; ++u) {
+                    const float p = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), j + u));
+                    b0[u & 1] = fmaf(p, static_cast<float>(hv[u][0]), b0[u & 1]);
+                    b1[u & 1] = fmaf(p, static_cast<float>(hv[u][1]), b1[u & 1]);
+                }
             }
+            for (; j < cnt; ++j) {
+                const int jj = jw + j;
+                const float p = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), j));
+                half2_t hv;
+                __builtin_memcpy(&hv, &S.u.tkv.v[jj][((L >> 2) ^ (jj & 15)) * 8 + slot8], 4);
+                b0[0] = fmaf(p, static_cast<float>(hv[0]), b0[0]);
+                b1[0] = fmaf(p, static_cast<float>(hv[1]), b1[0]);
+            }
+            acc0 = b0[0] + b0[1];
+            acc1 = b1[0] + b1[1];
         }
-        for (; j < cnt; ++j) {
-            const int jj = j0 + j;
-            const float p = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), j));
-            half2_t hv;
-            __builtin_memcpy(&hv, &S.u.tkv.v[jj][((L >> 2) ^ (jj & 15)) * 8 + slot8], 4);
-            b0[0] = fmaf(p, static_cast<float>(hv[0]), b0[0]);
-            b1[0] = fmaf(p, static_cast<float>(hv[1]), b1[0]);
-        }
-        acc0 = b0[0] + b0[1];
-        acc1 = b1[0] + b1[1];
     }
     PROF_MARK(a, S);
-    // combine the four waves' (max, sum, accumulator) and publish o / l
+    // the four waves' (max, sum, accumulator) -> the range's partial, published as one chunk
     if (L == 0) {
         S.red[w] = mw;
         S.red[NW + w] = lw;
@@ -642,22 +648,53 @@ __device__ bool talker_attention(const Args &a, const Ctx &cx, float qkw, int il
     S.opart[w][2 * L] = acc0;
     S.opart[w][2 * L + 1] = acc1;
     __syncthreads();
-    float M = S.red[0];
+    {
+        float M = S.red[0];
 #pragma unroll
-    for (int i = 1; i < NW; ++i) M = fmaxf(M, S.red[i]);
-    float sc[NW], den = 0.f;
+        for (int i = 1; i < NW; ++i) M = fmaxf(M, S.red[i]);
+        float sc[NW], den = 0.f;
 #pragma unroll
-    for (int i = 0; i < NW; ++i) {
-        sc[i] = S.red[i] == -INFINITY ? 0.f : expf(S.red[i] - M);
-        den = fmaf(S.red[NW + i], sc[i], den);
+        for (int i = 0; i < NW; ++i) {
+            sc[i] = S.red[i] == -INFINITY ? 0.f : expf(S.red[i] - M);
+            den = fmaf(S.red[NW + i], sc[i], den);
+        }
+        uint64_t *ap = a.mb + MB_AP + (h * NR + r) * AP_W;
+        for (int i = tid(); i < AP_W; i += BT) {
+            float v = 0.f;
+            if (i < HD) {
+#pragma unroll
+                for (int k = 0; k < NW; ++k) v = fmaf(S.opart[k][i], sc[k], v);
+            } else if (i == HD) {
+                v = M;
+            } else if (i == HD + 1) {
+                v = den;
+            }
+            mb_put(ap + i, v, tag_ap);
+        }
     }
-    const float inv = 1.f / den;
-    for (int i = tid(); i < HD * NREP; i += BT) {      // one (value, copy) per iteration
-        const int d = i % HD, r = i / HD;
-        float o = 0.f;
+    PROF_MARK(a, S);
+    if (r != 0) return true;
+    // combine head h's NR partials in range order: out = sum_r o_r e^(m_r - M) / sum_r l_r e^(m_r - M)
+    float *P = S.u.m.big;
+    if (!gather<NR * AP_W, AP_W, false>(a, MB_AP + h * NR * AP_W, tag_ap, P, S)) return false;
+    if (tid() < HD) {
+        float M = -INFINITY;
 #pragma unroll
-        for (int k = 0; k < NW; ++k) o = fmaf(S.opart[k][d], sc[k], o);
-        mb_put(a.mb + r * MB_WORDS + MB_ATT + h * HD + d, o * inv, tag_att);
+        for (int k = 0; k < NR; ++k) M = fmaxf(M, P[k * AP_W + HD]);
+        float num = 0.f, den = 0.f;
+#pragma unroll
+        for (int k = 0; k < NR; ++k) {
+            const float mk = P[k * AP_W + HD];
+            const float wk = mk == -INFINITY ? 0.f : expf(mk - M);
+            den = fmaf(P[k * AP_W + HD + 1], wk, den);
+            num = fmaf(P[k * AP_W + tid()], wk, num);
+        }
+        S.opart[0][tid()] = num / den;
+    }
+    __syncthreads();
+    for (int i = tid(); i < HD * NREP; i += BT) {      // one (value, copy) per iteration
+        const int d = i % HD, c = i / HD;
+        mb_put(a.mb + c * MB_WORDS + MB_ATT + h * HD + d, S.opart[0][d], tag_att);
     }
     PROF_MARK(a, S);
     return true;
@@ -781,12 +818,12 @@ __device__ __forceinline__ bool run_layer(const Args &a, const Ctx &cx, Regs &R,
     const float qkw = R.qkw;     // this layer's q/k norm weight; the prefetch below replaces it
     if (has_next) load_qkv(R, N);
 
+    const uint32_t t_ap = TALKER ? seq.next() : 0u;
     const uint32_t t_att = seq.next();
-    if (blk() < NH) {
-        bool ok;
-        if constexpr (TALKER) ok = talker_attention(a, cx, qkw, gi, t_qkv, t_att, S);
-        else ok = cp_attention<T>(a, qkw, (gi - a.n_tl) % a.n_cl, p0, t_qkv, t_att, S);
-        if (!ok) return false;
+    if constexpr (TALKER) {
+        if (!talker_attention(a, cx, qkw, gi, t_qkv, t_ap, t_att, S)) return false;
+    } else if (blk() < NH) {
+        if (!cp_attention<T>(a, qkw, (gi - a.n_tl) % a.n_cl, p0, t_qkv, t_att, S)) return false;
     }
     if (!gather_rows<T, QD, HD>(a, MB_ATT, t_att, S.u.m.big, S)) return false;
     const uint32_t t_x2 = seq.next();
@@ -1101,7 +1138,7 @@ navi_status navi_frame_create(const navi_model_params *p, const navi_tensor_ref 
     w.eps_c = p->cp.rms_eps;
 
     if ((st = f->alloc(f->dw, 1, err, errlen)) != NAVI_OK) return fail(st);
-    if ((st = f->alloc(f->mb, static_cast<size_t>(MB_WORDS) * NREP, err, errlen)) != NAVI_OK) return fail(st);
+    if ((st = f->alloc(f->mb, static_cast<size_t>(MB_TOTAL), err, errlen)) != NAVI_OK) return fail(st);
     if ((st = f->alloc(f->ctl, 32, err, errlen)) != NAVI_OK) return fail(st);
     if ((st = f->alloc(f->step_out, H, err, errlen)) != NAVI_OK) return fail(st);
     if ((st = f->alloc(f->seen, VT, err, errlen)) != NAVI_OK) return fail(st);
