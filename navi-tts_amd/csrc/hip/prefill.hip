@@ -353,12 +353,13 @@ __global__ void __launch_bounds__(BT) k_assemble_rows(const float *A, const floa
 
 int tiles_m(int M) { return M <= 16 ? 1 : M <= 32 ? 2 : M <= 48 ? 3 : 4; }
 
-// Number of K splits: enough blocks to cover the 256 CUs about twice, K / S a multiple of 32.
+// Number of K splits: enough blocks to cover the 256 CUs (at most 384), each split at least 256
+// deep (a block's weight stream and staging amortise its fixed cost), K / S a multiple of 32.
 int pick_splits(int M, int K, int N) {
     const int mt = tiles_m(M);
     const int blocks = (N / 64) * ((M + 16 * mt - 1) / (16 * mt));
     int s = 1;
-    while (s * 2 * blocks <= 512 && (K / 32) % (s * 2) == 0 && K / (s * 2) >= 64) s *= 2;
+    while (s * 2 * blocks <= 384 && (K / 32) % (s * 2) == 0 && K / (s * 2) >= 256) s *= 2;
     return s;
 }
 

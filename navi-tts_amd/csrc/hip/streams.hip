@@ -126,21 +126,21 @@ __global__ void __launch_bounds__(BT) k_st_attn(const float *q, const StreamMeta
     const float s0 = wave_sum(e0), s1 = wave_sum(e1);
     __syncthreads();                                      // red reads done, probabilities published
     if (l == 0) { red[0][wv] = s0; red[1][wv] = s1; }
-    // V: wave w sums keys j = w, w + 4, ...; lane l owns dims 2l, 2l + 1 of both heads
+    // V: wave w sums keys w * 64 .. w * 64 + 63 of the range, all 64 rows' loads in flight at
+    // once; lane l owns dims 2l, 2l + 1 of both heads
     float a00 = 0.f, a01 = 0.f, a10 = 0.f, a11 = 0.f;
-    const uint16_t *vp = vb + static_cast<size_t>(j0) * KVD + 2 * l;
-    for (int jb = wv; jb < cnt; jb += NW * 8) {
-        uint32_t vv[8];
+    {
+        constexpr int KW = KPS / NW;
+        const int jw = wv * KW, nw = max(0, min(KW, cnt - jw));
+        const uint16_t *vp = vb + static_cast<size_t>(j0 + jw) * KVD + 2 * l;
+        uint32_t vv[KW];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            const int j = jb + NW * u;
-            vv[u] = j < cnt ? gld(reinterpret_cast<const uint32_t *>(vp + static_cast<size_t>(j) * KVD)) : 0u;
-        }
+        for (int u = 0; u < KW; ++u)
+            vv[u] = u < nw ? gld(reinterpret_cast<const uint32_t *>(vp + static_cast<size_t>(u) * KVD)) : 0u;
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            const int j = jb + NW * u;
-            if (j < cnt) {
-                const float p0 = sc[0][j], p1 = sc[1][j];
+        for (int u = 0; u < KW; ++u) {
+            if (u < nw) {
+                const float p0 = sc[0][jw + u], p1 = sc[1][jw + u];
                 const float v0 = h2f(static_cast<uint16_t>(vv[u])), v1 = h2f(static_cast<uint16_t>(vv[u] >> 16));
                 a00 = fmaf(p0, v0, a00);
                 a01 = fmaf(p0, v1, a01);
