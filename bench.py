@@ -301,6 +301,15 @@ def main():
         gbs = b["total"] / (dev_ms * 1e-3) / 1e9
         print(f"[bench] device ms/frame mean {dev_ms:.4f} median {np.median(dev)/1e3:.4f} min {dev.min()/1e3:.4f}; "
               f"wall {wall_ms:.4f} ms/frame; {gbs:.0f} GB/s over {b['total']/1e9:.4f} GB", flush=True, file=sys.stderr)
+        # the same frames as one on-device loop (navi_frame_run_many): no host round trip per frame
+        pad = trail.ptr
+        t0 = time.perf_counter()
+        codes, _, loop_us = frame.run_many(kv, N_PAST, trail.ptr, 0, pad, s, 2, args.warmup, args.steps)
+        abi.lib().navi_device_synchronize()
+        loop_wall = (time.perf_counter() - t0) * 1e3 / args.steps
+        loop = {"frames": int(len(codes)), "n_past": f"{N_PAST}..{N_PAST + args.steps - 1}",
+                "device_ms_per_frame": round(loop_us / 1e3 / args.steps, 4), "wall_ms_per_frame": round(loop_wall, 4)}
+        print(f"[bench] frame loop: {json.dumps(loop)}", flush=True, file=sys.stderr)
         extra = None
         if not args.no_streaming:
             print("[bench] prefill, streaming utterance and vocoder", flush=True, file=sys.stderr)
@@ -328,6 +337,7 @@ def main():
                          "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
                          "bytes_per_frame": b["total"], "kernel": "k_frame"},
             "cpu_baseline": cpu,
+            "frame_loop": loop,
         }
         if extra:
             line.update(extra)

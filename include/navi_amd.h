@@ -149,6 +149,20 @@ navi_status navi_frame_reset(navi_frame *f);
 navi_status navi_frame_run(navi_frame *f, const navi_kv_view *kv, int32_t n_past, int32_t skip_talker,
                            const float *d_hidden, const float *d_logits, const float *d_trailing,
                            const navi_sampling *s, uint64_t seed, int32_t frame_index, navi_frame_result *out);
+/* The on-device frame loop (the "next" step after Frame::run: graph.cpp:90-105 calls run once per
+ * frame and syncs on each): up to n_frames frames enqueued back to back, no host round trip between
+ * them. Frame i runs as navi_frame_run would with frame index frame_index0 + i, trailing row i of
+ * d_trailing (n_trailing rows of f32 [hidden]) then d_tts_pad, the same seeds; with skip_first,
+ * frame 0 is run_first from d_hidden / d_logits, else frame i is a talker step at n_past0 + i
+ * (writing KV row n_past0 + i). A frame that samples EOS ends the loop on the device (it is
+ * counted: *eos = 1, its codes are the last row); a timed-out frame ends it with
+ * NAVI_ERR_TIMEOUT. codes_out: host i32 [n_frames][16], the first *n_done rows valid; *us: device
+ * time of the whole loop (may be NULL). n_frames <= 4096. */
+navi_status navi_frame_run_many(navi_frame *f, const navi_kv_view *kv, int32_t n_past0, int32_t skip_first,
+                                const float *d_hidden, const float *d_logits, const float *d_trailing, int32_t n_trailing,
+                                const float *d_tts_pad, const navi_sampling *s, uint64_t seed, int32_t frame_index0,
+                                int32_t n_frames, int32_t *codes_out, int32_t *n_done, int32_t *eos, double *us, char *err,
+                                size_t errlen);
 /* Frame::d_step_out (frame.hip:812): next frame's step embedding, f32[hidden]. */
 float *navi_frame_step_out(navi_frame *f);
 int32_t navi_frame_grid_blocks(const navi_frame *f);

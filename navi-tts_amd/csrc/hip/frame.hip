@@ -41,6 +41,7 @@ constexpr int QD = NH * HD, KVD = NKV * HD, QKV = QD + 2 * KVD;
 constexpr int NCB = 16, CPH = NCB - 1, GRP = NH / NKV;
 constexpr int MAX_TL = 32, MAX_CL = 5;
 constexpr int MAX_POS = 4096;          // talker KV positions a frame may attend over
+constexpr int MAX_RUN = 4096;          // frames per navi_frame_run_many call
 constexpr int KCH = 256;               // talker K/V rows staged in LDS per chunk
 constexpr float ATT_SCALE = 0.08838834764831845f;   // 1/sqrt(128)
 
@@ -97,6 +98,7 @@ struct Args {
     uint32_t epoch;
     float *tap_hidden, *tap_logits, *tap_cp_logits;
     uint64_t *prof;       // per block [PROF_SLOTS] s_memrealtime stamps (null: off)
+    uint32_t *stop;       // frame loop: nonzero = an earlier frame of the loop ended it (null: single frame)
 };
 
 // This block's slice of one layer (and of the heads), 160 registers per lane:
@@ -199,12 +201,19 @@ __device__ __forceinline__ float block_max(float v, Smem &S) {
 
 __device__ __forceinline__ bool aborted(const Args &a) { return ctl_peek(a.abort_word) == a.epoch; }
 
+// The first wait over its spin cap: every other wait of this launch gives up, and a frame loop
+// runs no further frame.
+__device__ __forceinline__ void abort_frame(const Args &a) {
+    ctl_put(a.abort_word, a.epoch);
+    if (a.stop) ctl_put(a.stop, 2u);
+}
+
 // Polls one word until it carries `tag`; false on spin cap or abort.
 __device__ __forceinline__ bool poll_word(const Args &a, uint64_t *p, uint32_t tag, uint64_t &w) {
     uint64_t spins = 0;
     while (tag_of(w) != tag) {
         if (++spins >= a.spin_cap || ((spins & 63u) == 0 && aborted(a))) {
-            ctl_put(a.abort_word, a.epoch);
+            abort_frame(a);
             return false;
         }
         w = mb_peek(p);
@@ -241,7 +250,7 @@ __device__ __forceinline__ bool gather(const Args &a, int off, uint32_t tag, flo
             for (int q = 0; q < NQ; ++q) done &= tag_of(sw[q]) == tag;
             if (done) break;
             if (++spins >= a.spin_cap || ((spins & 63u) == 0 && aborted(a))) {
-                ctl_put(a.abort_word, a.epoch);
+                abort_frame(a);
                 ok = false;
                 break;
             }
@@ -855,6 +864,9 @@ __device__ __forceinline__ void load_row_f16(const uint16_t *src, float *dst) {
 
 __global__ void __launch_bounds__(BT, 1) k_frame(Args a, const Weights *__restrict__ Wp, uint16_t *const *__restrict__ kvp) {
     __shared__ Smem S;
+    // frame loop: an earlier frame (a finished launch, so every block reads the same word) sampled
+    // EOS or timed out; this frame does not run
+    if (a.stop && ctl_peek(a.stop) != 0u) return;
     if (tid() == 0) { S.fail = 0; S.prof_i = 0; }
     const Ctx cx{Wp, kvp};
     const Weights &W = *Wp;
@@ -988,6 +1000,7 @@ __global__ void __launch_bounds__(BT, 1) k_frame(Args a, const Weights *__restri
     if (blk() == 0 && tid() == 0) {
         for (int c = 0; c < NCB; ++c) gst(a.codes_out + c, static_cast<int32_t>(S.codes[c]));
         if (S.codes[0] != a.eos_id) gst(a.seen + S.codes[0], static_cast<uint8_t>(1u));
+        else if (a.stop) ctl_put(a.stop, 1u);
     }
 }
 
@@ -1021,6 +1034,8 @@ struct navi_frame {
     bool taps = false;
     uint16_t **kv_dev = nullptr;   // [2][MAX_TL] per-layer K/V pointers as the kernel reads them
     uint64_t *prof = nullptr;      // [NB][PROF_SLOTS] when profiling is on
+    int32_t *run_codes = nullptr;  // frame loop: [MAX_RUN][16] codes of each frame
+    uint32_t *stop = nullptr;      // frame loop: 1 = EOS sampled, 2 = a frame timed out
     uint16_t *kv_host[2][MAX_TL] = {};
     uint32_t epoch = 0;
     int grid = NB, occ = 0;
@@ -1140,6 +1155,8 @@ navi_status navi_frame_create(const navi_model_params *p, const navi_tensor_ref 
     if ((st = f->alloc(f->dw, 1, err, errlen)) != NAVI_OK) return fail(st);
     if ((st = f->alloc(f->mb, static_cast<size_t>(MB_TOTAL), err, errlen)) != NAVI_OK) return fail(st);
     if ((st = f->alloc(f->ctl, 32, err, errlen)) != NAVI_OK) return fail(st);
+    if ((st = f->alloc(f->run_codes, static_cast<size_t>(MAX_RUN) * NCB, err, errlen)) != NAVI_OK) return fail(st);
+    if ((st = f->alloc(f->stop, 1, err, errlen)) != NAVI_OK) return fail(st);
     if ((st = f->alloc(f->step_out, H, err, errlen)) != NAVI_OK) return fail(st);
     if ((st = f->alloc(f->seen, VT, err, errlen)) != NAVI_OK) return fail(st);
     if ((st = f->alloc(f->tap, H + VT + CPH * VC, err, errlen)) != NAVI_OK) return fail(st);
@@ -1199,43 +1216,41 @@ float *navi_frame_step_out(navi_frame *f) { return f ? f->step_out : nullptr; }
 int32_t navi_frame_grid_blocks(const navi_frame *f) { return f ? f->grid : 0; }
 int32_t navi_frame_occupancy_per_mp(const navi_frame *f) { return f ? f->occ : 0; }
 
-navi_status navi_frame_run(navi_frame *f, const navi_kv_view *kv, int32_t n_past, int32_t skip_talker,
-                           const float *d_hidden, const float *d_logits, const float *d_trailing,
-                           const navi_sampling *s, uint64_t seed, int32_t frame_index, navi_frame_result *out) {
-    if (!out) return NAVI_ERR_INVALID;
-    std::memset(out, 0, sizeof(*out));
-    auto fail = [&](navi_status st, const char *msg) {
-        out->ok = 0;
-        out->status = st;
-        std::snprintf(out->error, sizeof(out->error), "%s", msg);
-        return st;
-    };
-    if (!f || !s || !d_trailing) return fail(NAVI_ERR_INVALID, "frame: null argument");
-    Args a{};
-    if (skip_talker) {
-        if (!d_hidden || !d_logits) return fail(NAVI_ERR_INVALID, "frame: run_first needs the prefill's hidden and logits");
-        a.hidden_in = d_hidden;
-        a.logits_in = d_logits;
-    } else {
-        if (!kv || !kv->k || !kv->v) return fail(NAVI_ERR_INVALID, "frame: run needs a KV cache");
-        if (n_past >= kv->max_pos || n_past >= MAX_POS) return fail(NAVI_ERR_KV_FULL, "KV cache full");
-        if (n_past < 0) return fail(NAVI_ERR_INVALID, "frame: negative n_past");
-        if (kv->n_layer != f->p.talker.n_layer || kv->kv_dim != KVD) return fail(NAVI_ERR_INVALID, "KV cache layer count mismatch");
-        bool same = true;
-        for (int l = 0; l < kv->n_layer; ++l) same = same && f->kv_host[0][l] == kv->k[l] && f->kv_host[1][l] == kv->v[l];
-        if (!same) {
-            for (int l = 0; l < kv->n_layer; ++l) { f->kv_host[0][l] = kv->k[l]; f->kv_host[1][l] = kv->v[l]; }
-            if (hipMemcpyAsync(f->kv_dev, f->kv_host, sizeof(f->kv_host), hipMemcpyHostToDevice, device_state().stream) != hipSuccess)
-                return fail(NAVI_ERR_HIP, "frame: KV pointer upload failed");
-            if (hipStreamSynchronize(device_state().stream) != hipSuccess) return fail(NAVI_ERR_HIP, "frame: KV pointer upload failed");
+} // extern "C"
+
+namespace {
+
+// KV view checks for frames up to n_past_max, and the per-layer pointer table upload when the
+// cache changed (frame.hip:787-810 run's checks). msg: the reference's error text on failure.
+navi_status frame_kv(navi_frame *f, const navi_kv_view *kv, int n_past_min, int n_past_max, const char *&msg) {
+    if (!kv || !kv->k || !kv->v) { msg = "frame: run needs a KV cache"; return NAVI_ERR_INVALID; }
+    if (n_past_max >= kv->max_pos || n_past_max >= MAX_POS) { msg = "KV cache full"; return NAVI_ERR_KV_FULL; }
+    if (n_past_min < 0) { msg = "frame: negative n_past"; return NAVI_ERR_INVALID; }
+    if (kv->n_layer != f->p.talker.n_layer || kv->kv_dim != KVD) { msg = "KV cache layer count mismatch"; return NAVI_ERR_INVALID; }
+    bool same = true;
+    for (int l = 0; l < kv->n_layer; ++l) same = same && f->kv_host[0][l] == kv->k[l] && f->kv_host[1][l] == kv->v[l];
+    if (!same) {
+        for (int l = 0; l < kv->n_layer; ++l) { f->kv_host[0][l] = kv->k[l]; f->kv_host[1][l] = kv->v[l]; }
+        if (hipMemcpyAsync(f->kv_dev, f->kv_host, sizeof(f->kv_host), hipMemcpyHostToDevice, device_state().stream) != hipSuccess ||
+            hipStreamSynchronize(device_state().stream) != hipSuccess) {
+            msg = "frame: KV pointer upload failed";
+            return NAVI_ERR_HIP;
         }
     }
+    return NAVI_OK;
+}
 
+// The launch arguments of one frame (Impl::launch, frame.hip:653-681: per-frame seeds, a new epoch).
+Args frame_args(navi_frame *f, int n_past, bool skip_talker, const float *d_hidden, const float *d_logits,
+                const float *d_trailing, const navi_sampling *s, uint64_t seed, int frame_index, int32_t *codes_out) {
+    Args a{};
+    a.hidden_in = skip_talker ? d_hidden : nullptr;
+    a.logits_in = skip_talker ? d_logits : nullptr;
     a.mb = f->mb;
     a.eps_t = f->p.talker.rms_eps;
     a.eps_c = f->p.cp.rms_eps;
     a.abort_word = f->ctl + NCB;
-    a.codes_out = reinterpret_cast<int32_t *>(f->ctl);
+    a.codes_out = codes_out;
     a.n_tl = f->p.talker.n_layer;
     a.n_cl = f->p.cp.n_layer;
     a.n_past = n_past;
@@ -1265,12 +1280,45 @@ navi_status navi_frame_run(navi_frame *f, const navi_kv_view *kv, int32_t n_past
         a.tap_logits = f->tap + H;
         a.tap_cp_logits = f->tap + H + VT;
     }
-    hipStream_t st = device_state().stream;
-    if (hipEventRecord(f->ev0, st) != hipSuccess) return fail(NAVI_ERR_HIP, "frame: hipEventRecord failed");
+    return a;
+}
+
+hipError_t frame_launch(navi_frame *f, Args &a) {
     const Weights *wp = f->dw;
     uint16_t *const *kvp = f->kv_dev;
     void *args[] = {&a, &wp, &kvp};
-    const hipError_t e = hipLaunchCooperativeKernel(reinterpret_cast<const void *>(k_frame), dim3(f->grid), dim3(BT), args, 0, st);
+    return hipLaunchCooperativeKernel(reinterpret_cast<const void *>(k_frame), dim3(f->grid), dim3(BT), args, 0,
+                                      device_state().stream);
+}
+
+} // namespace
+
+extern "C" {
+
+navi_status navi_frame_run(navi_frame *f, const navi_kv_view *kv, int32_t n_past, int32_t skip_talker,
+                           const float *d_hidden, const float *d_logits, const float *d_trailing,
+                           const navi_sampling *s, uint64_t seed, int32_t frame_index, navi_frame_result *out) {
+    if (!out) return NAVI_ERR_INVALID;
+    std::memset(out, 0, sizeof(*out));
+    auto fail = [&](navi_status st, const char *msg) {
+        out->ok = 0;
+        out->status = st;
+        std::snprintf(out->error, sizeof(out->error), "%s", msg);
+        return st;
+    };
+    if (!f || !s || !d_trailing) return fail(NAVI_ERR_INVALID, "frame: null argument");
+    if (skip_talker) {
+        if (!d_hidden || !d_logits) return fail(NAVI_ERR_INVALID, "frame: run_first needs the prefill's hidden and logits");
+    } else {
+        const char *msg = nullptr;
+        const navi_status st = frame_kv(f, kv, n_past, n_past, msg);
+        if (st != NAVI_OK) return fail(st, msg);
+    }
+    Args a = frame_args(f, n_past, skip_talker != 0, d_hidden, d_logits, d_trailing, s, seed, frame_index,
+                        reinterpret_cast<int32_t *>(f->ctl));
+    hipStream_t st = device_state().stream;
+    if (hipEventRecord(f->ev0, st) != hipSuccess) return fail(NAVI_ERR_HIP, "frame: hipEventRecord failed");
+    const hipError_t e = frame_launch(f, a);
     if (e != hipSuccess) {
         std::string m = std::string("cooperative launch failed: ") + hipGetErrorString(e);
         return fail(NAVI_ERR_LAUNCH, m.c_str());
@@ -1287,6 +1335,82 @@ navi_status navi_frame_run(navi_frame *f, const navi_kv_view *kv, int32_t n_past
     out->eos = out->codes[0] == f->p.codec_eos_id;
     out->ok = 1;
     out->status = NAVI_OK;
+    return NAVI_OK;
+}
+
+navi_status navi_frame_run_many(navi_frame *f, const navi_kv_view *kv, int32_t n_past0, int32_t skip_first,
+                                const float *d_hidden, const float *d_logits, const float *d_trailing, int32_t n_trailing,
+                                const float *d_tts_pad, const navi_sampling *s, uint64_t seed, int32_t frame_index0,
+                                int32_t n_frames, int32_t *codes_out, int32_t *n_done, int32_t *eos, double *us, char *err,
+                                size_t errlen) {
+    if (!f || !s || !codes_out || !n_done || (!d_trailing && n_trailing > 0) || !d_tts_pad || n_trailing < 0) {
+        set_err(err, errlen, "frame: null argument");
+        return NAVI_ERR_INVALID;
+    }
+    *n_done = 0;
+    if (eos) *eos = 0;
+    if (us) *us = 0.0;
+    if (n_frames < 1 || n_frames > MAX_RUN) {
+        set_err(err, errlen, "frame: %d frames per loop, 1..%d allowed", n_frames, MAX_RUN);
+        return NAVI_ERR_INVALID;
+    }
+    if (skip_first && (!d_hidden || !d_logits)) {
+        set_err(err, errlen, "frame: run_first needs the prefill's hidden and logits");
+        return NAVI_ERR_INVALID;
+    }
+    const int first_talker = skip_first ? 1 : 0;
+    if (first_talker < n_frames) {
+        const char *msg = nullptr;
+        const navi_status st = frame_kv(f, kv, n_past0 + first_talker, n_past0 + n_frames - 1, msg);
+        if (st != NAVI_OK) {
+            set_err(err, errlen, "%s", msg);
+            return st;
+        }
+    }
+    hipStream_t st = device_state().stream;
+    const uint32_t e0 = f->epoch;
+    NAVI_TRY_HIP(hipMemsetAsync(f->stop, 0, sizeof(uint32_t), st), err, errlen);
+    NAVI_TRY_HIP(hipEventRecord(f->ev0, st), err, errlen);
+    for (int i = 0; i < n_frames; ++i) {
+        const bool skip = skip_first && i == 0;
+        const float *trail = i < n_trailing ? d_trailing + static_cast<size_t>(i) * H : d_tts_pad;
+        Args a = frame_args(f, skip ? 0 : n_past0 + i, skip, d_hidden, d_logits, trail, s, seed, frame_index0 + i,
+                            f->run_codes + static_cast<size_t>(i) * NCB);
+        a.stop = f->stop;
+        const hipError_t e = frame_launch(f, a);
+        if (e != hipSuccess) {
+            (void) hipStreamSynchronize(st);
+            set_err(err, errlen, "cooperative launch failed: %s", hipGetErrorString(e));
+            return NAVI_ERR_LAUNCH;
+        }
+    }
+    uint32_t ctl[NCB + 1] = {}, stop = 0;
+    NAVI_TRY_HIP(hipEventRecord(f->ev1, st), err, errlen);
+    NAVI_TRY_HIP(hipMemcpyAsync(codes_out, f->run_codes, static_cast<size_t>(n_frames) * NCB * sizeof(int32_t),
+                                hipMemcpyDeviceToHost, st), err, errlen);
+    NAVI_TRY_HIP(hipMemcpyAsync(ctl, f->ctl, sizeof(ctl), hipMemcpyDeviceToHost, st), err, errlen);
+    NAVI_TRY_HIP(hipMemcpyAsync(&stop, f->stop, sizeof(stop), hipMemcpyDeviceToHost, st), err, errlen);
+    NAVI_TRY_HIP(hipStreamSynchronize(st), err, errlen);
+    float ms = 0.f;
+    (void) hipEventElapsedTime(&ms, f->ev0, f->ev1);
+    if (us) *us = ms * 1000.0;
+    // a timed-out frame stamped its epoch (one of this loop's) and stopped the loop
+    const uint32_t aw = ctl[NCB];
+    if (stop == 2u || (aw - e0 - 1u) < static_cast<uint32_t>(n_frames) * EPOCH_STRIDE) {
+        const int bad = static_cast<int>((aw - e0) / EPOCH_STRIDE) - 1;
+        *n_done = bad > 0 ? bad : 0;
+        set_err(err, errlen, "frame %d: frame dataflow wait timed out: the persistent grid could not run to completion",
+                frame_index0 + *n_done);
+        return NAVI_ERR_TIMEOUT;
+    }
+    int done = n_frames;
+    for (int i = 0; i < n_frames; ++i)
+        if (codes_out[static_cast<size_t>(i) * NCB] == f->p.codec_eos_id) {
+            done = i + 1;
+            if (eos) *eos = 1;
+            break;
+        }
+    *n_done = done;
     return NAVI_OK;
 }
 

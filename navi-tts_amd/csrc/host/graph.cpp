@@ -88,25 +88,42 @@ extern "C" navi_status navi_synth(navi_talker *t, navi_frame *f, navi_vocoder *v
         if (on_pcm) on_pcm(pcm.data(), static_cast<int32_t>(pcm.size()), user);
         return NAVI_OK;
     };
-    for (int i = 0; i < req->max_frames; ++i) {
-        const float *trailing = i < pr.n_trailing ? pr.trailing + static_cast<size_t>(i) * H : pr.tts_pad;
-        navi_frame_result r{};
-        if (i == 0)
-            navi_frame_run(f, nullptr, 0, 1, navi_talker_hidden(t), navi_talker_logits(t), trailing, &req->sampling, req->seed, 0, &r);
-        else
-            navi_frame_run(f, &kv, pr.n_prefill + i - 1, 0, nullptr, nullptr, trailing, &req->sampling, req->seed, i, &r);
-        if (!r.ok) {
-            put_err(err, errlen, "frame %d: %s", i, r.error);
-            return r.status != NAVI_OK ? static_cast<navi_status>(r.status) : NAVI_ERR_HIP;
+    // Frames run in on-device loops of exactly the vocoder's batch sizes (first batch, then
+    // vocoder_batch): no host round trip between the frames of a batch, the same PCM batches the
+    // reference's per-frame loop produces.
+    std::vector<int32_t> batch_codes(static_cast<size_t>(std::max(batch, first)) * 16);
+    for (int i = 0; i < req->max_frames && !stats->eos;) {
+        // the flush below empties pending; a loop never crosses the end of the KV cache, so a full
+        // cache fails at the frame that hits it, after the frames before it were delivered
+        const int fit = kv.max_pos - (pr.n_prefill - 1 + i);
+        const int want = std::max(1, std::min({i == 0 ? first : batch, req->max_frames - i, fit}));
+        const int n_trail_left = std::max(0, pr.n_trailing - i);
+        int32_t done = 0, eos = 0;
+        double us = 0.0;
+        // global frame g >= 1 runs at n_prefill + g - 1; frame 0 is run_first from the prefill's outputs
+        const navi_status s = navi_frame_run_many(f, &kv, pr.n_prefill - 1 + i, i == 0 ? 1 : 0,
+                                                  navi_talker_hidden(t), navi_talker_logits(t),
+                                                  n_trail_left ? pr.trailing + static_cast<size_t>(i) * H : nullptr, n_trail_left,
+                                                  pr.tts_pad, &req->sampling, req->seed, i, want, batch_codes.data(), &done, &eos,
+                                                  &us, err, errlen);
+        if (s != NAVI_OK) {
+            if (err && errlen) {
+                char tmp[256];
+                std::snprintf(tmp, sizeof tmp, "%s", err);
+                put_err(err, errlen, "frame %d: %s", i + done, tmp);
+            }
+            return s;
         }
-        stats->frames_ms += r.us / 1000.0;
-        if (r.eos) {
+        stats->frames_ms += us / 1000.0;
+        const int kept = eos ? done - 1 : done;
+        codes.insert(codes.end(), batch_codes.begin(), batch_codes.begin() + static_cast<size_t>(kept) * 16);
+        stats->n_frames += kept;
+        pending += kept;
+        i += done;
+        if (eos) {
             stats->eos = 1;
             break;
         }
-        codes.insert(codes.end(), r.codes, r.codes + 16);
-        ++stats->n_frames;
-        ++pending;
         if ((st = flush(false)) != NAVI_OK) return st;
     }
     stats->hit_cap = !stats->eos;

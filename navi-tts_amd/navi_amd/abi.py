@@ -23,7 +23,7 @@ NAVI_OK, NAVI_ERR_TIMEOUT, NAVI_ERR_LAUNCH, NAVI_ERR_KV_FULL, NAVI_ERR_INVALID, 
 EXPORTS = [
     "navi_device_open", "navi_device_stream", "navi_device_synchronize", "navi_build_arch",
     "navi_mem_alloc", "navi_mem_free", "navi_mem_h2d", "navi_mem_d2h", "navi_mem_d2d", "navi_mem_zero",
-    "navi_frame_create", "navi_frame_destroy", "navi_frame_reset", "navi_frame_run", "navi_frame_step_out",
+    "navi_frame_create", "navi_frame_destroy", "navi_frame_reset", "navi_frame_run", "navi_frame_run_many", "navi_frame_step_out",
     "navi_frame_grid_blocks", "navi_frame_occupancy_per_mp", "navi_frame_set_taps", "navi_frame_tap_hidden",
     "navi_frame_tap_logits", "navi_frame_tap_cp_logits", "navi_frame_set_profile", "navi_frame_profile",
     "navi_talker_create", "navi_talker_destroy", "navi_talker_build_prompt", "navi_talker_prefill", "navi_talker_kv",
@@ -155,6 +155,9 @@ def lib() -> C.CDLL:
     L.navi_frame_reset.argtypes = [C.c_void_p]
     L.navi_frame_run.argtypes = [C.c_void_p, C.POINTER(KvView), C.c_int32, C.c_int32, C.c_void_p, C.c_void_p, C.c_void_p,
                                  C.POINTER(Sampling), C.c_uint64, C.c_int32, C.POINTER(FrameResult)]
+    L.navi_frame_run_many.argtypes = [C.c_void_p, C.POINTER(KvView), C.c_int32, C.c_int32, C.c_void_p, C.c_void_p, C.c_void_p,
+                                      C.c_int32, C.c_void_p, C.POINTER(Sampling), C.c_uint64, C.c_int32, C.c_int32, C.c_void_p,
+                                      C.POINTER(C.c_int32), C.POINTER(C.c_int32), C.POINTER(C.c_double), E, C.c_size_t]
     L.navi_frame_step_out.argtypes = [C.c_void_p]
     L.navi_frame_step_out.restype = C.c_void_p
     for f in ("navi_frame_grid_blocks", "navi_frame_occupancy_per_mp"):
@@ -422,6 +425,22 @@ class Frame:
         if r.ok:
             kv.n_used = n_past + 1
         return r
+
+    def run_many(self, kv, n_past0: int, d_trailing: int, n_trailing: int, d_tts_pad: int, s: Sampling, seed: int,
+                 frame_index0: int, n_frames: int, skip_first: bool = False, d_hidden: int | None = None,
+                 d_logits: int | None = None):
+        """navi_frame_run_many: (codes [n_done][16], eos, device us of the loop)."""
+        codes = np.zeros((n_frames, 16), dtype=np.int32)
+        done, eos, us = C.c_int32(), C.c_int32(), C.c_double()
+        err = C.create_string_buffer(256)
+        _check(lib().navi_frame_run_many(self.h, C.byref(kv.view) if kv is not None else None, n_past0, 1 if skip_first else 0,
+                                         d_hidden, d_logits, d_trailing, n_trailing, d_tts_pad, C.byref(s),
+                                         C.c_uint64(seed & ((1 << 64) - 1)), frame_index0, n_frames, codes.ctypes.data,
+                                         C.byref(done), C.byref(eos), C.byref(us), err, 256), err)
+        last = n_past0 + done.value - 1
+        if kv is not None and done.value > (1 if skip_first else 0):
+            kv.n_used = last + 1
+        return codes[:done.value], bool(eos.value), us.value
 
     @property
     def d_step_out(self) -> int:

@@ -168,3 +168,56 @@ def test_kv_full_is_an_error(sess):
     s = sess.abi.Sampling.greedy()
     r = sess.frame.run(sess.kv, sess.kv.max_pos, sess.trailing(0), s, 0, 1)
     assert not r.ok and r.status == sess.abi.NAVI_ERR_KV_FULL and b"KV cache full" in r.error
+
+
+def test_frame_loop_matches_single_frames(sess):
+    """navi_frame_run_many: the frames of an on-device loop are the frames navi_frame_run gives
+    one call at a time (same kernel, same inputs, same seeds: bit-identical codes)."""
+    s = sess.abi.Sampling.make(min_frames=12)
+    n = 12
+    sess.frame.reset()
+    single = []
+    for i in range(n):
+        r = sess.gpu_frame(i, s, 5)
+        assert r.ok, r.error
+        single.append(list(r.codes))
+    step_single = sess.frame.step_out()
+    sess.frame.reset()
+    pad = sess.d_trail.ptr + 4 * 1024 * sess.n_trail
+    codes, eos, us = sess.frame.run_many(sess.kv, sess.n_prefill - 1, sess.d_trail.ptr, sess.n_trail, pad, s, 5, 0, n,
+                                         skip_first=True, d_hidden=sess.d_hidden.ptr, d_logits=sess.d_logits.ptr)
+    log(f"loop of {n} frames: {us / n:.1f} us/frame device, eos={eos}")
+    assert not eos and codes.shape == (n, 16)
+    assert [list(c) for c in codes] == single
+    np.testing.assert_array_equal(sess.frame.step_out(), step_single)
+
+
+def test_frame_loop_stops_at_eos(sess):
+    """A frame that samples EOS ends the loop on the device; it is the last row returned."""
+    s = sess.abi.Sampling.greedy(min_frames=0)
+    lg = sess.logits.copy()
+    lg[2050] = 1e4                                     # EOS wins the greedy pick of frame 0
+    d_lg = sess.abi.DeviceBuffer(4 * lg.size)
+    d_lg.upload(lg.astype(np.float32))
+    sess.frame.reset()
+    pad = sess.d_trail.ptr + 4 * 1024 * sess.n_trail
+    codes, eos, _ = sess.frame.run_many(sess.kv, sess.n_prefill - 1, sess.d_trail.ptr, sess.n_trail, pad, s, 0, 0, 8,
+                                        skip_first=True, d_hidden=sess.d_hidden.ptr, d_logits=d_lg.ptr)
+    log(f"eos loop: {len(codes)} frame(s), first code {codes[0][0] if len(codes) else None}")
+    assert eos and codes.shape == (1, 16) and codes[0][0] == 2050
+
+
+def test_frame_loop_timeout_is_an_error(sess):
+    """A wait past its spin cap ends the loop with NAVI_ERR_TIMEOUT; the next loop runs normally."""
+    tight = sess.abi.Frame(sess.W, spin_cap=1)
+    s = sess.abi.Sampling.greedy(min_frames=4)
+    pad = sess.d_trail.ptr + 4 * 1024 * sess.n_trail
+    with pytest.raises(sess.abi.NaviError) as e:
+        tight.run_many(sess.kv, sess.n_prefill - 1, sess.d_trail.ptr, sess.n_trail, pad, s, 0, 0, 4,
+                       skip_first=True, d_hidden=sess.d_hidden.ptr, d_logits=sess.d_logits.ptr)
+    assert e.value.status == sess.abi.NAVI_ERR_TIMEOUT and "timed out" in str(e.value)
+    tight.close()
+    sess.frame.reset()
+    codes, eos, _ = sess.frame.run_many(sess.kv, sess.n_prefill - 1, sess.d_trail.ptr, sess.n_trail, pad, s, 0, 0, 4,
+                                        skip_first=True, d_hidden=sess.d_hidden.ptr, d_logits=sess.d_logits.ptr)
+    assert codes.shape == (4, 16)
