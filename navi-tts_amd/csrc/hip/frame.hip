@@ -127,7 +127,7 @@ struct Smem {
         struct {
             union {
                 float big[2 * FF];  // att [T][QD] | h [T][FF]
-                struct { float lg[VT]; int idx[VT]; } samp;
+                struct { float lg[VT]; alignas(16) int idx[VT]; } samp;   // idx: the sampler's counters
             };
             uint16_t ckv[2][MAX_CL][NCB][HD];   // this block's cp K/V (kv head blockIdx/2), whole frame
         } m;
@@ -795,7 +795,7 @@ __device__ bool cp_attention(const Args &a, float qkw, int il, int p0, uint32_t 
 // ---- sampling: block_sample (sampler.h) on this block's LDS ----------------------
 
 __device__ __forceinline__ SampleLds sample_lds(Smem &S) {
-    return SampleLds{S.u.m.samp.lg, reinterpret_cast<unsigned (*)[256]>(S.u.m.samp.idx), S.sred, S.sidx, &S.isel[2]};
+    return SampleLds{S.u.m.samp.lg, reinterpret_cast<unsigned *>(S.u.m.samp.idx), S.sred, S.sidx, &S.isel[2]};
 }
 
 // ---- the frame ---------------------------------------------------------------

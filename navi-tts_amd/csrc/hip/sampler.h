@@ -25,11 +25,17 @@ __device__ __forceinline__ uint32_t pcg32_next(uint64_t &s) {
     return (xs >> rot) | (xs << ((0u - rot) & 31u));
 }
 
+// Radix-select counters: pass 0 keeps 4 copies of each of its 256 bins ([digit][lane & 3], so the
+// lanes of one atomic instruction that share a top byte, nearly all of them, spread over 4 banks);
+// passes 1-3 one 256-bin histogram each.
+constexpr int SAMPLE_HIST_WORDS = 4 * 256 + 3 * 256;
+
 // LDS the sampler works in (all block-shared): lg[V] holds the (already modified) logits on entry
-// and is overwritten; hist: 4 x 256 counters; sred: 2 * NW floats; sidx: NW ints; sel: 1 int.
+// and is overwritten; hist: SAMPLE_HIST_WORDS counters, 16-byte aligned; sred: 2 * NW floats;
+// sidx: NW ints; sel: 1 int.
 struct SampleLds {
     float *lg;
-    unsigned (*hist)[256];
+    unsigned *hist;
     float *sred;
     int *sidx;
     int *sel;
@@ -41,9 +47,12 @@ struct SampleLds {
 // exact top-k threshold (the k-th largest by a 4-pass 8-bit radix select over monotone keys,
 // values >= it survive), e^(v - max), and wave 0 draws with the PCG32 u over the survivors in
 // index order with the fused running sum of the reference (`cum += p * inv_sum` compiles to an
-// FMA under hipcc's default contraction). Each radix pass costs one barrier: the four histograms
-// are cleared up front, and every wave finds the digit itself from the shared histogram with a
-// DPP prefix sum. The result is the same in every thread.
+// FMA under hipcc's default contraction). Each radix pass costs one barrier: the histograms are
+// cleared up front, and every wave finds the digit itself from the shared histogram with a DPP
+// prefix sum. The select stops early once the chosen bin lies wholly inside the top k (its count
+// is the number still needed): the bin's lowest value then admits exactly the same survivors as
+// the k-th largest value would. The draw reads the candidates 8 chunks of 64 at a time. The
+// result is the same in every thread.
 template <int V, int BT>
 __device__ __forceinline__ int block_sample(float temperature, int top_k, uint64_t seed, const SampleLds &L) {
     constexpr int PER = V / BT, NW = BT / WAVE;
@@ -69,11 +78,12 @@ __device__ __forceinline__ int block_sample(float temperature, int top_k, uint64
             if (L.sred[w] > v || (L.sred[w] == v && L.sidx[w] < i0)) { v = L.sred[w]; i0 = L.sidx[w]; }
         return i0;
     }
-    unsigned (*hist)[256] = L.hist;
+    unsigned *const hist = L.hist;
     const bool topk = top_k > 0 && top_k < V;
     if (topk) {
+        static_assert(SAMPLE_HIST_WORDS % BT == 0, "histogram clear");
 #pragma unroll
-        for (int p = 0; p < 4; ++p) hist[p][tid] = 0u;
+        for (int p = 0; p < SAMPLE_HIST_WORDS / BT; ++p) hist[p * BT + tid] = 0u;
     }
     float lmx = -INFINITY;
 #pragma unroll
@@ -91,29 +101,48 @@ __device__ __forceinline__ int block_sample(float temperature, int top_k, uint64
 #pragma unroll
         for (int p = 0; p < 4; ++p) {
             const int shift = 24 - 8 * p;
+            unsigned *const hp = hist + (p == 0 ? 0 : 1024 + (p - 1) * 256);
 #pragma unroll
             for (int k = 0; k < PER; ++k) {
                 const unsigned key = float_key(x[k]);
-                if ((key & mask) == prefix) atomicAdd(&hist[p][(key >> shift) & 0xFFu], 1u);
+                if (p == 0) atomicAdd(&hp[(key >> 24) * 4 + (lane & 3)], 1u);
+                else if ((key & mask) == prefix) atomicAdd(&hp[(key >> shift) & 0xFFu], 1u);
             }
             __syncthreads();
             // lane l owns digits 255-4l .. 252-4l (descending); every wave finds the digit itself
             int c[4], tot = 0;
+            if (p == 0) {
+                // digits 252-4l+q, q = 0..3: four replicas each, 16 consecutive words
+                const u32x4_t *h4 = reinterpret_cast<const u32x4_t *>(hp + (252 - 4 * lane) * 4);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) { c[j] = static_cast<int>(hist[p][255 - 4 * lane - j]); tot += c[j]; }
+                for (int q = 0; q < 4; ++q) {
+                    const u32x4_t r = h4[q];
+                    c[3 - q] = static_cast<int>((r.x + r.y) + (r.z + r.w));
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) c[j] = static_cast<int>(hp[255 - 4 * lane - j]);
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) tot += c[j];
             int above = wave_incl_scan(tot) - tot;
-            int dsel = -1, nsel = 0;
+            int dsel = -1, nsel = 0, csel = 0;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                if (dsel < 0 && above < need && above + c[j] >= need) { dsel = 255 - 4 * lane - j; nsel = need - above; }
+                if (dsel < 0 && above < need && above + c[j] >= need) { dsel = 255 - 4 * lane - j; nsel = need - above; csel = c[j]; }
                 above += c[j];
             }
             const uint64_t hit = __ballot(dsel >= 0);
             const int src = hit ? static_cast<int>(__builtin_ctzll(hit)) : 0;   // exactly one lane finds it
             const int digit = __builtin_amdgcn_readlane(dsel, src);
             need = __builtin_amdgcn_readlane(nsel, src);
+            const int cnt = __builtin_amdgcn_readlane(csel, src);
             prefix |= static_cast<unsigned>(digit) << shift;
             mask |= 0xFFu << shift;
+            // The whole bin survives: its lowest float admits exactly the same values as the k-th
+            // largest. Not for the bin that starts at +0 (-0 compares equal to it but keys below
+            // it) nor for one whose lowest key is a NaN pattern.
+            if (need == cnt && prefix >= 0x00800000u && prefix != 0x80000000u) break;
         }
         thr = key_float(prefix);
     }
@@ -138,16 +167,21 @@ __device__ __forceinline__ int block_sample(float temperature, int top_k, uint64
         int chosen = V - 1;
         float cum = 0.f;
         bool found = false;
-        for (int k = 0; k < PER && !found; ++k) {
-            for (int w = 0; w < NW && !found; ++w) {
-                const int base = k * BT + w * WAVE;
-                const float ev = L.lg[base + lane];
-                uint64_t nz = __ballot(ev != 0.f);
-                while (nz && !found) {
+        // index i = k * BT + tid = 64 c + lane: chunk c holds indices 64c .. 64c + 63, in order
+        constexpr int NCH = V / WAVE, BATCH = 8;
+        static_assert(NCH % BATCH == 0, "draw batches");
+        for (int c0 = 0; c0 < NCH && !found; c0 += BATCH) {
+            float ev[BATCH];
+#pragma unroll
+            for (int q = 0; q < BATCH; ++q) ev[q] = L.lg[(c0 + q) * WAVE + lane];
+#pragma unroll
+            for (int q = 0; q < BATCH; ++q) {
+                uint64_t nz = found ? 0ull : __ballot(ev[q] != 0.f);
+                while (nz) {
                     const int b = static_cast<int>(__builtin_ctzll(nz));
                     nz &= nz - 1;
-                    cum = fmaf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(ev), b)), inv, cum);
-                    if (cum >= u) { chosen = base + b; found = true; }
+                    cum = fmaf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(ev[q]), b)), inv, cum);
+                    if (cum >= u) { chosen = (c0 + q) * WAVE + b; found = true; nz = 0; }
                 }
             }
         }

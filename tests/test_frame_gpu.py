@@ -148,6 +148,64 @@ def test_sampler_matches_oracle_on_device_logits(sess):
             seen[cb0] = True
 
 
+def edge_logits():
+    """Codebook-0 logits shaped to reach the sampler's corner cases (indices >= 2048 other than
+    EOS are suppressed, and EOS is gated at frame 0, so only the first 2048 entries count):
+    (name, logits, temperature, top_k)."""
+    rng = np.random.default_rng(5)
+    V, A = 3072, 2048
+    out = []
+    base = np.clip(rng.normal(0.0, 1.0, V), -6.0, 3.5).astype(np.float32)
+    ties = base.copy()                      # 20 above, 100 tied at the top-50 threshold
+    idx = rng.choice(A, 120, replace=False)
+    ties[idx[:20]] = rng.uniform(5.0, 6.0, 20)
+    ties[idx[20:]] = 4.0
+    out.append(("ties", ties, 0.9, 50))
+    out.append(("ties-greedy", ties, 0.0, 50))
+    narrow = (1.0 + 1e-4 * rng.random(V)).astype(np.float32)    # one top byte, deep radix passes
+    out.append(("narrow", narrow, 0.9, 50))
+    zeros = -rng.uniform(0.5, 4.0, V).astype(np.float32)         # threshold at 0 with +0 and -0 tied
+    idx = rng.choice(A, 110, replace=False)
+    zeros[idx[:30]] = rng.uniform(1.0, 3.0, 30)
+    zeros[idx[30:70]] = 0.0
+    zeros[idx[70:]] = -0.0
+    out.append(("zeros", zeros, 0.9, 50))
+    tiny = -rng.uniform(0.5, 4.0, V).astype(np.float32)          # k-th value in the bin that starts at +0
+    idx = rng.choice(A, 110, replace=False)
+    tiny[idx[:49]] = rng.uniform(1.0, 3.0, 49)
+    tiny[idx[49]] = np.float32(1.5e-38)
+    tiny[idx[50:]] = -0.0
+    out.append(("tiny", tiny, 1.0, 50))
+    wide = (rng.normal(0.0, 40.0, V)).astype(np.float32)
+    out.append(("wide", wide, 0.9, 50))
+    out.append(("k-beyond-finite", base, 0.9, 3000))   # k-th largest is -inf: all finite values survive
+    out.append(("k1", base, 0.9, 1))
+    out.append(("k0", base, 0.9, 0))
+    out.append(("kV", base, 0.9, V))
+    return out
+
+
+def test_sampler_edge_cases_match_oracle(sess):
+    """Codebook-0 sampling of crafted logits (frame 0 takes them as the prefill's output) picks
+    what the oracle's sample_talker picks: threshold ties, one shared top byte, +0/-0 at the
+    threshold, a threshold bin that starts at +0 with -0 below it, top_k past the finite values,
+    top_k 1, 0 and V."""
+    from oracle import rng, sampler as osamp
+    d_lg = sess.abi.DeviceBuffer(4 * 3072)
+    for name, lg, temp, k in edge_logits():
+        d_lg.upload(np.ascontiguousarray(lg, dtype=np.float32))
+        for seed in (1, 2, 3):
+            s_gpu = sess.abi.Sampling.make(temperature=temp, top_k=k)
+            s_ora = osamp.Sampling(temperature=temp, top_k=k)
+            sess.frame.reset()
+            r = sess.frame.run_first(sess.d_hidden.ptr, d_lg.ptr, sess.trailing(0), s_gpu, seed, 0)
+            assert r.ok, r.error
+            tseed, _ = rng.frame_seeds(seed, 0)
+            want = osamp.sample_talker(lg, np.zeros(3072, bool), s_ora, tseed, 0, 2050, 2048)
+            log(f"{name} T {temp} k {k} seed {seed}: gpu {r.codes[0]} oracle {want}")
+            assert r.codes[0] == want, name
+
+
 def test_timeout_fails_cleanly_then_recovers(sess):
     """frame.h:33-36 spin cap: a cap of 1 fails the frame with 'timed out' (test_frame.cpp:99-119)."""
     import time
