@@ -129,10 +129,14 @@ struct Smem {
                 float big[2 * FF];  // att [T][QD] | h [T][FF]
                 struct { float lg[VT]; alignas(16) int idx[VT]; } samp;   // idx: the sampler's counters
             };
-            uint16_t ckv[2][MAX_CL][NCB][HD];   // this block's cp K/V (kv head blockIdx/2), whole frame
+            // this block's cp K/V (kv head blockIdx/2), whole frame, zero until written; K rows
+            // keep 16-byte chunk c at slot c ^ (row & 15)
+            uint16_t ckv[2][MAX_CL][NCB][HD];
+            float rope[2][NCB][HD / 2];      // cp RoPE cos / sin of positions 0..15, dim pairs
         } m;
     } u;
     float invf[2][HD / 2];          // RoPE inverse frequencies (talker, cp)
+    float trope[2][HD / 2];         // talker RoPE cos / sin at this frame's position
     LayerPtrs lp[MAX_TL + MAX_CL];  // weight pointers, copied once: a scalar load of the table in
     const uint16_t *emb[CPH];       // global memory misses the scalar cache under the weight stream
     const uint16_t *lmh[CPH];
@@ -565,8 +569,7 @@ __device__ bool talker_attention(const Args &a, const Ctx &cx, float qkw, int il
     // the current k) with the pair (l, l + 64) in lane l, q copied to the wave's own LDS row for
     // the score loop, the current key's score and value in registers.
     const int L = lane(), w = wave();
-    float sn, cs;
-    sincosf(static_cast<float>(pos) * S.invf[0][L], &sn, &cs);
+    const float cs = S.trope[0][L], sn = S.trope[1][L];
     float qa, qb;
     head_norm_pair(S.q[0], S.nw, a.eps_t, qa, qb);
     S.qw[w][L] = qa * cs - qb * sn;
@@ -710,7 +713,8 @@ __device__ bool talker_attention(const Args &a, const Ctx &cx, float qkw, int il
 }
 
 // Code-predictor attention for q head h = blockIdx over T rows at positions p0..p0+T-1;
-// K/V of this block's kv head live in S.ckv for the whole frame.
+// K/V of this block's kv head live in S.u.m.ckv for the whole frame (rows not yet written are
+// zero), RoPE cos/sin in S.u.m.rope (the frame's table of the 16 cp positions).
 template <int T>
 __device__ bool cp_attention(const Args &a, float qkw, int il, int p0, uint32_t tag_qkv, uint32_t tag_att, Smem &S) {
     const int h = blk(), g = h / GRP;
@@ -719,17 +723,16 @@ __device__ bool cp_attention(const Args &a, float qkw, int il, int p0, uint32_t 
     if (!gather_head<T>(a, h, g, tag_qkv, S)) return false;
     PROF_MARK(a, S);
     // Wave t computes row t (position p0 + t) alone: head norms and RoPE of q (into the wave's
-    // own LDS row) and of the new keys 0..T-1, written with the new values into S.ckv (every
+    // own LDS row) and of the new keys 0..T-1, written with the new values into ckv (every
     // computing wave writes the same values, so each reads back what it wrote itself; later
-    // positions' passes read them after many barriers); then lane j scores key j against the
-    // whole q row (no cross-lane reduction per key), the softmax, the value sum (lane l: dims
-    // 2l, 2l + 1) and the publication.
+    // positions' passes read them after many barriers). Scores: lanes 4j..4j+3 take key j, a
+    // quarter of the head each (dims 32s..32s+31), summed by two DPP steps. Value sum: lane l
+    // owns dims 2l, 2l+1; all 16 rows are read at once (rows >= n are zero, weight 0).
     const int L = lane(), w = wave();
     if (w >= T) return true;
     const int t = w, pos = p0 + t, n = pos + 1;
     {
-        float sn, cs;
-        sincosf(static_cast<float>(pos) * S.invf[1][L], &sn, &cs);
+        const float cs = S.u.m.rope[0][pos][L], sn = S.u.m.rope[1][pos][L];
         float x0, x1;
         head_norm_pair(S.q[t], S.nw, a.eps_c, x0, x1);
         S.qw[w][L] = x0 * cs - x1 * sn;
@@ -737,51 +740,49 @@ __device__ bool cp_attention(const Args &a, float qkw, int il, int p0, uint32_t 
     }
 #pragma unroll
     for (int u = 0; u < T; ++u) {
-        float sn, cs;
-        sincosf(static_cast<float>(p0 + u) * S.invf[1][L], &sn, &cs);
+        const int pu = p0 + u;
+        const float cs = S.u.m.rope[0][pu][L], sn = S.u.m.rope[1][pu][L];
         float x0, x1;
         head_norm_pair(S.k[u], S.nw + HD, a.eps_c, x0, x1);
-        S.u.m.ckv[0][il][p0 + u][L] = f2h(x0 * cs - x1 * sn);
-        S.u.m.ckv[0][il][p0 + u][L + HD / 2] = f2h(x0 * sn + x1 * cs);
-        S.u.m.ckv[1][il][p0 + u][2 * L] = f2h(S.v[u][2 * L]);
-        S.u.m.ckv[1][il][p0 + u][2 * L + 1] = f2h(S.v[u][2 * L + 1]);
+        uint16_t *kr = S.u.m.ckv[0][il][pu];
+        kr[(((L >> 3) ^ (pu & 15)) << 3) + (L & 7)] = f2h(x0 * cs - x1 * sn);
+        kr[((((L + HD / 2) >> 3) ^ (pu & 15)) << 3) + (L & 7)] = f2h(x0 * sn + x1 * cs);
+        S.u.m.ckv[1][il][pu][2 * L] = f2h(S.v[u][2 * L]);
+        S.u.m.ckv[1][il][pu][2 * L + 1] = f2h(S.v[u][2 * L + 1]);
     }
-    float sl = -INFINITY;
-    if (L < n) {
+    const int j = L >> 2, sq = L & 3;
+    float sc;
+    {
+        const uint16_t *kr = S.u.m.ckv[0][il][j];
+        const float *qr = &S.qw[w][sq * 32];
         float acc = 0.f;
 #pragma unroll
-        for (int c = 0; c < HD / 8; ++c) {
+        for (int c = 0; c < 4; ++c) {
             uint4 kk;
-            __builtin_memcpy(&kk, &S.u.m.ckv[0][il][L][c * 8], 16);
-            acc = dot8(kk, &S.qw[w][c * 8], acc);
+            __builtin_memcpy(&kk, kr + (((sq * 4 + c) ^ j) << 3), 16);
+            acc = dot8(kk, qr + c * 8, acc);
         }
-        sl = acc * ATT_SCALE;
+        acc += dpp_mov<0xB1>(acc);       // quad_perm [1,0,3,2]
+        acc += dpp_mov<0x4E>(acc);       // quad_perm [2,3,0,1]: the 4 lanes of key j hold its dot
+        sc = j < n ? acc * ATT_SCALE : -INFINITY;
     }
-    const float m = wave_max(sl);
-    const float e = L < n ? expf(sl - m) : 0.f;
-    const float inv = 1.f / wave_sum(e);
-    float o0 = 0.f, o1 = 0.f, p0a = 0.f, p1a = 0.f;
-    int j = 0;
-    for (; j + 2 <= n; j += 2) {
-        const float pa = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), j));
-        const float pb = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), j + 1));
-        half2_t ha, hb;
-        __builtin_memcpy(&ha, &S.u.m.ckv[1][il][j][2 * L], 4);
-        __builtin_memcpy(&hb, &S.u.m.ckv[1][il][j + 1][2 * L], 4);
-        o0 = fmaf(pa, static_cast<float>(ha[0]), o0);
-        o1 = fmaf(pa, static_cast<float>(ha[1]), o1);
-        p0a = fmaf(pb, static_cast<float>(hb[0]), p0a);
-        p1a = fmaf(pb, static_cast<float>(hb[1]), p1a);
+    const float m = wave_max(sc);
+    const float e = j < n ? expf(sc - m) : 0.f;
+    const float inv = 1.f / wave_sum(sq == 0 ? e : 0.f);
+    half2_t hv[NCB];
+#pragma unroll
+    for (int r = 0; r < NCB; ++r) __builtin_memcpy(&hv[r], &S.u.m.ckv[1][il][r][2 * L], 4);
+    float o0 = 0.f, o1 = 0.f, q0 = 0.f, q1 = 0.f;
+#pragma unroll
+    for (int r = 0; r < NCB; r += 2) {
+        const float pa = lane_value(e, 4 * r), pb = lane_value(e, 4 * r + 4);
+        o0 = fmaf(pa, static_cast<float>(hv[r][0]), o0);
+        o1 = fmaf(pa, static_cast<float>(hv[r][1]), o1);
+        q0 = fmaf(pb, static_cast<float>(hv[r + 1][0]), q0);
+        q1 = fmaf(pb, static_cast<float>(hv[r + 1][1]), q1);
     }
-    if (j < n) {
-        const float pa = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), j));
-        half2_t ha;
-        __builtin_memcpy(&ha, &S.u.m.ckv[1][il][j][2 * L], 4);
-        o0 = fmaf(pa, static_cast<float>(ha[0]), o0);
-        o1 = fmaf(pa, static_cast<float>(ha[1]), o1);
-    }
-    o0 = (o0 + p0a) * inv;
-    o1 = (o1 + p1a) * inv;
+    o0 = (o0 + q0) * inv;
+    o1 = (o1 + q1) * inv;
 #pragma unroll
     for (int r = 0; r < NREP; ++r) {
         uint64_t *dst = a.mb + r * MB_WORDS + MB_ATT + t * QD + h * HD + 2 * L;
@@ -885,6 +886,12 @@ __global__ void __launch_bounds__(BT, 1) k_frame(Args a, const Weights *__restri
         if (tid() < CPH) { S.emb[tid()] = gld(W.cp_emb + tid()); S.lmh[tid()] = gld(W.lm_head + tid()); }
     }
     __syncthreads();
+    if (tid() < HD / 2) {
+        float sn, cs;
+        sincosf(static_cast<float>(a.n_past) * S.invf[0][tid()], &sn, &cs);
+        S.trope[0][tid()] = cs;
+        S.trope[1][tid()] = sn;
+    }
     uint32_t seen_bits = 0;
     for (int k = 0; k < VT / BT; ++k) seen_bits |= (gld(a.seen + tid() + k * BT) ? 1u : 0u) << k;
     load_norm(R.fn, a.skip_talker ? W.cp_norm : W.tl_norm);
@@ -950,6 +957,18 @@ __global__ void __launch_bounds__(BT, 1) k_frame(Args a, const Weights *__restri
     for (int i = tid(); i < H; i += BT) {
         S.x[0][i] = S.xn[0][i];
         S.x[1][i] = h2f(gld(W.codec_emb + static_cast<size_t>(cb0) * H + i));
+    }
+    if (blk() < NH) {            // the cp attention blocks: K/V rows not yet written read as zero
+        constexpr int NV = static_cast<int>(sizeof(S.u.m.ckv) / sizeof(u32x4_t));
+        u32x4_t *z = reinterpret_cast<u32x4_t *>(&S.u.m.ckv[0][0][0][0]);
+        for (int i = tid(); i < NV; i += BT) z[i] = u32x4_t{0u, 0u, 0u, 0u};
+        for (int i = tid(); i < NCB * HD / 2; i += BT) {
+            const int pos = i / (HD / 2), l = i % (HD / 2);
+            float sn, cs;
+            sincosf(static_cast<float>(pos) * S.invf[1][l], &sn, &cs);
+            S.u.m.rope[0][pos][l] = cs;
+            S.u.m.rope[1][pos][l] = sn;
+        }
     }
     __syncthreads();
     for (int il = 0; il < a.n_cl; ++il, ++gi)
