@@ -344,8 +344,12 @@ __device__ __forceinline__ void xfrag(const float *x, int base, float (&xf)[NC][
 }
 
 // ---- weight prefetch: this block's slice of one layer -----------------------
+// Talker weights are read once per frame and stream past with the non-temporal hint. The code
+// predictor's 5 layers and heads (220 MB) are read 15 times per frame: plain loads let the
+// memory-side cache serve the repeats (60 us per frame less at n_past 256 than streaming them).
+__device__ __forceinline__ uint4 ldw(const uint16_t *p, bool reuse) { return reuse ? ldg16(p) : ldg16_stream(p); }
 
-__device__ __forceinline__ void load_qkv(Regs &R, const LayerPtrs &L) {
+__device__ __forceinline__ void load_qkv(Regs &R, const LayerPtrs &L, bool reuse) {
     const int rb = blk() * (QKV / NB);
     const uint16_t *M;
     int base;
@@ -356,36 +360,36 @@ __device__ __forceinline__ void load_qkv(Regs &R, const LayerPtrs &L) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
         const uint16_t *p = M + static_cast<size_t>(wave() * 4 + r) * H + lane() * 8;
-        R.qkv[r][0] = ldg16_stream(p);
-        R.qkv[r][1] = ldg16_stream(p + 512);
+        R.qkv[r][0] = ldw(p, reuse);
+        R.qkv[r][1] = ldw(p + 512, reuse);
     }
     load_norm(R.ln1, L.ln1);
     R.qkw = gld((wave() < 2 ? L.qn : L.kn) + (tid() & (HD - 1)));
 }
 
-__device__ __forceinline__ void load_o(Regs &R, const LayerPtrs &L) {
+__device__ __forceinline__ void load_o(Regs &R, const LayerPtrs &L, bool reuse) {
     const uint16_t *p = sgpr_ptr(L.wo + static_cast<size_t>(blk() * (H / NB)) * QD) + static_cast<size_t>(wave()) * QD + lane() * 8;
 #pragma unroll
-    for (int c = 0; c < 4; ++c) R.o[c] = ldg16_stream(p + c * 512);
+    for (int c = 0; c < 4; ++c) R.o[c] = ldw(p + c * 512, reuse);
 }
 
-__device__ __forceinline__ void load_gu(Regs &R, const LayerPtrs &L) {
+__device__ __forceinline__ void load_gu(Regs &R, const LayerPtrs &L, bool reuse) {
     constexpr int RB = FF / NB;   // 12 gate + 12 up rows per block
 #pragma unroll
     for (int r = 0; r < 6; ++r) {
         const int vr = wave() * 3 + (r % 3);               // r < 3: gate row vr, r >= 3: up row vr
         const uint16_t *M = sgpr_ptr((r < 3 ? L.wg : L.wu) + static_cast<size_t>(blk() * RB) * H);
         const uint16_t *p = M + static_cast<size_t>(vr) * H + lane() * 8;
-        R.gu[r][0] = ldg16_stream(p);
-        R.gu[r][1] = ldg16_stream(p + 512);
+        R.gu[r][0] = ldw(p, reuse);
+        R.gu[r][1] = ldw(p + 512, reuse);
     }
     load_norm(R.ln2, L.ln2);
 }
 
-__device__ __forceinline__ void load_dn(Regs &R, const LayerPtrs &L) {
+__device__ __forceinline__ void load_dn(Regs &R, const LayerPtrs &L, bool reuse) {
     const uint16_t *p = sgpr_ptr(L.wd + static_cast<size_t>(blk() * (H / NB)) * FF) + static_cast<size_t>(wave()) * FF + lane() * 8;
 #pragma unroll
-    for (int c = 0; c < 6; ++c) R.dn[c] = ldg16_stream(p + c * 512);
+    for (int c = 0; c < 6; ++c) R.dn[c] = ldw(p + c * 512, reuse);
 }
 
 __device__ __forceinline__ void load_th(Regs &R, const uint16_t *head) {
@@ -401,8 +405,8 @@ __device__ __forceinline__ void load_lm(Regs &R, const uint16_t *head) {
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
         const uint16_t *p = head + static_cast<size_t>(blk() * (VC / NB) + wave() * 2 + r) * H + lane() * 8;
-        R.lm[r][0] = ldg16_stream(p);
-        R.lm[r][1] = ldg16_stream(p + 512);
+        R.lm[r][0] = ldg16(p);
+        R.lm[r][1] = ldg16(p + 512);
     }
 }
 
@@ -818,6 +822,7 @@ __device__ __forceinline__ bool run_layer(const Args &a, const Ctx &cx, Regs &R,
     const int n_total = a.n_tl + CPH * a.n_cl;
     const bool has_next = gi + 1 < n_total;
     const LayerPtrs &N = layer_at(a, S, has_next ? gi + 1 : gi);
+    const bool next_cp = gi + 1 >= a.n_tl;
     const float eps = TALKER ? a.eps_t : a.eps_c;
 
     norm_prep<T>(S.x, R.ln1, S.xn, S);
@@ -826,7 +831,7 @@ __device__ __forceinline__ bool run_layer(const Args &a, const Ctx &cx, Regs &R,
     const uint32_t t_qkv = seq.next();
     qkv_phase<T>(a, R, S, t_qkv, sc);
     const float qkw = R.qkw;     // this layer's q/k norm weight; the prefetch below replaces it
-    if (has_next) load_qkv(R, N);
+    if (has_next) load_qkv(R, N, next_cp);
 
     const uint32_t t_ap = TALKER ? seq.next() : 0u;
     const uint32_t t_att = seq.next();
@@ -838,19 +843,19 @@ __device__ __forceinline__ bool run_layer(const Args &a, const Ctx &cx, Regs &R,
     if (!gather_rows<T, QD, HD>(a, MB_ATT, t_att, S.u.m.big, S)) return false;
     const uint32_t t_x2 = seq.next();
     o_phase<T>(a, R, S, t_x2);
-    if (has_next) load_o(R, N);
+    if (has_next) load_o(R, N, next_cp);
 
     if (!gather_rows<T, H, H / NB>(a, MB_X2, t_x2, &S.x[0][0], S)) return false;
     norm_prep<T>(S.x, R.ln2, S.xn, S);
     norm_scale<T>(eps, sc, S);
     const uint32_t t_h = seq.next();
     gu_phase<T>(a, R, S, t_h, sc);
-    if (has_next) load_gu(R, N);
+    if (has_next) load_gu(R, N, next_cp);
 
     if (!gather_rows<T, FF, FF / NB>(a, MB_H, t_h, S.u.m.big, S)) return false;
     const uint32_t t_x = seq.next();
     down_phase<T>(a, R, S, t_x);
-    if (has_next) load_dn(R, N);
+    if (has_next) load_dn(R, N, next_cp);
     if (head) {                  // the pass's head slice, issued one phase before it is needed
         if constexpr (TALKER) load_th(R, head);
         else load_lm(R, head);
@@ -898,7 +903,8 @@ __global__ void __launch_bounds__(BT, 1) k_frame(Args a, const Weights *__restri
     const int first = a.skip_talker ? a.n_tl : 0;
     {
         const LayerPtrs &L0 = layer_at(a, S, first);
-        load_qkv(R, L0); load_o(R, L0); load_gu(R, L0); load_dn(R, L0);
+        const bool cp0 = first >= a.n_tl;
+        load_qkv(R, L0, cp0); load_o(R, L0, cp0); load_gu(R, L0, cp0); load_dn(R, L0, cp0);
     }
     __syncthreads();
 
