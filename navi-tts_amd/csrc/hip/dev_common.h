@@ -24,21 +24,38 @@ __device__ __forceinline__ float dpp_mov(float v) {
 __device__ __forceinline__ float lane_value(float v, int l) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
 }
+// A DPP read of v for a reduction step; with bound_ctrl the compiler fuses it into the
+// consuming v_add/v_max (one instruction per step).
+template <int CTRL>
+__device__ __forceinline__ float dpp_red(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, true));
+}
+template <int CTRL, int ROWS>
+__device__ __forceinline__ float dpp_rows(float v, float old) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(old), __float_as_int(v), CTRL, ROWS, 0xF, false));
+}
 
+// Sum over the 64 lanes, the same value in every lane: quad_perm, row_half_mirror and row_mirror
+// make each 16-lane row hold its row sum r_k; row_bcast:15 into rows 1 and 3 and row_bcast:31 into
+// rows 2 and 3 leave (r3 + r2) + (r1 + r0) in lane 63.
 __device__ __forceinline__ float wave_sum(float v) {
-    v += dpp_mov<0xB1>(v);      // quad_perm [1,0,3,2]
-    v += dpp_mov<0x4E>(v);      // quad_perm [2,3,0,1]
-    v += dpp_mov<0x141>(v);     // row_half_mirror
-    v += dpp_mov<0x140>(v);     // row_mirror
-    return (lane_value(v, 0) + lane_value(v, 16)) + (lane_value(v, 32) + lane_value(v, 48));
+    v += dpp_red<0xB1>(v);      // quad_perm [1,0,3,2]
+    v += dpp_red<0x4E>(v);      // quad_perm [2,3,0,1]
+    v += dpp_red<0x141>(v);     // row_half_mirror
+    v += dpp_red<0x140>(v);     // row_mirror
+    v += dpp_rows<0x142, 0xA>(v, 0.f);
+    v += dpp_rows<0x143, 0xC>(v, 0.f);
+    return lane_value(v, 63);
 }
 
 __device__ __forceinline__ float wave_max(float v) {
-    v = fmaxf(v, dpp_mov<0xB1>(v));
-    v = fmaxf(v, dpp_mov<0x4E>(v));
-    v = fmaxf(v, dpp_mov<0x141>(v));
-    v = fmaxf(v, dpp_mov<0x140>(v));
-    return fmaxf(fmaxf(lane_value(v, 0), lane_value(v, 16)), fmaxf(lane_value(v, 32), lane_value(v, 48)));
+    v = fmaxf(v, dpp_red<0xB1>(v));
+    v = fmaxf(v, dpp_red<0x4E>(v));
+    v = fmaxf(v, dpp_red<0x141>(v));
+    v = fmaxf(v, dpp_red<0x140>(v));
+    v = fmaxf(v, dpp_rows<0x142, 0xA>(v, v));
+    v = fmaxf(v, dpp_rows<0x143, 0xC>(v, v));
+    return lane_value(v, 63);
 }
 
 // Inclusive prefix sum over the 64 lanes: row_shr 1/2/4/8 within each 16-lane row, then
@@ -56,12 +73,13 @@ __device__ __forceinline__ int wave_incl_scan(int v) {
 }
 
 __device__ __forceinline__ int wave_min_int(int v) {
-    v = min(v, __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false));
-    v = min(v, __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, false));
-    v = min(v, __builtin_amdgcn_mov_dpp(v, 0x141, 0xF, 0xF, false));
-    v = min(v, __builtin_amdgcn_mov_dpp(v, 0x140, 0xF, 0xF, false));
-    return min(min(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16)),
-               min(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
+    v = min(v, __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, true));
+    v = min(v, __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, true));
+    v = min(v, __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, true));
+    v = min(v, __builtin_amdgcn_update_dpp(0, v, 0x140, 0xF, 0xF, true));
+    v = min(v, __builtin_amdgcn_update_dpp(v, v, 0x142, 0xA, 0xF, false));
+    v = min(v, __builtin_amdgcn_update_dpp(v, v, 0x143, 0xC, 0xF, false));
+    return __builtin_amdgcn_readlane(v, 63);
 }
 
 __device__ __forceinline__ float h2f(uint16_t h) {
