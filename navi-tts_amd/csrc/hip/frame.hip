@@ -598,25 +598,37 @@ __device__ bool talker_attention(const Args &a, const Ctx &cx, float qkw, int il
     wait_vm_all();
     __syncthreads();                                       // every wave's part of the range has landed
     PROF_MARK(a, S);
-    // Per-wave online softmax over the wave's keys (wave w: range rows w*64 .. w*64+63); wave 0 of
-    // the last range also takes the current key. Lane L owns value dims 2L, 2L + 1.
+    // Scores of the range's keys, every wave: lanes 16q..16q+15 take key j = base + q (base =
+    // 4w + 16i), lane 16q + c multiplying the key's 16-byte chunk c with q[8c .. 8c+7]; the 16
+    // lanes sum by DPP within their row and lane 16q keeps the score in S.sc[j].
+    {
+        const int q4 = L >> 4, c = L & 15;
+        float qf[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) qf[e] = S.qw[w][c * 8 + e];
+        for (int base = 4 * w; base < n; base += 4 * NW) {   // base <= 252: rows base + q4 < KCH
+            const int j = base + q4;
+            const u32x4_t kv4 = *reinterpret_cast<const u32x4_t *>(&S.u.tkv.k[j][(c ^ (j & 15)) * 8]);
+            uint4 kk;
+            __builtin_memcpy(&kk, &kv4, 16);
+            float acc = dot8(kk, qf, 0.f);
+            acc += dpp_red<0xB1>(acc);
+            acc += dpp_red<0x4E>(acc);
+            acc += dpp_red<0x141>(acc);
+            acc += dpp_red<0x140>(acc);
+            if (c == 0 && j < n) S.sc[j] = acc * ATT_SCALE;
+        }
+    }
+    __syncthreads();
+    // Per-wave softmax over the wave's keys (wave w: rows w*per .. w*per + per - 1, per =
+    // ceil(n / 4) <= 64, lane-per-key); wave 0 of the last range also takes the current key. Lane L
+    // owns value dims 2L, 2L + 1.
     float mw = -INFINITY, lw = 0.f, acc0 = 0.f, acc1 = 0.f;
     const int slot8 = 2 * (L & 3);
     {
-        const int jw = w * WAVE, cnt = max(0, min(WAVE, n - jw));
-        float sj = -INFINITY;
-        if (L < cnt) {
-            const int jj = jw + L;
-            float acc = 0.f;
-#pragma unroll
-            for (int c = 0; c < HD / 8; ++c) {
-                const u32x4_t kv4 = *reinterpret_cast<const u32x4_t *>(&S.u.tkv.k[jj][(c ^ (jj & 15)) * 8]);
-                uint4 kk;
-                __builtin_memcpy(&kk, &kv4, 16);
-                acc = dot8(kk, &S.qw[w][c * 8], acc);
-            }
-            sj = acc * ATT_SCALE;
-        }
+        const int per = (n + NW - 1) / NW;
+        const int jw = w * per, cnt = max(0, min(per, n - jw));
+        const float sj = L < cnt ? S.sc[jw + L] : -INFINITY;
         const bool cur = last && w == 0;
         float mn = wave_max(sj);
         if (cur) mn = fmaxf(mn, s_cur);
@@ -625,31 +637,23 @@ __device__ bool talker_attention(const Args &a, const Ctx &cx, float qkw, int il
             const float ec = cur ? expf(s_cur - mn) : 0.f;
             lw = wave_sum(e) + ec;
             mw = mn;
-            // V sum in groups of 8 keys: the 8 LDS reads are issued before the first FMA, and 2
-            // independent accumulator pairs halve the FMA chains (key j's weight: lane j's e)
+            // V sum in groups of 8 keys: the 8 LDS reads are issued before the first FMA (rows
+            // past cnt repeat the last row with weight 0), and 2 independent accumulator pairs
+            // halve the FMA chains (key j's weight: lane j's e)
             float b0[2] = {ec * vc0, 0.f}, b1[2] = {ec * vc1, 0.f};
-            int j = 0;
-            for (; j + 8 <= cnt; j += 8) {
+            for (int j = 0; j < cnt; j += 8) {
                 half2_t hv[8];
 #pragma unroll
                 for (int u = 0; u < 8; ++u) {
-                    const int jj = jw + j + u;
+                    const int jj = jw + min(j + u, cnt - 1);
                     __builtin_memcpy(&hv[u], &S.u.tkv.v[jj][((L >> 2) ^ (jj & 15)) * 8 + slot8], 4);
                 }
 #pragma unroll
                 for (int u = 0; u < 8; ++u) {
-                    const float p = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), j + u));
+                    const float p = lane_value(e, j + u);
                     b0[u & 1] = fmaf(p, static_cast<float>(hv[u][0]), b0[u & 1]);
                     b1[u & 1] = fmaf(p, static_cast<float>(hv[u][1]), b1[u & 1]);
                 }
-            }
-            for (; j < cnt; ++j) {
-                const int jj = jw + j;
-                const float p = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), j));
-                half2_t hv;
-                __builtin_memcpy(&hv, &S.u.tkv.v[jj][((L >> 2) ^ (jj & 15)) * 8 + slot8], 4);
-                b0[0] = fmaf(p, static_cast<float>(hv[0]), b0[0]);
-                b1[0] = fmaf(p, static_cast<float>(hv[1]), b1[0]);
             }
             acc0 = b0[0] + b0[1];
             acc1 = b1[0] + b1[1];
@@ -694,16 +698,18 @@ __device__ bool talker_attention(const Args &a, const Ctx &cx, float qkw, int il
     float *P = S.u.m.big;
     if (!gather<NR * AP_W, AP_W, false>(a, MB_AP + h * NR * AP_W, tag_ap, P, S)) return false;
     if (tid() < HD) {
-        float M = -INFINITY;
-#pragma unroll
-        for (int k = 0; k < NR; ++k) M = fmaxf(M, P[k * AP_W + HD]);
+        // lane k (mod 16) computes partial k's weight once; the weights go round by readlane
+        static_assert(NR == 16, "one partial per lane of a 16-lane row");
+        const int k = L & (NR - 1);
+        const float mk = P[k * AP_W + HD], lk = P[k * AP_W + HD + 1];
+        const float M = wave_max(mk);
+        const float wk = mk == -INFINITY ? 0.f : expf(mk - M);
         float num = 0.f, den = 0.f;
 #pragma unroll
-        for (int k = 0; k < NR; ++k) {
-            const float mk = P[k * AP_W + HD];
-            const float wk = mk == -INFINITY ? 0.f : expf(mk - M);
-            den = fmaf(P[k * AP_W + HD + 1], wk, den);
-            num = fmaf(P[k * AP_W + tid()], wk, num);
+        for (int k2 = 0; k2 < NR; ++k2) {
+            const float wv = lane_value(wk, k2);
+            den = fmaf(lane_value(lk, k2), wv, den);
+            num = fmaf(P[k2 * AP_W + tid()], wv, num);
         }
         S.opart[0][tid()] = num / den;
     }

@@ -279,3 +279,62 @@ def test_frame_loop_timeout_is_an_error(sess):
     codes, eos, _ = sess.frame.run_many(sess.kv, sess.n_prefill - 1, sess.d_trail.ptr, sess.n_trail, pad, s, 0, 0, 4,
                                         skip_first=True, d_hidden=sess.d_hidden.ptr, d_logits=sess.d_logits.ptr)
     assert codes.shape == (4, 16)
+
+
+@pytest.mark.parametrize("n_past", [700, 2500])
+def test_long_context_frames_match_oracle(small_blob, n_past):
+    """Talker attention over long cached contexts on random f16 K/V rows: 44 and 157 keys per
+    key range (several score passes per wave, several value groups per wave). Two greedy frames,
+    teacher-forced: talker hidden/logits and cp logits within tolerance, codes equal to the
+    oracle's except near ties, the next step input bit-exact."""
+    import torch
+    from navi_amd import abi
+    from oracle import sampler as osamp
+    from oracle.model import Oracle
+    from gpu_util import check_greedy_frame
+    ora = Oracle(small_blob)
+    abi.device_open()
+    W = abi.DeviceWeights(small_blob, select=lambda t: t.name.startswith("talker."))
+    fr = abi.Frame(W)
+    max_pos = n_past + 4
+    L = ora.tp.n_layer
+    kv_o = ora.new_kv(max_pos)
+    kv_d = abi.KvCache(L, max_pos, 1024)
+    rng = np.random.default_rng(n_past)
+    for l in range(L):
+        k = rng.standard_normal((n_past, 1024)).astype(np.float16)
+        v = rng.standard_normal((n_past, 1024)).astype(np.float16)
+        kv_o[l][0][:n_past] = torch.from_numpy(k.astype(np.float32))
+        kv_o[l][1][:n_past] = torch.from_numpy(v.astype(np.float32))
+        kv_d.fill(l, k, v, 0)
+    step = rng.standard_normal(1024).astype(np.float32)
+    trail = rng.standard_normal(1024).astype(np.float32)
+    d_trail = abi.DeviceBuffer(trail.nbytes)
+    d_trail.upload(trail)
+    abi.upload(fr.d_step_out, step)
+    s_gpu = abi.Sampling.greedy(min_frames=4)
+    s_ora = osamp.Sampling(temperature=0.0, top_k=50, repetition_penalty=1.05, cp_temperature=0.0, cp_top_k=50,
+                           min_frames=4)
+    fr.reset()
+    fr.set_taps(True)
+    ora.reset()
+    flips = []
+    for f in range(2):
+        r = fr.run(kv_d, n_past + f, d_trail.ptr, s_gpu, 9, f)
+        assert r.ok, r.error
+        hid, lg, cpl = fr.taps()
+        dbg = {}
+        codes = list(r.codes)
+        _, step = ora.frame(s_ora, 9, f, trail, kv=kv_o, n_past=n_past + f, step_in=step, debug=dbg, force=codes)
+        e_h, c_h = compare(hid, dbg["hidden"])
+        e_l, c_l = compare(lg, dbg["logits"])
+        e_c = max(compare(cpl[p], dbg["cp_logits"][p])[0] for p in range(15))
+        c_c = min(compare(cpl[p], dbg["cp_logits"][p])[1] for p in range(15))
+        log(f"n_past {n_past + f}: hidden {e_h:.2e}/{c_h:.7f} logits {e_l:.2e}/{c_l:.7f} cp {e_c:.2e}/{c_c:.7f} codes {codes}")
+        assert e_h < TOL_ABS and c_h > TOL_COS
+        assert e_l < TOL_ABS and c_l > TOL_COS
+        assert e_c < TOL_ABS and c_c > TOL_COS
+        check_greedy_frame(f, codes, dbg, flips)
+        np.testing.assert_array_equal(abi.download(fr.d_step_out, np.float32, 1024), step)
+    assert len(flips) <= 1, flips
+    fr.close()
