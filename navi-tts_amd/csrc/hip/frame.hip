@@ -806,6 +806,7 @@ __device__ bool cp_attention(const Args &a, float qkw, int il, int p0, uint32_t 
 // ---- sampling: block_sample (sampler.h) on this block's LDS ----------------------
 
 __device__ __forceinline__ SampleLds sample_lds(Smem &S) {
+    static_assert(VT >= SAMPLE_LDS_WORDS, "sampler counters fit the idx array");
     return SampleLds{S.u.m.samp.lg, reinterpret_cast<unsigned *>(S.u.m.samp.idx), S.sred, S.sidx, &S.isel[2]};
 }
 

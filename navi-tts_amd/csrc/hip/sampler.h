@@ -29,9 +29,11 @@ __device__ __forceinline__ uint32_t pcg32_next(uint64_t &s) {
 // lanes of one atomic instruction that share a top byte, nearly all of them, spread over 4 banks);
 // passes 1-3 one 256-bin histogram each.
 constexpr int SAMPLE_HIST_WORDS = 4 * 256 + 3 * 256;
+// The sampler's LDS counters plus one 64-bit candidate mask per 64-index chunk (V <= 4096).
+constexpr int SAMPLE_LDS_WORDS = SAMPLE_HIST_WORDS + 2 * 64;
 
 // LDS the sampler works in (all block-shared): lg[V] holds the (already modified) logits on entry
-// and is overwritten; hist: SAMPLE_HIST_WORDS counters, 16-byte aligned; sred: 2 * NW floats;
+// and is overwritten; hist: SAMPLE_LDS_WORDS words, 16-byte aligned; sred: 2 * NW floats;
 // sidx: NW ints; sel: 1 int.
 struct SampleLds {
     float *lg;
@@ -51,8 +53,8 @@ struct SampleLds {
 // cleared up front, and every wave finds the digit itself from the shared histogram with a DPP
 // prefix sum. The select stops early once the chosen bin lies wholly inside the top k (its count
 // is the number still needed): the bin's lowest value then admits exactly the same survivors as
-// the k-th largest value would. The draw reads the candidates 8 chunks of 64 at a time. The
-// result is the same in every thread.
+// the k-th largest value would. The draw compacts the candidates in index order and runs the
+// fused running sum as a lane-to-lane DPP chain (below). The result is the same in every thread.
 template <int V, int BT>
 __device__ __forceinline__ int block_sample(float temperature, int top_k, uint64_t seed, const SampleLds &L) {
     constexpr int PER = V / BT, NW = BT / WAVE;
@@ -146,15 +148,36 @@ __device__ __forceinline__ int block_sample(float temperature, int top_k, uint64
         }
         thr = key_float(prefix);
     }
+    // e = e^(x - max) for the survivors; chunk c = k * NW + wave (indices 64c .. 64c + 63) records
+    // which of its lanes hold a candidate (e != 0)
+    constexpr int NCH = V / WAVE;
+    static_assert(NCH <= WAVE, "one chunk per lane in the prefix");
+    uint64_t *const cmask = reinterpret_cast<uint64_t *>(hist + SAMPLE_HIST_WORDS);
+    float e[PER];
     float ls = 0.f;
 #pragma unroll
     for (int k = 0; k < PER; ++k) {
-        const float e = x[k] >= thr ? expf(x[k] - mx) : 0.f;
-        L.lg[k * BT + tid] = e;
-        ls += e;
+        e[k] = x[k] >= thr ? expf(x[k] - mx) : 0.f;
+        ls += e[k];
+        const uint64_t bm = __ballot(e[k] != 0.f);
+        if (lane == 0) cmask[k * NW + wave] = bm;
     }
     ls = wave_sum(ls);
     if (lane == 0) L.sred[NW + wave] = ls;
+    __syncthreads();
+    // the candidates compacted in index order into lg (the logits are in registers by now): chunk
+    // c starts after the candidates of chunks 0..c-1, a DPP prefix sum with one chunk per lane
+    const uint64_t lm = lane < NCH ? cmask[lane] : 0ull;
+    const int lc = __builtin_popcountll(lm);
+    const int incl = wave_incl_scan(lc), excl = incl - lc;
+    const int ncand = __builtin_amdgcn_readlane(incl, WAVE - 1);
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+        const uint64_t bm = __ballot(e[k] != 0.f);
+        const int below = static_cast<int>(__builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(bm >> 32),
+                                                                     __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(bm), 0u)));
+        if (e[k] != 0.f) L.lg[__builtin_amdgcn_readlane(excl, k * NW + wave) + below] = e[k];
+    }
     __syncthreads();
     if (wave == 0) {
         float ssum = 0.f;
@@ -165,25 +188,41 @@ __device__ __forceinline__ int block_sample(float temperature, int top_k, uint64
         (void) pcg32_next(st); (void) pcg32_next(st); (void) pcg32_next(st);
         const float u = static_cast<float>(pcg32_next(st) >> 8) * (1.0f / 16777216.0f);
         int chosen = V - 1;
-        float cum = 0.f;
-        bool found = false;
-        // index i = k * BT + tid = 64 c + lane: chunk c holds indices 64c .. 64c + 63, in order
-        constexpr int NCH = V / WAVE, BATCH = 8;
-        static_assert(NCH % BATCH == 0, "draw batches");
-        for (int c0 = 0; c0 < NCH && !found; c0 += BATCH) {
-            float ev[BATCH];
+        float carry = 0.f;
+        // The running sum over the candidates, 64 at a time: lane j takes candidate g + j, and
+        // every step lane j recomputes fma(p_j, inv, value of lane j - 1) (lane 0: the carry),
+        // DPP wave_shr:1 moving the values one lane up. After s steps lanes 0..s-1 hold exactly
+        // the sequential sums, so m steps give the reference's chain for the group. The sums
+        // never decrease, so the lanes below u are a prefix and their count is the pick.
+        for (int g = 0; g < ncand; g += WAVE) {
+            const int m = min(WAVE, ncand - g);
+            const float pc = lane < m ? L.lg[g + lane] : 0.f;
+            float cum = carry;
+            // steps past m recompute the same values (lane j - 1 is final by then): 8 per trip
+            for (int step = 0; step < m; step += 8) {
 #pragma unroll
-            for (int q = 0; q < BATCH; ++q) ev[q] = L.lg[(c0 + q) * WAVE + lane];
-#pragma unroll
-            for (int q = 0; q < BATCH; ++q) {
-                uint64_t nz = found ? 0ull : __ballot(ev[q] != 0.f);
-                while (nz) {
-                    const int b = static_cast<int>(__builtin_ctzll(nz));
-                    nz &= nz - 1;
-                    cum = fmaf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(ev[q]), b)), inv, cum);
-                    if (cum >= u) { chosen = (c0 + q) * WAVE + b; found = true; nz = 0; }
+                for (int q = 0; q < 8; ++q) {
+                    const float sh = __int_as_float(
+                        __builtin_amdgcn_update_dpp(__float_as_int(carry), __float_as_int(cum), 0x138, 0xF, 0xF, false));
+                    cum = fmaf(pc, inv, sh);
                 }
             }
+            const int nb = __builtin_popcountll(__ballot(lane < m && cum < u));
+            if (nb < m) {
+                // candidate pos = g + nb: its chunk is the first whose inclusive count exceeds pos,
+                // and it is the (pos - start)-th set lane of that chunk's mask
+                const int pos = g + nb;
+                const int cs = __builtin_popcountll(__ballot(lane < NCH && incl <= pos));
+                const int r = pos - __builtin_amdgcn_readlane(excl, cs);
+                const uint32_t mlo = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(lm)), cs));
+                const uint32_t mhi = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(lm >> 32)), cs));
+                const uint64_t mk = (static_cast<uint64_t>(mhi) << 32) | mlo;
+                const int rank = static_cast<int>(__builtin_amdgcn_mbcnt_hi(mhi, __builtin_amdgcn_mbcnt_lo(mlo, 0u)));
+                const uint64_t hit = __ballot(((mk >> lane) & 1ull) && rank == r);
+                chosen = cs * WAVE + static_cast<int>(__builtin_ctzll(hit));
+                break;
+            }
+            carry = lane_value(cum, m - 1);
         }
         if (lane == 0) *L.sel = chosen;
     }

@@ -277,7 +277,7 @@ __global__ void __launch_bounds__(BT) k_st_talker_sample(const float *logits, in
                                                          float *cp_x, int32_t *codes) {
     constexpr int VT = 3072;
     __shared__ float lg[VT];
-    __shared__ __align__(16) unsigned hist[SAMPLE_HIST_WORDS];
+    __shared__ __align__(16) unsigned hist[SAMPLE_LDS_WORDS];
     __shared__ float sred[2 * NW];
     __shared__ int sidx[NW], sel;
     const int m = blockIdx.x;
@@ -312,7 +312,7 @@ __global__ void __launch_bounds__(BT) k_st_cp_sample(const float *logits, const 
                                                      const uint16_t *next_emb, int H, float *x, int32_t *codes) {
     constexpr int VC = 2048;
     __shared__ float lg[VC];
-    __shared__ __align__(16) unsigned hist[SAMPLE_HIST_WORDS];
+    __shared__ __align__(16) unsigned hist[SAMPLE_LDS_WORDS];
     __shared__ float sred[2 * NW];
     __shared__ int sidx[NW], sel;
     const int m = blockIdx.x;
