@@ -326,6 +326,10 @@ float *navi_streams_step_out(navi_streams *h);           /* device f32 [max_stre
  * [max_streams][hidden], raw codec logits [max_streams][talker vocab] and the 15 cp logit rows
  * [max_streams][15][cp vocab] to device buffers. */
 navi_status navi_streams_set_taps(navi_streams *h, int32_t on);
+/* Replays each run from a captured HIP graph (on by default; runs with taps on are always
+ * enqueued directly). Off: every kernel is launched by the host each run, the reference point
+ * the graph replays are tested against. */
+navi_status navi_streams_set_graphs(navi_streams *h, int32_t on);
 const float *navi_streams_tap_hidden(const navi_streams *h);
 const float *navi_streams_tap_logits(const navi_streams *h);
 const float *navi_streams_tap_cp_logits(const navi_streams *h);

@@ -48,6 +48,26 @@ __device__ __forceinline__ float wave_sum(float v) {
     return lane_value(v, 63);
 }
 
+// wave_sum of N values at once, one DPP stage for all of them before the next (the N chains
+// interleave instead of waiting out each step's hazard); each result as wave_sum's.
+template <int N>
+__device__ __forceinline__ void wave_sum_n(float (&v)[N]) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] += dpp_red<0xB1>(v[i]);
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] += dpp_red<0x4E>(v[i]);
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] += dpp_red<0x141>(v[i]);
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] += dpp_red<0x140>(v[i]);
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] += dpp_rows<0x142, 0xA>(v[i], 0.f);
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] += dpp_rows<0x143, 0xC>(v[i], 0.f);
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] = lane_value(v[i], 63);
+}
+
 __device__ __forceinline__ float wave_max(float v) {
     v = fmaxf(v, dpp_red<0xB1>(v));
     v = fmaxf(v, dpp_red<0x4E>(v));
@@ -105,6 +125,25 @@ __device__ __forceinline__ float dot8(const uint4 w, const float *x, float acc) 
 #pragma unroll
     for (int i = 0; i < 8; ++i) acc = fmaf(static_cast<float>(h[i]), x[i], acc);
     return acc;
+}
+
+// acc[r] = this lane's 16 weights of row r (two 16-byte fragments) times xf, accumulated in
+// dot8(w[r][1], xf[1], dot8(w[r][0], xf[0], 0))'s order; element-major so the R chains interleave.
+template <int R>
+__device__ __forceinline__ void dot16_rows(const uint4 (&w)[R][2], const float (&xf)[2][8], float (&acc)[R]) {
+    half8_t h[R][2];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        __builtin_memcpy(&h[r][0], &w[r][0], 16);
+        __builtin_memcpy(&h[r][1], &w[r][1], 16);
+        acc[r] = 0.f;
+    }
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+#pragma unroll
+            for (int r = 0; r < R; ++r) acc[r] = fmaf(static_cast<float>(h[r][c][i]), xf[c][i], acc[r]);
 }
 
 // Global memory accessed through address space 1, so the compiler emits global_* (counted by

@@ -417,13 +417,12 @@ __device__ __forceinline__ void qkv_phase(const Args &a, const Regs &R, Smem &S,
     const int row0 = blk() * (QKV / NB) + wave() * 4;
 #pragma unroll
     for (int t = 0; t < T; ++t) {
-        float xf[2][8];
+        float xf[2][8], d[4];
         xfrag<2>(S.xn[t], 0, xf);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const float d = wave_sum(dot8(R.qkv[r][1], xf[1], dot8(R.qkv[r][0], xf[0], 0.f))) * sc[t];
-            if (lane() == r) mb_put(a.mb + MB_QKV + t * QKV + row0 + r, d, tag);
-        }
+        dot16_rows<4>(R.qkv, xf, d);
+        wave_sum_n<4>(d);
+        const int L = lane();
+        if (L < 4) mb_put(a.mb + MB_QKV + t * QKV + row0 + L, (L == 0 ? d[0] : L == 1 ? d[1] : L == 2 ? d[2] : d[3]) * sc[t], tag);
     }
 }
 
@@ -454,8 +453,10 @@ __device__ __forceinline__ void gu_phase(const Args &a, const Regs &R, Smem &S, 
         float xf[2][8];
         xfrag<2>(S.xn[t], 0, xf);
         float d[6];
+        dot16_rows<6>(R.gu, xf, d);
+        wave_sum_n<6>(d);
 #pragma unroll
-        for (int r = 0; r < 6; ++r) d[r] = wave_sum(dot8(R.gu[r][1], xf[1], dot8(R.gu[r][0], xf[0], 0.f))) * sc[t];
+        for (int r = 0; r < 6; ++r) d[r] *= sc[t];
         // lane 8r + c publishes h row 3w + r to copy c
         const int r = lane() >> 3, c = lane() & 7;
         if (r < 3) {
@@ -927,13 +928,13 @@ __global__ void __launch_bounds__(BT, 1) k_frame(Args a, const Weights *__restri
         load_norm(R.fn, W.cp_norm);
         const uint32_t t_lg = seq.next();
         {
-            float xf[2][8];
+            float xf[2][8], d[3];
             xfrag<2>(S.xn[0], 0, xf);
+            dot16_rows<3>(R.th, xf, d);
+            wave_sum_n<3>(d);
 #pragma unroll
-            for (int r = 0; r < 3; ++r) {
-                const float d = wave_sum(dot8(R.th[r][1], xf[1], dot8(R.th[r][0], xf[0], 0.f))) * hsc[0];
-                if (lane() < NREP) mb_put(a.mb + lane() * MB_WORDS + MB_LG + blk() * (VT / NB) + wave() * 3 + r, d, t_lg);
-            }
+            for (int r = 0; r < 3; ++r)
+                if (lane() < NREP) mb_put(a.mb + lane() * MB_WORDS + MB_LG + blk() * (VT / NB) + wave() * 3 + r, d[r] * hsc[0], t_lg);
         }
         if (!gather<VT, VT / NB>(a, MB_LG, t_lg, S.u.m.samp.lg, S)) return;
         // the post-norm hidden the code predictor takes: each thread scales the elements it wrote
@@ -997,13 +998,13 @@ __global__ void __launch_bounds__(BT, 1) k_frame(Args a, const Weights *__restri
         norm_scale<1>(a.eps_c, hsc, S);
         const uint32_t t_lg = seq.next();
         {
-            float xf[2][8];
+            float xf[2][8], d[2];
             xfrag<2>(S.xn[0], 0, xf);
+            dot16_rows<2>(R.lm, xf, d);
+            wave_sum_n<2>(d);
 #pragma unroll
-            for (int r = 0; r < 2; ++r) {
-                const float d = wave_sum(dot8(R.lm[r][1], xf[1], dot8(R.lm[r][0], xf[0], 0.f))) * hsc[0];
-                if (lane() < NREP) mb_put(a.mb + lane() * MB_WORDS + MB_LG + blk() * (VC / NB) + wave() * 2 + r, d, t_lg);
-            }
+            for (int r = 0; r < 2; ++r)
+                if (lane() < NREP) mb_put(a.mb + lane() * MB_WORDS + MB_LG + blk() * (VC / NB) + wave() * 2 + r, d[r] * hsc[0], t_lg);
         }
         if (!gather<VC, VC / NB>(a, MB_LG, t_lg, S.u.m.samp.lg, S)) return;
         if (a.tap_cp_logits && blk() == 0) {

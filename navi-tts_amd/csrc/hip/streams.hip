@@ -22,6 +22,7 @@
 #include "sampler.h"
 
 #include <algorithm>
+#include <cstring>
 #include <cmath>
 #include <string>
 #include <vector>
@@ -360,6 +361,13 @@ struct LayerW {
 using namespace navi_amd;
 using namespace navi_amd::ms;
 
+// The step's activations and split-K workspace, and the HIP stream it runs on.
+struct StreamWork {
+    float *x = nullptr, *xn = nullptr, *q = nullptr, *att = nullptr, *h = nullptr, *part = nullptr, *apart = nullptr;
+    float *lg = nullptr;
+    hipStream_t st = nullptr;
+};
+
 struct navi_streams {
     navi_model_params p{};
     int H = 0, NQ = 0, NKV = 0, QD = 0, KVD = 0, F = 0, VT = 0, VC = 0, TL = 0, CL = 0;
@@ -370,9 +378,8 @@ struct navi_streams {
     const uint16_t *codec_head = nullptr, *codec_emb = nullptr;
     EmbTable cp_emb{};
     const uint16_t *lm_head[CPH] = {};
-    // work buffers
-    float *x = nullptr, *xn = nullptr, *q = nullptr, *att = nullptr, *h = nullptr, *part = nullptr, *apart = nullptr;
-    float *lg = nullptr, *step = nullptr, *invf_t = nullptr, *invf_c = nullptr;
+    StreamWork work;
+    float *step = nullptr, *invf_t = nullptr, *invf_c = nullptr;
     size_t part_floats = 0;
     uint16_t *cpk = nullptr, *cpv = nullptr;
     uint8_t *seen = nullptr;
@@ -383,9 +390,15 @@ struct navi_streams {
     std::vector<uint16_t *> kh, vh;                 // host copy of the tables
     std::vector<StreamMeta> hmeta;
     float *tap = nullptr;                           // taps: hidden [ms][H] | logits [ms][VT] | cp logits [ms][15][VC]
+    bool taps_on = false;
     hipEvent_t ev0 = nullptr, ev1 = nullptr;
     double last_ms = 0;
     std::vector<void *> owned;
+    // The step as one HIP graph (about 950 launches), captured again when what the kernels take by
+    // value changes: stream count, key ranges, input pointers, sampling arguments.
+    bool use_graphs = true;
+    hipGraphExec_t gexec = nullptr;
+    std::vector<int> gkey;
 
     float *tap_hidden() const { return tap; }
     float *tap_logits() const { return tap ? tap + static_cast<size_t>(ms) * H : nullptr; }
@@ -402,6 +415,7 @@ struct navi_streams {
     }
 
     ~navi_streams() {
+        if (gexec) (void) hipGraphExecDestroy(gexec);
         if (ev0) (void) hipEventDestroy(ev0);
         if (ev1) (void) hipEventDestroy(ev1);
         for (void *v : owned) (void) hipFree(v);
@@ -445,20 +459,91 @@ navi_status bind_layers(const char *who, const navi_tensor_ref *t, int n, const 
 // One decoder layer over `rows` rows (x: residual in/out, xn: its RMSNorm with ln1 on entry, the
 // next norm's output on exit). attend(part, S) consumes the q|k|v partials and writes h.att.
 template <class Attend>
-void layer(navi_streams &h, const LayerW &w, const float *next_norm, float eps, int rows, Attend attend, hipStream_t s) {
+void layer(navi_streams &h, StreamWork &g, const LayerW &w, const float *next_norm, float eps, int rows, Attend attend) {
     const int H = h.H, QKVW = h.QD + 2 * h.KVD;
+    hipStream_t s = g.st;
     int S = pf::pick_splits(rows, H, QKVW);
-    pf::launch_partial3(h.xn, H, rows, w.wq, h.QD, w.wk, h.KVD, w.wv, h.KVD, H, S, h.part, QKVW, 0, h.flag, s);
+    pf::launch_partial3(g.xn, H, rows, w.wq, h.QD, w.wk, h.KVD, w.wv, h.KVD, H, S, g.part, QKVW, 0, h.flag, s);
     attend(S);
     S = pf::pick_splits(rows, h.QD, H);
-    pf::launch_partial(h.att, h.QD, rows, w.wo, h.QD, H, S, h.part, H, 0, h.flag, s);
-    pf::launch_resid_norm(h.part, S, nullptr, h.x, w.ln2, eps, h.xn, rows, H, s);
+    pf::launch_partial(g.att, h.QD, rows, w.wo, h.QD, H, S, g.part, H, 0, h.flag, s);
+    pf::launch_resid_norm(g.part, S, nullptr, g.x, w.ln2, eps, g.xn, rows, H, s);
     S = pf::pick_splits(rows, H, 2 * h.F);
-    pf::launch_partial3(h.xn, H, rows, w.wg, h.F, w.wu, h.F, nullptr, 0, H, S, h.part, 2 * h.F, 0, h.flag, s);
-    pf::launch_swiglu(h.part, S, rows, h.F, h.h, s);
+    pf::launch_partial3(g.xn, H, rows, w.wg, h.F, w.wu, h.F, nullptr, 0, H, S, g.part, 2 * h.F, 0, h.flag, s);
+    pf::launch_swiglu(g.part, S, rows, h.F, g.h, s);
     S = pf::pick_splits(rows, h.F, H);
-    pf::launch_partial(h.h, h.F, rows, w.wd, h.F, H, S, h.part, H, 0, h.flag, s);
-    pf::launch_resid_norm(h.part, S, nullptr, h.x, next_norm, eps, h.xn, rows, H, s);
+    pf::launch_partial(g.h, h.F, rows, w.wd, h.F, H, S, g.part, H, 0, h.flag, s);
+    pf::launch_resid_norm(g.part, S, nullptr, g.x, next_norm, eps, g.xn, rows, H, s);
+}
+
+// The frame of streams i0 .. i0 + n - 1 (per-stream state at those offsets), on g.st.
+navi_status run_group(navi_streams *h, StreamWork &g, int i0, int n, int zsplits, const float *step_in,
+                      const float *d_trailing, const SampleArgs &sa, char *err, size_t errlen) {
+    hipStream_t s = g.st;
+    const int H = h->H, QKVW = h->QD + 2 * h->KVD;
+    const float et = h->p.talker.rms_eps, ec = h->p.cp.rms_eps;
+    const StreamMeta *meta = h->meta + i0;
+    uint8_t *seen = h->seen + static_cast<size_t>(i0) * h->VT;
+    int32_t *codes = h->codes + static_cast<size_t>(i0) * NCB;
+    uint16_t *cpk = h->cpk + static_cast<size_t>(i0) * h->CL * NCB * h->KVD;
+    uint16_t *cpv = h->cpv + static_cast<size_t>(i0) * h->CL * NCB * h->KVD;
+
+    // talker step over the group's streams
+    pf::launch_resid_norm(nullptr, 0, step_in, g.x, h->tl[0].ln1, et, g.xn, n, H, s);
+    for (int l = 0; l < h->TL; ++l) {
+        const float *next = l + 1 < h->TL ? h->tl[l + 1].ln1 : h->tl_norm;
+        uint16_t *const *kt = h->ktab + static_cast<size_t>(l) * h->ms + i0;
+        uint16_t *const *vt = h->vtab + static_cast<size_t>(l) * h->ms + i0;
+        layer(*h, g, h->tl[l], next, et, n, [&](int S) {
+            hipLaunchKernelGGL(k_st_qkv_finish, dim3(n), dim3(BT), QKVW * sizeof(float), s, g.part, S, n, h->NQ, h->NKV,
+                               h->tl[l].qn, h->tl[l].kn, et, h->invf_t, meta, kt, vt, g.q);
+            hipLaunchKernelGGL(k_st_attn, dim3(n, h->NKV, zsplits), dim3(BT), 0, s, g.q, meta, kt, vt, h->NQ, h->NKV, h->splits,
+                               g.apart);
+            hipLaunchKernelGGL(k_st_attn_combine, dim3(n, h->NKV), dim3(BT), 0, s, g.apart, meta, h->NQ, h->NKV, h->splits,
+                               g.att);
+        });
+    }
+    // head + codebook 0; the cp input rows (hidden, codec_emb[cb0]) per stream
+    int S = pf::pick_splits(n, H, h->VT);
+    pf::launch_partial(g.xn, H, n, h->codec_head, H, h->VT, S, g.part, h->VT, 0, h->flag, s);
+    pf::launch_finish_linear(g.part, S, n, h->VT, nullptr, nullptr, 0, g.lg, h->VT, s);
+    if (h->taps_on) {
+        NAVI_TRY_HIP(hipMemcpyAsync(h->tap_hidden() + static_cast<size_t>(i0) * H, g.xn, static_cast<size_t>(n) * H * 4,
+                                    hipMemcpyDeviceToDevice, s), err, errlen);
+        NAVI_TRY_HIP(hipMemcpyAsync(h->tap_logits() + static_cast<size_t>(i0) * h->VT, g.lg, static_cast<size_t>(n) * h->VT * 4,
+                                    hipMemcpyDeviceToDevice, s), err, errlen);
+    }
+    hipLaunchKernelGGL(k_st_talker_sample, dim3(n), dim3(BT), 0, s, g.lg, h->VT, meta, seen, sa, g.xn, h->codec_emb, H, g.x,
+                       codes);
+
+    // code predictor: positions 0 and 1 as one 2-row pass per stream, then one row per position
+    for (int pos = 1; pos < NCB; ++pos) {
+        const int T = pos == 1 ? 2 : 1, p0 = pos == 1 ? 0 : pos, rows = n * T;
+        pf::launch_resid_norm(nullptr, 0, g.x, g.x, h->cl[0].ln1, ec, g.xn, rows, H, s);
+        for (int l = 0; l < h->CL; ++l) {
+            const float *next = l + 1 < h->CL ? h->cl[l + 1].ln1 : h->cp_norm;
+            layer(*h, g, h->cl[l], next, ec, rows, [&](int S2) {
+                hipLaunchKernelGGL(k_st_cp_attn, dim3(n, h->NKV), dim3(BT), 0, s, g.part, S2, rows, T, p0, h->NQ, h->NKV,
+                                   h->cl[l].qn, h->cl[l].kn, ec, h->invf_c, l, h->CL, cpk, cpv, g.att);
+            });
+        }
+        // lm_head[pos - 1] on the last row of each stream
+        S = pf::pick_splits(n, H, h->VC);
+        pf::launch_partial(g.xn + static_cast<size_t>(T - 1) * H, T * H, n, h->lm_head[pos - 1], H, h->VC, S, g.part, h->VC, 0,
+                           h->flag, s);
+        pf::launch_finish_linear(g.part, S, n, h->VC, nullptr, nullptr, 0, g.lg, h->VC, s);
+        if (h->taps_on)
+            NAVI_TRY_HIP(hipMemcpy2DAsync(h->tap_cp() + (static_cast<size_t>(i0) * CPH + (pos - 1)) * h->VC,
+                                          static_cast<size_t>(CPH) * h->VC * 4, g.lg, static_cast<size_t>(h->VC) * 4,
+                                          static_cast<size_t>(h->VC) * 4, n, hipMemcpyDeviceToDevice, s),
+                         err, errlen);
+        hipLaunchKernelGGL(k_st_cp_sample, dim3(n), dim3(BT), 0, s, g.lg, meta, sa, pos,
+                           pos < CPH ? h->cp_emb.cp_emb[pos - 1] : nullptr, H, g.x, codes);
+    }
+    hipLaunchKernelGGL(k_st_assemble, dim3(n), dim3(BT), 0, s, codes, h->codec_emb, h->cp_emb,
+                       d_trailing + static_cast<size_t>(i0) * H, H, h->step + static_cast<size_t>(i0) * H);
+    NAVI_TRY_HIP(hipGetLastError(), err, errlen);
+    return NAVI_OK;
 }
 
 } // namespace
@@ -526,14 +611,16 @@ navi_status navi_streams_create(const navi_model_params *p, const navi_tensor_re
     h->part_floats = pf_need;
 #define SA(ptr, n_) \
     if ((st = h->alloc(ptr, (n_), err, errlen)) != NAVI_OK) return fail(st)
-    SA(h->x, R * H);
-    SA(h->xn, R * H);
-    SA(h->q, static_cast<size_t>(max_streams) * h->QD);
-    SA(h->att, R * h->QD);
-    SA(h->h, R * h->F);
-    SA(h->part, pf_need);
-    SA(h->apart, static_cast<size_t>(max_streams) * h->NKV * h->splits * 2 * (HD + 2));
-    SA(h->lg, static_cast<size_t>(max_streams) * h->VT);
+    StreamWork &g = h->work;
+    SA(g.x, R * H);
+    SA(g.xn, R * H);
+    SA(g.q, static_cast<size_t>(max_streams) * h->QD);
+    SA(g.att, R * h->QD);
+    SA(g.h, R * h->F);
+    SA(g.part, pf_need);
+    SA(g.apart, static_cast<size_t>(max_streams) * h->NKV * h->splits * 2 * (HD + 2));
+    SA(g.lg, static_cast<size_t>(max_streams) * h->VT);
+    g.st = device_state().stream;
     SA(h->step, static_cast<size_t>(max_streams) * H);
     SA(h->invf_t, HD / 2);
     SA(h->invf_c, HD / 2);
@@ -579,11 +666,20 @@ navi_status navi_streams_reset(navi_streams *h, int32_t stream) {
     return hipMemsetAsync(h->seen + off, 0, n, s) == hipSuccess && hipStreamSynchronize(s) == hipSuccess ? NAVI_OK : NAVI_ERR_HIP;
 }
 
+navi_status navi_streams_set_graphs(navi_streams *h, int32_t on) {
+    if (!h) return NAVI_ERR_INVALID;
+    h->use_graphs = on != 0;
+    return NAVI_OK;
+}
+
 navi_status navi_streams_set_taps(navi_streams *h, int32_t on) {
     if (!h) return NAVI_ERR_INVALID;
+    h->taps_on = on != 0;
     if (!on || h->tap) return NAVI_OK;
     char err[8];
-    return h->alloc(h->tap, static_cast<size_t>(h->ms) * (h->H + h->VT + CPH * h->VC), err, sizeof err);
+    const navi_status st = h->alloc(h->tap, static_cast<size_t>(h->ms) * (h->H + h->VT + CPH * h->VC), err, sizeof err);
+    if (st != NAVI_OK) h->taps_on = false;
+    return st;
 }
 
 const float *navi_streams_tap_hidden(const navi_streams *h) { return h ? h->tap_hidden() : nullptr; }
@@ -606,7 +702,6 @@ navi_status navi_streams_run(navi_streams *h, int32_t n, const navi_kv_view *kv,
         return NAVI_ERR_INVALID;
     }
     bool tab_changed = false;
-    int zsplits = 1;                                        // key ranges of the longest context
     for (int i = 0; i < n; ++i) {
         if (kv[i].n_layer != h->TL || kv[i].kv_dim != h->KVD || !kv[i].k || !kv[i].v) {
             set_err(err, errlen, "streams: stream %d: KV cache layer count or width mismatch", i);
@@ -624,7 +719,6 @@ navi_status navi_streams_run(navi_streams *h, int32_t n, const navi_kv_view *kv,
                 tab_changed = true;
             }
         }
-        zsplits = std::max(zsplits, (n_past[i] + 1 + KPS - 1) / KPS);
         StreamMeta &m = h->hmeta[i];
         m.n_past = n_past[i];
         m.frame_index = frame_index[i];
@@ -632,7 +726,6 @@ navi_status navi_streams_run(navi_streams *h, int32_t n, const navi_kv_view *kv,
         m.cp_seed = splitmix64(m.talker_seed ^ 0x9FB21C651E98DF25ull);
     }
     hipStream_t s = device_state().stream;
-    const int H = h->H, QKVW = h->QD + 2 * h->KVD;
     if (tab_changed) {
         NAVI_TRY_HIP(hipMemcpyAsync(h->ktab, h->kh.data(), h->kh.size() * sizeof(uint16_t *), hipMemcpyHostToDevice, s), err, errlen);
         NAVI_TRY_HIP(hipMemcpyAsync(h->vtab, h->vh.data(), h->vh.size() * sizeof(uint16_t *), hipMemcpyHostToDevice, s), err, errlen);
@@ -642,61 +735,46 @@ navi_status navi_streams_run(navi_streams *h, int32_t n, const navi_kv_view *kv,
     NAVI_TRY_HIP(hipEventRecord(h->ev0, s), err, errlen);
     SampleArgs sa{smp->temperature, smp->repetition_penalty, smp->cp_temperature, smp->top_k, smp->cp_top_k, smp->min_frames,
                   h->p.codec_eos_id, h->VT - 1024};
-    const float et = h->p.talker.rms_eps, ec = h->p.cp.rms_eps;
-
-    // talker step over the n streams
-    pf::launch_resid_norm(nullptr, 0, d_step_in ? d_step_in : h->step, h->x, h->tl[0].ln1, et, h->xn, n, H, s);
-    for (int l = 0; l < h->TL; ++l) {
-        const float *next = l + 1 < h->TL ? h->tl[l + 1].ln1 : h->tl_norm;
-        layer(*h, h->tl[l], next, et, n, [&](int S) {
-            hipLaunchKernelGGL(k_st_qkv_finish, dim3(n), dim3(BT), QKVW * sizeof(float), s, h->part, S, n, h->NQ, h->NKV,
-                               h->tl[l].qn, h->tl[l].kn, et, h->invf_t, h->meta, h->ktab + static_cast<size_t>(l) * h->ms,
-                               h->vtab + static_cast<size_t>(l) * h->ms, h->q);
-            hipLaunchKernelGGL(k_st_attn, dim3(n, h->NKV, zsplits), dim3(BT), 0, s, h->q, h->meta,
-                               h->ktab + static_cast<size_t>(l) * h->ms, h->vtab + static_cast<size_t>(l) * h->ms, h->NQ,
-                               h->NKV, h->splits, h->apart);
-            hipLaunchKernelGGL(k_st_attn_combine, dim3(n, h->NKV), dim3(BT), 0, s, h->apart, h->meta, h->NQ, h->NKV, h->splits,
-                               h->att);
-        }, s);
-    }
-    // head + codebook 0; the cp input rows (hidden, codec_emb[cb0]) per stream
-    int S = pf::pick_splits(n, H, h->VT);
-    pf::launch_partial(h->xn, H, n, h->codec_head, H, h->VT, S, h->part, h->VT, 0, h->flag, s);
-    pf::launch_finish_linear(h->part, S, n, h->VT, nullptr, nullptr, 0, h->lg, h->VT, s);
-    if (h->tap) {
-        NAVI_TRY_HIP(hipMemcpyAsync(h->tap_hidden(), h->xn, static_cast<size_t>(n) * H * 4, hipMemcpyDeviceToDevice, s), err, errlen);
-        NAVI_TRY_HIP(hipMemcpyAsync(h->tap_logits(), h->lg, static_cast<size_t>(n) * h->VT * 4, hipMemcpyDeviceToDevice, s), err,
-                     errlen);
-    }
-    hipLaunchKernelGGL(k_st_talker_sample, dim3(n), dim3(BT), 0, s, h->lg, h->VT, h->meta, h->seen, sa, h->xn, h->codec_emb, H,
-                       h->x, h->codes);
-
-    // code predictor: positions 0 and 1 as one 2-row pass per stream, then one row per position
-    for (int pos = 1; pos < NCB; ++pos) {
-        const int T = pos == 1 ? 2 : 1, p0 = pos == 1 ? 0 : pos, rows = n * T;
-        pf::launch_resid_norm(nullptr, 0, h->x, h->x, h->cl[0].ln1, ec, h->xn, rows, H, s);
-        for (int l = 0; l < h->CL; ++l) {
-            const float *next = l + 1 < h->CL ? h->cl[l + 1].ln1 : h->cp_norm;
-            layer(*h, h->cl[l], next, ec, rows, [&](int S2) {
-                hipLaunchKernelGGL(k_st_cp_attn, dim3(n, h->NKV), dim3(BT), 0, s, h->part, S2, rows, T, p0, h->NQ, h->NKV,
-                                   h->cl[l].qn, h->cl[l].kn, ec, h->invf_c, l, h->CL, h->cpk, h->cpv, h->att);
-            }, s);
+    // the step after the uploads above, replayed from a graph unless taps are on or graphs are off
+    int zs = 1;                                             // key ranges of the longest context
+    for (int i = 0; i < n; ++i) zs = std::max(zs, (n_past[i] + 1 + KPS - 1) / KPS);
+    const float *step_base = d_step_in ? d_step_in : h->step;
+    auto enqueue = [&]() { return run_group(h, h->work, 0, n, zs, step_base, d_trailing, sa, err, errlen); };
+    if (h->use_graphs && !h->taps_on) {
+        std::vector<int> key{n, zs};
+        for (const void *ptr : {static_cast<const void *>(step_base), static_cast<const void *>(d_trailing)}) {
+            const uint64_t u = reinterpret_cast<uint64_t>(ptr);
+            key.push_back(static_cast<int>(u & 0xFFFFFFFFu));
+            key.push_back(static_cast<int>(u >> 32));
         }
-        // lm_head[pos - 1] on the last row of each stream
-        S = pf::pick_splits(n, H, h->VC);
-        pf::launch_partial(h->xn + static_cast<size_t>(T - 1) * H, T * H, n, h->lm_head[pos - 1], H, h->VC, S, h->part, h->VC, 0,
-                           h->flag, s);
-        pf::launch_finish_linear(h->part, S, n, h->VC, nullptr, nullptr, 0, h->lg, h->VC, s);
-        if (h->tap)
-            NAVI_TRY_HIP(hipMemcpy2DAsync(h->tap_cp() + static_cast<size_t>(pos - 1) * h->VC, static_cast<size_t>(CPH) * h->VC * 4,
-                                          h->lg, static_cast<size_t>(h->VC) * 4, static_cast<size_t>(h->VC) * 4, n,
-                                          hipMemcpyDeviceToDevice, s),
-                         err, errlen);
-        hipLaunchKernelGGL(k_st_cp_sample, dim3(n), dim3(BT), 0, s, h->lg, h->meta, sa, pos,
-                           pos < CPH ? h->cp_emb.cp_emb[pos - 1] : nullptr, H, h->x, h->codes);
+        int sw[sizeof(SampleArgs) / sizeof(int)];
+        static_assert(sizeof(SampleArgs) % sizeof(int) == 0, "sampling args as words");
+        std::memcpy(sw, &sa, sizeof sa);
+        key.insert(key.end(), sw, sw + sizeof sw / sizeof sw[0]);
+        if (!h->gexec || key != h->gkey) {
+            if (h->gexec) {
+                (void) hipGraphExecDestroy(h->gexec);
+                h->gexec = nullptr;
+            }
+            NAVI_TRY_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal), err, errlen);
+            const navi_status st = enqueue();
+            hipGraph_t graph = nullptr;
+            const hipError_t ec = hipStreamEndCapture(s, &graph);
+            if (st != NAVI_OK) {
+                if (graph) (void) hipGraphDestroy(graph);
+                return st;
+            }
+            NAVI_TRY_HIP(ec, err, errlen);
+            const hipError_t ei = hipGraphInstantiateWithFlags(&h->gexec, graph, 0);
+            (void) hipGraphDestroy(graph);
+            NAVI_TRY_HIP(ei, err, errlen);
+            h->gkey = key;
+        }
+        NAVI_TRY_HIP(hipGraphLaunch(h->gexec, s), err, errlen);
+    } else {
+        const navi_status st = enqueue();
+        if (st != NAVI_OK) return st;
     }
-    hipLaunchKernelGGL(k_st_assemble, dim3(n), dim3(BT), 0, s, h->codes, h->codec_emb, h->cp_emb, d_trailing, H, h->step);
-    NAVI_TRY_HIP(hipGetLastError(), err, errlen);
     NAVI_TRY_HIP(hipEventRecord(h->ev1, s), err, errlen);
     uint32_t bad = 0;
     NAVI_TRY_HIP(hipMemcpyAsync(codes_out, h->codes, static_cast<size_t>(n) * NCB * sizeof(int32_t), hipMemcpyDeviceToHost, s), err,

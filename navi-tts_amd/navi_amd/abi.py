@@ -31,7 +31,8 @@ EXPORTS = [
     "navi_vocoder_create", "navi_vocoder_destroy", "navi_vocoder_reset", "navi_vocoder_decode",
     "navi_vocoder_samples_per_frame", "navi_vocoder_max_chunk_frames", "navi_vocoder_last_ms", "navi_synth",
     "navi_streams_create", "navi_streams_destroy", "navi_streams_reset", "navi_streams_run", "navi_streams_step_out",
-    "navi_streams_max_streams", "navi_streams_last_ms", "navi_streams_set_taps", "navi_streams_tap_hidden",
+    "navi_streams_max_streams", "navi_streams_last_ms", "navi_streams_set_taps", "navi_streams_set_graphs",
+    "navi_streams_tap_hidden",
     "navi_streams_tap_logits", "navi_streams_tap_cp_logits",
 ]
 
@@ -203,6 +204,7 @@ def lib() -> C.CDLL:
     L.navi_streams_run.argtypes = [C.c_void_p, C.c_int32, C.POINTER(KvView), C.c_void_p, C.c_void_p, C.c_void_p,
                                    C.POINTER(Sampling), C.c_void_p, C.c_void_p, C.c_void_p, E, C.c_size_t]
     L.navi_streams_set_taps.argtypes = [C.c_void_p, C.c_int32]
+    L.navi_streams_set_graphs.argtypes = [C.c_void_p, C.c_int32]
     for f in ("navi_streams_step_out", "navi_streams_tap_hidden", "navi_streams_tap_logits", "navi_streams_tap_cp_logits"):
         getattr(L, f).argtypes = [C.c_void_p]
         getattr(L, f).restype = C.c_void_p
@@ -501,6 +503,9 @@ class Streams:
 
     def set_taps(self, on: bool):
         _check(lib().navi_streams_set_taps(self.h, 1 if on else 0), what="navi_streams_set_taps")
+
+    def set_graphs(self, on: bool):
+        _check(lib().navi_streams_set_graphs(self.h, 1 if on else 0), what="navi_streams_set_graphs")
 
     def run(self, kvs, n_past, d_trailing: int, s: Sampling, seeds, frame_index, d_step_in: int | None = None):
         """codes [n][16] (int32) for streams 0..n-1; kvs: one KvCache (or TalkerKv) per stream."""

@@ -153,3 +153,30 @@ def test_errors(batch):
     with pytest.raises(b.abi.NaviError) as e:
         b.st.run(b.kv_d * 2, [1] * 10, b.d_trail.ptr, s, [0] * 10, [0] * 10, d_step_in=b.d_step.ptr)
     assert e.value.status == b.abi.NAVI_ERR_INVALID
+
+
+def test_graph_replays_match_eager(batch):
+    """Runs replayed from the captured graph (the default) give the codes and next step inputs of
+    runs whose kernels the host launches one by one: four sampled steps from the same start, each
+    replay preceded by the run's own uploads and followed by its copies and synchronisation."""
+    b = batch
+    n = len(b.n_past)
+    s = b.abi.Sampling.make(min_frames=2)
+
+    def steps(graphs):
+        b.st.set_graphs(graphs)
+        b.st.reset()
+        out = []
+        for f in range(4):
+            codes = b.st.run(b.kv_d, [p + f for p in b.n_past], b.d_trail.ptr, s, b.seeds, [f] * n,
+                             d_step_in=b.d_step.ptr if f == 0 else None)
+            out.append((codes.copy(), b.st.step_out(n).copy()))
+        return out
+
+    b.st.set_taps(False)
+    eager = steps(False)
+    graph = steps(True)
+    for f, ((ce, se), (cg, sg)) in enumerate(zip(eager, graph)):
+        log(f"step {f}: eager {ce[:, :4].tolist()} graph {cg[:, :4].tolist()}")
+        np.testing.assert_array_equal(cg, ce)
+        np.testing.assert_array_equal(sg, se)
