@@ -225,15 +225,30 @@ __device__ __forceinline__ bool poll_word(const Args &a, uint64_t *p, uint32_t t
     return true;
 }
 
+// RMSNorm weights of this thread's elements (tid + k * BT), by value so they stay in registers.
+struct NormW {
+    float v[H / BT];
+};
+__device__ __forceinline__ NormW normw(const float (&w)[H / BT]) {
+    NormW n;
+#pragma unroll
+    for (int k = 0; k < H / BT; ++k) n.v[k] = w[k];
+    return n;
+}
+
 // Block-wide: N tagged words at mailbox offset `off` -> dst (LDS f32). Uniform result.
+// With NORM (N == H) the same pass does norm_prep's work: xn[i] = x[i] * w[i] and this wave's
+// sum of x^2 in S.red[red + wave] (same order, so the same bits), published by the final barrier.
 // The vector is written in chunks of CH words by N/CH producers. Wave 0 first polls
 // one sentinel per producer (its chunk's last word) while the other waves sleep in
 // the barrier; then every thread reads the whole vector once, re-polling only the
 // rare word whose tag is not yet visible. Polling N words from every thread instead
 // floods the coherent path: 4.9 us vs 2.8 us for N = 3072 on MI355X.
-template <int N, int CH, bool REPL = true>
-__device__ __forceinline__ bool gather(const Args &a, int off, uint32_t tag, float *dst, Smem &S) {
+template <int N, int CH, bool REPL = true, bool NORM = false>
+__device__ __forceinline__ bool gather(const Args &a, int off, uint32_t tag, float *dst, Smem &S, NormW nw = {},
+                                       float *xn = nullptr, int red = 0) {
     static_assert(N % BT == 0 && N % CH == 0, "gather size");
+    static_assert(!NORM || N == H, "norm of the residual stream");
     constexpr int PER = N / BT, NPROD = N / CH;
     uint64_t *const mb = sgpr_ptr(a.mb + (REPL ? xcc_copy() * MB_WORDS : 0) + off);
     PROF_MARK(a, S);
@@ -270,11 +285,21 @@ __device__ __forceinline__ bool gather(const Args &a, int off, uint32_t tag, flo
 #pragma unroll
     for (int k = 0; k < PER; ++k) w[k] = mb_peek(mb + tid() + k * BT);
     bool ok = true;
+    float ss = 0.f;
 #pragma unroll
     for (int k = 0; k < PER; ++k) {
         const int i = tid() + k * BT;
         if (ok) ok = poll_word(a, mb + i, tag, w[k]);
-        dst[i] = val_of(w[k]);
+        const float v = val_of(w[k]);
+        dst[i] = v;
+        if constexpr (NORM) {
+            ss = fmaf(v, v, ss);
+            xn[i] = v * nw.v[k];
+        }
+    }
+    if constexpr (NORM) {
+        ss = wave_sum(ss);
+        if (lane() == 0) S.red[red + wave()] = ss;
     }
     if (!ok) S.fail = 1;
     __syncthreads();
@@ -283,11 +308,13 @@ __device__ __forceinline__ bool gather(const Args &a, int off, uint32_t tag, flo
 }
 
 // T rows of N words each (row stride N in the mailbox and in dst), one row at a time.
-template <int T, int N, int CH>
-__device__ __forceinline__ bool gather_rows(const Args &a, int off, uint32_t tag, float *dst, Smem &S) {
+template <int T, int N, int CH, bool NORM = false>
+__device__ __forceinline__ bool gather_rows(const Args &a, int off, uint32_t tag, float *dst, Smem &S, NormW nw = {},
+                                            float *xn = nullptr) {
 #pragma unroll
     for (int t = 0; t < T; ++t)
-        if (!gather<N, CH>(a, off + t * N, tag, dst + t * N, S)) return false;
+        if (!gather<N, CH, true, NORM>(a, off + t * N, tag, dst + t * N, S, nw, NORM ? xn + t * N : nullptr, t * NW))
+            return false;
     return true;
 }
 
@@ -312,6 +339,13 @@ __device__ __forceinline__ void norm_prep(const float (*x)[H], const float (&w)[
         if (lane() == 0) S.red[t * NW + wave()] = ss;
     }
     __syncthreads();
+}
+
+__device__ __forceinline__ float norm_scale_row(float eps, int row, const Smem &S) {
+    float ss = 0.f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) ss += S.red[row * NW + w];
+    return rsqrtf(ss / static_cast<float>(H) + eps);
 }
 
 template <int T>
@@ -824,16 +858,18 @@ __device__ __forceinline__ const LayerPtrs &layer_at(const Args &a, const Smem &
 
 // One decoder layer over T rows held in S.x (its input); leaves its output in S.x.
 // gi: global layer index (talker layers, then n_cl cp layers per cp pass).
+// normed: S.xn and the norm's partial sums are already there (the previous layer's last gather
+// made them). next_final: the output feeds the final norm (R.fn) and a head, not another layer.
 template <int T, bool TALKER>
 __device__ __forceinline__ bool run_layer(const Args &a, const Ctx &cx, Regs &R, int gi, int p0, Seq &seq, Smem &S,
-                                          const uint16_t *head = nullptr) {
+                                          const uint16_t *head, bool normed, bool next_final) {
     const int n_total = a.n_tl + CPH * a.n_cl;
     const bool has_next = gi + 1 < n_total;
     const LayerPtrs &N = layer_at(a, S, has_next ? gi + 1 : gi);
     const bool next_cp = gi + 1 >= a.n_tl;
     const float eps = TALKER ? a.eps_t : a.eps_c;
 
-    norm_prep<T>(S.x, R.ln1, S.xn, S);
+    if (!normed) norm_prep<T>(S.x, R.ln1, S.xn, S);
     float sc[T];
     norm_scale<T>(eps, sc, S);
     const uint32_t t_qkv = seq.next();
@@ -853,8 +889,7 @@ __device__ __forceinline__ bool run_layer(const Args &a, const Ctx &cx, Regs &R,
     o_phase<T>(a, R, S, t_x2);
     if (has_next) load_o(R, N, next_cp);
 
-    if (!gather_rows<T, H, H / NB>(a, MB_X2, t_x2, &S.x[0][0], S)) return false;
-    norm_prep<T>(S.x, R.ln2, S.xn, S);
+    if (!gather_rows<T, H, H / NB, true>(a, MB_X2, t_x2, &S.x[0][0], S, normw(R.ln2), &S.xn[0][0])) return false;
     norm_scale<T>(eps, sc, S);
     const uint32_t t_h = seq.next();
     gu_phase<T>(a, R, S, t_h, sc);
@@ -869,7 +904,10 @@ __device__ __forceinline__ bool run_layer(const Args &a, const Ctx &cx, Regs &R,
         else load_lm(R, head);
     }
 
-    return gather_rows<T, H, H / NB>(a, MB_X, t_x, &S.x[0][0], S);
+    // R.ln1 holds the next layer's weights by now (load_qkv above); the last layer of the frame
+    // is always next_final
+    return gather_rows<T, H, H / NB, true>(a, MB_X, t_x, &S.x[0][0], S, next_final ? normw(R.fn) : normw(R.ln1),
+                                           &S.xn[0][0]);
 }
 
 __device__ __forceinline__ void load_row_f16(const uint16_t *src, float *dst) {
@@ -921,8 +959,9 @@ __global__ void __launch_bounds__(BT, 1) k_frame(Args a, const Weights *__restri
         for (int i = tid(); i < H; i += BT) S.x[0][i] = gld(a.step_in + i);
         __syncthreads();
         for (int il = 0; il < a.n_tl; ++il)
-            if (!run_layer<1, true>(a, cx, R, il, a.n_past, seq, S, il == a.n_tl - 1 ? W.codec_head : nullptr)) return;
-        norm_prep<1>(S.x, R.fn, S.xn, S);
+            if (!run_layer<1, true>(a, cx, R, il, a.n_past, seq, S, il == a.n_tl - 1 ? W.codec_head : nullptr, il > 0,
+                                    il == a.n_tl - 1))
+                return;
         float hsc[1];
         norm_scale<1>(a.eps_t, hsc, S);
         load_norm(R.fn, W.cp_norm);
@@ -986,25 +1025,27 @@ __global__ void __launch_bounds__(BT, 1) k_frame(Args a, const Weights *__restri
     }
     __syncthreads();
     for (int il = 0; il < a.n_cl; ++il, ++gi)
-        if (!run_layer<2, false>(a, cx, R, gi, 0, seq, S, il == a.n_cl - 1 ? S.lmh[0] : nullptr)) return;
+        if (!run_layer<2, false>(a, cx, R, gi, 0, seq, S, il == a.n_cl - 1 ? S.lmh[0] : nullptr, il > 0, il == a.n_cl - 1))
+            return;
     for (int pos = 1; pos < NCB; ++pos) {
         if (pos > 1) {
             for (int il = 0; il < a.n_cl; ++il, ++gi)
-                if (!run_layer<1, false>(a, cx, R, gi, pos, seq, S, il == a.n_cl - 1 ? S.lmh[pos - 1] : nullptr)) return;
+                if (!run_layer<1, false>(a, cx, R, gi, pos, seq, S, il == a.n_cl - 1 ? S.lmh[pos - 1] : nullptr, il > 0,
+                                         il == a.n_cl - 1))
+                    return;
         }
+        // the last layer's gather normed every row with the cp norm; the head takes the last row
         const int row = pos == 1 ? 1 : 0;
-        norm_prep<1>(reinterpret_cast<const float (*)[H]>(S.x[row]), R.fn, S.xn, S);
-        float hsc[1];
-        norm_scale<1>(a.eps_c, hsc, S);
+        const float hsc0 = norm_scale_row(a.eps_c, row, S);
         const uint32_t t_lg = seq.next();
         {
             float xf[2][8], d[2];
-            xfrag<2>(S.xn[0], 0, xf);
+            xfrag<2>(S.xn[row], 0, xf);
             dot16_rows<2>(R.lm, xf, d);
             wave_sum_n<2>(d);
 #pragma unroll
             for (int r = 0; r < 2; ++r)
-                if (lane() < NREP) mb_put(a.mb + lane() * MB_WORDS + MB_LG + blk() * (VC / NB) + wave() * 2 + r, d[r] * hsc[0], t_lg);
+                if (lane() < NREP) mb_put(a.mb + lane() * MB_WORDS + MB_LG + blk() * (VC / NB) + wave() * 2 + r, d[r] * hsc0, t_lg);
         }
         if (!gather<VC, VC / NB>(a, MB_LG, t_lg, S.u.m.samp.lg, S)) return;
         if (a.tap_cp_logits && blk() == 0) {
