@@ -275,7 +275,7 @@ __global__ void __launch_bounds__(BT) k_st_qkv_finish(const float *part, int S, 
 // vector) to part[m][g][s][h] = {m, l, o[HD]}.
 __global__ void __launch_bounds__(BT) k_st_attn(const float *q, const StreamMeta *meta, uint16_t *const *kcache,
                                                 uint16_t *const *vcache, int nq, int nkv, int splits, float *part) {
-    __shared__ float qs[2][HD], sc[2][KPS], red[2][NW], opart[NW][2][HD];
+    __shared__ float qs[2][HD], sc[2][KPS], red[2][NW], opart[NW][4][2][HD];
     const int m = blockIdx.x, g = blockIdx.y, s = blockIdx.z;
     const int n = meta[m].n_past + 1, j0 = s * KPS, j1 = min(n, j0 + KPS), cnt = max(0, j1 - j0);
     const int QD = nq * HD, KVD = nkv * HD;
@@ -284,25 +284,58 @@ __global__ void __launch_bounds__(BT) k_st_attn(const float *q, const StreamMeta
     qs[threadIdx.x >> 7][threadIdx.x & (HD - 1)] = gld(q + static_cast<size_t>(m) * QD + g * 2 * HD + threadIdx.x);
     __syncthreads();
     const uint16_t *kb = kcache[m] + g * HD, *vb = vcache[m] + g * HD;
-    float d0 = -INFINITY, d1 = -INFINITY;
-    if (static_cast<int>(threadIdx.x) < cnt) {
-        const NAVI_GLOBAL u32x4_t *kp = (const NAVI_GLOBAL u32x4_t *) (kb + static_cast<size_t>(j0 + threadIdx.x) * KVD);
-        u32x4_t kr[HD / 8];
+    u32x4_t vr[KPS / NW / 4];
+    // Scores, 16 lanes per key: wave w takes keys 64w .. 64w + 63 of the range, four per load
+    // instruction (lane 16r + c reads 16-byte chunk c of key 4i + r, so each instruction reads
+    // four whole 256-byte rows), summed by DPP within the 16-lane row; lane 16r keeps the two
+    // heads' scores in sc.
+    {
+        const int c = l & 15, r = l >> 4;
+        float q0[8], q1[8];
 #pragma unroll
-        for (int c = 0; c < HD / 8; ++c) kr[c] = kp[c];
-        float a0 = 0.f, a1 = 0.f;
+        for (int e = 0; e < 8; ++e) {
+            q0[e] = qs[0][c * 8 + e];
+            q1[e] = qs[1][c * 8 + e];
+        }
+        constexpr int KI = KPS / NW / 4;
+        u32x4_t kr[KI];
 #pragma unroll
-        for (int c = 0; c < HD / 8; ++c)
+        for (int i = 0; i < KI; ++i) {
+            const int jl = wv * (KPS / NW) + 4 * i + r;
+            kr[i] = jl < cnt ? *(const NAVI_GLOBAL u32x4_t *) (kb + static_cast<size_t>(j0 + jl) * KVD + c * 8)
+                             : u32x4_t{0u, 0u, 0u, 0u};
+        }
+        // the same keys' V chunks are loaded now too (they do not depend on the scores): one
+        // memory latency per block instead of two
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int i = c * 8 + e * 2;
-                const float k0 = h2f(static_cast<uint16_t>(kr[c][e])), k1 = h2f(static_cast<uint16_t>(kr[c][e] >> 16));
-                a0 = fmaf(qs[0][i + 1], k1, fmaf(qs[0][i], k0, a0));
-                a1 = fmaf(qs[1][i + 1], k1, fmaf(qs[1][i], k0, a1));
+        for (int i = 0; i < KI; ++i) {
+            const int jl = wv * (KPS / NW) + 4 * i + r;
+            vr[i] = jl < cnt ? *(const NAVI_GLOBAL u32x4_t *) (vb + static_cast<size_t>(j0 + jl) * KVD + c * 8)
+                             : u32x4_t{0u, 0u, 0u, 0u};
+        }
+#pragma unroll
+        for (int i = 0; i < KI; ++i) {
+            const int jl = wv * (KPS / NW) + 4 * i + r;
+            uint4 k4;
+            __builtin_memcpy(&k4, &kr[i], 16);
+            float a0 = dot8(k4, q0, 0.f), a1 = dot8(k4, q1, 0.f);
+            a0 += dpp_red<0xB1>(a0);
+            a1 += dpp_red<0xB1>(a1);
+            a0 += dpp_red<0x4E>(a0);
+            a1 += dpp_red<0x4E>(a1);
+            a0 += dpp_red<0x141>(a0);
+            a1 += dpp_red<0x141>(a1);
+            a0 += dpp_red<0x140>(a0);
+            a1 += dpp_red<0x140>(a1);
+            if (c == 0) {
+                sc[0][jl] = a0 * ATT_SCALE;
+                sc[1][jl] = a1 * ATT_SCALE;
             }
-        d0 = a0 * ATT_SCALE;
-        d1 = a1 * ATT_SCALE;
+        }
     }
+    __syncthreads();
+    const bool mine = static_cast<int>(threadIdx.x) < cnt;
+    const float d0 = mine ? sc[0][threadIdx.x] : -INFINITY, d1 = mine ? sc[1][threadIdx.x] : -INFINITY;
     float mx0 = wave_max(d0), mx1 = wave_max(d1);
     if (l == 0) { red[0][wv] = mx0; red[1][wv] = mx1; }
     __syncthreads();
@@ -315,37 +348,43 @@ __global__ void __launch_bounds__(BT) k_st_attn(const float *q, const StreamMeta
     const float s0 = wave_sum(e0), s1 = wave_sum(e1);
     __syncthreads();                                      // red reads done, probabilities published
     if (l == 0) { red[0][wv] = s0; red[1][wv] = s1; }
-    // V: wave w sums keys w * 64 .. w * 64 + 63 of the range, all 64 rows' loads in flight at
-    // once; lane l owns dims 2l, 2l + 1 of both heads
-    float a00 = 0.f, a01 = 0.f, a10 = 0.f, a11 = 0.f;
+    // V: wave w sums keys w * 64 .. w * 64 + 63 of the range; lane 16r + c holds 16-byte chunk c
+    // (dims 8c .. 8c + 7) of keys 4i + r, i = 0..15 (loaded with the K chunks above), for both
+    // heads; the 4 x 4 partials per dim are summed in LDS below.
     {
-        constexpr int KW = KPS / NW;
-        const int jw = wv * KW, nw = max(0, min(KW, cnt - jw));
-        const uint16_t *vp = vb + static_cast<size_t>(j0 + jw) * KVD + 2 * l;
-        uint32_t vv[KW];
+        constexpr int KI = KPS / NW / 4;
+        const int c = l & 15, r = l >> 4, jw = wv * (KPS / NW);
+        float o0[8], o1[8];
 #pragma unroll
-        for (int u = 0; u < KW; ++u)
-            vv[u] = u < nw ? gld(reinterpret_cast<const uint32_t *>(vp + static_cast<size_t>(u) * KVD)) : 0u;
+        for (int e = 0; e < 8; ++e) o0[e] = o1[e] = 0.f;
 #pragma unroll
-        for (int u = 0; u < KW; ++u) {
-            if (u < nw) {
-                const float p0 = sc[0][jw + u], p1 = sc[1][jw + u];
-                const float v0 = h2f(static_cast<uint16_t>(vv[u])), v1 = h2f(static_cast<uint16_t>(vv[u] >> 16));
-                a00 = fmaf(p0, v0, a00);
-                a01 = fmaf(p0, v1, a01);
-                a10 = fmaf(p1, v0, a10);
-                a11 = fmaf(p1, v1, a11);
+        for (int i = 0; i < KI; ++i) {
+            const int jl = jw + 4 * i + r;
+            const float p0 = sc[0][jl], p1 = sc[1][jl];      // 0 past cnt
+            half8_t hv;
+            __builtin_memcpy(&hv, &vr[i], 16);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float v = static_cast<float>(hv[e]);
+                o0[e] = fmaf(p0, v, o0[e]);
+                o1[e] = fmaf(p1, v, o1[e]);
             }
         }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            opart[wv][r][0][c * 8 + e] = o0[e];
+            opart[wv][r][1][c * 8 + e] = o1[e];
+        }
     }
-    opart[wv][0][2 * l] = a00;
-    opart[wv][0][2 * l + 1] = a01;
-    opart[wv][1][2 * l] = a10;
-    opart[wv][1][2 * l + 1] = a11;
     __syncthreads();
     const int hh = threadIdx.x >> 7, d = threadIdx.x & (HD - 1);
     float *o = out + hh * (HD + 2);
-    gst(o + 2 + d, opart[0][hh][d] + opart[1][hh][d] + opart[2][hh][d] + opart[3][hh][d]);
+    float acc = 0.f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc += opart[w][r][hh][d];
+    gst(o + 2 + d, acc);
     if (d == 0) {
         gst(o, hh ? mx1 : mx0);
         gst(o + 1, red[hh][0] + red[hh][1] + red[hh][2] + red[hh][3]);
