@@ -265,6 +265,37 @@ int32_t navi_vocoder_samples_per_frame(const navi_vocoder *v);   /* Vocoder::sam
 int32_t navi_vocoder_max_chunk_frames(const navi_vocoder *v);    /* Vocoder::max_chunk_frames */
 double navi_vocoder_last_ms(const navi_vocoder *v);              /* Vocoder::last_ms: device time of the last decode */
 
+/* ---- speaker encoder: 24 kHz audio -> speaker embedding (speaker.h:17-38) ------------ */
+
+typedef struct navi_speaker navi_speaker;
+
+typedef struct {                       /* the speaker fields of params.h:53-55 (params.cpp:97-104) */
+    int32_t sample_rate;               /* 24000 */
+    int32_t enc_dim;                   /* 1024: the embedding width (the talker's hidden) */
+    int32_t n_fft, num_mels, hop, win; /* 1024, 128, 256, 1024 (win must equal n_fft, a power of 2) */
+    float   fmin, fmax;                /* 0, 12000 */
+} navi_speaker_params;
+
+/* SpeakerEncoder::mel (speaker.hip:269-303): host log-mel [num_mels][*n_frames] of a mono
+ * waveform in [-1, 1] (reflect padding (n_fft - hop) / 2, periodic Hann, |FFT|, slaney
+ * filterbank, log(max(., 1e-5))). mel_out == NULL only sets *n_frames; otherwise capacity (in
+ * floats) must hold num_mels * n_frames. Fails with NAVI_ERR_INVALID ("too short") when
+ * n <= (n_fft - hop) / 2. No device work. */
+navi_status navi_speaker_mel(const navi_speaker_params *p, const float *wav, int64_t n, float *mel_out, int64_t capacity,
+                             int32_t *n_frames, char *err, size_t errlen);
+/* SpeakerEncoder::create (speaker.hip:219-260): binds the speaker_encoder.* tensors by name
+ * (shapes as params.cpp:165-194) and sizes the work buffers for max_seconds of audio. */
+navi_status navi_speaker_create(const navi_speaker_params *p, const navi_tensor_ref *tensors, int32_t n_tensors,
+                                double max_seconds, navi_speaker **out, char *err, size_t errlen);
+void navi_speaker_destroy(navi_speaker *h);
+/* SpeakerEncoder::embed_mel (speaker.hip:305-321): host mel [num_mels][n_frames] -> host
+ * emb[enc_dim]. n_frames in [5, the max_seconds bound] (longer: "longer than the encoder's
+ * max_seconds", as the reference). Synchronous. */
+navi_status navi_speaker_embed_mel(navi_speaker *h, const float *mel, int32_t n_frames, float *emb, char *err, size_t errlen);
+/* SpeakerEncoder::embed (speaker.hip:323-327): navi_speaker_mel then navi_speaker_embed_mel. */
+navi_status navi_speaker_embed(navi_speaker *h, const float *wav, int64_t n, float *emb, char *err, size_t errlen);
+double navi_speaker_last_ms(const navi_speaker *h);      /* SpeakerEncoder::last_ms: device time of the last embed */
+
 /* ---- one request end to end (Graph::synth, graph.cpp:52-111) ------------------------ */
 
 typedef struct {                       /* graph.h SynthRequest, with the text already tokenized */

@@ -32,6 +32,8 @@ EXPORTS = [
     "navi_vocoder_samples_per_frame", "navi_vocoder_max_chunk_frames", "navi_vocoder_last_ms", "navi_synth",
     "navi_streams_create", "navi_streams_destroy", "navi_streams_reset", "navi_streams_run", "navi_streams_step_out",
     "navi_streams_max_streams", "navi_streams_last_ms", "navi_streams_set_taps", "navi_streams_set_graphs",
+    "navi_speaker_mel", "navi_speaker_create", "navi_speaker_destroy", "navi_speaker_embed_mel", "navi_speaker_embed",
+    "navi_speaker_last_ms",
     "navi_streams_tap_hidden",
     "navi_streams_tap_logits", "navi_streams_tap_cp_logits",
 ]
@@ -103,6 +105,11 @@ class VocoderParams(C.Structure):
                 ("codebook_size", C.c_int32), ("n_q", C.c_int32), ("n_semantic", C.c_int32),
                 ("decoder_dim", C.c_int32), ("sliding_window", C.c_int32), ("upsampling_ratios", C.c_int32 * 2),
                 ("upsample_rates", C.c_int32 * 4), ("samples_per_frame", C.c_int32)]
+
+
+class SpeakerParams(C.Structure):
+    _fields_ = [("sample_rate", C.c_int32), ("enc_dim", C.c_int32), ("n_fft", C.c_int32), ("num_mels", C.c_int32),
+                ("hop", C.c_int32), ("win", C.c_int32), ("fmin", C.c_float), ("fmax", C.c_float)]
 
 
 class SynthRequest(C.Structure):
@@ -192,6 +199,16 @@ def lib() -> C.CDLL:
         getattr(L, f).argtypes = [C.c_void_p]
     L.navi_vocoder_last_ms.argtypes = [C.c_void_p]
     L.navi_vocoder_last_ms.restype = C.c_double
+    L.navi_speaker_mel.argtypes = [C.POINTER(SpeakerParams), C.c_void_p, C.c_int64, C.c_void_p, C.c_int64,
+                                   C.POINTER(C.c_int32), E, C.c_size_t]
+    L.navi_speaker_create.argtypes = [C.POINTER(SpeakerParams), C.POINTER(TensorRef), C.c_int32, C.c_double,
+                                      C.POINTER(C.c_void_p), E, C.c_size_t]
+    L.navi_speaker_destroy.argtypes = [C.c_void_p]
+    L.navi_speaker_destroy.restype = None
+    L.navi_speaker_embed_mel.argtypes = [C.c_void_p, C.c_void_p, C.c_int32, C.c_void_p, E, C.c_size_t]
+    L.navi_speaker_embed.argtypes = [C.c_void_p, C.c_void_p, C.c_int64, C.c_void_p, E, C.c_size_t]
+    L.navi_speaker_last_ms.argtypes = [C.c_void_p]
+    L.navi_speaker_last_ms.restype = C.c_double
     L.navi_synth.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.POINTER(SynthRequest), PCM_CALLBACK, C.c_void_p,
                              C.POINTER(SynthStats), E, C.c_size_t]
     L.navi_linear.argtypes = [C.c_void_p, C.c_int32, C.c_int32, C.c_void_p, C.c_int32, C.c_int32, C.c_void_p, C.c_void_p,
@@ -702,6 +719,75 @@ class Vocoder:
 
     def last_ms(self) -> float:
         return lib().navi_vocoder_last_ms(self.h)
+
+
+# ---- speaker encoder -------------------------------------------------------------------
+
+def speaker_params(kv: dict) -> SpeakerParams:
+    """The speaker fields of read_params (params.cpp:97-104)."""
+    return SpeakerParams(kv["speaker.sample_rate"], kv["speaker.enc_dim"], kv["speaker.mel.n_fft"],
+                         kv["speaker.mel.num_mels"], kv["speaker.mel.hop_size"], kv["speaker.mel.win_size"],
+                         float(kv["speaker.mel.fmin"]), float(kv["speaker.mel.fmax"]))
+
+
+def speaker_mel(kv_or_params, wav) -> np.ndarray:
+    """navi_speaker_mel (SpeakerEncoder::mel, speaker.hip:269-303): log-mel [num_mels][T] of a mono
+    waveform in [-1, 1], computed on the host by the library."""
+    p = kv_or_params if isinstance(kv_or_params, SpeakerParams) else speaker_params(kv_or_params)
+    x = np.ascontiguousarray(wav, dtype=np.float32).reshape(-1)
+    n = C.c_int32()
+    err = C.create_string_buffer(256)
+    _check(lib().navi_speaker_mel(C.byref(p), x.ctypes.data, x.size, None, 0, C.byref(n), err, 256), err)
+    out = np.empty((p.num_mels, n.value), np.float32)
+    _check(lib().navi_speaker_mel(C.byref(p), x.ctypes.data, x.size, out.ctypes.data, out.size, C.byref(n), err, 256), err)
+    return out
+
+
+class Speaker:
+    """speaker.h:17-38 (SpeakerEncoder) over navi_speaker_*."""
+
+    def __init__(self, weights: DeviceWeights, max_seconds: float = 30.0):
+        self.params = speaker_params(weights.kv)
+        refs, self._keep = weights.refs()
+        h = C.c_void_p()
+        err = C.create_string_buffer(256)
+        _check(lib().navi_speaker_create(C.byref(self.params), refs, len(refs), max_seconds, C.byref(h), err, 256), err)
+        self.h = h.value
+
+    def close(self):
+        if self.h:
+            lib().navi_speaker_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def mel(self, wav) -> np.ndarray:
+        return speaker_mel(self.params, wav)
+
+    def embed(self, wav) -> np.ndarray:
+        """[enc_dim] embedding of a mono 24 kHz waveform in [-1, 1]."""
+        x = np.ascontiguousarray(wav, dtype=np.float32).reshape(-1)
+        out = np.empty(self.params.enc_dim, np.float32)
+        err = C.create_string_buffer(256)
+        _check(lib().navi_speaker_embed(self.h, x.ctypes.data, x.size, out.ctypes.data, err, 256), err)
+        return out
+
+    def embed_mel(self, mel) -> np.ndarray:
+        """... from a precomputed mel [num_mels][T]."""
+        m = np.ascontiguousarray(mel, dtype=np.float32)
+        if m.ndim != 2 or m.shape[0] != self.params.num_mels:
+            raise ValueError(f"speaker: mel must be [{self.params.num_mels}][T], got {m.shape}")
+        out = np.empty(self.params.enc_dim, np.float32)
+        err = C.create_string_buffer(256)
+        _check(lib().navi_speaker_embed_mel(self.h, m.ctypes.data, m.shape[1], out.ctypes.data, err, 256), err)
+        return out
+
+    def last_ms(self) -> float:
+        return lib().navi_speaker_last_ms(self.h)
 
 
 # ---- one request end to end ------------------------------------------------------------

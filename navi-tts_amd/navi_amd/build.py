@@ -24,7 +24,7 @@ HIP_FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-Wall", "-
              "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
              "-I", str(ROOT / "include"), "-I", str(PKG / "csrc" / "hip")]
 
-HIP_SOURCES = ["device.hip", "frame.hip", "prefill.hip", "vocoder.hip", "streams.hip"]
+HIP_SOURCES = ["device.hip", "frame.hip", "prefill.hip", "vocoder.hip", "streams.hip", "speaker.hip"]
 HOST_SOURCES = ["graph.cpp"]          # csrc/host: C++ over the C ABI, no device code
 HOST_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-Wextra", "-I", str(ROOT / "include")]
 

@@ -51,3 +51,18 @@ def small_blob(scratch_dir):
 def full_blob(scratch_dir):
     """the full 0.6B talker + 5-layer code predictor, seed 0."""
     return _blob(scratch_dir, "full_seed0.navi", 0, parts=("talker", "cp"))
+
+
+@pytest.fixture(scope="session")
+def speaker_blob(scratch_dir):
+    """The speaker encoder's tensors only (random init, seed 3)."""
+    return _blob(scratch_dir, "speaker.navi", 3, parts=("speaker",))
+
+
+@pytest.fixture(scope="session")
+def speaker_fixture():
+    """The reference's own speaker fixture, first 2 s (tests/golden/make_speaker_fixture.py):
+    (wav f32 as runtime/audio/wav.cpp reads it, log-mel frames 0..185 [128][186])."""
+    import numpy as np
+    z = np.load(ROOT / "tests" / "golden" / "speaker_mel_prefix.npz", allow_pickle=False)
+    return z["wav_s16"].astype(np.float32) / np.float32(32768.0), z["mel"]
