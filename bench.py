@@ -78,7 +78,7 @@ def measured_traffic():
 def make_blob(path: Path):
     from navi_amd import blob
     if not path.exists():
-        blob.write_random_blob(path, SEED, parts=("talker", "cp", "codec"))
+        blob.write_random_blob(path, SEED, parts=("talker", "cp", "codec", "speaker"))
 
 
 def vocoder_flops_per_frame(kv: dict) -> float:
@@ -212,6 +212,42 @@ def streaming_and_vocoder(W, kv: dict, abi) -> dict:
     }
 
 
+def speaker_flops_per_frame(kv: dict) -> float:
+    """Dense multiply-adds per mel frame of the ECAPA-TDNN (speaker.hip:175-217), x 2 flops:
+    block 0 (k5, 128 -> 512), per SE-Res2Net block two 512 x 512 k1 convs and seven 64 x 64 k3
+    convs, MFA 1536 x 1536, attentive pooling 1536 -> 128 -> 1536 (its mean/std columns are a
+    per-utterance bias, not per frame); the SE and fc GEMVs are per utterance and left out."""
+    M = kv["speaker.mel.num_mels"]
+    per = 512 * M * 5 + 3 * (2 * 512 * 512 + 7 * 64 * 64 * 3) + 1536 * 1536 + 2 * 1536 * 128
+    return 2.0 * per
+
+
+def speaker_encoder(W, kv: dict, abi, seconds=(3.0, 10.0)) -> dict:
+    """navi_speaker_embed on synthetic audio (the per-clone step before the prompt, bench.cpp:144):
+    host log-mel + device ECAPA-TDNN; device time of the network from its own events."""
+    rng = np.random.default_rng(SEED)
+    spk = abi.Speaker(W, max_seconds=max(seconds))
+    out = {"config": "voice clone: N(0, 0.1) audio at 24 kHz, random-init ECAPA-TDNN (seed 1)"}
+    fl = speaker_flops_per_frame(kv)
+    for sec in seconds:
+        wav = (rng.standard_normal(int(sec * kv["speaker.sample_rate"])) * 0.1).astype(np.float32)
+        mel = spk.mel(wav)
+        spk.embed_mel(mel)
+        dev = []
+        for _ in range(5):
+            spk.embed_mel(mel)
+            dev.append(spk.last_ms())
+        t0 = time.perf_counter()
+        spk.embed(wav)
+        wall = (time.perf_counter() - t0) * 1e3
+        ms = float(np.median(dev))
+        out[f"{sec:g}s"] = {"frames": int(mel.shape[1]), "device_ms": round(ms, 3), "embed_wall_ms": round(wall, 2),
+                            "tflops": round(fl * mel.shape[1] / (ms * 1e-3) / 1e12, 2)}
+    out["gflop_per_second_of_audio"] = round(fl * kv["speaker.sample_rate"] / kv["speaker.mel.hop_size"] / 1e9, 3)
+    spk.close()
+    return {"speaker": out}
+
+
 def cpu_baseline(path: Path, frames: int) -> dict:
     """The oracle (PyTorch f32 on the host cores) on the same workload, `frames` frames."""
     import torch
@@ -319,6 +355,10 @@ def main():
             ms_ = multistream(W, kvd, abi)
             print(f"[bench] {json.dumps(ms_)}", flush=True, file=sys.stderr)
             extra.update(ms_)
+            print("[bench] speaker encoder", flush=True, file=sys.stderr)
+            sp = speaker_encoder(W, kvd, abi)
+            print(f"[bench] {json.dumps(sp)}", flush=True, file=sys.stderr)
+            extra.update(sp)
         del frame, W, kv
         cpu = None
         if args.cpu_frames > 0:

@@ -36,7 +36,8 @@ typedef enum {
     NAVI_ERR_KV_FULL = 3,        /* n_past >= max_pos (frame.hip:800) */
     NAVI_ERR_INVALID = 4,        /* bad argument / shape / missing tensor */
     NAVI_ERR_HIP = 5,            /* a HIP runtime call failed */
-    NAVI_ERR_UNSUPPORTED = 6     /* model shape or device this build does not run */
+    NAVI_ERR_UNSUPPORTED = 6,    /* model shape or device this build does not run */
+    NAVI_ERR_CANCELLED = 7       /* the PCM consumer stopped the request (navi_synth's callback) */
 } navi_status;
 
 /* ---- device (runtime/device/device.h:100-123) ---------------------------- */
@@ -319,12 +320,16 @@ typedef struct {                       /* graph.h SynthStats */
     double prefill_ms, frames_ms, vocoder_ms, total_ms, ttfa_ms, audio_s, rtf;
 } navi_synth_stats;
 
-/* PCM of each vocoder batch, in order; n samples at 24 kHz. */
-typedef void (*navi_pcm_callback)(const float *pcm, int32_t n, void *user);
+/* PCM of each vocoder batch, in order; n samples at 24 kHz. Returns 0 to go on; non-zero stops
+ * the request, which is how an exception thrown by Graph::synth's on_pcm (the server's "client
+ * stopped reading", server.cpp:431-437) ends it: no further frame runs and navi_synth returns
+ * NAVI_ERR_CANCELLED with the stats of what was delivered. */
+typedef int32_t (*navi_pcm_callback)(const float *pcm, int32_t n, void *user);
 
 /* Graph::synth: prompt -> prefill -> frames until EOS or max_frames -> vocoder in batches
- * (first_batch frames first, then vocoder_batch), PCM handed to on_pcm per batch. Frame and
- * vocoder are reset first; the frame runs on the talker's KV cache. Wall-clock stats. */
+ * (first_batch frames first, then vocoder_batch), PCM handed to on_pcm per batch on the calling
+ * thread. Frame and vocoder are reset first; the frame runs on the talker's KV cache. Wall-clock
+ * stats. */
 navi_status navi_synth(navi_talker *t, navi_frame *f, navi_vocoder *v, const navi_synth_request *req,
                        navi_pcm_callback on_pcm, void *user, navi_synth_stats *stats, char *err, size_t errlen);
 

@@ -85,7 +85,10 @@ extern "C" navi_status navi_synth(navi_talker *t, navi_frame *f, navi_vocoder *v
             stats->ttfa_ms = ms_since(t0);
             first_audio = false;
         }
-        if (on_pcm) on_pcm(pcm.data(), static_cast<int32_t>(pcm.size()), user);
+        if (on_pcm && on_pcm(pcm.data(), static_cast<int32_t>(pcm.size()), user) != 0) {
+            put_err(err, errlen, "synth: stopped by the PCM consumer after %d frames", stats->n_frames);
+            return NAVI_ERR_CANCELLED;
+        }
         return NAVI_OK;
     };
     // Frames run in on-device loops of exactly the vocoder's batch sizes (first batch, then
@@ -124,12 +127,15 @@ extern "C" navi_status navi_synth(navi_talker *t, navi_frame *f, navi_vocoder *v
             stats->eos = 1;
             break;
         }
-        if ((st = flush(false)) != NAVI_OK) return st;
+        if ((st = flush(false)) != NAVI_OK) {
+            stats->total_ms = ms_since(t0);
+            return st;
+        }
     }
     stats->hit_cap = !stats->eos;
-    if ((st = flush(true)) != NAVI_OK) return st;
+    st = flush(true);
     stats->total_ms = ms_since(t0);
     stats->audio_s = static_cast<double>(stats->n_frames) * spf / 24000.0;
     stats->rtf = stats->audio_s > 0 ? stats->total_ms / 1000.0 / stats->audio_s : 0.0;
-    return NAVI_OK;
+    return st;
 }

@@ -17,7 +17,8 @@ from .navi_file import NaviFile
 
 LIB_PATH = Path(__file__).resolve().parent.parent / "lib" / "libnavi_amd.so"
 
-NAVI_OK, NAVI_ERR_TIMEOUT, NAVI_ERR_LAUNCH, NAVI_ERR_KV_FULL, NAVI_ERR_INVALID, NAVI_ERR_HIP, NAVI_ERR_UNSUPPORTED = range(7)
+(NAVI_OK, NAVI_ERR_TIMEOUT, NAVI_ERR_LAUNCH, NAVI_ERR_KV_FULL, NAVI_ERR_INVALID, NAVI_ERR_HIP, NAVI_ERR_UNSUPPORTED,
+ NAVI_ERR_CANCELLED) = range(8)
 
 # The exported entry points include/navi_amd.h declares (checked by the CPU tests).
 EXPORTS = [
@@ -128,7 +129,7 @@ class SynthStats(C.Structure):
         return {f: getattr(self, f) for f, _ in self._fields_}
 
 
-PCM_CALLBACK = C.CFUNCTYPE(None, C.POINTER(C.c_float), C.c_int32, C.c_void_p)
+PCM_CALLBACK = C.CFUNCTYPE(C.c_int32, C.POINTER(C.c_float), C.c_int32, C.c_void_p)
 
 
 class Prompt(C.Structure):
@@ -794,9 +795,12 @@ class Speaker:
 
 def synth(talker: "Talker", frame: Frame, vocoder: "Vocoder", *, ids=None, language: str = "english", speaker=None,
           prompt=None, seed: int = 0, max_frames: int = 600, sampling: Sampling | None = None, vocoder_batch: int = 0,
-          first_batch: int = 0):
+          first_batch: int = 0, on_pcm=None):
     """navi_synth (Graph::synth, graph.cpp:52-111). ids + speaker build the prompt; or `prompt` =
     (d_prefill, n_prefill, d_trailing, n_trailing, d_tts_pad) gives the rows directly.
+    on_pcm(chunk f32 array), if given, sees each vocoder batch as it is produced; an exception it
+    raises stops the request (no further frame runs) and propagates out of synth, as an exception
+    from Graph::synth's on_pcm does.
     Returns (SynthStats, pcm f32 array, [samples per vocoder batch])."""
     req = SynthRequest()
     keep = []
@@ -812,14 +816,25 @@ def synth(talker: "Talker", frame: Frame, vocoder: "Vocoder", *, ids=None, langu
     req.max_frames = max_frames
     req.sampling = sampling or Sampling.make()
     req.vocoder_batch, req.first_batch = vocoder_batch, first_batch
-    chunks = []
+    chunks, raised = [], []
 
-    def on_pcm(ptr, n, _user):
-        chunks.append(np.ctypeslib.as_array(ptr, shape=(n,)).copy())
+    def trampoline(ptr, n, _user):
+        chunk = np.ctypeslib.as_array(ptr, shape=(n,)).copy()
+        chunks.append(chunk)
+        if on_pcm is not None:
+            try:
+                on_pcm(chunk)
+            except BaseException as e:        # handed back to the caller after navi_synth returns
+                raised.append(e)
+                return 1
+        return 0
 
-    cb = PCM_CALLBACK(on_pcm)
+    cb = PCM_CALLBACK(trampoline)
     st = SynthStats()
     err = C.create_string_buffer(256)
-    _check(lib().navi_synth(talker.h, frame.h, vocoder.h, C.byref(req), cb, None, C.byref(st), err, 256), err)
+    status = lib().navi_synth(talker.h, frame.h, vocoder.h, C.byref(req), cb, None, C.byref(st), err, 256)
+    if raised and status == NAVI_ERR_CANCELLED:
+        raise raised[0]
+    _check(status, err)
     pcm = np.concatenate(chunks) if chunks else np.zeros(0, np.float32)
     return st, pcm, [c.size for c in chunks]
