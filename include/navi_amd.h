@@ -293,9 +293,14 @@ void navi_speaker_destroy(navi_speaker *h);
  * emb[enc_dim]. n_frames in [5, the max_seconds bound] (longer: "longer than the encoder's
  * max_seconds", as the reference). Synchronous. */
 navi_status navi_speaker_embed_mel(navi_speaker *h, const float *mel, int32_t n_frames, float *emb, char *err, size_t errlen);
-/* SpeakerEncoder::embed (speaker.hip:323-327): navi_speaker_mel then navi_speaker_embed_mel. */
+/* SpeakerEncoder::embed (speaker.hip:323-327): the log-mel of navi_speaker_mel, computed on the
+ * device in the same double precision (equal to float rounding), then the network.
+ * Errors as navi_speaker_mel and navi_speaker_embed_mel. Synchronous. */
 navi_status navi_speaker_embed(navi_speaker *h, const float *wav, int64_t n, float *emb, char *err, size_t errlen);
-double navi_speaker_last_ms(const navi_speaker *h);      /* SpeakerEncoder::last_ms: device time of the last embed */
+double navi_speaker_last_ms(const navi_speaker *h);      /* SpeakerEncoder::last_ms: device time of the last embed
+                                                            (front end included for navi_speaker_embed) */
+/* Diagnostics: the device log-mel of the last embed, time-major f32 [*n_frames][num_mels]. */
+const float *navi_speaker_tap_mel(const navi_speaker *h, int32_t *n_frames);
 
 /* ---- one request end to end (Graph::synth, graph.cpp:52-111) ------------------------ */
 

@@ -1,12 +1,14 @@
 // The speaker encoder on gfx950: the C ABI's navi_speaker_*.
 //
 // Replaces SpeakerEncoder (model/qwen3tts/speaker.h, speaker.hip:20-331): 24 kHz audio -> 128-bin
-// log-mel (host) -> ECAPA-TDNN (device) -> the 1024-d speaker embedding of a cloned voice. Runs
-// once per clone, on the prompt's path only. MI355X design:
+// log-mel -> ECAPA-TDNN -> the 1024-d speaker embedding of a cloned voice. Runs once per clone,
+// on the prompt's path only. MI355X design:
 //
-//  * Front end on the host, as the reference's: reflect padding (n_fft - hop) / 2, periodic Hann,
-//    a radix-2 FFT with double twiddles, |X| = sqrt(re^2 + im^2 + 1e-9), the slaney filterbank
-//    (librosa.filters.mel), log(max(., 1e-5)).
+//  * Front end: reflect padding (n_fft - hop) / 2, periodic Hann, |X| = sqrt(re^2 + im^2 + 1e-9),
+//    the slaney filterbank (librosa.filters.mel), log(max(., 1e-5)). navi_speaker_mel computes it
+//    on the host (the reference's static SpeakerEncoder::mel, in double); navi_speaker_embed on
+//    the device, one block per frame (k_logmel: FFT in LDS, also in double), so a clone uploads
+//    audio, not a spectrogram, and no host loop sits on its path.
 //  * Every conv (block 0 k5, the SE-Res2Net tdnn / dilated k3 / squeeze-excitation convs, MFA,
 //    attentive pooling, fc) is conv.h's implicit GEMM on the matrix cores with "same" reflect
 //    padding; ReLU, sigmoid and tanh(ReLU) are its epilogues, the Res2Net "slice + previous
@@ -15,8 +17,10 @@
 //  * Attentive statistics pooling: in [x | mean | std] the mean and std columns are the same at
 //    every time step, so their part of asp.tdnn is folded into a per-channel bias (one GEMV) and
 //    the conv runs over the 1536 x channels only: the [T][4608] concatenation is never built.
-//  * Time reductions (SE mean, pooling statistics, softmax over time) run 64 channels x 4 time
-//    quarters per block, summed in a fixed order: the same bits every run.
+//  * Time reductions (SE mean, pooling statistics, softmax over time) run 16 channels x 16 time
+//    slices per block, summed in a fixed order: the same bits every run. k=1 convs with few
+//    output tiles (the SE and fc GEMVs, attentive pooling on short clips) split their input
+//    channels over blocks; the partial sums are added in split order.
 #include "conv.h"
 #include "dev_common.h"
 #include "host_util.h"
@@ -24,6 +28,7 @@
 #include <algorithm>
 #include <cmath>
 #include <complex>
+#include <memory>
 #include <string>
 #include <vector>
 
@@ -33,20 +38,30 @@ namespace spk {
 using namespace cv;
 
 constexpr int C = 512, R = 64, SCALE = 8, SEC = 128, MFA = 1536, ASP = 128;
-constexpr int NCH = 64, NPART = BT / NCH;     // time reductions: 64 channels x 4 time quarters per block
+constexpr int NCH = 16, NPART = BT / NCH;     // time reductions: 16 channels x 16 time slices per block
 
 // ---- time reductions ---------------------------------------------------------------------
+// Thread (q, c) sums rows t = q, q + 16, ... of channel c; the 16 slice sums are added in slice
+// order by one thread: fixed association, the same bits every run.
+
+__device__ __forceinline__ float slice_total(float (&red)[NPART][NCH], int cl) {
+    float s = red[0][cl];
+#pragma unroll
+    for (int q = 1; q < NPART; ++q) s += red[q][cl];
+    return s;
+}
 
 // mean over time of x[t][c] (ld ldx), c < C_: out[c]
 __global__ void __launch_bounds__(BT) k_time_mean(const float *x, int T, int C_, int ldx, float *out) {
     __shared__ float red[NPART][NCH];
-    const int c = blockIdx.x * NCH + (threadIdx.x % NCH), q = threadIdx.x / NCH;
+    const int cl = threadIdx.x % NCH, c = blockIdx.x * NCH + cl, q = threadIdx.x / NCH;
     float s = 0.f;
     if (c < C_)
+#pragma unroll 4
         for (int t = q; t < T; t += NPART) s += gld(x + static_cast<size_t>(t) * ldx + c);
-    red[q][threadIdx.x % NCH] = s;
+    red[q][cl] = s;
     __syncthreads();
-    if (q == 0 && c < C_) gst(out + c, (((red[0][threadIdx.x] + red[1][threadIdx.x]) + red[2][threadIdx.x]) + red[3][threadIdx.x]) / static_cast<float>(T));
+    if (q == 0 && c < C_) gst(out + c, slice_total(red, cl) / static_cast<float>(T));
 }
 
 // y[t][c] = b[t][c] * g[c] + r[t][c]   (squeeze-excitation scale + the block's residual)
@@ -67,17 +82,19 @@ __global__ void __launch_bounds__(BT) k_stats(const float *x, const float *w, in
     const float u = 1.f / static_cast<float>(T);
     float s = 0.f;
     if (c < C_)
+#pragma unroll 4
         for (int t = q; t < T; t += NPART) {
             const size_t o = static_cast<size_t>(t) * ld + c;
             s = fmaf(w ? gld(w + o) : u, gld(x + o), s);
         }
     red[q][cl] = s;
     __syncthreads();
-    if (q == 0) mean[cl] = ((red[0][cl] + red[1][cl]) + red[2][cl]) + red[3][cl];
+    if (q == 0) mean[cl] = slice_total(red, cl);
     __syncthreads();
     const float m = mean[cl];
     float v = 0.f;
     if (c < C_)
+#pragma unroll 4
         for (int t = q; t < T; t += NPART) {
             const size_t o = static_cast<size_t>(t) * ld + c;
             const float d = gld(x + o) - m;
@@ -88,7 +105,7 @@ __global__ void __launch_bounds__(BT) k_stats(const float *x, const float *w, in
     __syncthreads();
     if (q == 0 && c < C_) {
         gst(out + c, m);
-        gst(out + C_ + c, sqrtf(fmaxf(((red[0][cl] + red[1][cl]) + red[2][cl]) + red[3][cl], 1e-12f)));
+        gst(out + C_ + c, sqrtf(fmaxf(slice_total(red, cl), 1e-12f)));
     }
 }
 
@@ -99,22 +116,30 @@ __global__ void __launch_bounds__(BT) k_time_softmax(float *a, int T, int C_, in
     const int cl = threadIdx.x % NCH, c = blockIdx.x * NCH + cl, q = threadIdx.x / NCH;
     float m = -INFINITY;
     if (c < C_)
+#pragma unroll 4
         for (int t = q; t < T; t += NPART) m = fmaxf(m, gld(a + static_cast<size_t>(t) * ld + c));
     red[q][cl] = m;
     __syncthreads();
-    if (q == 0) tot[cl] = fmaxf(fmaxf(red[0][cl], red[1][cl]), fmaxf(red[2][cl], red[3][cl]));
+    if (q == 0) {
+        float mx = red[0][cl];
+#pragma unroll
+        for (int i = 1; i < NPART; ++i) mx = fmaxf(mx, red[i][cl]);
+        tot[cl] = mx;
+    }
     __syncthreads();
     const float mx = tot[cl];
     float s = 0.f;
     if (c < C_)
+#pragma unroll 4
         for (int t = q; t < T; t += NPART) s += expf(gld(a + static_cast<size_t>(t) * ld + c) - mx);
     __syncthreads();
     red[q][cl] = s;
     __syncthreads();
-    if (q == 0) tot[cl] = ((red[0][cl] + red[1][cl]) + red[2][cl]) + red[3][cl];
+    if (q == 0) tot[cl] = slice_total(red, cl);
     __syncthreads();
     const float inv = 1.f / tot[cl];
     if (c < C_)
+#pragma unroll 4
         for (int t = q; t < T; t += NPART) {
             float *p = a + static_cast<size_t>(t) * ld + c;
             gst(p, expf(gld(p) - mx) * inv);
@@ -143,7 +168,75 @@ __global__ void k_take_cols(const uint16_t *src, int rows, int ld, int n, uint16
     gst(dst + i, gld(src + r * ld + c));
 }
 
-// ---- host mel front end (SpeakerEncoder::mel, speaker.hip:262-300) -------------------------
+// ---- device mel front end ------------------------------------------------------------------
+// The host front end's arithmetic in the same double precision, one block per frame
+// (SpeakerEncoder::mel, speaker.hip:269-303, computes it in f32 on one host thread; f32 leaves
+// low-energy bins of tonal audio with ~1e-2 relative error). The 1024-point real FFT is a
+// 512-point complex FFT of z[m] = x[2m] + i x[2m+1] (Stockham radix-2, naturally ordered, in
+// LDS) followed by the real-input split X[k] = E[k] + e^{-2 pi i k / 1024} O[k],
+// E = (Z[k] + conj Z[512-k]) / 2, O = (Z[k] - conj Z[512-k]) / 2i. Each filter sums only its
+// nonzero bins, in bin order as the host does.
+
+constexpr int NFFT = 1024, NH = NFFT / 2, NBIN = NH + 1, MELS = 128;
+
+struct MelTables {                       // built once at create
+    double2 tw[NH / 2];                  // e^{-2 pi i q / NH}: the half-length FFT's twiddles
+    double2 post[NBIN];                  // e^{-2 pi i k / NFFT}
+    double hann[NFFT];                   // periodic
+    int lo[MELS], hi[MELS];              // filter m's nonzero bins [lo, hi)
+    float fb[MELS][NBIN];                // librosa's f32 filterbank, as the host uses it
+};
+
+__device__ __forceinline__ double2 cmul(double2 a, double2 b) { return make_double2(a.x * b.x - a.y * b.y, a.x * b.y + a.y * b.x); }
+
+// mel[t][m] (time-major, the layout block 0's conv reads) for frame t = blockIdx.x
+__global__ void __launch_bounds__(BT) k_logmel(const float *wav, int64_t n, int pad, int hop, const MelTables *tb, float *mel) {
+    static_assert(NH / 2 == BT, "one butterfly per thread per stage");
+    __shared__ double2 buf[2][NH];
+    __shared__ double mag[NBIN];
+    const int t = blockIdx.x, j = threadIdx.x;
+    const int64_t base = static_cast<int64_t>(t) * hop - pad;
+    auto sample = [&](int i) {
+        int64_t q = base + i;
+        if (q < 0) q = -q;                                  // reflect padding (n > pad is checked)
+        if (q >= n) q = 2 * (n - 1) - q;
+        return static_cast<double>(gld(wav + q)) * tb->hann[i];
+    };
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+        const int m = j + r * BT;
+        buf[0][m] = make_double2(sample(2 * m), sample(2 * m + 1));
+    }
+    __syncthreads();
+    int cur = 0;
+    for (int ns = 1; ns < NH; ns <<= 1) {
+        const int k = j & (ns - 1);
+        const double2 a = buf[cur][j], b = cmul(buf[cur][j + NH / 2], tb->tw[k * (NH / (2 * ns))]);
+        const int o = 2 * (j - k) + k;
+        buf[cur ^ 1][o] = make_double2(a.x + b.x, a.y + b.y);
+        buf[cur ^ 1][o + ns] = make_double2(a.x - b.x, a.y - b.y);
+        cur ^= 1;
+        __syncthreads();
+    }
+    const double2 *Z = buf[cur];
+    for (int k = j; k < NBIN; k += BT) {
+        const double2 zk = Z[k & (NH - 1)], zr = Z[(NH - k) & (NH - 1)];
+        const double2 e = make_double2(0.5 * (zk.x + zr.x), 0.5 * (zk.y - zr.y));
+        const double2 o = make_double2(0.5 * (zk.y + zr.y), -0.5 * (zk.x - zr.x));
+        const double2 x = cmul(tb->post[k], o);
+        const double re = e.x + x.x, im = e.y + x.y;
+        mag[k] = sqrt(re * re + im * im + 1e-9);
+    }
+    __syncthreads();
+    if (j < MELS) {
+        const float *row = tb->fb[j];
+        double s = 0.0;
+        for (int k = gld(tb->lo + j), e = gld(tb->hi + j); k < e; ++k) s += static_cast<double>(gld(row + k)) * mag[k];
+        gst(mel + static_cast<size_t>(t) * MELS + j, static_cast<float>(log(fmax(s, 1e-5))));
+    }
+}
+
+// ---- host mel front end (SpeakerEncoder::mel, speaker.hip:269-303) -------------------------
 
 // librosa.filters.mel(sr, n_fft, n_mels, fmin, fmax): slaney mel scale and norm (speaker.hip:45-71)
 std::vector<float> mel_filterbank(int sr, int n_fft, int n_mels, double fmin, double fmax) {
@@ -210,6 +303,7 @@ void launch_spk(const ConvArgs &a, int pro, int epi, dim3 grid, hipStream_t s) {
     if constexpr (K == 3) NAVI_SPK(PRO_ADD2, EPI_RELU)
     NAVI_SPK(PRO_NONE, EPI_RELU)
     if constexpr (K == 1) {
+        NAVI_SPK(PRO_NONE, EPI_PARTIAL)
         NAVI_SPK(PRO_NONE, EPI_BIAS)
         NAVI_SPK(PRO_NONE, EPI_SIGMOID)
         NAVI_SPK(PRO_NONE, EPI_RELU_TANH)
@@ -232,6 +326,12 @@ struct navi_speaker {
     float *g2 = nullptr, *mean = nullptr, *g = nullptr, *gse = nullptr, *stats = nullptr, *pooled = nullptr, *bias2 = nullptr;
     float *emb = nullptr;
     uint32_t *flag = nullptr;
+    MelTables *tables = nullptr;              // the device front end's constants
+    float *part = nullptr;                    // split-K partial sums
+    size_t part_cap = 0;
+    float *wav = nullptr;                     // audio of the last navi_speaker_embed
+    int64_t wav_cap = 0;
+    int last_frames = 0;
     hipEvent_t ev0 = nullptr, ev1 = nullptr;
     double last_ms = 0;
     std::vector<void *> owned;
@@ -261,8 +361,25 @@ struct navi_speaker {
         ca.cps = cv.Cin; ca.lpad = (cv.K - 1) * cv.dil / 2; ca.reflect = 1;
         // 16-row tiles unless that already gives the chip two blocks per CU
         const int mt = ((cv.Cout + 63) / 64) * ((T + 63) / 64) >= 512 ? 4 : 1;
-        const dim3 grid((cv.Cout + 63) / 64, (T + 16 * mt - 1) / (16 * mt), 1);
+        dim3 grid((cv.Cout + 63) / 64, (T + 16 * mt - 1) / (16 * mt), 1);
         hipStream_t s = device_state().stream;
+        // under 96 blocks: split the input channels (>= 128 per split) so about 256 blocks run
+        const int blocks = static_cast<int>(grid.x * grid.y);
+        if (cv.K == 1 && pro == PRO_NONE && blocks < 96 && cv.Cin >= 256) {
+            int sp = std::min((256 + blocks - 1) / blocks, cv.Cin / 128);
+            while (sp > 1 && static_cast<size_t>(sp) * T * cv.Cout > part_cap) --sp;
+            if (sp > 1) {
+                ca.cps = ((cv.Cin + sp - 1) / sp + CCH - 1) / CCH * CCH;
+                sp = (cv.Cin + ca.cps - 1) / ca.cps;
+                ca.part = part;
+                grid.z = static_cast<unsigned>(sp);
+                launch_spk<1, 1>(ca, PRO_NONE, EPI_PARTIAL, grid, s);
+                const size_t n = static_cast<size_t>(T) * cv.Cout;
+                hipLaunchKernelGGL(k_conv_finish, dim3(static_cast<unsigned>((n + BT - 1) / BT)), dim3(BT), 0, s, ca, sp, epi);
+                NAVI_TRY_HIP(hipGetLastError(), err, errlen);
+                return NAVI_OK;
+            }
+        }
         switch (cv.K * 10 + mt) {
         case 11: launch_spk<1, 1>(ca, pro, epi, grid, s); break;
         case 14: launch_spk<4, 1>(ca, pro, epi, grid, s); break;
@@ -329,17 +446,55 @@ struct navi_speaker {
 
 namespace {
 
-navi_status check_params(const navi_speaker_params *p, char *err, size_t errlen) {
+// device: the front end of navi_speaker_embed (k_logmel) is built for the model's 1024-point FFT
+navi_status check_params(const navi_speaker_params *p, char *err, size_t errlen, bool device = false) {
     if (!p) {
         set_err(err, errlen, "speaker: null params");
         return NAVI_ERR_INVALID;
     }
     const bool pow2 = p->n_fft >= 16 && (p->n_fft & (p->n_fft - 1)) == 0;
     if (!pow2 || p->win != p->n_fft || p->hop < 1 || p->hop > p->n_fft || p->num_mels != 128 || p->sample_rate < 1 ||
-        p->enc_dim < 16 || p->enc_dim % 16 != 0 || !(p->fmax > p->fmin) || p->fmin < 0.f) {
+        p->enc_dim < 16 || p->enc_dim % 16 != 0 || !(p->fmax > p->fmin) || p->fmin < 0.f || (device && p->n_fft != NFFT)) {
         set_err(err, errlen, "speaker: unsupported front end (n_fft %d, win %d, hop %d, mels %d, dim %d)", p->n_fft, p->win, p->hop,
                 p->num_mels, p->enc_dim);
         return NAVI_ERR_UNSUPPORTED;
+    }
+    return NAVI_OK;
+}
+
+// reflect padding mirrors once: the widest pad (k3, dilation 4: 4 rows) must stay below T
+navi_status check_frames(const navi_speaker *h, int32_t T, char *err, size_t errlen) {
+    if (T < 5 || T > h->max_frames) {
+        set_err(err, errlen, "speaker: %d mel frames, this encoder takes 5..%d (raise max_seconds)", T, h->max_frames);
+        return NAVI_ERR_INVALID;
+    }
+    return NAVI_OK;
+}
+
+// The device part of an embed: (wav_n > 0) the front end from h->wav into h->mel, the network,
+// the embedding back to the host. Device time of both in last_ms.
+navi_status embed_device(navi_speaker *h, int T, int64_t wav_n, float *emb, char *err, size_t errlen) {
+    hipStream_t s = device_state().stream;
+    NAVI_TRY_HIP(hipMemsetAsync(h->flag, 0, 4, s), err, errlen);
+    NAVI_TRY_HIP(hipEventRecord(h->ev0, s), err, errlen);
+    if (wav_n > 0)
+        hipLaunchKernelGGL(k_logmel, dim3(static_cast<unsigned>(T)), dim3(BT), 0, s, h->wav, wav_n, (NFFT - h->p.hop) / 2, h->p.hop,
+                           h->tables, h->mel);
+    const navi_status st = h->run(T, err, errlen);
+    if (st != NAVI_OK) return st;
+    NAVI_TRY_HIP(hipEventRecord(h->ev1, s), err, errlen);
+    uint32_t bad = 0;
+    NAVI_TRY_HIP(hipMemcpyAsync(emb, h->emb, static_cast<size_t>(h->p.enc_dim) * sizeof(float), hipMemcpyDeviceToHost, s), err,
+                 errlen);
+    NAVI_TRY_HIP(hipMemcpyAsync(&bad, h->flag, 4, hipMemcpyDeviceToHost, s), err, errlen);
+    NAVI_TRY_HIP(hipStreamSynchronize(s), err, errlen);
+    float ms = 0.f;
+    (void) hipEventElapsedTime(&ms, h->ev0, h->ev1);
+    h->last_ms = ms;
+    h->last_frames = T;
+    if (bad) {
+        set_err(err, errlen, "speaker: an activation is outside the f16 range (|x| >= 65504 or NaN)");
+        return NAVI_ERR_INVALID;
     }
     return NAVI_OK;
 }
@@ -407,7 +562,7 @@ navi_status navi_speaker_mel(const navi_speaker_params *p, const float *wav, int
 
 navi_status navi_speaker_create(const navi_speaker_params *p, const navi_tensor_ref *tensors, int32_t n_tensors,
                                 double max_seconds, navi_speaker **out, char *err, size_t errlen) {
-    navi_status st = check_params(p, err, errlen);
+    navi_status st = check_params(p, err, errlen, true);
     if (st != NAVI_OK) return st;
     if (!tensors || !out || !(max_seconds > 0.0) || max_seconds > 600.0) {
         set_err(err, errlen, "speaker: bad argument (max_seconds %.1f)", max_seconds);
@@ -505,7 +660,34 @@ navi_status navi_speaker_create(const navi_speaker_params *p, const navi_tensor_
     SA(h->bias2, ASP);
     SA(h->emb, p->enc_dim);
     SA(h->flag, 1);
+    h->wav_cap = static_cast<int64_t>(h->max_frames + 2) * p->hop + NFFT;
+    SA(h->wav, static_cast<size_t>(h->wav_cap));
+    SA(h->tables, 1);
+    h->part_cap = size_t(2) << 20;
+    SA(h->part, h->part_cap);
 #undef SA
+    {   // the front end's tables, copied synchronously
+        auto tb = std::make_unique<MelTables>();
+        for (int q = 0; q < NH / 2; ++q)
+            tb->tw[q] = make_double2(std::cos(-2.0 * M_PI * q / NH), std::sin(-2.0 * M_PI * q / NH));
+        for (int k = 0; k < NBIN; ++k)
+            tb->post[k] = make_double2(std::cos(-2.0 * M_PI * k / NFFT), std::sin(-2.0 * M_PI * k / NFFT));
+        for (int i = 0; i < NFFT; ++i) tb->hann[i] = 0.5 - 0.5 * std::cos(2.0 * M_PI * i / NFFT);
+        const std::vector<float> fb = mel_filterbank(p->sample_rate, NFFT, MELS, p->fmin, p->fmax);
+        for (int m = 0; m < MELS; ++m) {
+            int lo = NBIN, hi = 0;
+            for (int k = 0; k < NBIN; ++k) {
+                tb->fb[m][k] = fb[static_cast<size_t>(m) * NBIN + k];
+                if (tb->fb[m][k] != 0.f) lo = std::min(lo, k), hi = k + 1;
+            }
+            tb->lo[m] = std::min(lo, hi);
+            tb->hi[m] = hi;
+        }
+        if (hipMemcpy(h->tables, tb.get(), sizeof(MelTables), hipMemcpyHostToDevice) != hipSuccess) {
+            set_err(err, errlen, "speaker: table upload failed");
+            return fail(NAVI_ERR_HIP);
+        }
+    }
     if (hipEventCreate(&h->ev0) != hipSuccess || hipEventCreate(&h->ev1) != hipSuccess || hipGetLastError() != hipSuccess ||
         hipStreamSynchronize(s) != hipSuccess) {
         set_err(err, errlen, "speaker: HIP setup failed");
@@ -526,53 +708,39 @@ navi_status navi_speaker_embed_mel(navi_speaker *h, const float *mel, int32_t n_
         set_err(err, errlen, "speaker: null argument");
         return NAVI_ERR_INVALID;
     }
-    // reflect padding mirrors once: the widest pad (k3, dilation 4: 4 rows) must stay below T
-    if (n_frames < 5 || n_frames > h->max_frames) {
-        set_err(err, errlen, "speaker: %d mel frames, this encoder takes 5..%d (raise max_seconds)", n_frames, h->max_frames);
-        return NAVI_ERR_INVALID;
-    }
+    navi_status st = check_frames(h, n_frames, err, errlen);
+    if (st != NAVI_OK) return st;
     const int T = n_frames, nm = h->p.num_mels;
     // [n_mels][T] -> time-major [T][n_mels]
     std::vector<float> tm(static_cast<size_t>(T) * nm);
     for (int m = 0; m < nm; ++m)
         for (int t = 0; t < T; ++t) tm[static_cast<size_t>(t) * nm + m] = mel[static_cast<size_t>(m) * T + t];
-    hipStream_t s = device_state().stream;
-    NAVI_TRY_HIP(hipMemcpyAsync(h->mel, tm.data(), tm.size() * sizeof(float), hipMemcpyHostToDevice, s), err, errlen);
-    NAVI_TRY_HIP(hipMemsetAsync(h->flag, 0, 4, s), err, errlen);
-    NAVI_TRY_HIP(hipEventRecord(h->ev0, s), err, errlen);
-    const navi_status st = h->run(T, err, errlen);
-    if (st != NAVI_OK) return st;
-    NAVI_TRY_HIP(hipEventRecord(h->ev1, s), err, errlen);
-    uint32_t bad = 0;
-    NAVI_TRY_HIP(hipMemcpyAsync(emb, h->emb, static_cast<size_t>(h->p.enc_dim) * sizeof(float), hipMemcpyDeviceToHost, s), err,
+    NAVI_TRY_HIP(hipMemcpyAsync(h->mel, tm.data(), tm.size() * sizeof(float), hipMemcpyHostToDevice, device_state().stream), err,
                  errlen);
-    NAVI_TRY_HIP(hipMemcpyAsync(&bad, h->flag, 4, hipMemcpyDeviceToHost, s), err, errlen);
-    NAVI_TRY_HIP(hipStreamSynchronize(s), err, errlen);
-    float ms = 0.f;
-    (void) hipEventElapsedTime(&ms, h->ev0, h->ev1);
-    h->last_ms = ms;
-    if (bad) {
-        set_err(err, errlen, "speaker: an activation is outside the f16 range (|x| >= 65504 or NaN)");
-        return NAVI_ERR_INVALID;
-    }
-    return NAVI_OK;
+    return embed_device(h, T, 0, emb, err, errlen);
 }
 
 navi_status navi_speaker_embed(navi_speaker *h, const float *wav, int64_t n, float *emb, char *err, size_t errlen) {
-    if (!h) {
+    if (!h || !wav || !emb) {
         set_err(err, errlen, "speaker: null argument");
         return NAVI_ERR_INVALID;
     }
     int32_t T = 0;
-    navi_status st = navi_speaker_mel(&h->p, wav, n, nullptr, 0, &T, err, errlen);
+    navi_status st = navi_speaker_mel(&h->p, wav, n, nullptr, 0, &T, err, errlen);   // length checks and the frame count
     if (st != NAVI_OK) return st;
-    if (T > h->max_frames) {
+    if (T > h->max_frames || n > h->wav_cap) {
         set_err(err, errlen, "speaker: reference audio longer than the encoder's max_seconds (%d frames > %d)", T, h->max_frames);
         return NAVI_ERR_INVALID;
     }
-    std::vector<float> mel(static_cast<size_t>(T) * h->p.num_mels);
-    if ((st = navi_speaker_mel(&h->p, wav, n, mel.data(), static_cast<int64_t>(mel.size()), &T, err, errlen)) != NAVI_OK) return st;
-    return navi_speaker_embed_mel(h, mel.data(), T, emb, err, errlen);
+    if ((st = check_frames(h, T, err, errlen)) != NAVI_OK) return st;
+    NAVI_TRY_HIP(hipMemcpyAsync(h->wav, wav, static_cast<size_t>(n) * sizeof(float), hipMemcpyHostToDevice, device_state().stream),
+                 err, errlen);
+    return embed_device(h, T, n, emb, err, errlen);
+}
+
+const float *navi_speaker_tap_mel(const navi_speaker *h, int32_t *n_frames) {
+    if (n_frames) *n_frames = h ? h->last_frames : 0;
+    return h ? h->mel : nullptr;
 }
 
 double navi_speaker_last_ms(const navi_speaker *h) { return h ? h->last_ms : 0.0; }

@@ -34,7 +34,7 @@ EXPORTS = [
     "navi_streams_create", "navi_streams_destroy", "navi_streams_reset", "navi_streams_run", "navi_streams_step_out",
     "navi_streams_max_streams", "navi_streams_last_ms", "navi_streams_set_taps", "navi_streams_set_graphs",
     "navi_speaker_mel", "navi_speaker_create", "navi_speaker_destroy", "navi_speaker_embed_mel", "navi_speaker_embed",
-    "navi_speaker_last_ms",
+    "navi_speaker_last_ms", "navi_speaker_tap_mel",
     "navi_streams_tap_hidden",
     "navi_streams_tap_logits", "navi_streams_tap_cp_logits",
 ]
@@ -210,6 +210,8 @@ def lib() -> C.CDLL:
     L.navi_speaker_embed.argtypes = [C.c_void_p, C.c_void_p, C.c_int64, C.c_void_p, E, C.c_size_t]
     L.navi_speaker_last_ms.argtypes = [C.c_void_p]
     L.navi_speaker_last_ms.restype = C.c_double
+    L.navi_speaker_tap_mel.argtypes = [C.c_void_p, C.POINTER(C.c_int32)]
+    L.navi_speaker_tap_mel.restype = C.c_void_p
     L.navi_synth.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.POINTER(SynthRequest), PCM_CALLBACK, C.c_void_p,
                              C.POINTER(SynthStats), E, C.c_size_t]
     L.navi_linear.argtypes = [C.c_void_p, C.c_int32, C.c_int32, C.c_void_p, C.c_int32, C.c_int32, C.c_void_p, C.c_void_p,
@@ -789,6 +791,14 @@ class Speaker:
 
     def last_ms(self) -> float:
         return lib().navi_speaker_last_ms(self.h)
+
+    def tap_mel(self) -> np.ndarray:
+        """The device log-mel of the last embed as [num_mels][T] (navi_speaker_tap_mel)."""
+        n = C.c_int32()
+        ptr = lib().navi_speaker_tap_mel(self.h, C.byref(n))
+        out = np.empty((n.value, self.params.num_mels), np.float32)
+        _check(lib().navi_mem_d2h(out.ctypes.data, ptr, out.nbytes), what="navi_mem_d2h")
+        return out.T.copy()
 
 
 # ---- one request end to end ------------------------------------------------------------

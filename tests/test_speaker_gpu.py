@@ -56,6 +56,33 @@ def test_embed_audio_matches_oracle(spk, speaker_fixture):
     check(s.embed(wav), ora.embed(wav), "fixture audio")
 
 
+def test_device_mel_matches_host_mel_and_fixture(spk, speaker_fixture):
+    """navi_speaker_embed's front end (k_logmel, double-precision FFT in LDS) against the host's
+    navi_speaker_mel (double, another FFT algorithm): equal up to float rounding of the output
+    (1e-5 absolute on values down to log(1e-5) = -11.5), including a pure tone whose high bins
+    sit at sidelobe level. Against the reference's f32 fixture: within its own f32 error (the
+    host's double result sits 3.3e-4 from it)."""
+    abi, W, _ = spk
+    wav, mel_ref = speaker_fixture
+    s = abi.Speaker(W)
+    for name, x in (("fixture audio", wav),
+                    ("noise 1300", (np.random.default_rng(5).standard_normal(1300) * 0.2).astype(np.float32)),
+                    ("tone + silence", np.concatenate([np.sin(np.arange(24000) * 0.05).astype(np.float32) * 0.5,
+                                                       np.zeros(7000, np.float32)]))):
+        log(f"speaker device mel, {name}")
+        s.embed(x)
+        dev = s.tap_mel()
+        host = s.mel(x)
+        assert dev.shape == host.shape
+        d = np.abs(dev.astype(np.float64) - host)
+        rel = float(np.sqrt(np.mean(d ** 2) / np.mean(host.astype(np.float64) ** 2)))
+        log(f"  {dev.shape[1]} frames: max abs {d.max():.2e}, rel rms {rel:.2e}, device {s.last_ms():.3f} ms")
+        assert d.max() <= 1e-5 and rel <= 1e-7
+        if name == "fixture audio":
+            inner = dev.shape[1] - 3
+            assert np.abs(dev[:, :inner] - mel_ref[:, :inner]).max() <= 1e-3
+
+
 @pytest.mark.parametrize("n", [1300, 9001, 3 * 24000 + 517])
 def test_ragged_lengths(spk, n):
     abi, W, ora = spk
