@@ -19,7 +19,7 @@
 //    the conv runs over the 1536 x channels only: the [T][4608] concatenation is never built.
 //  * Time reductions (SE mean, pooling statistics, softmax over time) run 16 channels x 16 time
 //    slices per block, summed in a fixed order: the same bits every run. k=1 convs with few
-//    output tiles (the SE and fc GEMVs, attentive pooling on short clips) split their input
+//    output tiles (the SE and fc GEMVs, attentive pooling's 128-channel conv) split their input
 //    channels over blocks; the partial sums are added in split order.
 #include "conv.h"
 #include "dev_common.h"
@@ -363,9 +363,9 @@ struct navi_speaker {
         const int mt = ((cv.Cout + 63) / 64) * ((T + 63) / 64) >= 512 ? 4 : 1;
         dim3 grid((cv.Cout + 63) / 64, (T + 16 * mt - 1) / (16 * mt), 1);
         hipStream_t s = device_state().stream;
-        // under 96 blocks: split the input channels (>= 128 per split) so about 256 blocks run
+        // under 192 blocks: split the input channels (>= 128 per split) so about 256 blocks run
         const int blocks = static_cast<int>(grid.x * grid.y);
-        if (cv.K == 1 && pro == PRO_NONE && blocks < 96 && cv.Cin >= 256) {
+        if (cv.K == 1 && pro == PRO_NONE && blocks < 192 && cv.Cin >= 256) {
             int sp = std::min((256 + blocks - 1) / blocks, cv.Cin / 128);
             while (sp > 1 && static_cast<size_t>(sp) * T * cv.Cout > part_cap) --sp;
             if (sp > 1) {
