@@ -10,16 +10,20 @@
 //    bits of the activation: the products keep f32-level accuracy while the weights stream
 //    at the matrix cores' f16 rate. Activations must lie inside the f16 range; a device flag
 //    turns anything else into an error instead of an infinity.
-//  * A block owns 64 output columns (one 16-column MFMA tile per wave) and up to 64 rows;
-//    K is split across blocks so that even N = 1024 fills the 256 CUs. Split-K partials go to
-//    a workspace and are summed in a fixed order by the "finish" kernels, which also apply
-//    the epilogue (bias, SiLU, residual + the next RMSNorm, SwiGLU, q/k head norms + RoPE +
-//    the f16 K/V store): deterministic results and no extra pass for the epilogues.
+//  * The linear (navi_linear, the prompt's text projection): a block owns 64 output columns (one
+//    16-column MFMA tile per wave) and up to 64 rows; K is split across blocks so that even
+//    N = 1024 fills the 256 CUs. Split-K partials go to a workspace and are summed in a fixed
+//    order by the "finish" kernels, which also apply the epilogue (bias, SiLU, residual):
+//    deterministic results.
+//  * The prefill's layers: six launches each. q|k|v, o, gate|up and down are whole-K row
+//    projections (rows.h) with the input RMSNorm, SwiGLU and the residual add fused in; one
+//    kernel applies the q/k head norms + RoPE and stores K/V as f16; then the attention.
 //  * Causal prefill attention: one block per (row, q head), scores over keys 0..row from the
 //    f16 cache, exactly as the frame's decode attention will later read them.
 #include "dev_common.h"
 #include "host_util.h"
 #include "linear.h"
+#include "rows.h"
 
 #include <algorithm>
 #include <cmath>
@@ -538,7 +542,9 @@ navi_status navi_talker_create(const navi_model_params *p, const navi_tensor_ref
     navi_status st = ensure_device(err, errlen);
     if (st != NAVI_OK) return st;
     const navi_xformer_params &x = p->talker;
-    if (x.head_dim != HD || x.hidden % 1024 != 0 || x.n_head != 2 * x.n_kv_head || x.ff % 64 != 0 || x.vocab % 64 != 0 ||
+    // the prefill's row projections are built for hidden 1024, 16 q heads (K = 2048 into o) and
+    // ff 3072 (K = 3072 into down): the 0.6B talker
+    if (x.head_dim != HD || x.n_head != 2 * x.n_kv_head || x.n_head != 16 || x.ff != 3072 || x.vocab % 64 != 0 ||
         p->text_hidden % 64 != 0 || x.hidden != 1024) {
         set_err(err, errlen, "talker: unsupported shape (hidden %d, head_dim %d, ff %d, vocab %d, text_hidden %d)", x.hidden,
                 x.head_dim, x.ff, x.vocab, p->text_hidden);
@@ -721,33 +727,35 @@ navi_status navi_talker_prefill(navi_talker *t, const float *d_rows, int32_t n_r
     hipStream_t s = device_state().stream;
     NAVI_TRY_HIP(hipMemsetAsync(t->flag, 0, 4, s), err, errlen);
     NAVI_TRY_HIP(hipEventRecord(t->ev0, s), err, errlen);
-    hipLaunchKernelGGL(k_resid_norm, dim3(T), dim3(BT), 0, s, nullptr, 0, d_rows, t->x, t->layers[0].ln1, t->eps, t->xn, T, H);
+    // Six launches per layer: q|k|v (RMSNorm fused) -> q/k norms + RoPE + K/V store -> attention
+    // -> o (+ residual) -> gate|up (RMSNorm and SwiGLU fused) -> down (+ residual); every
+    // projection one whole-K MFMA kernel (rows.h), no split-K partials.
+    NAVI_TRY_HIP(hipMemcpyAsync(t->x, d_rows, static_cast<size_t>(T) * H * sizeof(float), hipMemcpyDeviceToDevice, s), err,
+                 errlen);
     const float scale = 1.f / std::sqrt(static_cast<float>(HD));
     const size_t att_lds = static_cast<size_t>(2) * T * sizeof(float);
     for (int l = 0; l < t->L; ++l) {
         const LayerW &w = t->layers[l];
-        int S = pick_splits(T, H, QKVW);
-        launch_partial3(t->xn, H, T, w.wq, t->QD, w.wk, t->KVD, w.wv, t->KVD, H, S, t->part, QKVW, 0, t->flag, s);
-        hipLaunchKernelGGL(k_qkv_finish, dim3(T), dim3(BT), QKVW * sizeof(float), s, t->part, S, T, t->NQ, t->NKV, w.qn,
+        rows::launch_rows(rows::EPI_PLAIN, true, t->x, H, T, H, w.ln1, t->eps, w.wq, t->QD, w.wk, t->KVD, w.wv, t->KVD, t->part,
+                          QKVW, t->flag, s);
+        hipLaunchKernelGGL(k_qkv_finish, dim3(T), dim3(BT), QKVW * sizeof(float), s, t->part, 1, T, t->NQ, t->NKV, w.qn,
                            w.kn, t->eps, t->invf, 0, t->q, t->kk[l], t->vv[l]);
         hipLaunchKernelGGL(k_attn_prefill, dim3(T, t->NKV), dim3(BT), att_lds, s, t->q, t->kk[l], t->vv[l], t->NQ, t->NKV, 0,
                            scale, t->att);
-        S = pick_splits(T, t->QD, H);
-        launch_partial(t->att, t->QD, T, w.wo, t->QD, H, S, t->part, H, 0, t->flag, s);
-        hipLaunchKernelGGL(k_resid_norm, dim3(T), dim3(BT), 0, s, t->part, S, nullptr, t->x, w.ln2, t->eps, t->xn, T, H);
-        S = pick_splits(T, H, 2 * t->F);
-        launch_partial3(t->xn, H, T, w.wg, t->F, w.wu, t->F, nullptr, 0, H, S, t->part, 2 * t->F, 0, t->flag, s);
-        hipLaunchKernelGGL(k_swiglu, dim3(T), dim3(BT), 0, s, t->part, S, T, t->F, t->h);
-        S = pick_splits(T, t->F, H);
-        launch_partial(t->h, t->F, T, w.wd, t->F, H, S, t->part, H, 0, t->flag, s);
-        const float *next = l + 1 < t->L ? t->layers[l + 1].ln1 : t->final_norm;
-        hipLaunchKernelGGL(k_resid_norm, dim3(T), dim3(BT), 0, s, t->part, S, nullptr, t->x, next, t->eps, t->xn, T, H);
+        rows::launch_rows(rows::EPI_RESID, false, t->att, t->QD, T, t->QD, nullptr, 0.f, w.wo, H, nullptr, 0, nullptr, 0, t->x,
+                          H, t->flag, s);
+        rows::launch_rows(rows::EPI_SWIGLU, true, t->x, H, T, H, w.ln2, t->eps, w.wg, t->F, w.wu, t->F, nullptr, 0, t->h, t->F,
+                          t->flag, s);
+        rows::launch_rows(rows::EPI_RESID, false, t->h, t->F, T, t->F, nullptr, 0.f, w.wd, H, nullptr, 0, nullptr, 0, t->x, H,
+                          t->flag, s);
     }
-    const float *last = t->xn + static_cast<size_t>(T - 1) * H;
+    // the last row: final RMSNorm (the post-norm hidden the frame takes), then the codec head
+    float *last = t->xn + static_cast<size_t>(T - 1) * H;
+    hipLaunchKernelGGL(k_resid_norm, dim3(1), dim3(BT), 0, s, nullptr, 0, t->x + static_cast<size_t>(T - 1) * H,
+                       t->x + static_cast<size_t>(T - 1) * H, t->final_norm, t->eps, last, 1, H);
     NAVI_TRY_HIP(hipMemcpyAsync(t->hidden, last, H * 4, hipMemcpyDeviceToDevice, s), err, errlen);
-    const int S = pick_splits(1, H, t->V);
-    launch_partial(last, H, 1, t->head, H, t->V, S, t->part, t->V, 0, t->flag, s);
-    hipLaunchKernelGGL(k_finish_linear, dim3(1), dim3(BT), 0, s, t->part, S, 1, t->V, nullptr, nullptr, 0, t->logits, t->V);
+    rows::launch_rows(rows::EPI_PLAIN, false, last, H, 1, H, nullptr, 0.f, t->head, t->V, nullptr, 0, nullptr, 0, t->logits, t->V,
+                      t->flag, s);
     NAVI_TRY_HIP(hipGetLastError(), err, errlen);
     NAVI_TRY_HIP(hipEventRecord(t->ev1, s), err, errlen);
     NAVI_TRY_HIP(hipEventSynchronize(t->ev1), err, errlen);

@@ -19,6 +19,7 @@
 #include "dev_common.h"
 #include "host_util.h"
 #include "linear.h"
+#include "rows.h"
 #include "sampler.h"
 
 #include <algorithm>
@@ -29,6 +30,8 @@
 
 namespace navi_amd {
 namespace ms {
+
+using namespace rows;
 
 constexpr int BT = 256, NW = BT / WAVE;
 constexpr int HD = 128, NCB = 16, CPH = NCB - 1;
@@ -41,194 +44,6 @@ struct StreamMeta {
     int n_past, frame_index;
     uint64_t talker_seed, cp_seed;
 };
-
-// ---- projections over the streams: Y = X W^T, whole K in one block ------------------------
-//
-// A block owns 16 output columns (SwiGLU: 16 gate and the matching 16 up columns) for up to 64
-// rows; its 4 waves take a quarter of K each, loading their A rows (f32, split into f16 hi + lo
-// for two v_mfma_f32_16x16x32_f16 each) and W rows (f16) straight from global memory, 4 MFMA
-// steps' loads in flight at a time, no LDS staging. The 4 waves' tiles are summed in LDS in wave
-// order. With NORM the rows are the residual stream: A is multiplied by the RMSNorm weight as it
-// is loaded, every lane sums the squares of its elements, and the row scale rsqrt(mean(x^2) + eps)
-// (sums taken in a fixed order, the same in every block) multiplies the results. Epilogues:
-// plain store, SiLU(gate) * up, or an add into the residual stream. No split-K partials and no
-// finish kernels (the decode's kernel count is what bounds it).
-enum { EPI_PLAIN = 0, EPI_SWIGLU = 1, EPI_RESID = 2 };
-
-struct RowArgs {
-    const float *a;                   // A [M][lda] f32
-    const float *ln;                  // NORM: RMSNorm weight [K]
-    const uint16_t *w0, *w1, *w2;     // W rows [0, n1) of w0, [n1, n2) of w1, [n2, ..) of w2, each [rows][K]
-    float *y;                         // PLAIN / SWIGLU: [M][ldy] output; RESID: the residual stream, added to
-    uint32_t *flag;                   // set when an activation is outside the f16 range
-    int lda, M, K, n1, n2, F, ldy;    // F: SWIGLU gate rows [0, F), up rows [F, 2F) of the combined W
-    float eps;
-};
-
-typedef _Float16 rhalf8 __attribute__((ext_vector_type(8)));
-
-// NWV waves per block, each one batch of KS MFMA steps (32 k each): K = 32 KS NWV. Every load of
-// a wave is issued before its first MFMA (the whole chain is one memory latency), and the kernels
-// stay small (no unrolled K loop, so the decode's few kernels stay in the instruction cache).
-template <int MT, int EPI, bool NORM, int NWV, int KS>
-__global__ void __launch_bounds__(NWV * WAVE) k_rows(RowArgs a) {
-    constexpr int NT = EPI == EPI_SWIGLU ? 2 : 1, K = 32 * KS * NWV;
-    __shared__ f32x4_t red[NWV][NT][MT][WAVE];
-    __shared__ float ssq[NWV][MT][WAVE];
-    __shared__ float rscale[MT * 16];
-    const int w = static_cast<int>(threadIdx.x) / WAVE, l = static_cast<int>(threadIdx.x) & (WAVE - 1);
-    const int c = l & 15, kq = l >> 4, m0 = blockIdx.y * (MT * 16);
-    const int nb = blockIdx.x * 16 + c;
-    auto wrow = [&](int n) {
-        return n < a.n1 ? a.w0 + static_cast<size_t>(n) * K
-             : n < a.n2 ? a.w1 + static_cast<size_t>(n - a.n1) * K : a.w2 + static_cast<size_t>(n - a.n2) * K;
-    };
-    const int kbeg = w * (K / NWV) + 8 * kq;
-    u32x4_t bv[NT][KS];
-    f32x4_t av[KS][MT][2], lv[KS][2];
-    {
-        const uint16_t *wr[NT];
-        wr[0] = wrow(nb);
-        if constexpr (NT == 2) wr[NT - 1] = wrow(a.F + nb);
-#pragma unroll
-        for (int st = 0; st < KS; ++st) {
-            const int k = kbeg + 32 * st;
-#pragma unroll
-            for (int t = 0; t < NT; ++t) bv[t][st] = *(const NAVI_GLOBAL u32x4_t *) (wr[t] + k);
-#pragma unroll
-            for (int i = 0; i < MT; ++i) {
-                const int m = m0 + 16 * i + c;
-                if (m < a.M) {
-                    const NAVI_GLOBAL f32x4_t *p = (const NAVI_GLOBAL f32x4_t *) (a.a + static_cast<size_t>(m) * a.lda + k);
-                    av[st][i][0] = p[0];
-                    av[st][i][1] = p[1];
-                } else {
-                    av[st][i][0] = av[st][i][1] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-                }
-            }
-            if constexpr (NORM) {
-                const NAVI_GLOBAL f32x4_t *p = (const NAVI_GLOBAL f32x4_t *) (a.ln + k);
-                lv[st][0] = p[0];
-                lv[st][1] = p[1];
-            }
-        }
-    }
-    f32x4_t acc[NT][MT];
-    float ss[MT];
-#pragma unroll
-    for (int i = 0; i < MT; ++i) {
-        ss[i] = 0.f;
-#pragma unroll
-        for (int t = 0; t < NT; ++t) acc[t][i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    }
-    bool bad = false;
-#pragma unroll
-    for (int st = 0; st < KS; ++st) {
-        rhalf8 b[NT];
-#pragma unroll
-        for (int t = 0; t < NT; ++t) __builtin_memcpy(&b[t], &bv[t][st], 16);
-#pragma unroll
-        for (int i = 0; i < MT; ++i) {
-            rhalf8 hi, lo;
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                float v = av[st][i][j >> 2][j & 3];
-                if constexpr (NORM) {
-                    ss[i] = fmaf(v, v, ss[i]);
-                    v *= lv[st][j >> 2][j & 3];
-                }
-                bad |= !(fabsf(v) < 65504.f);
-                const _Float16 h = static_cast<_Float16>(v);
-                hi[j] = h;
-                lo[j] = static_cast<_Float16>(v - static_cast<float>(h));
-            }
-#pragma unroll
-            for (int t = 0; t < NT; ++t) {
-                acc[t][i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(hi, b[t], acc[t][i], 0, 0, 0);
-                acc[t][i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(lo, b[t], acc[t][i], 0, 0, 0);
-            }
-        }
-    }
-    if (bad) gst(a.flag, 1u);
-#pragma unroll
-    for (int i = 0; i < MT; ++i) {
-#pragma unroll
-        for (int t = 0; t < NT; ++t) red[w][t][i][l] = acc[t][i];
-        if constexpr (NORM) ssq[w][i][l] = ss[i];
-    }
-    __syncthreads();
-    if constexpr (NORM) {
-        // row r of the tile: lanes r % 16 + 16 q of every wave hold its sums of squares
-        if (threadIdx.x < MT * 16) {
-            const int i = threadIdx.x / 16, r = threadIdx.x % 16;
-            float t = 0.f;
-#pragma unroll
-            for (int ww = 0; ww < NWV; ++ww)
-#pragma unroll
-                for (int q = 0; q < 4; ++q) t += ssq[ww][i][r + 16 * q];
-            rscale[threadIdx.x] = rsqrtf(t / static_cast<float>(K) + a.eps);
-        }
-        __syncthreads();
-    }
-    // wave i finishes M-tile i: lane l holds column c of rows 4 (l / 16) + r, r = 0..3
-    if (w < MT) {
-        const int i = w;
-        f32x4_t v[NT];
-#pragma unroll
-        for (int t = 0; t < NT; ++t) {
-            v[t] = red[0][t][i][l];
-#pragma unroll
-            for (int ww = 1; ww < NWV; ++ww) v[t] += red[ww][t][i][l];
-        }
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int mr = 16 * i + 4 * kq + r, m = m0 + mr;
-            if (m >= a.M) continue;
-            float *dst = a.y + static_cast<size_t>(m) * a.ldy + nb;
-            const float sc = NORM ? rscale[mr] : 1.f;
-            if constexpr (EPI == EPI_PLAIN) {
-                *dst = v[0][r] * sc;
-            } else if constexpr (EPI == EPI_SWIGLU) {
-                const float g = v[0][r] * sc, u = v[NT - 1][r] * sc;
-                *dst = g / (1.f + expf(-g)) * u;
-            } else {
-                *dst += v[0][r];
-            }
-        }
-    }
-}
-
-template <int MT>
-void launch_rows_mt(int epi, bool norm, const dim3 &grid, const RowArgs &ra, hipStream_t s) {
-    // K = hidden (1024) for q|k|v, gate|up and the heads: 8 waves x 4 steps; the residual adds
-    // (K = 2048 for o, 3072 for down) one 16-row tile per block: 16 waves x 4 or 6 steps
-    if (epi == EPI_SWIGLU) hipLaunchKernelGGL((k_rows<MT, EPI_SWIGLU, true, 8, 4>), grid, dim3(8 * WAVE), 0, s, ra);
-    else if (epi == EPI_RESID) {
-        if constexpr (MT == 1) {
-            if (ra.K == 2048) hipLaunchKernelGGL((k_rows<1, EPI_RESID, false, 16, 4>), grid, dim3(16 * WAVE), 0, s, ra);
-            else hipLaunchKernelGGL((k_rows<1, EPI_RESID, false, 16, 6>), grid, dim3(16 * WAVE), 0, s, ra);
-        }
-    } else if (norm) hipLaunchKernelGGL((k_rows<MT, EPI_PLAIN, true, 8, 4>), grid, dim3(8 * WAVE), 0, s, ra);
-    else hipLaunchKernelGGL((k_rows<MT, EPI_PLAIN, false, 8, 4>), grid, dim3(8 * WAVE), 0, s, ra);
-}
-
-// Y = A W^T over M rows (K: 1024 for PLAIN and SWIGLU, 2048 or 3072 for RESID; N a multiple of
-// 16). SWIGLU: W = gate (w0, F rows) | up (w1, F rows), y [M][F]; RESID: y (the residual stream)
-// += A W^T; norm (SWIGLU always): A is the residual stream, RMSNorm'd with ln and eps on the way in.
-void launch_rows(int epi, bool norm, const float *A, int lda, int M, int K, const float *ln, float eps, const uint16_t *w0,
-                 int n0, const uint16_t *w1, int n1, const uint16_t *w2, int n2, float *y, int ldy, uint32_t *flag,
-                 hipStream_t s) {
-    const int F = epi == EPI_SWIGLU ? n0 : 0, N = epi == EPI_SWIGLU ? n0 : n0 + n1 + n2;
-    const RowArgs ra{A, ln, w0, w1, w2, y, flag, lda, M, K, n0, n0 + n1, F, ldy, eps};
-    const int mt = epi == EPI_RESID ? 1 : M <= 16 ? 1 : M <= 32 ? 2 : M <= 48 ? 3 : 4;
-    const dim3 grid(N / 16, (M + 16 * mt - 1) / (16 * mt));
-    switch (mt) {
-    case 1: launch_rows_mt<1>(epi, norm, grid, ra, s); break;
-    case 2: launch_rows_mt<2>(epi, norm, grid, ra, s); break;
-    case 3: launch_rows_mt<3>(epi, norm, grid, ra, s); break;
-    default: launch_rows_mt<4>(epi, norm, grid, ra, s); break;
-    }
-}
 
 // ---- talker: q/k norms + RoPE + K/V store, per stream -----------------------------------
 
