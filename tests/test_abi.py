@@ -53,7 +53,7 @@ STRUCTS = {
     "navi_tensor_ref": abi.TensorRef, "navi_kv_view": abi.KvView, "navi_sampling": abi.Sampling,
     "navi_frame_options": abi.FrameOptions, "navi_frame_result": abi.FrameResult, "navi_prompt": abi.Prompt,
     "navi_vocoder_params": abi.VocoderParams, "navi_synth_request": abi.SynthRequest,
-    "navi_synth_stats": abi.SynthStats,
+    "navi_synth_stats": abi.SynthStats, "navi_speaker_params": abi.SpeakerParams,
 }
 
 
@@ -86,3 +86,15 @@ def test_header_compiles_as_c_and_cpp(tmp_path):
         src.write_text('#include "navi_amd.h"\nint main(void) { return NAVI_OK; }\n')
         subprocess.run([comp, "-Wall", "-Werror", "-I", str(ROOT / "include"), "-o", str(tmp_path / f"a_{lang}"), str(src)],
                        check=True)
+
+
+def test_graph_facade_compiles(tmp_path):
+    """navi_graph.hpp (the reference's Graph signatures over the C ABI) is self-contained C++20."""
+    import subprocess
+    src = tmp_path / "g.cpp"
+    src.write_text('#include "navi_graph.hpp"\n'
+                   'int main() { navi::qwen3tts::SynthRequest r; r.ids = {1, 2, 3}; navi::qwen3tts::SynthStats s;\n'
+                   '  return static_cast<int>(r.ids.size()) + s.n_frames + navi::qwen3tts::STREAM_BATCH; }\n')
+    r = subprocess.run(["g++", "-std=c++20", "-Wall", "-Wextra", "-Werror", "-fsyntax-only", f"-I{ROOT / 'include'}",
+                        f"-I{ROOT / 'navi-tts_amd' / 'csrc' / 'host'}", str(src)], capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
