@@ -248,6 +248,20 @@ def speaker_encoder(W, kv: dict, abi, seconds=(3.0, 10.0)) -> dict:
     return {"speaker": out}
 
 
+def host_cpu() -> str:
+    """The host CPU's model name and the cores this process may use."""
+    name = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    name = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return f"{name}, {len(os.sched_getaffinity(0))} cores available"
+
+
 def cpu_baseline(path: Path, frames: int) -> dict:
     """The oracle (PyTorch f32 on the host cores) on the same workload, `frames` frames."""
     import torch
@@ -270,7 +284,7 @@ def cpu_baseline(path: Path, frames: int) -> dict:
     for i in range(frames):
         _, step = ora.frame(s, 2, i + 1, trail, kv=kvo, n_past=N_PAST, step_in=step)
     ms = (time.perf_counter() - t0) * 1e3 / frames
-    return {"value": round(ms, 2), "unit": "ms/frame", "cores": threads, "kind": "port",
+    return {"value": round(ms, 2), "unit": "ms/frame", "cores": threads, "kind": "port", "cpu": host_cpu(),
             "sample": f"{frames} frames at n_past={N_PAST} after 1 warm-up frame, full 0.6B random-init model, "
                       f"PyTorch f32 restatement (oracle/) with torch.set_num_threads({threads})"}
 
