@@ -52,18 +52,38 @@ __device__ __forceinline__ float snake(float v, float za, float zb) {
     return v + sn * sn * zb;
 }
 
-// y (and z) at output (row, co) from the accumulated sum (EPI_PARTIAL excluded).
-__device__ __forceinline__ void conv_epilogue(const ConvArgs &a, int epi, size_t o, int co, float v) {
-    if (a.bias) v += gld(a.bias + co);
+// The per-output-channel operands of the epilogue, loaded once per thread (a thread's outputs
+// share their channel).
+struct EpiCol {
+    float bias, scale, za, zb;
+};
+__device__ __forceinline__ EpiCol epi_col(const ConvArgs &a, int epi, int co) {
+    EpiCol c{0.f, 1.f, 0.f, 0.f};
+    if (a.bias) c.bias = gld(a.bias + co);
+    if (epi == EPI_SCALE_RESIDUAL) c.scale = gld(a.scale + co);
+    if (a.z) {
+        c.za = gld(a.za + co);
+        c.zb = gld(a.zb + co);
+    }
+    return c;
+}
+__device__ __forceinline__ bool epi_has_res(int epi) { return epi == EPI_RESIDUAL || epi == EPI_SCALE_RESIDUAL; }
+
+// y (and z) at output offset o from the accumulated sum v (EPI_PARTIAL excluded); res: the
+// residual at o, loaded by the caller before any of its stores (the residual stream is usually
+// y itself, so a load after a store could not be hoisted and every output would wait a memory
+// round trip).
+__device__ __forceinline__ void conv_store(const ConvArgs &a, int epi, size_t o, const EpiCol &c, float v, float res) {
+    if (a.bias) v += c.bias;
     if (epi == EPI_GELU) v = 0.5f * v * (1.f + erff(v * 0.70710678118654752f));
-    else if (epi == EPI_RESIDUAL) v += gld(a.res + o);
-    else if (epi == EPI_SCALE_RESIDUAL) v = v * gld(a.scale + co) + gld(a.res + o);
+    else if (epi == EPI_RESIDUAL) v += res;
+    else if (epi == EPI_SCALE_RESIDUAL) v = v * c.scale + res;
     else if (epi == EPI_CLAMP) v = fminf(fmaxf(v, -1.f), 1.f);
     else if (epi == EPI_RELU) v = fmaxf(v, 0.f);
     else if (epi == EPI_SIGMOID) v = 1.f / (1.f + expf(-v));
     else if (epi == EPI_RELU_TANH) v = tanhf(fmaxf(v, 0.f));
     if (a.y) gst(a.y + o, v);
-    if (a.z) gst(a.z + o, snake(v, gld(a.za + co), gld(a.zb + co)));
+    if (a.z) gst(a.z + o, snake(v, c.za, c.zb));
 }
 
 namespace {
@@ -187,15 +207,158 @@ __global__ void __launch_bounds__(BT) k_conv_mfma(ConvArgs a) {
     if (!live) return;
     const int co = n0 + (l & 15);
     float *part = a.part + static_cast<size_t>(split) * a.T * a.phases * a.Cout;
+    if constexpr (EPI == EPI_PARTIAL) {
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int t = t0 + i * 16 + (l >> 4) * 4 + r;
+                if (t < a.T) gst(part + (static_cast<size_t>(t) * a.phases + phase) * a.Cout + co, acc[i][r]);
+            }
+    } else {
+        // every load of the epilogue first, then the stores
+        const EpiCol cc = epi_col(a, EPI, co);
+        float res[MT][4];
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int t = t0 + i * 16 + (l >> 4) * 4 + r;
+                res[i][r] = epi_has_res(EPI) && t < a.T ? gld(a.res + (static_cast<size_t>(t) * a.phases + phase) * a.ldy + co) : 0.f;
+            }
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int t = t0 + i * 16 + (l >> 4) * 4 + r;
+                if (t < a.T) conv_store(a, EPI, (static_cast<size_t>(t) * a.phases + phase) * a.ldy + co, cc, acc[i][r], res[i][r]);
+            }
+    }
+}
+
+// The 96-channel convs (the codec decoder's last block and its final conv): a block covers
+// RB = 64 MT rows and every output channel (Cout = 16 NCT). The whole input window (the rows plus
+// the (K-1) dil causal halo, all 96 channels, f16 hi + lo) is staged in LDS once, and so is each
+// tap's weight slice [Cout][96], one tap ahead of its MFMAs: the four waves (16 MT rows each)
+// read both operands from LDS, and the input is read ~1.4x instead of the 64-column blocks'
+// ~3.7x. Per output the sum runs over taps, then 32-channel steps, in an order that does not
+// depend on T. Causal (rows before 0 from hist), no K split, no prologue, phases 1, dil <= 9.
+template <int K, int NCT, int MT, int EPI>
+__global__ void __launch_bounds__(BT) k_conv_c96(ConvArgs a) {
+    constexpr int CIN = 96, LD = CIN + 8, RB = 64 * MT, MAXROWS = RB + (K - 1) * 9, CO = 16 * NCT;
+    constexpr int WCH = CO * (CIN / 8), WIT = (WCH + BT - 1) / BT;   // 16-byte chunks of a tap's weights
+    __shared__ __align__(16) _Float16 xhi[MAXROWS * LD];
+    __shared__ __align__(16) _Float16 xlo[MAXROWS * LD];
+    __shared__ __align__(16) _Float16 wt[2][CO * LD];
+    const int H = (K - 1) * a.dil, rows = RB + H;
+    const int wv = threadIdx.x >> 6, l = threadIdx.x & 63;
+    const int t0 = blockIdx.x * RB;
+    auto load_w = [&](int j, u32x4_t (&r)[WIT]) {
+#pragma unroll
+        for (int k = 0; k < WIT; ++k) {
+            const int i = threadIdx.x + k * BT, co = i / (CIN / 8), c8 = i - co * (CIN / 8);
+            if (i < WCH) r[k] = *(const NAVI_GLOBAL u32x4_t *) (a.w + (static_cast<size_t>(co) * K + j) * CIN + c8 * 8);
+        }
+    };
+    auto store_w = [&](int buf, const u32x4_t (&r)[WIT]) {
+#pragma unroll
+        for (int k = 0; k < WIT; ++k) {
+            const int i = threadIdx.x + k * BT, co = i / (CIN / 8), c8 = i - co * (CIN / 8);
+            if (i < WCH) *reinterpret_cast<u32x4_t *>(&wt[buf][co * LD + c8 * 8]) = r[k];
+        }
+    };
+    u32x4_t wr[WIT];
+    load_w(0, wr);
+    // the input window: all of its loads go out IB float4 per thread at a time before any is used
+    bool bad = false;
+    {
+        constexpr int q4 = CIN / 4, IT = (MAXROWS * q4 + BT - 1) / BT, IB = IT < 12 ? IT : 12;
+#pragma unroll
+        for (int b0 = 0; b0 < IT; b0 += IB) {
+            f32x4_t sv[IB];
+#pragma unroll
+            for (int k = 0; k < IB; ++k) {
+                const int i = threadIdx.x + (b0 + k) * BT, r = i / q4, c = (i - r * q4) * 4, t = t0 - a.lpad + r;
+                sv[k] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+                if (b0 + k < IT && r < rows) {
+                    if (t >= 0 && t < a.T) sv[k] = *(const NAVI_GLOBAL f32x4_t *) (a.x + static_cast<size_t>(t) * a.ldx + c);
+                    else if (t < 0 && a.hist) sv[k] = *(const NAVI_GLOBAL f32x4_t *) (a.hist + static_cast<size_t>(H + t) * CIN + c);
+                }
+            }
+#pragma unroll
+            for (int k = 0; k < IB; ++k) {
+                const int i = threadIdx.x + (b0 + k) * BT, r = i / q4, c = (i - r * q4) * 4;
+                if (b0 + k >= IT || r >= rows) continue;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    bad |= !(fabsf(sv[k][e]) < 65504.f);
+                    const _Float16 h = static_cast<_Float16>(sv[k][e]);
+                    xhi[r * LD + c + e] = h;
+                    xlo[r * LD + c + e] = static_cast<_Float16>(sv[k][e] - static_cast<float>(h));
+                }
+            }
+        }
+    }
+    if (bad) gst(a.flag, 1u);
+    store_w(0, wr);
+    __syncthreads();
+    f32x4_t acc[MT][NCT];
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int n = 0; n < NCT; ++n) acc[i][n] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < K; ++j) {
+        const int buf = j & 1;
+        if (j + 1 < K) load_w(j + 1, wr);                   // next tap's weights, in flight meanwhile
+#pragma unroll
+        for (int ks = 0; ks < CIN / 32; ++ks) {
+            half8v b[NCT];
+#pragma unroll
+            for (int n = 0; n < NCT; ++n)
+                b[n] = *reinterpret_cast<const half8v *>(&wt[buf][(n * 16 + (l & 15)) * LD + ks * 32 + (l >> 4) * 8]);
+#pragma unroll
+            for (int i = 0; i < MT; ++i) {
+                const int r = wv * (16 * MT) + i * 16 + (l & 15) + j * a.dil;
+                const half8v h = *reinterpret_cast<const half8v *>(&xhi[r * LD + ks * 32 + (l >> 4) * 8]);
+                const half8v o = *reinterpret_cast<const half8v *>(&xlo[r * LD + ks * 32 + (l >> 4) * 8]);
+#pragma unroll
+                for (int n = 0; n < NCT; ++n) {
+                    acc[i][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(h, b[n], acc[i][n], 0, 0, 0);
+                    acc[i][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(o, b[n], acc[i][n], 0, 0, 0);
+                }
+            }
+        }
+        if (j + 1 < K) {
+            store_w(buf ^ 1, wr);                           // last read in tap j - 1, before the barrier below it
+            __syncthreads();
+        }
+    }
+    // every load of the epilogue first (column operands, residuals), then the stores
+    EpiCol cc[NCT];
+#pragma unroll
+    for (int n = 0; n < NCT; ++n) cc[n] = epi_col(a, EPI, n * 16 + (l & 15));
+    float res[MT][4][NCT];
 #pragma unroll
     for (int i = 0; i < MT; ++i)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const int t = t0 + i * 16 + (l >> 4) * 4 + r;
+            const int t = t0 + wv * (16 * MT) + i * 16 + (l >> 4) * 4 + r;
+#pragma unroll
+            for (int n = 0; n < NCT; ++n)
+                res[i][r][n] = epi_has_res(EPI) && t < a.T ? gld(a.res + static_cast<size_t>(t) * a.ldy + n * 16 + (l & 15)) : 0.f;
+        }
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int t = t0 + wv * (16 * MT) + i * 16 + (l >> 4) * 4 + r;
             if (t >= a.T) continue;
-            const size_t row = static_cast<size_t>(t) * a.phases + phase;
-            if (EPI == EPI_PARTIAL) gst(part + row * a.Cout + co, acc[i][r]);
-            else conv_epilogue(a, EPI, row * a.ldy + co, co, acc[i][r]);
+#pragma unroll
+            for (int n = 0; n < NCT; ++n) {
+                const int co = n * 16 + (l & 15);
+                conv_store(a, EPI, static_cast<size_t>(t) * a.ldy + co, cc[n], acc[i][n][r], res[i][r][n]);
+            }
         }
 }
 
@@ -217,7 +380,7 @@ __global__ void __launch_bounds__(BT) k_conv_finish(ConvArgs a, int splits, int 
         for (int j = 0; j < 8; ++j)
             if (s0 + j < splits) v = s0 + j == 0 ? t[j] : v + t[j];
     }
-    conv_epilogue(a, epi, row * a.ldy + co, co, v);
+    conv_store(a, epi, row * a.ldy + co, epi_col(a, epi, co), v, epi_has_res(epi) ? gld(a.res + row * a.ldy + co) : 0.f);
 }
 
 // [Cout][Cin][K] -> [Cout][K][Cin]

@@ -19,6 +19,9 @@
 //  * Few output tiles (short chunks, narrow layers): the input channels are split over up to
 //    S blocks per tile and the partial sums added in split order by a finish kernel, so a
 //    16-frame chunk still spreads over the 256 CUs.
+//  * The last decoder block's 96-channel convs and the final conv run on k_conv_c96: a block
+//    stages its whole input window and each tap's weights in LDS and covers every output
+//    channel, reading the input ~1.4x instead of ~3.7x.
 //  * Streaming state: each causal conv keeps its last (K-1)*dil input rows (the history the
 //    next chunk's first rows read), the ConvNeXt depthwise conv its last 6, the attention its
 //    K/V in a ring of >= window + chunk positions: chunked decoding equals one-shot decoding.
@@ -305,6 +308,28 @@ void launch_k(const ConvArgs &a, int pro, int epi, dim3 grid, hipStream_t s) {
 
 int conv_mt(int T) { return T <= 16 ? 1 : 4; }
 
+// The 96-channel convs of the last decoder block (k7 and k1) and the final 96 -> 16 conv run on
+// k_conv_c96 (input window and weights staged in LDS, every output channel in one block). Chosen
+// by the conv's shape only, so every chunking of the codes runs the same kernel.
+bool conv_is_c96(const Conv &c) {
+    return c.phases == 1 && c.S == 1 && c.dil <= 9 && (c.K == 7 || c.K == 1) && c.Cin == 96 && (c.Cout == 96 || c.Cout == 16);
+}
+
+bool launch_c96(const Conv &c, const ConvArgs &a, int pro, int epi, int T, hipStream_t s) {
+    if (pro != PRO_NONE) return false;
+    const dim3 grid((T + 127) / 128);
+#define NAVI_C96(K_, NCT_, E_)                                                                  \
+    if (c.K == K_ && c.Cout == 16 * NCT_ && epi == E_) {                                       \
+        hipLaunchKernelGGL((k_conv_c96<K_, NCT_, 2, E_>), grid, dim3(BT), 0, s, a);             \
+        return true;                                                                            \
+    }
+    NAVI_C96(7, 6, EPI_BIAS)
+    NAVI_C96(1, 6, EPI_RESIDUAL)
+    NAVI_C96(7, 1, EPI_CLAMP)
+#undef NAVI_C96
+    return false;
+}
+
 // Input-channel splits of a conv over T rows: when the output tiles alone would leave most of the
 // 256 CUs idle, the channel chunks are spread over up to S blocks per tile (at least 2 chunks each)
 // and summed by k_conv_finish.
@@ -322,20 +347,9 @@ int conv_splits(const Conv &c, int T) {
 }
 
 
-// Runs one conv over T input rows; updates its history afterwards. z (optional): also write
-// Snake(y) with the Snake parameters of zc, the conv that consumes this output.
-navi_status run_conv(navi_vocoder &v, Conv &c, int pro, int epi, const float *x, int T, int ldx, float *y, int ldy,
-                     const float *res, const float *scale, char *err, size_t errlen, float *z = nullptr,
-                     const Conv *zc = nullptr) {
+// k_conv_mfma over T rows (input-channel splits summed by k_conv_finish).
+navi_status launch_generic(navi_vocoder &v, const Conv &c, ConvArgs &a, int pro, int epi, int T, char *err, size_t errlen) {
     hipStream_t s = device_state().stream;
-    ConvArgs a{};
-    a.x = x; a.hist = c.hist; a.w = c.w; a.bias = c.bias; a.res = res; a.scale = scale;
-    a.y = y; a.z = z; a.flag = v.flag; a.ldx = ldx; a.ldy = ldy; a.T = T; a.Cin = c.Cin; a.Cout = c.Cout;
-    a.dil = c.dil; a.phases = c.phases; a.lpad = (c.K - 1) * c.dil;   // causal
-    if (z) {
-        a.za = zc->sa;
-        a.zb = zc->sb;
-    }
     const int mt = conv_mt(T), S = c.S;
     const int chunks = (c.Cin + CCH - 1) / CCH;
     a.cps = (chunks + S - 1) / S * CCH;
@@ -364,6 +378,32 @@ navi_status run_conv(navi_vocoder &v, Conv &c, int pro, int epi, const float *x,
     if (S > 1) {
         const size_t n = static_cast<size_t>(T) * c.phases * c.Cout;
         hipLaunchKernelGGL(k_conv_finish, dim3(static_cast<unsigned>((n + BT - 1) / BT)), dim3(BT), 0, s, a, S, epi);
+    }
+    return NAVI_OK;
+}
+
+// Runs one conv over T input rows; updates its history afterwards. z (optional): also write
+// Snake(y) with the Snake parameters of zc, the conv that consumes this output.
+navi_status run_conv(navi_vocoder &v, Conv &c, int pro, int epi, const float *x, int T, int ldx, float *y, int ldy,
+                     const float *res, const float *scale, char *err, size_t errlen, float *z = nullptr,
+                     const Conv *zc = nullptr) {
+    hipStream_t s = device_state().stream;
+    ConvArgs a{};
+    a.x = x; a.hist = c.hist; a.w = c.w; a.bias = c.bias; a.res = res; a.scale = scale;
+    a.y = y; a.z = z; a.flag = v.flag; a.ldx = ldx; a.ldy = ldy; a.T = T; a.Cin = c.Cin; a.Cout = c.Cout;
+    a.dil = c.dil; a.phases = c.phases; a.lpad = (c.K - 1) * c.dil;   // causal
+    if (z) {
+        a.za = zc->sa;
+        a.zb = zc->sb;
+    }
+    if (conv_is_c96(c)) {
+        if (!launch_c96(c, a, pro, epi, T, s)) {
+            set_err(err, errlen, "vocoder: no 96-channel conv kernel for K=%d Cout=%d epilogue %d", c.K, c.Cout, epi);
+            return NAVI_ERR_UNSUPPORTED;
+        }
+    } else {
+        const navi_status st = launch_generic(v, c, a, pro, epi, T, err, errlen);
+        if (st != NAVI_OK) return st;
     }
     if (c.H > 0) {
         const size_t nh = static_cast<size_t>(c.H) * c.Cin;
