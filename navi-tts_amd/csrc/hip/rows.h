@@ -147,6 +147,16 @@ __global__ void __launch_bounds__(NWV * WAVE) k_rows(RowArgs a) {
 #pragma unroll
             for (int ww = 1; ww < NWV; ++ww) v[t] += red[ww][t][i][l];
         }
+        // RESID: the four residual values are loaded before the first store (a load after a
+        // store to the same buffer would wait for it: four memory round trips instead of one)
+        float old[4] = {0.f, 0.f, 0.f, 0.f};
+        if constexpr (EPI == EPI_RESID) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int m = m0 + 16 * i + 4 * kq + r;
+                if (m < a.M) old[r] = a.y[static_cast<size_t>(m) * a.ldy + nb];
+            }
+        }
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int mr = 16 * i + 4 * kq + r, m = m0 + mr;
@@ -159,7 +169,7 @@ __global__ void __launch_bounds__(NWV * WAVE) k_rows(RowArgs a) {
                 const float g = v[0][r] * sc, u = v[NT - 1][r] * sc;
                 *dst = g / (1.f + expf(-g)) * u;
             } else {
-                *dst += v[0][r];
+                *dst = old[r] + v[0][r];
             }
         }
     }

@@ -138,11 +138,21 @@ __global__ void __launch_bounds__(BT) k_time_softmax(float *a, int T, int C_, in
     if (q == 0) tot[cl] = slice_total(red, cl);
     __syncthreads();
     const float inv = 1.f / tot[cl];
+    // in place: four rows' loads go out before their stores (a load after a store to the same
+    // array would wait for it)
     if (c < C_)
-#pragma unroll 4
-        for (int t = q; t < T; t += NPART) {
-            float *p = a + static_cast<size_t>(t) * ld + c;
-            gst(p, expf(gld(p) - mx) * inv);
+        for (int t0 = q; t0 < T; t0 += 4 * NPART) {
+            float v[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const int t = t0 + k * NPART;
+                v[k] = t < T ? gld(a + static_cast<size_t>(t) * ld + c) : 0.f;
+            }
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const int t = t0 + k * NPART;
+                if (t < T) gst(a + static_cast<size_t>(t) * ld + c, expf(v[k] - mx) * inv);
+            }
         }
 }
 
