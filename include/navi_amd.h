@@ -297,6 +297,7 @@ navi_status navi_speaker_embed_mel(navi_speaker *h, const float *mel, int32_t n_
  * device in the same double precision (equal to float rounding), then the network.
  * Errors as navi_speaker_mel and navi_speaker_embed_mel. Synchronous. */
 navi_status navi_speaker_embed(navi_speaker *h, const float *wav, int64_t n, float *emb, char *err, size_t errlen);
+int32_t navi_speaker_dim(const navi_speaker *h);         /* the embedding width (enc_dim) embed writes */
 double navi_speaker_last_ms(const navi_speaker *h);      /* SpeakerEncoder::last_ms: device time of the last embed
                                                             (front end included for navi_speaker_embed) */
 /* Diagnostics: the device log-mel of the last embed, time-major f32 [*n_frames][num_mels]. */

@@ -753,6 +753,8 @@ const float *navi_speaker_tap_mel(const navi_speaker *h, int32_t *n_frames) {
     return h ? h->mel : nullptr;
 }
 
+int32_t navi_speaker_dim(const navi_speaker *h) { return h ? h->p.enc_dim : 0; }
+
 double navi_speaker_last_ms(const navi_speaker *h) { return h ? h->last_ms : 0.0; }
 
 } // extern "C"

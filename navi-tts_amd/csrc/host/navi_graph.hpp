@@ -77,7 +77,7 @@ public:
     // graph.h:64-65
     std::vector<float> embed_speaker(std::span<const float> wav_24k) {
         if (!s_) throw Error("graph: no speaker encoder");
-        std::vector<float> out(1024);
+        std::vector<float> out(static_cast<size_t>(navi_speaker_dim(s_)));
         char err[256] = {};
         check(navi_speaker_embed(s_, wav_24k.data(), static_cast<int64_t>(wav_24k.size()), out.data(), err, sizeof err), err);
         return out;

@@ -34,7 +34,7 @@ EXPORTS = [
     "navi_streams_create", "navi_streams_destroy", "navi_streams_reset", "navi_streams_run", "navi_streams_step_out",
     "navi_streams_max_streams", "navi_streams_last_ms", "navi_streams_set_taps", "navi_streams_set_graphs",
     "navi_speaker_mel", "navi_speaker_create", "navi_speaker_destroy", "navi_speaker_embed_mel", "navi_speaker_embed",
-    "navi_speaker_last_ms", "navi_speaker_tap_mel",
+    "navi_speaker_last_ms", "navi_speaker_tap_mel", "navi_speaker_dim",
     "navi_streams_tap_hidden",
     "navi_streams_tap_logits", "navi_streams_tap_cp_logits",
 ]
@@ -210,6 +210,8 @@ def lib() -> C.CDLL:
     L.navi_speaker_embed.argtypes = [C.c_void_p, C.c_void_p, C.c_int64, C.c_void_p, E, C.c_size_t]
     L.navi_speaker_last_ms.argtypes = [C.c_void_p]
     L.navi_speaker_last_ms.restype = C.c_double
+    L.navi_speaker_dim.argtypes = [C.c_void_p]
+    L.navi_speaker_dim.restype = C.c_int32
     L.navi_speaker_tap_mel.argtypes = [C.c_void_p, C.POINTER(C.c_int32)]
     L.navi_speaker_tap_mel.restype = C.c_void_p
     L.navi_synth.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.POINTER(SynthRequest), PCM_CALLBACK, C.c_void_p,
