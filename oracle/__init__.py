@@ -12,6 +12,8 @@ It restates, from the reference's own sources (cited per function):
 * `model`     - talker decode step, 16-position code-predictor pass, next-step assembly
                 (frame.hip:300-579), prompt assembly and prefill (model/qwen3tts/talker.hip:20-117, 283-399);
 * `navi_read` - the `.navi` reader (docs/navi-format.md; runtime/weights/navi_file.cpp:79-148);
+* `vocoder`   - the codec decoder, codes -> PCM (model/qwen3tts/vocoder.hip:20-343, kernels.h:72-242);
+* `speaker`   - the speaker encoder's log-mel front end and ECAPA-TDNN (model/qwen3tts/speaker.hip:46-331);
 * `csrc/sampler.c` + `csampler` - a second, C restatement of the seeding, the radix k-th-largest
                 select and the draw (the same frame.hip lines), used to cross-check `rng`/`sampler`.
 
@@ -26,7 +28,14 @@ Pinning (tests/test_oracle_*.py, tests/test_blob.py):
   softmax; suppression / EOS gate / penalty special cases;
 * model: decoder layer vs transformers' Qwen3DecoderLayer (random weights, non-unit norms), with a
   planted-mistake control; prefill == sequential decode; RoPE and RMSNorm closed forms; the
-  assembly order; prompt layout vs the reference's fixtures (row counts, speaker row).
+  assembly order; prompt layout vs the reference's fixtures (row counts, speaker row);
+* vocoder: SnakeBeta, the residual unit, ConvNeXt and the sliding-window transformer layer vs
+  transformers' Qwen3-Omni code2wav modules; causal and transposed convs vs brute-force loops;
+  the RVQ front end vs an explicit sum; causality of the whole decoder;
+* speaker: the log-mel vs the reference's own fixture (speaker_mels.npy, first 2 s of
+  voice_1.wav); the "same" reflect conv vs torch.nn.Conv1d(padding_mode="reflect");
+  weighted statistics vs numpy.average; the whole network on a time-constant mel vs its closed
+  form, with a planted-mistake control.
 Parity unpinned: none of the functions above. The per-frame composition (`Oracle.frame`) is the
 composition of pinned pieces.
 """
