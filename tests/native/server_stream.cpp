@@ -210,7 +210,7 @@ int navi_test_server_stream(navi_talker *t, navi_frame *f, navi_vocoder *v, navi
         int pushed = 0;
         double abort_ms = 0;
         {
-            ChunkQueue q;
+            ChunkQueue q(1);                              // one slot: the second push waits for the abort
             const auto t0 = std::chrono::steady_clock::now();
             std::thread worker([&] { stream_worker(g, sr, q, st3, err3); });
             bool d = false;
