@@ -4,7 +4,8 @@ Same f16 weights (random init, seed 3) on both sides; the device stages activati
 hi + lo pairs through the matrix cores and accumulates in f32, the oracle is PyTorch f32, so the
 bar is on the embedding as a whole: relative RMS error <= 1e-3 and cosine >= 0.99999.
 Inputs: the reference's own fixture mel (speaker_mels.npy frames 0..185) and audio (voice_1.wav,
-first 2 s), ragged noise lengths down to the 5-frame minimum, two calls in a row on one handle
+first 2 s), ragged noise lengths from the 5-frame minimum to 30 s (the default bound), two calls
+in a row on one handle
 (long then short), the max_seconds bound, and the reference's error cases (too short, too long).
 """
 import numpy as np
@@ -90,6 +91,18 @@ def test_ragged_lengths(spk, n):
     s = abi.Speaker(W, max_seconds=5.0)
     log(f"speaker embed, noise {n} samples ({abi.speaker_mel(W.kv, wav).shape[1]} frames)")
     check(s.embed(wav), ora.embed(wav), f"{n} samples")
+
+
+def test_thirty_seconds_the_default_maximum(spk):
+    """The longest clip a default handle takes (max_seconds 30: 2,814 mel frames of audio)."""
+    abi, W, ora = spk
+    s = abi.Speaker(W)                            # max_seconds = 30
+    n = 30 * 24000 - 256                          # 2,811 frames: inside the 2,814-frame bound
+    wav = (np.random.default_rng(30).standard_normal(n) * 0.1).astype(np.float32)
+    log(f"speaker embed, 30 s of noise ({abi.speaker_mel(W.kv, wav).shape[1]} frames)")
+    got = s.embed(wav)
+    log(f"  device {s.last_ms():.3f} ms")
+    check(got, ora.embed(wav), "30 s")
 
 
 def test_long_then_short_on_one_handle(spk):
