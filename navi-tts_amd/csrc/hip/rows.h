@@ -9,8 +9,9 @@
 namespace navi_amd {
 namespace rows {
 
-// A block owns 16 output columns (SwiGLU: 16 gate and the matching 16 up columns) for up to 64
-// rows (more rows: more blocks along y); its NWV waves take a slice of K each, loading their A
+// A block owns 16 output columns (SwiGLU: 16 gate and the matching 16 up columns; above 64 rows,
+// several such groups) for up to 64 rows (more rows: more blocks along y); its NWV waves take a
+// slice of K each, loading their A
 // rows (f32, split into f16 hi + lo for two v_mfma_f32_16x16x32_f16 each) and W rows (f16)
 // straight from global memory, all KS MFMA steps' loads in flight at once, no LDS staging. The
 // waves' tiles are summed in LDS in wave order. With NORM the rows are the residual stream: A is multiplied by the RMSNorm weight as it
@@ -37,31 +38,40 @@ typedef _Float16 rhalf8 __attribute__((ext_vector_type(8)));
 // NWV waves per block, each one batch of KS MFMA steps (32 k each): K = 32 KS NWV. Every load of
 // a wave is issued before its first MFMA (the whole chain is one memory latency), and the kernels
 // stay small (no unrolled K loop, so the decode's few kernels stay in the instruction cache).
-template <int MT, int EPI, bool NORM, int NWV, int KS>
+// CG column groups: the block owns 16 CG output columns and every wave applies its A registers to
+// all of them, so A (f32, the bulk of a block's reads once the rows pass a few dozen) is read
+// N / (16 CG) times per launch instead of N / 16. A column's sums are the same at any CG.
+template <int MT, int EPI, bool NORM, int NWV, int KS, int CG = 1>
 __global__ void __launch_bounds__(NWV * WAVE) k_rows(RowArgs a) {
     constexpr int NT = EPI == EPI_SWIGLU ? 2 : 1, K = 32 * KS * NWV;
-    __shared__ f32x4_t red[NWV][NT][MT][WAVE];
+    static_assert(CG * MT <= NWV, "one finishing wave per output tile");
+    __shared__ f32x4_t red[NWV][NT][CG][MT][WAVE];
     __shared__ float ssq[NWV][MT][WAVE];
     __shared__ float rscale[MT * 16];
     const int w = static_cast<int>(threadIdx.x) / WAVE, l = static_cast<int>(threadIdx.x) & (WAVE - 1);
     const int c = l & 15, kq = l >> 4, m0 = blockIdx.y * (MT * 16);
-    const int nb = blockIdx.x * 16 + c;
+    const int nb0 = blockIdx.x * (16 * CG) + c;        // column of group 0; group g: nb0 + 16 g
     auto wrow = [&](int n) {
         return n < a.n1 ? a.w0 + static_cast<size_t>(n) * K
              : n < a.n2 ? a.w1 + static_cast<size_t>(n - a.n1) * K : a.w2 + static_cast<size_t>(n - a.n2) * K;
     };
     const int kbeg = w * (K / NWV) + 8 * kq;
-    u32x4_t bv[NT][KS];
+    u32x4_t bv[NT][CG][KS];
     f32x4_t av[KS][MT][2], lv[KS][2];
     {
-        const uint16_t *wr[NT];
-        wr[0] = wrow(nb);
-        if constexpr (NT == 2) wr[NT - 1] = wrow(a.F + nb);
+        const uint16_t *wr[NT][CG];
+#pragma unroll
+        for (int g = 0; g < CG; ++g) {
+            wr[0][g] = wrow(nb0 + 16 * g);
+            if constexpr (NT == 2) wr[NT - 1][g] = wrow(a.F + nb0 + 16 * g);
+        }
 #pragma unroll
         for (int st = 0; st < KS; ++st) {
             const int k = kbeg + 32 * st;
 #pragma unroll
-            for (int t = 0; t < NT; ++t) bv[t][st] = *(const NAVI_GLOBAL u32x4_t *) (wr[t] + k);
+            for (int t = 0; t < NT; ++t)
+#pragma unroll
+                for (int g = 0; g < CG; ++g) bv[t][g][st] = *(const NAVI_GLOBAL u32x4_t *) (wr[t][g] + k);
 #pragma unroll
             for (int i = 0; i < MT; ++i) {
                 const int m = m0 + 16 * i + c;
@@ -80,20 +90,24 @@ __global__ void __launch_bounds__(NWV * WAVE) k_rows(RowArgs a) {
             }
         }
     }
-    f32x4_t acc[NT][MT];
+    f32x4_t acc[NT][CG][MT];
     float ss[MT];
 #pragma unroll
     for (int i = 0; i < MT; ++i) {
         ss[i] = 0.f;
 #pragma unroll
-        for (int t = 0; t < NT; ++t) acc[t][i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+            for (int g = 0; g < CG; ++g) acc[t][g][i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     }
     bool bad = false;
 #pragma unroll
     for (int st = 0; st < KS; ++st) {
-        rhalf8 b[NT];
+        rhalf8 b[NT][CG];
 #pragma unroll
-        for (int t = 0; t < NT; ++t) __builtin_memcpy(&b[t], &bv[t][st], 16);
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+            for (int g = 0; g < CG; ++g) __builtin_memcpy(&b[t][g], &bv[t][g][st], 16);
 #pragma unroll
         for (int i = 0; i < MT; ++i) {
             rhalf8 hi, lo;
@@ -110,17 +124,21 @@ __global__ void __launch_bounds__(NWV * WAVE) k_rows(RowArgs a) {
                 lo[j] = static_cast<_Float16>(v - static_cast<float>(h));
             }
 #pragma unroll
-            for (int t = 0; t < NT; ++t) {
-                acc[t][i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(hi, b[t], acc[t][i], 0, 0, 0);
-                acc[t][i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(lo, b[t], acc[t][i], 0, 0, 0);
-            }
+            for (int t = 0; t < NT; ++t)
+#pragma unroll
+                for (int g = 0; g < CG; ++g) {
+                    acc[t][g][i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(hi, b[t][g], acc[t][g][i], 0, 0, 0);
+                    acc[t][g][i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(lo, b[t][g], acc[t][g][i], 0, 0, 0);
+                }
         }
     }
     if (bad) gst(a.flag, 1u);
 #pragma unroll
     for (int i = 0; i < MT; ++i) {
 #pragma unroll
-        for (int t = 0; t < NT; ++t) red[w][t][i][l] = acc[t][i];
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+            for (int g = 0; g < CG; ++g) red[w][t][g][i][l] = acc[t][g][i];
         if constexpr (NORM) ssq[w][i][l] = ss[i];
     }
     __syncthreads();
@@ -137,15 +155,16 @@ __global__ void __launch_bounds__(NWV * WAVE) k_rows(RowArgs a) {
         }
         __syncthreads();
     }
-    // wave i finishes M-tile i: lane l holds column c of rows 4 (l / 16) + r, r = 0..3
-    if (w < MT) {
-        const int i = w;
+    // wave g MT + i finishes column group g of M-tile i: lane l holds column c of rows
+    // 4 (l / 16) + r, r = 0..3
+    if (w < CG * MT) {
+        const int g = w / MT, i = w % MT, nb = nb0 + 16 * g;
         f32x4_t v[NT];
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
-            v[t] = red[0][t][i][l];
+            v[t] = red[0][t][g][i][l];
 #pragma unroll
-            for (int ww = 1; ww < NWV; ++ww) v[t] += red[ww][t][i][l];
+            for (int ww = 1; ww < NWV; ++ww) v[t] += red[ww][t][g][i][l];
         }
         // RESID: the four residual values are loaded before the first store (a load after a
         // store to the same buffer would wait for it: four memory round trips instead of one)
@@ -189,6 +208,25 @@ void launch_rows_mt(int epi, bool norm, const dim3 &grid, const RowArgs &ra, hip
     else hipLaunchKernelGGL((k_rows<MT, EPI_PLAIN, false, 8, 4>), grid, dim3(8 * WAVE), 0, s, ra);
 }
 
+template <int MT, int EPI, bool NORM, int NWV, int KS, int CG>
+bool launch_wide(int M, int N, const RowArgs &ra, hipStream_t s) {
+    if (N % (16 * CG) != 0) return false;
+    const dim3 grid(N / (16 * CG), (M + 16 * MT - 1) / (16 * MT));
+    hipLaunchKernelGGL((k_rows<MT, EPI, NORM, NWV, KS, CG>), grid, dim3(NWV * WAVE), 0, s, ra);
+    return true;
+}
+
+// More than 64 rows (a prefill's prompt): blocks over several column groups. false: N does not
+// split into the groups, the caller takes the one-group kernels.
+bool launch_rows_wide(int epi, bool norm, int M, int N, const RowArgs &ra, hipStream_t s) {
+    if (epi == EPI_SWIGLU) return launch_wide<2, EPI_SWIGLU, true, 8, 4, 2>(M, N, ra, s);
+    if (epi == EPI_RESID)
+        return ra.K == 2048 ? launch_wide<2, EPI_RESID, false, 16, 4, 2>(M, N, ra, s)
+                            : launch_wide<1, EPI_RESID, false, 16, 6, 2>(M, N, ra, s);
+    return norm ? launch_wide<2, EPI_PLAIN, true, 8, 4, 4>(M, N, ra, s)
+                : launch_wide<2, EPI_PLAIN, false, 8, 4, 4>(M, N, ra, s);
+}
+
 // Y = A W^T over M rows (K: 1024 for PLAIN and SWIGLU, 2048 or 3072 for RESID; N a multiple of
 // 16). SWIGLU: W = gate (w0, F rows) | up (w1, F rows), y [M][F]; RESID: y (the residual stream)
 // += A W^T; norm (SWIGLU always): A is the residual stream, RMSNorm'd with ln and eps on the way in.
@@ -197,6 +235,7 @@ void launch_rows(int epi, bool norm, const float *A, int lda, int M, int K, cons
                  hipStream_t s) {
     const int F = epi == EPI_SWIGLU ? n0 : 0, N = epi == EPI_SWIGLU ? n0 : n0 + n1 + n2;
     const RowArgs ra{A, ln, w0, w1, w2, y, flag, lda, M, K, n0, n0 + n1, F, ldy, eps};
+    if (M > 64 && launch_rows_wide(epi, norm, M, N, ra, s)) return;
     const int mt = epi == EPI_RESID ? 1 : M <= 16 ? 1 : M <= 32 ? 2 : M <= 48 ? 3 : 4;
     const dim3 grid(N / 16, (M + 16 * mt - 1) / (16 * mt));
     switch (mt) {
