@@ -333,6 +333,109 @@ __global__ void __launch_bounds__(BT) k_attn_prefill(const float *q, const uint1
     gst(out + static_cast<size_t>(m) * QD + (g * 2 + hh) * HD + d, acc / (hh ? s1 : s0));
 }
 
+// k_attn_prefill for rows with at most SHORT_KEYS keys (prompts of up to 256 rows). Wave w takes
+// keys 64w .. 64w + 63; lane 16r + c reads 16-byte chunk c of key 4i + r, so one load instruction
+// covers four whole 256-byte key rows, and every K and V chunk of the block is issued before the
+// first score: one memory latency per block where the loop above pays one per 32 keys of V.
+// Scores are summed over a key's 16 lanes by DPP; thread t owns key t for the softmax.
+constexpr int SHORT_KEYS = 256;
+__global__ void __launch_bounds__(BT) k_attn_prefill_short(const float *q, const uint16_t *kc, const uint16_t *vc, int nq,
+                                                           int nkv, int pos0, float scale, float *out) {
+    constexpr int NWV = BT / WAVE, KW = SHORT_KEYS / NWV, KI = KW / 4;
+    static_assert(SHORT_KEYS == BT, "one key per thread in the softmax");
+    __shared__ float qs[2][HD], sc[2][SHORT_KEYS], red[2][NWV], opart[NWV][4][2][HD];
+    const int m = blockIdx.x, g = blockIdx.y, n = pos0 + m + 1;
+    const int QD = nq * HD, KVD = nkv * HD;
+    const int wv = threadIdx.x >> 6, l = threadIdx.x & 63, c = l & 15, r = l >> 4;
+    qs[threadIdx.x >> 7][threadIdx.x & (HD - 1)] = gld(q + static_cast<size_t>(m) * QD + g * 2 * HD + threadIdx.x);
+    const uint16_t *kb = kc + g * HD + c * 8, *vb = vc + g * HD + c * 8;
+    u32x4_t kr[KI], vr[KI];
+#pragma unroll
+    for (int i = 0; i < KI; ++i) {
+        const int j = wv * KW + 4 * i + r;
+        kr[i] = j < n ? *(const NAVI_GLOBAL u32x4_t *) (kb + static_cast<size_t>(j) * KVD) : u32x4_t{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int i = 0; i < KI; ++i) {
+        const int j = wv * KW + 4 * i + r;
+        vr[i] = j < n ? *(const NAVI_GLOBAL u32x4_t *) (vb + static_cast<size_t>(j) * KVD) : u32x4_t{0u, 0u, 0u, 0u};
+    }
+    __syncthreads();                                      // qs
+    {
+        float q0[8], q1[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            q0[e] = qs[0][c * 8 + e];
+            q1[e] = qs[1][c * 8 + e];
+        }
+#pragma unroll
+        for (int i = 0; i < KI; ++i) {
+            uint4 k4;
+            __builtin_memcpy(&k4, &kr[i], 16);
+            float a0 = dot8(k4, q0, 0.f), a1 = dot8(k4, q1, 0.f);
+            a0 += dpp_red<0xB1>(a0);
+            a1 += dpp_red<0xB1>(a1);
+            a0 += dpp_red<0x4E>(a0);
+            a1 += dpp_red<0x4E>(a1);
+            a0 += dpp_red<0x141>(a0);
+            a1 += dpp_red<0x141>(a1);
+            a0 += dpp_red<0x140>(a0);
+            a1 += dpp_red<0x140>(a1);
+            if (c == 0) {
+                const int j = wv * KW + 4 * i + r;
+                sc[0][j] = a0 * scale;
+                sc[1][j] = a1 * scale;
+            }
+        }
+    }
+    __syncthreads();
+    const bool mine = static_cast<int>(threadIdx.x) < n;
+    const float d0 = mine ? sc[0][threadIdx.x] : -INFINITY, d1 = mine ? sc[1][threadIdx.x] : -INFINITY;
+    float mx0 = wave_max(d0), mx1 = wave_max(d1);
+    if (l == 0) { red[0][wv] = mx0; red[1][wv] = mx1; }
+    __syncthreads();
+    mx0 = fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3]));
+    mx1 = fmaxf(fmaxf(red[1][0], red[1][1]), fmaxf(red[1][2], red[1][3]));
+    const float e0 = mine ? expf(d0 - mx0) : 0.f, e1 = mine ? expf(d1 - mx1) : 0.f;
+    sc[0][threadIdx.x] = e0;                              // 0 past the last key
+    sc[1][threadIdx.x] = e1;
+    const float s0 = wave_sum(e0), s1 = wave_sum(e1);
+    __syncthreads();                                      // red reads done, probabilities published
+    if (l == 0) { red[0][wv] = s0; red[1][wv] = s1; }
+    {
+        float o0[8], o1[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o0[e] = o1[e] = 0.f;
+#pragma unroll
+        for (int i = 0; i < KI; ++i) {
+            const int j = wv * KW + 4 * i + r;
+            const float p0 = sc[0][j], p1 = sc[1][j];
+            half8_t hv;
+            __builtin_memcpy(&hv, &vr[i], 16);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float v = static_cast<float>(hv[e]);
+                o0[e] = fmaf(p0, v, o0[e]);
+                o1[e] = fmaf(p1, v, o1[e]);
+            }
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            opart[wv][r][0][c * 8 + e] = o0[e];
+            opart[wv][r][1][c * 8 + e] = o1[e];
+        }
+    }
+    __syncthreads();
+    const int hh = threadIdx.x >> 7, d = threadIdx.x & (HD - 1);
+    float acc = 0.f;
+#pragma unroll
+    for (int w = 0; w < NWV; ++w)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) acc += opart[w][rr][hh][d];
+    const float sum = red[hh][0] + red[hh][1] + red[hh][2] + red[hh][3];
+    gst(out + static_cast<size_t>(m) * QD + (g * 2 + hh) * HD + d, acc / sum);
+}
+
 // rows[t] = table[ids[t]] (f16 -> f32), k_gather_rows (talker.hip:20-25).
 __global__ void __launch_bounds__(BT) k_gather_rows(const uint16_t *table, const int32_t *ids, int width, float *out) {
     const uint16_t *src = table + static_cast<size_t>(gld(ids + blockIdx.x)) * width;
@@ -740,8 +843,12 @@ navi_status navi_talker_prefill(navi_talker *t, const float *d_rows, int32_t n_r
                           QKVW, t->flag, s);
         hipLaunchKernelGGL(k_qkv_finish, dim3(T), dim3(BT), QKVW * sizeof(float), s, t->part, 1, T, t->NQ, t->NKV, w.qn,
                            w.kn, t->eps, t->invf, 0, t->q, t->kk[l], t->vv[l]);
-        hipLaunchKernelGGL(k_attn_prefill, dim3(T, t->NKV), dim3(BT), att_lds, s, t->q, t->kk[l], t->vv[l], t->NQ, t->NKV, 0,
-                           scale, t->att);
+        if (T <= SHORT_KEYS)
+            hipLaunchKernelGGL(k_attn_prefill_short, dim3(T, t->NKV), dim3(BT), 0, s, t->q, t->kk[l], t->vv[l], t->NQ, t->NKV,
+                               0, scale, t->att);
+        else
+            hipLaunchKernelGGL(k_attn_prefill, dim3(T, t->NKV), dim3(BT), att_lds, s, t->q, t->kk[l], t->vv[l], t->NQ,
+                               t->NKV, 0, scale, t->att);
         rows::launch_rows(rows::EPI_RESID, false, t->att, t->QD, T, t->QD, nullptr, 0.f, w.wo, H, nullptr, 0, nullptr, 0, t->x,
                           H, t->flag, s);
         rows::launch_rows(rows::EPI_SWIGLU, true, t->x, H, T, H, w.ln2, t->eps, w.wg, t->F, w.wu, t->F, nullptr, 0, t->h, t->F,
