@@ -161,9 +161,12 @@ def streaming_and_vocoder(W, kv: dict, abi) -> dict:
     tail = [kv["text.im_end_id"], 198, kv["text.im_start_id"], kv["text.assistant_id"], 198]
     ids = head + rng.integers(0, 151643, 128).tolist() + tail
     spk = rng.standard_normal(1024).astype(np.float32)
-    t0 = time.perf_counter()
-    pr = talker.build_prompt(ids, "english", spk)
-    build_ms = (time.perf_counter() - t0) * 1e3
+    builds = []
+    for _ in range(3):                  # the first call also loads the kernels: report a warm one
+        t0 = time.perf_counter()
+        pr = talker.build_prompt(ids, "english", spk)
+        builds.append((time.perf_counter() - t0) * 1e3)
+    build_ms = builds[-1]
     n_pre = pr.n_prefill + 120
     rows = abi.DeviceBuffer(4 * 1024 * n_pre)
     abi.lib().navi_mem_d2d(rows.ptr, pr.prefill, 4 * 1024 * pr.n_prefill)
@@ -201,7 +204,9 @@ def streaming_and_vocoder(W, kv: dict, abi) -> dict:
         "prefill_ms": {"rows_10": round(pre_ms[pr.n_prefill], 3), "rows_130": round(pre_ms[n_pre], 3)},
         "streaming": {"config": "configs[2]: 128 text ids prefilled (130 rows), speaker N(0,1), 240 frames, "
                                 "top-k 50, T 0.9, seed 2, first vocoder batch 4 then 16",
-                      "ttfa_ms": round(st.ttfa_ms, 2), "prompt_build_ms": round(build_ms, 2),
+                      "ttfa_ms": round(st.ttfa_ms, 2), "prompt_build_ms": round(build_ms, 3),
+                      # the reference's TTFA starts at the request, before the prompt rows exist
+                      "ttfa_with_prompt_build_ms": round(st.ttfa_ms + build_ms, 2),
                       "rtf": round(st.rtf, 4), "total_ms": round(st.total_ms, 1),
                       "frames_ms_per_frame": round(st.frames_ms / max(st.n_frames, 1), 4),
                       "vocoder_ms": round(st.vocoder_ms, 2), "n_frames": st.n_frames, "audio_s": round(st.audio_s, 2)},
