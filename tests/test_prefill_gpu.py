@@ -4,8 +4,8 @@
   tiles, partial K steps and split-K, with bias, SiLU and residual; an activation outside the
   f16 range is an error, not an infinity;
 * build_prompt against Oracle.build_prompt (the reference's layout, talker.hip:283-352);
-* prefill against Oracle.prefill at T = 1, T = 10 (the reference's layout), T = 130 (BASELINE's
-  streaming configuration) and T = 264 (the most a handle takes): post-norm hidden and logits
+* prefill against Oracle.prefill at T = 1, T = 10 (the reference's layout), T = 65, T = 130
+  (BASELINE's streaming configuration), T = 256 and T = 264 (the most a handle takes): post-norm hidden and logits
   within 2e-2 max abs and cosine > 0.9995 (the north star's bar), K/V cache rows within a few
   f16 ulps;
 * device prompt + device prefill + device frames == oracle codes (greedy).
@@ -126,7 +126,10 @@ def test_prompt_matches_oracle(side, language):
         assert np.abs(got - want).max() < 1e-4
 
 
-@pytest.mark.parametrize("T", [1, 10, 130, 264])      # 264: the handle's maximum (max_prompt_tokens 256 + 8)
+# 65: the first row count on the column-group row projections; 256: the most keys the
+# short-context attention takes (every thread owns a key); 264: the handle's maximum
+# (max_prompt_tokens 256 + 8), on the general attention kernel
+@pytest.mark.parametrize("T", [1, 10, 65, 130, 256, 264])
 def test_prefill_matches_oracle(abi, side, T):
     rng = np.random.default_rng(T)
     rows = rng.standard_normal((T, 1024)).astype(np.float32)
