@@ -181,6 +181,13 @@ const float *navi_frame_tap_cp_logits(const navi_frame *f);
  * blocks 0..n_blocks-1 (slots past a block's last stamp are 0 for a fresh buffer). */
 navi_status navi_frame_set_profile(navi_frame *f, int32_t enabled);
 navi_status navi_frame_profile(const navi_frame *f, uint64_t *out, int32_t n_blocks, int32_t n_slots);
+/* Test hooks for the launch epoch and the spin cap (no reference counterpart). Each launch uses
+ * the epoch after the current one (+4096); epochs wrap after 2^20 launches, and the wrap clears
+ * the mailboxes and the abort word first. set_epoch takes a multiple of 4096 up to 2^32 - 4096 so
+ * a test can reach the wrap; set_spin_cap changes the polls per wait (0 = the default). */
+navi_status navi_frame_set_epoch(navi_frame *f, uint32_t epoch);
+uint32_t navi_frame_epoch(const navi_frame *f);
+navi_status navi_frame_set_spin_cap(navi_frame *f, uint64_t spin_cap);
 
 /* ---- talker: prompt rows, prefill, KV cache (talker.h:34-67) ----------------- */
 

@@ -1277,6 +1277,20 @@ navi_status navi_frame_profile(const navi_frame *f, uint64_t *out, int32_t n_blo
     return NAVI_OK;
 }
 
+navi_status navi_frame_set_epoch(navi_frame *f, uint32_t epoch) {
+    if (!f || epoch % EPOCH_STRIDE != 0 || epoch > 0xFFFFFFFFu - EPOCH_STRIDE + 1u) return NAVI_ERR_INVALID;
+    f->epoch = epoch;
+    return NAVI_OK;
+}
+
+uint32_t navi_frame_epoch(const navi_frame *f) { return f ? f->epoch : 0u; }
+
+navi_status navi_frame_set_spin_cap(navi_frame *f, uint64_t spin_cap) {
+    if (!f) return NAVI_ERR_INVALID;
+    f->opt.spin_cap = spin_cap ? spin_cap : 2000000ull;
+    return NAVI_OK;
+}
+
 navi_status navi_frame_set_taps(navi_frame *f, int32_t enabled) {
     if (!f) return NAVI_ERR_INVALID;
     f->taps = enabled != 0;
@@ -1345,8 +1359,6 @@ Args frame_args(navi_frame *f, int n_past, bool skip_talker, const float *d_hidd
     a.talker_seed = splitmix64(seed ^ (static_cast<uint64_t>(frame_index) * 0xA24BAED4963EE407ull));
     a.cp_seed = splitmix64(a.talker_seed ^ 0x9FB21C651E98DF25ull);
     a.spin_cap = f->opt.spin_cap;
-    f->epoch += EPOCH_STRIDE;
-    if (f->epoch == 0) f->epoch = EPOCH_STRIDE;
     a.epoch = f->epoch;
     a.prof = f->prof;
     if (f->taps) {
@@ -1355,6 +1367,23 @@ Args frame_args(navi_frame *f, int n_past, bool skip_talker, const float *d_hidd
         a.tap_cp_logits = f->tap + H + VT;
     }
     return a;
+}
+
+// Advances the launch epoch (Impl::launch's barrier reset, frame.hip:660). Tags are epoch + phase in
+// 32 bits, so epochs repeat after 2^20 launches. When the epoch wraps, the mailboxes and the abort
+// word are cleared on the stream before the next launch (tag 0 is never used): neither a stale
+// mailbox word nor the stamp of an old timed-out launch can then match a tag of a later launch.
+hipError_t advance_epoch(navi_frame *f) {
+    uint64_t next = static_cast<uint64_t>(f->epoch) + EPOCH_STRIDE;
+    if (next > (1ull << 32) - EPOCH_STRIDE) {
+        hipStream_t st = device_state().stream;
+        hipError_t e = hipMemsetAsync(f->mb, 0, static_cast<size_t>(MB_TOTAL) * sizeof(uint64_t), st);
+        if (e == hipSuccess) e = hipMemsetAsync(f->ctl + NCB, 0, sizeof(uint32_t), st);
+        if (e != hipSuccess) return e;
+        next = EPOCH_STRIDE;
+    }
+    f->epoch = static_cast<uint32_t>(next);
+    return hipSuccess;
 }
 
 hipError_t frame_launch(navi_frame *f, Args &a) {
@@ -1388,6 +1417,7 @@ navi_status navi_frame_run(navi_frame *f, const navi_kv_view *kv, int32_t n_past
         const navi_status st = frame_kv(f, kv, n_past, n_past, msg);
         if (st != NAVI_OK) return fail(st, msg);
     }
+    if (advance_epoch(f) != hipSuccess) return fail(NAVI_ERR_HIP, "frame: epoch reset failed");
     Args a = frame_args(f, n_past, skip_talker != 0, d_hidden, d_logits, d_trailing, s, seed, frame_index,
                         reinterpret_cast<int32_t *>(f->ctl));
     hipStream_t st = device_state().stream;
@@ -1442,12 +1472,14 @@ navi_status navi_frame_run_many(navi_frame *f, const navi_kv_view *kv, int32_t n
         }
     }
     hipStream_t st = device_state().stream;
-    const uint32_t e0 = f->epoch;
+    std::vector<uint32_t> epochs(static_cast<size_t>(n_frames));
     NAVI_TRY_HIP(hipMemsetAsync(f->stop, 0, sizeof(uint32_t), st), err, errlen);
     NAVI_TRY_HIP(hipEventRecord(f->ev0, st), err, errlen);
     for (int i = 0; i < n_frames; ++i) {
         const bool skip = skip_first && i == 0;
         const float *trail = i < n_trailing ? d_trailing + static_cast<size_t>(i) * H : d_tts_pad;
+        NAVI_TRY_HIP(advance_epoch(f), err, errlen);
+        epochs[static_cast<size_t>(i)] = f->epoch;
         Args a = frame_args(f, skip ? 0 : n_past0 + i, skip, d_hidden, d_logits, trail, s, seed, frame_index0 + i,
                             f->run_codes + static_cast<size_t>(i) * NCB);
         a.stop = f->stop;
@@ -1468,10 +1500,12 @@ navi_status navi_frame_run_many(navi_frame *f, const navi_kv_view *kv, int32_t n
     float ms = 0.f;
     (void) hipEventElapsedTime(&ms, f->ev0, f->ev1);
     if (us) *us = ms * 1000.0;
-    // a timed-out frame stamped its epoch (one of this loop's) and stopped the loop
-    const uint32_t aw = ctl[NCB];
-    if (stop == 2u || (aw - e0 - 1u) < static_cast<uint32_t>(n_frames) * EPOCH_STRIDE) {
-        const int bad = static_cast<int>((aw - e0) / EPOCH_STRIDE) - 1;
+    // A timed-out frame stamped its epoch and stopped the loop. A stamp older than this loop holds an
+    // epoch below all of this loop's (epochs rise between wraps, and a wrap clears the stamp).
+    int bad = -1;
+    for (int i = 0; i < n_frames && bad < 0; ++i)
+        if (epochs[static_cast<size_t>(i)] == ctl[NCB]) bad = i;
+    if (stop == 2u || bad >= 0) {
         *n_done = bad > 0 ? bad : 0;
         set_err(err, errlen, "frame %d: frame dataflow wait timed out: the persistent grid could not run to completion",
                 frame_index0 + *n_done);

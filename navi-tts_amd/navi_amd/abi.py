@@ -27,6 +27,7 @@ EXPORTS = [
     "navi_frame_create", "navi_frame_destroy", "navi_frame_reset", "navi_frame_run", "navi_frame_run_many", "navi_frame_step_out",
     "navi_frame_grid_blocks", "navi_frame_occupancy_per_mp", "navi_frame_set_taps", "navi_frame_tap_hidden",
     "navi_frame_tap_logits", "navi_frame_tap_cp_logits", "navi_frame_set_profile", "navi_frame_profile",
+    "navi_frame_set_epoch", "navi_frame_epoch", "navi_frame_set_spin_cap",
     "navi_talker_create", "navi_talker_destroy", "navi_talker_build_prompt", "navi_talker_prefill", "navi_talker_kv",
     "navi_talker_hidden", "navi_talker_logits", "navi_talker_last_ms", "navi_linear",
     "navi_vocoder_create", "navi_vocoder_destroy", "navi_vocoder_reset", "navi_vocoder_decode",
@@ -174,6 +175,10 @@ def lib() -> C.CDLL:
     L.navi_frame_set_taps.argtypes = [C.c_void_p, C.c_int32]
     L.navi_frame_set_profile.argtypes = [C.c_void_p, C.c_int32]
     L.navi_frame_profile.argtypes = [C.c_void_p, C.c_void_p, C.c_int32, C.c_int32]
+    L.navi_frame_set_epoch.argtypes = [C.c_void_p, C.c_uint32]
+    L.navi_frame_epoch.argtypes = [C.c_void_p]
+    L.navi_frame_epoch.restype = C.c_uint32
+    L.navi_frame_set_spin_cap.argtypes = [C.c_void_p, C.c_uint64]
     for f in ("navi_frame_tap_hidden", "navi_frame_tap_logits", "navi_frame_tap_cp_logits"):
         getattr(L, f).argtypes = [C.c_void_p]
         getattr(L, f).restype = C.c_void_p
@@ -434,6 +439,17 @@ class Frame:
 
     def set_taps(self, on: bool):
         _check(lib().navi_frame_set_taps(self.h, 1 if on else 0), what="navi_frame_set_taps")
+
+    def set_epoch(self, epoch: int):
+        """Test hook: the next launch uses epoch + 4096 (wrapping past 2^32 - 4096)."""
+        _check(lib().navi_frame_set_epoch(self.h, epoch), what="navi_frame_set_epoch")
+
+    @property
+    def epoch(self) -> int:
+        return int(lib().navi_frame_epoch(self.h))
+
+    def set_spin_cap(self, spin_cap: int):
+        _check(lib().navi_frame_set_spin_cap(self.h, C.c_uint64(spin_cap)), what="navi_frame_set_spin_cap")
 
     def _run(self, kv, n_past, skip, d_hidden, d_logits, d_trailing, s, seed, frame_index) -> FrameResult:
         r = FrameResult()

@@ -35,7 +35,11 @@ Pinning (tests/test_oracle_*.py, tests/test_blob.py):
 * speaker: the log-mel vs the reference's own fixture (speaker_mels.npy, first 2 s of
   voice_1.wav); the "same" reflect conv vs torch.nn.Conv1d(padding_mode="reflect");
   weighted statistics vs numpy.average; the whole network on a time-constant mel vs its closed
-  form, with a planted-mistake control.
+  form, and on real speech frames vs transformers' ECAPA_TimeDelayNet, each with a planted-mistake
+  control;
+* code predictor wiring (`Oracle.code_predictor`: which embedding feeds which position, which
+  lm_head scores it, the cache positions) vs transformers' Qwen3-Omni talker code predictor
+  (random weights, greedy codes and every position's logits), with four planted-mistake controls.
 Parity unpinned: none of the functions above. The per-frame composition (`Oracle.frame`) is the
 composition of pinned pieces.
 """

@@ -234,13 +234,17 @@ class Oracle:
         """run_first (hidden/logits given) or run (kv, n_past, step_in). Returns (codes, step_out).
         With `force` (16 codes): teacher forcing; the oracle's own choices go to debug["cb0_choice"]
         and debug["cp_choice"], the forced codes drive the repetition set, the code predictor and
-        the next step. debug["cb0_scores"] holds the modified logits cb0 is chosen from."""
+        the next step. debug["cb0_scores"] holds the modified logits cb0 is chosen from, debug["modify"]
+        applies the same modification (this frame's repetition set and gates) to other logits."""
         if hidden is None:
             hidden, logits = self.talker_step(step_in, kv, n_past)
         if debug is not None:
             debug["hidden"], debug["logits"] = np.asarray(hidden, F32), np.asarray(logits, F32)
             debug["cb0_scores"] = sampler.talker_modified_logits(logits, self.seen, self.eos_id, self.tp.vocab - 1024,
                                                                  frame_index, s.min_frames, s.repetition_penalty)
+            seen0 = self.seen.copy()
+            debug["modify"] = lambda lg: sampler.talker_modified_logits(lg, seen0, self.eos_id, self.tp.vocab - 1024,
+                                                                        frame_index, s.min_frames, s.repetition_penalty)
         tseed, cseed = rng.frame_seeds(seed, frame_index)
         cb0 = sampler.sample_talker(logits, self.seen, s, tseed, frame_index, self.eos_id, self.tp.vocab - 1024)
         if debug is not None:

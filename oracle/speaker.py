@@ -25,8 +25,9 @@ fixture (tests/reference/voice_1.wav -> speaker_mels.npy, first 2 s; tests/golde
 against torch.nn.Conv1d(padding="same", padding_mode="reflect"); `weighted_stats` against
 numpy.average; `embed_mel` on a time-constant mel against a closed form (every conv reduces to a
 matrix of summed taps, the pooled std to 1e-6, the attention to 1/T). The block wiring (slice
-order, residuals, concatenation orders) follows speaker.hip:175-220 and is pinned only through
-that closed form, which shares it: no fixture with these random weights exists.
+order, residuals, concatenation orders) follows speaker.hip:175-220 and is pinned by that closed
+form and by transformers' ECAPA_TimeDelayNet (qwen2_5_omni/modeling_qwen2_5_omni.py:2630), an
+independent implementation of the same network loaded with the same weights (equal on real speech).
 """
 from __future__ import annotations
 

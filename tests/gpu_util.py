@@ -1,6 +1,9 @@
-"""Shared helpers for the GPU parity tests (compare, cosine, oracle prefill on device)."""
+"""Shared helpers for the GPU parity tests (compare, cosine, oracle prefill on device, the greedy
+decision gate and its record)."""
 from __future__ import annotations
 
+import json
+import os
 import sys
 
 import numpy as np
@@ -33,30 +36,56 @@ def device_from_oracle_prefill(ora, kv_oracle, n_prefill, kv_dev):
     kv_dev.n_used = n_prefill
 
 
-# A greedy decision the device may take differently from the oracle only when the oracle's own
-# scores put the device's pick within NEAR_TIE of its maximum: accumulation order (f32 sums in a
-# different order, the K/V cache in f16) moves logits by ~1e-4..1e-3 at the full model's depth,
-# so a tie closer than that is not decidable across implementations.
-NEAR_TIE = 5e-3
+def _row_err(dev, ora):
+    """max |device score - oracle score| over the entries finite on both sides (suppressed entries are
+    -inf on both)."""
+    dev, ora = np.asarray(dev, np.float64), np.asarray(ora, np.float64)
+    fin = np.isfinite(dev) & np.isfinite(ora)
+    assert np.array_equal(np.isfinite(dev), np.isfinite(ora)), "suppressed entries differ"
+    return float(np.abs(dev[fin] - ora[fin]).max())
 
 
-def greedy_decisions(codes, dbg):
-    """[(position, device code, oracle code, oracle score gap)] for the 16 decisions of a frame run
-    with teacher forcing; gap = oracle max score - oracle score of the device's code."""
-    out = []
-    scores = [np.asarray(dbg["cb0_scores"], np.float64)] + [np.asarray(x, np.float64) for x in dbg["cp_logits"]]
+def check_greedy_frame(i, codes, dbg, record, dev_logits, dev_cp_logits):
+    """The greedy gate for the 16 decisions of frame i (teacher-forced oracle, so one flip does not
+    end the comparison). For each position p:
+    * the device's code is the argmax of the device's OWN scores (its logits taps, modified by the
+      oracle's sampler rules for cb0): given identical logits, the decision is bit-exact;
+    * it equals the oracle's code, unless the oracle's own scores put the device's code within
+      2 x err_p of their maximum, where err_p = max |device - oracle| over that very row: only then
+      can that row's measured logit error reorder the two (a per-decision bound, not a fixed one).
+    Every decision goes into `record` (dicts: frame, pos, dev, ora, gap, err, margin)."""
+    dev_scores = [dbg["modify"](dev_logits)] + [np.asarray(x, np.float64) for x in dev_cp_logits]
+    ora_scores = [np.asarray(dbg["cb0_scores"], np.float64)] + [np.asarray(x, np.float64) for x in dbg["cp_logits"]]
     choices = [dbg["cb0_choice"]] + list(dbg["cp_choice"])
-    for p, (sc, oc) in enumerate(zip(scores, choices)):
-        dc = int(codes[p])
-        out.append((p, dc, int(oc), float(sc.max() - sc[dc])))
-    return out
+    for p in range(len(choices)):
+        dc, oc = int(codes[p]), int(choices[p])
+        sc, dv = ora_scores[p], np.asarray(dev_scores[p], np.float64)
+        own = int(np.argmax(dv))
+        err = _row_err(dv, sc)
+        gap = float(sc.max() - sc[dc])
+        record.append(dict(frame=int(i), pos=p, dev=dc, ora=oc, gap=gap, err=err, margin=top2_margin(sc)))
+        assert dc == own, f"frame {i} position {p}: device code {dc} is not the argmax {own} of its own scores"
+        if dc != oc:
+            log(f"  frame {i} position {p}: device {dc} oracle {oc}, oracle gap {gap:.2e}, row error {err:.2e}")
+            assert gap <= 2.0 * err, (f"frame {i} position {p}: device {dc} vs oracle {oc}: gap {gap:.3e} exceeds "
+                                      f"2 x the row's logit error {err:.3e}")
 
 
-def check_greedy_frame(i, codes, dbg, flips):
-    """Asserts every decision of frame i is the oracle's, or a near tie (recorded in flips)."""
-    for p, dc, oc, gap in greedy_decisions(codes, dbg):
-        if dc == oc:
-            continue
-        log(f"  frame {i} position {p}: device {dc} oracle {oc}, oracle score gap {gap:.2e}")
-        assert gap <= NEAR_TIE, f"frame {i} position {p}: device {dc} vs oracle {oc}, gap {gap:.3e} is not a near tie"
-        flips.append((i, p, dc, oc, gap))
+def summarize_decisions(name, record):
+    """Logs the decision count and writes the record to $NAVI_DECISION_LOG/<name>.json when set."""
+    flips = [r for r in record if r["dev"] != r["ora"]]
+    n = len(record)
+    closest = min(record, key=lambda r: r["margin"]) if record else None
+    log(f"{name}: {n - len(flips)} of {n} greedy decisions identical; flips "
+        f"{[(r['frame'], r['pos'], round(r['gap'], 7), round(r['err'], 7)) for r in flips]}; "
+        f"max row error {max((r['err'] for r in record), default=0):.2e}; "
+        f"smallest oracle top-2 margin {closest['margin'] if closest else 0:.2e}")
+    out = os.environ.get("NAVI_DECISION_LOG")
+    if out:
+        os.makedirs(out, exist_ok=True)
+        with open(os.path.join(out, f"{name}.json"), "w") as f:
+            json.dump({"name": name, "decisions": n, "identical": n - len(flips), "flips": flips,
+                       "max_row_err": max((r["err"] for r in record), default=0.0),
+                       "min_margin": closest["margin"] if closest else None,
+                       "margins_below_1e-3": sum(1 for r in record if r["margin"] < 1e-3)}, f, indent=1)
+    return flips

@@ -6,15 +6,17 @@ language "english"; 24 greedy frames with repetition penalty 1.05 and EOS suppre
 24 frames. Everything runs on the device through the C ABI (prompt rows, prefill, frames)
 and is compared with the oracle doing the same on the CPU: the prefill's hidden and logits
 within 2e-2 max abs and cosine > 0.9995; every frame's logits within 2e-2; every one of the
-24 x 16 greedy decisions identical, except a decision whose oracle top-2 gap is below
-gpu_util.NEAR_TIE (at most two such flips). The oracle is teacher-forced with the device's
-codes, so one near-tie flip does not end the comparison.
+24 x 16 greedy decisions gated by gpu_util.check_greedy_frame: the device's code is the argmax of
+its own logits (bit-exact given identical logits) and the oracle's code, unless the oracle's scores
+put the device's code within 2 x that row's measured logit error of their maximum. The oracle is
+teacher-forced with the device's codes, so such a flip does not end the comparison. The decision
+record (count, flips, row errors, margins) is written when NAVI_DECISION_LOG names a directory.
 """
 import numpy as np
 import pytest
 import torch
 
-from gpu_util import check_greedy_frame, compare, log
+from gpu_util import check_greedy_frame, compare, log, summarize_decisions
 
 pytestmark = pytest.mark.gpu
 
@@ -58,7 +60,7 @@ def test_config0_greedy_end_to_end(full_blob):
     ora.reset()
     frame.set_taps(True)
     step = None
-    flips, us = [], []
+    record, us = [], []
     for i in range(N_FRAMES):
         trail_d = pr.trailing + 4 * 1024 * i if i < pr.n_trailing else pr.tts_pad
         trail_h = otrail[i] if i < otrail.shape[0] else opad
@@ -78,10 +80,9 @@ def test_config0_greedy_end_to_end(full_blob):
         thid, tlg, tcp = frame.taps()
         lg_err = max(compare(tlg, dbg["logits"])[0], compare(tcp, np.stack(dbg["cp_logits"]))[0])
         exact = [dbg["cb0_choice"]] + list(dbg["cp_choice"]) == codes
-        log(f"  frame {i:2d}: {'exact' if exact else 'near-tie'} cb0 {codes[0]}, logits max abs err {lg_err:.2e}, "
+        log(f"  frame {i:2d}: {'exact' if exact else 'flip'} cb0 {codes[0]}, logits max abs err {lg_err:.2e}, "
             f"{r.us:.0f} us")
         assert lg_err < 2e-2
-        check_greedy_frame(i, codes, dbg, flips)
-    log(f"config0: {N_FRAMES} frames, {16 * N_FRAMES - len(flips)} of {16 * N_FRAMES} greedy decisions identical, "
-        f"near-tie flips {flips}; mean device {np.mean(us[1:]):.0f} us/frame (talker frames)")
-    assert len(flips) <= 2
+        check_greedy_frame(i, codes, dbg, record, tlg, tcp)
+    summarize_decisions("config0_greedy_24_frames", record)
+    log(f"config0: mean device {np.mean(us[1:]):.0f} us/frame (talker frames)")

@@ -7,7 +7,9 @@
 * the whole ECAPA-TDNN on a time-constant mel against a closed form: every conv of a constant
   signal is its summed taps times the value, the pooled std is sqrt(1e-12) and the attention is
   uniform, so the network reduces to a chain of matrix products. A planted mistake (the SE-Res2Net
-  residual dropped) must break the agreement.
+  residual dropped) must break the agreement;
+* the whole ECAPA-TDNN on real speech frames against transformers' ECAPA_TimeDelayNet (an independent
+  implementation, same weights by tensor name), with a planted mistake (Res2Net slices reversed).
 """
 import numpy as np
 import pytest
@@ -100,3 +102,44 @@ def test_embed_mel_time_constant_closed_form(speaker_blob):
     print(f"constant-mel embedding vs closed form: rel-rms {e:.2e}")
     assert e < 1e-4
     assert rel_rms(got, closed_form(ora.p, v, drop_residual=True)) > 1e-2     # the check can fail
+
+
+def _library_ecapa(ora):
+    """transformers' ECAPA_TimeDelayNet (qwen2_5_omni/modeling_qwen2_5_omni.py:2630), an independent
+    implementation of the same network, configured with Qwen3-TTS's shapes and loaded with the
+    blob's weights by tensor name (the reference's names, params.cpp:165-195, are the HF ones)."""
+    from transformers.models.qwen2_5_omni.configuration_qwen2_5_omni import Qwen2_5OmniDiTConfig
+    from transformers.models.qwen2_5_omni.modeling_qwen2_5_omni import ECAPA_TimeDelayNet
+    cfg = Qwen2_5OmniDiTConfig()
+    cfg.mel_dim, cfg.enc_dim = 128, ora.p["fc.weight"].shape[0]
+    cfg.enc_channels = [512, 512, 512, 512, 1536]
+    cfg.enc_kernel_sizes = [5, 3, 3, 3, 1]
+    cfg.enc_dilations = [1, 2, 3, 4, 1]
+    cfg.enc_attention_channels, cfg.enc_res2net_scale, cfg.enc_se_channels = 128, 8, 128
+    net = ECAPA_TimeDelayNet(cfg).eval()
+    net.load_state_dict({k: v.clone() for k, v in ora.p.items()}, strict=True)
+    return net
+
+
+@pytest.mark.parametrize("T", [5, 37, 186])
+def test_embed_mel_matches_transformers_ecapa(speaker_blob, speaker_fixture, T):
+    """The whole network (block wiring, Res2Net slice order, SE, MFA concatenation order, attentive
+    pooling) against the library model on real speech frames (the reference's mel fixture) and on
+    the 5-frame minimum. A planted mistake (Res2Net slices fed in reverse order) must fail."""
+    ora = osp.SpeakerOracle(speaker_blob)
+    net = _library_ecapa(ora)
+    mel = np.ascontiguousarray(speaker_fixture[1][:, :T], dtype=np.float32)
+    with torch.no_grad():
+        want = net(torch.from_numpy(mel.T)[None])[0].numpy()
+    got = ora.embed_mel(mel)
+    e = rel_rms(got, want)
+    print(f"T={T}: oracle vs transformers ECAPA rel-rms {e:.2e}")
+    assert e < 1e-5
+    # planted: the Res2Net chain visits its slices in reverse order
+    orig = torch.split
+    try:
+        torch.split = lambda t, n, dim=0: tuple(reversed(orig(t, n, dim=dim))) if n == ora.R else orig(t, n, dim=dim)
+        bad = ora.embed_mel(mel)
+    finally:
+        torch.split = orig
+    assert rel_rms(bad, want) > 1e-2

@@ -4,10 +4,12 @@
   tiles, partial K steps and split-K, with bias, SiLU and residual; an activation outside the
   f16 range is an error, not an infinity;
 * build_prompt against Oracle.build_prompt (the reference's layout, talker.hip:283-352);
-* prefill against Oracle.prefill at T = 1, T = 10 (the reference's layout), T = 65, T = 130
-  (BASELINE's streaming configuration), T = 256 and T = 264 (the most a handle takes): post-norm hidden and logits
-  within 2e-2 max abs and cosine > 0.9995 (the north star's bar), K/V cache rows within a few
-  f16 ulps;
+* prefill against Oracle.prefill at T = 1, T = 10 (the reference's layout), T = 32 and 48 (the
+  2- and 3-tile single-group row projections), T = 65, T = 130 (BASELINE's streaming
+  configuration), T = 256 and T = 264 (the most a 256-token handle takes), and on a handle sized as
+  the reference's (max_prompt_tokens 1024, talker.h:37; MAX_KEYS 1024, talker.hip:86) at T = 512,
+  1024 and 1032 (its maximum): post-norm hidden and logits within 2e-2 max abs and cosine > 0.9995
+  (the north star's bar), K/V cache rows within a few f16 ulps;
 * device prompt + device prefill + device frames == oracle codes (greedy).
 """
 import numpy as np
@@ -93,11 +95,11 @@ def test_linear_rejects_bad_shapes(abi):
 
 
 class Side:
-    def __init__(self, abi, path):
+    def __init__(self, abi, path, max_prompt_tokens=256, max_positions=512):
         from oracle.model import Oracle
         self.ora = Oracle(path)
         self.W = abi.DeviceWeights(path, select=lambda t: t.name.startswith("talker."))
-        self.talker = abi.Talker(self.W, max_prompt_tokens=256, max_positions=512)
+        self.talker = abi.Talker(self.W, max_prompt_tokens=max_prompt_tokens, max_positions=max_positions)
         self.frame = abi.Frame(self.W)
 
 
@@ -129,8 +131,24 @@ def test_prompt_matches_oracle(side, language):
 # 65: the first row count on the column-group row projections; 256: the most keys the
 # short-context attention takes (every thread owns a key); 264: the handle's maximum
 # (max_prompt_tokens 256 + 8), on the general attention kernel
-@pytest.mark.parametrize("T", [1, 10, 65, 130, 256, 264])
+@pytest.mark.parametrize("T", [1, 10, 32, 48, 65, 130, 256, 264])
 def test_prefill_matches_oracle(abi, side, T):
+    _check_prefill(abi, side, T)
+
+
+@pytest.fixture(scope="module")
+def side_long(abi, small_blob):
+    s = Side(abi, small_blob, max_prompt_tokens=1024, max_positions=2048)
+    yield s
+    s.talker.close()
+
+
+@pytest.mark.parametrize("T", [512, 1024, 1032])
+def test_long_prefill_matches_oracle(abi, side_long, T):
+    _check_prefill(abi, side_long, T)
+
+
+def _check_prefill(abi, side, T):
     rng = np.random.default_rng(T)
     rows = rng.standard_normal((T, 1024)).astype(np.float32)
     d = abi.DeviceBuffer(rows.nbytes)
