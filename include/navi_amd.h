@@ -236,6 +236,18 @@ double navi_talker_last_ms(const navi_talker *t);         /* Talker::last_ms: de
 navi_status navi_linear(const float *d_x, int32_t ldx, int32_t M, const uint16_t *w, int32_t K, int32_t N,
                         const float *bias, const float *residual, int32_t act, float *d_y, int32_t ldy,
                         char *err, size_t errlen);
+/* navi_linear without any allocation. No counterpart in the reference: it is for callers that
+ * cannot allocate device memory (code under HIP graph capture, serving loops or harnesses that
+ * forbid hipMalloc). Same arguments, kernels and results (bit-identical) as navi_linear, but the
+ * split-K partials live in a fixed 8 MiB array of the library on each GPU (held until the process
+ * ends) instead of a workspace the library allocates: S x M x N floats must fit in its
+ * 2,097,088 floats (S, navi_linear's K-split count, is at most K / 256 and falls as the output
+ * tiles grow), else NAVI_ERR_INVALID says so. The device must already be open
+ * (navi_device_open). Every call on a GPU shares that array and leaves its partials there; calls
+ * that overlap on one GPU (several host threads or streams) race. */
+navi_status navi_linear_noalloc(const float *d_x, int32_t ldx, int32_t M, const uint16_t *w, int32_t K, int32_t N,
+                                const float *bias, const float *residual, int32_t act, float *d_y, int32_t ldy,
+                                char *err, size_t errlen);
 
 /* ---- vocoder: codes -> 24 kHz PCM (vocoder.h:27-55) -------------------------- */
 

@@ -517,6 +517,21 @@ struct LinearWs {
     uint32_t *flag = nullptr;
 } g_ws;
 
+// navi_linear_noalloc's fixed workspace: bytes [0, 256) hold the f16-range flag, the rest the
+// split-K partials. Each GPU the library runs on holds its own copy until the process ends.
+constexpr size_t SCRATCH_BYTES = size_t(8) << 20;
+constexpr size_t SCRATCH_FLAG_BYTES = 256;
+constexpr size_t SCRATCH_FLOATS = (SCRATCH_BYTES - SCRATCH_FLAG_BYTES) / sizeof(float);
+static __device__ __align__(256) unsigned char scratch[SCRATCH_BYTES];
+
+// Device address of `scratch` per device (the array's name in host code is only a stand-in).
+constexpr int MAX_DEVICES = 64;
+void *g_scratch_dev[MAX_DEVICES] = {};
+
+__global__ void k_clear_word(uint32_t *w) {
+    if (threadIdx.x == 0) gst(w, 0u);
+}
+
 struct LayerW {
     const float *ln1, *ln2, *qn, *kn;
     const uint16_t *wq, *wk, *wv, *wo, *wg, *wu, *wd;
@@ -889,6 +904,60 @@ navi_status navi_talker_kv(navi_talker *t, navi_kv_view *out, int32_t *n_used) {
 const float *navi_talker_hidden(const navi_talker *t) { return t ? t->hidden : nullptr; }
 const float *navi_talker_logits(const navi_talker *t) { return t ? t->logits : nullptr; }
 double navi_talker_last_ms(const navi_talker *t) { return t ? t->last_ms : 0.0; }
+
+// navi_linear with its workspace in `scratch`: the same split count and kernels, so the same bits;
+// no allocation on any path (the device must already be open).
+navi_status navi_linear_noalloc(const float *d_x, int32_t ldx, int32_t M, const uint16_t *w, int32_t K, int32_t N,
+                                const float *bias, const float *residual, int32_t act, float *d_y, int32_t ldy, char *err,
+                                size_t errlen) {
+    if (!d_x || !w || !d_y) {
+        set_err(err, errlen, "linear: null argument");
+        return NAVI_ERR_INVALID;
+    }
+    if (!linear_shape_ok(d_x, ldx, M, w, K, N) || ldy < N || (act != 0 && act != 1)) {
+        set_err(err, errlen, "linear: unsupported shape or alignment (M %d, K %d, N %d, ldx %d, ldy %d, act %d)", M, K, N,
+                ldx, ldy, act);
+        return NAVI_ERR_INVALID;
+    }
+    DeviceState &ds = device_state();
+    if (!ds.open) {
+        set_err(err, errlen, "linear_noalloc: open the device first (navi_device_open)");
+        return NAVI_ERR_INVALID;
+    }
+    NAVI_TRY_HIP(hipSetDevice(ds.device), err, errlen);
+    if (ds.device < 0 || ds.device >= MAX_DEVICES) {
+        set_err(err, errlen, "linear_noalloc: device index %d out of range", ds.device);
+        return NAVI_ERR_UNSUPPORTED;
+    }
+    const int S = pick_splits(M, K, N);
+    const size_t need = static_cast<size_t>(S) * M * N;
+    if (need > SCRATCH_FLOATS) {
+        set_err(err, errlen, "linear_noalloc: %d K-splits x %d rows x %d columns need %zu floats of workspace; the "
+                "fixed scratch holds %zu (use navi_linear)", S, M, N, need, SCRATCH_FLOATS);
+        return NAVI_ERR_INVALID;
+    }
+    void *&base = g_scratch_dev[ds.device];
+    if (!base) {
+        void *ptr = nullptr;
+        NAVI_TRY_HIP(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)), err, errlen);
+        base = ptr;
+    }
+    uint32_t *flag = static_cast<uint32_t *>(base);
+    float *part = reinterpret_cast<float *>(static_cast<unsigned char *>(base) + SCRATCH_FLAG_BYTES);
+    hipStream_t s = ds.stream;
+    hipLaunchKernelGGL(k_clear_word, dim3(1), dim3(64), 0, s, flag);
+    launch_partial(d_x, ldx, M, w, K, N, S, part, N, 0, flag, s);
+    hipLaunchKernelGGL(k_finish_linear, dim3(M), dim3(BT), 0, s, part, S, M, N, bias, residual, act, d_y, ldy);
+    NAVI_TRY_HIP(hipGetLastError(), err, errlen);
+    uint32_t f = 0;
+    NAVI_TRY_HIP(hipMemcpyAsync(&f, flag, 4, hipMemcpyDeviceToHost, s), err, errlen);
+    NAVI_TRY_HIP(hipStreamSynchronize(s), err, errlen);
+    if (f) {
+        set_err(err, errlen, "linear: an activation is outside the f16 range (|x| >= 65504 or NaN)");
+        return NAVI_ERR_INVALID;
+    }
+    return NAVI_OK;
+}
 
 navi_status navi_linear(const float *d_x, int32_t ldx, int32_t M, const uint16_t *w, int32_t K, int32_t N,
                         const float *bias, const float *residual, int32_t act, float *d_y, int32_t ldy, char *err,

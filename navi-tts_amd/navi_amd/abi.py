@@ -29,7 +29,7 @@ EXPORTS = [
     "navi_frame_tap_logits", "navi_frame_tap_cp_logits", "navi_frame_set_profile", "navi_frame_profile",
     "navi_frame_set_epoch", "navi_frame_epoch", "navi_frame_set_spin_cap",
     "navi_talker_create", "navi_talker_destroy", "navi_talker_build_prompt", "navi_talker_prefill", "navi_talker_kv",
-    "navi_talker_hidden", "navi_talker_logits", "navi_talker_last_ms", "navi_linear",
+    "navi_talker_hidden", "navi_talker_logits", "navi_talker_last_ms", "navi_linear", "navi_linear_noalloc",
     "navi_vocoder_create", "navi_vocoder_destroy", "navi_vocoder_reset", "navi_vocoder_decode",
     "navi_vocoder_samples_per_frame", "navi_vocoder_max_chunk_frames", "navi_vocoder_last_ms", "navi_synth",
     "navi_streams_create", "navi_streams_destroy", "navi_streams_reset", "navi_streams_run", "navi_streams_step_out",
@@ -223,6 +223,7 @@ def lib() -> C.CDLL:
                              C.POINTER(SynthStats), E, C.c_size_t]
     L.navi_linear.argtypes = [C.c_void_p, C.c_int32, C.c_int32, C.c_void_p, C.c_int32, C.c_int32, C.c_void_p, C.c_void_p,
                               C.c_int32, C.c_void_p, C.c_int32, E, C.c_size_t]
+    L.navi_linear_noalloc.argtypes = L.navi_linear.argtypes
     L.navi_streams_create.argtypes = [C.POINTER(ModelParams), C.POINTER(TensorRef), C.c_int32, C.c_int32, C.c_int32,
                                       C.POINTER(C.c_void_p), E, C.c_size_t]
     L.navi_streams_destroy.argtypes = [C.c_void_p]
@@ -676,10 +677,11 @@ class Talker:
 
 
 def linear(d_x: int, ldx: int, M: int, w: int, K: int, N: int, d_y: int, ldy: int, bias: int | None = None,
-           residual: int | None = None, act: int = 0):
-    """navi_linear: d_y = act(d_x . w^T + bias) + residual on the device."""
+           residual: int | None = None, act: int = 0, noalloc: bool = False):
+    """navi_linear (navi_linear_noalloc with noalloc): d_y = act(d_x . w^T + bias) + residual on the device."""
     err = C.create_string_buffer(256)
-    _check(lib().navi_linear(d_x, ldx, M, w, K, N, bias, residual, act, d_y, ldy, err, 256), err)
+    fn = lib().navi_linear_noalloc if noalloc else lib().navi_linear
+    _check(fn(d_x, ldx, M, w, K, N, bias, residual, act, d_y, ldy, err, 256), err)
 
 
 # ---- vocoder ---------------------------------------------------------------------------
