@@ -16,8 +16,9 @@ constexpr int LDW = CCH + 8;             // padded LDS row (halves)
 
 typedef _Float16 half8v __attribute__((ext_vector_type(8)));
 
-// Prologues (applied to the input as it is staged): SILU_GATE silu(x[ci]) * x[Cin + ci]; ADD2 x + x2.
-enum Pro { PRO_NONE = 0, PRO_SILU_GATE = 2, PRO_ADD2 = 3 };
+// Prologues (applied to the input as it is staged): SILU_GATE silu(x[ci]) * x[Cin + ci]; ADD2 x + x2;
+// RVQ: the input rows are not read from x but gathered from the codebooks by the frame's codes.
+enum Pro { PRO_NONE = 0, PRO_SILU_GATE = 2, PRO_ADD2 = 3, PRO_RVQ = 4 };
 // Epilogues after the bias: RELU_TANH is tanh(max(v, 0)); PARTIAL stores split-K partial sums.
 enum Epi { EPI_BIAS = 0, EPI_GELU = 1, EPI_RESIDUAL = 2, EPI_SCALE_RESIDUAL = 3, EPI_CLAMP = 4, EPI_PARTIAL = 5,
            EPI_RELU = 6, EPI_SIGMOID = 7, EPI_RELU_TANH = 8 };
@@ -38,6 +39,14 @@ struct ConvArgs {
     float *part;           // EPI_PARTIAL: [splits][T * phases][Cout] partial sums, no bias
     uint32_t *flag;        // set when a (prologue-applied) activation is outside the f16 range
     const float *x2;       // PRO_ADD2: second input, same layout as x
+    // When set: the causal history the next chunk reads (the last (K-1) dil rows of [hist ; x]),
+    // written by this launch into the other buffer of the conv's history pair.
+    float *hnext;
+    // PRO_RVQ: codes [T][nq]; input channel ci < Cin/2 of frame t is cb0[code 0][ci], channel
+    // Cin/2 + c the sum over q = 1..nq-1 of cbr[q-1][code q][c] (codebooks [cbsize][Cin/2] f16).
+    const int32_t *codes;
+    const uint16_t *cb0, *cbr;
+    int nq, cbsize;
     int ldx, ldy, T, Cin, Cout, dil, phases, cps;   // cps: input channels per K split
     // Output t reads input rows t - lpad + j * dil (j < K): lpad = (K-1) dil is the causal conv,
     // (K-1) dil / 2 the "same" one. Rows outside [0, T) read hist / zero, or with reflect their
@@ -84,6 +93,62 @@ __device__ __forceinline__ void conv_store(const ConvArgs &a, int epi, size_t o,
     else if (epi == EPI_RELU_TANH) v = tanhf(fmaxf(v, 0.f));
     if (a.y) gst(a.y + o, v);
     if (a.z) gst(a.z + o, snake(v, c.za, c.zb));
+}
+
+// rows [0, H) of out = the last H rows of [hist ; x] (C channels; hist [H][C], x rows of stride
+// ldx): the causal history a conv (or the ConvNeXt depthwise conv) reads in the next chunk. out is
+// the other buffer of the history pair, which the running launch does not read, so every block of
+// the launch can copy an equal share of it, each with its loads issued before its stores.
+__device__ __forceinline__ void carry_rows(const float *hist, const float *x, int ldx, int T, int H, int C, float *out) {
+    const int q = C >> 2, n = H * q;
+    const int nb = gridDim.x * gridDim.y * gridDim.z;
+    const int b = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+    const int per = (n + nb - 1) / nb, i0 = b * per, i1 = min(n, i0 + per);
+    constexpr int U = 4;
+    for (int i = i0 + static_cast<int>(threadIdx.x); i < i1; i += U * BT) {
+        f32x4_t v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int k = i + u * BT;
+            if (k < i1) {
+                const int r = k / q, c = (k - r * q) * 4, src = r + T - H;   // row of x, or of hist if < 0
+                v[u] = src >= 0 ? ld4(x + static_cast<size_t>(src) * ldx + c) : ld4(hist + static_cast<size_t>(src + H) * C + c);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int k = i + u * BT;
+            if (k < i1) {
+                const int r = k / q, c = (k - r * q) * 4;
+                st4(out + static_cast<size_t>(r) * C + c, v[u]);
+            }
+        }
+    }
+}
+
+// Four input channels ci..ci+3 of the RVQ front end at frame t (PRO_RVQ): the semantic codebook's
+// row, or the rest codebooks' rows summed in f32 in codebook order (k_rvq, vocoder.hip:125-143).
+// All the row loads of the sum are issued before the first add.
+__device__ __forceinline__ f32x4_t rvq_row4(const ConvArgs &a, int t, int ci) {
+    const int half = a.Cin >> 1;
+    const int32_t *code = a.codes + static_cast<size_t>(t) * a.nq;
+    auto unpack = [](u32x2_t w) {
+        return f32x4_t{h2f(static_cast<uint16_t>(w.x)), h2f(static_cast<uint16_t>(w.x >> 16)), h2f(static_cast<uint16_t>(w.y)),
+                       h2f(static_cast<uint16_t>(w.y >> 16))};
+    };
+    if (ci < half) return unpack(gld(reinterpret_cast<const u32x2_t *>(a.cb0 + static_cast<size_t>(gld(code)) * half + ci)));
+    constexpr int MAXQ = 16;
+    u32x2_t w[MAXQ - 1];
+#pragma unroll
+    for (int q = 1; q < MAXQ; ++q)
+        if (q < a.nq)
+            w[q - 1] = gld(reinterpret_cast<const u32x2_t *>(a.cbr + (static_cast<size_t>(q - 1) * a.cbsize + gld(code + q)) * half +
+                                                            (ci - half)));
+    f32x4_t v = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int q = 1; q < MAXQ; ++q)
+        if (q < a.nq) v += unpack(w[q - 1]);
+    return v;
 }
 
 namespace {
@@ -134,7 +199,9 @@ __global__ void __launch_bounds__(BT) k_conv_mfma(ConvArgs a) {
             av[it] = f32x4_t{0.f, 0.f, 0.f, 0.f};
             if (TWO) au[it] = av[it];
             if (r < rows) {
-                if (t >= 0 && t < a.T) {
+                if (PRO == PRO_RVQ) {
+                    if (t >= 0 && t < a.T) av[it] = rvq_row4(a, t, ci);
+                } else if (t >= 0 && t < a.T) {
                     const float *row = a.x + static_cast<size_t>(t) * a.ldx;
                     av[it] = *(const NAVI_GLOBAL f32x4_t *) (row + ci);
                     if (PRO == PRO_SILU_GATE) au[it] = *(const NAVI_GLOBAL f32x4_t *) (row + a.Cin + ci);
@@ -204,7 +271,11 @@ __global__ void __launch_bounds__(BT) k_conv_mfma(ConvArgs a) {
         }
     }
     if (bad) gst(a.flag, 1u);
-    if (!live) return;
+    // the next chunk's history last: its stores wait for its loads, which nothing else needs
+    if (!live) {
+        if (a.hnext) carry_rows(a.hist, a.x, a.ldx, a.T, H, a.Cin, a.hnext);
+        return;
+    }
     const int co = n0 + (l & 15);
     float *part = a.part + static_cast<size_t>(split) * a.T * a.phases * a.Cout;
     if constexpr (EPI == EPI_PARTIAL) {
@@ -234,6 +305,7 @@ __global__ void __launch_bounds__(BT) k_conv_mfma(ConvArgs a) {
                 if (t < a.T) conv_store(a, EPI, (static_cast<size_t>(t) * a.phases + phase) * a.ldy + co, cc, acc[i][r], res[i][r]);
             }
     }
+    if (a.hnext) carry_rows(a.hist, a.x, a.ldx, a.T, H, a.Cin, a.hnext);
 }
 
 // The 96-channel convs (the codec decoder's last block and its final conv): a block covers
@@ -360,6 +432,7 @@ __global__ void __launch_bounds__(BT) k_conv_c96(ConvArgs a) {
                 conv_store(a, EPI, static_cast<size_t>(t) * a.ldy + co, cc[n], acc[i][n][r], res[i][r][n]);
             }
         }
+    if (a.hnext) carry_rows(a.hist, a.x, a.ldx, a.T, H, CIN, a.hnext);
 }
 
 // Sum of the K-split partials in split order, then the epilogue (EPI_PARTIAL's second half).

@@ -156,6 +156,7 @@ template <class T>
 __device__ __forceinline__ void gst(T *p, T v) { *(NAVI_GLOBAL T *) p = v; }
 
 typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
+typedef unsigned u32x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 // 16-byte global load as a native vector (a HIP uint4 struct copy through an address-space-1

@@ -22,9 +22,15 @@
 //  * The last decoder block's 96-channel convs and the final conv run on k_conv_c96: a block
 //    stages its whole input window and each tap's weights in LDS and covers every output
 //    channel, reading the input ~1.4x instead of ~3.7x.
+//  * The RVQ front end is the first conv's prologue (its input rows are gathered from the
+//    codebooks while being staged); RoPE and the K/V ring append are folded into the windowed
+//    attention kernel; the ConvNeXt depthwise conv + LayerNorm runs one wave per row with
+//    register-only reductions.
 //  * Streaming state: each causal conv keeps its last (K-1)*dil input rows (the history the
 //    next chunk's first rows read), the ConvNeXt depthwise conv its last 6, the attention its
 //    K/V in a ring of >= window + chunk positions: chunked decoding equals one-shot decoding.
+//    A history is a pair of buffers: each launch reads one and its blocks write the next chunk's
+//    into the other, so no launch exists only to update it.
 #include "conv.h"
 #include "dev_common.h"
 #include "host_util.h"
@@ -38,33 +44,6 @@ namespace navi_amd {
 namespace vc {
 
 using namespace cv;
-
-// new[r] = row r of the last H rows of [old ; x] (the causal history for the next chunk).
-__global__ void __launch_bounds__(BT) k_hist_update(const float *old, const float *x, int T, int H, int C, int ldx,
-                                                    float *out) {
-    const size_t i = static_cast<size_t>(blockIdx.x) * BT + threadIdx.x;
-    if (i >= static_cast<size_t>(H) * C) return;
-    const int r = static_cast<int>(i / C), c = static_cast<int>(i % C), src = r + T;
-    gst(out + i, src < H ? gld(old + static_cast<size_t>(src) * C + c) : gld(x + static_cast<size_t>(src - H) * ldx + c));
-}
-
-// e[t] = [cb_first[c0] | sum_{q>=1} cb_rest[q-1][c_q]] (k_rvq, vocoder.hip:125-143).
-__global__ void __launch_bounds__(BT) k_rvq(const int32_t *codes, int n_q, const uint16_t *cb_first, const uint16_t *cb_rest,
-                                            int dim, int cb_size, float *e) {
-    const int t = blockIdx.x;
-    const int32_t *c = codes + static_cast<size_t>(t) * n_q;
-    for (int i = threadIdx.x; i < 2 * dim; i += BT) {
-        float v;
-        if (i < dim) {
-            v = h2f(gld(cb_first + static_cast<size_t>(gld(c)) * dim + i));
-        } else {
-            v = 0.f;
-            for (int q = 1; q < n_q; ++q)
-                v += h2f(gld(cb_rest + (static_cast<size_t>(q - 1) * cb_size + gld(c + q)) * dim + (i - dim)));
-        }
-        gst(e + static_cast<size_t>(t) * 2 * dim + i, v);
-    }
-}
 
 // y[t] = RMSNorm(x[t]) * w over C channels.
 __global__ void __launch_bounds__(BT) k_rmsnorm(const float *x, const float *w, int C, float eps, float *y) {
@@ -82,99 +61,158 @@ __global__ void __launch_bounds__(BT) k_rmsnorm(const float *x, const float *w, 
     for (int c = threadIdx.x; c < C; c += BT) gst(y + static_cast<size_t>(blockIdx.x) * C + c, gld(row + c) * scale * gld(w + c));
 }
 
-// ConvNeXt front: causal depthwise k7 conv + LayerNorm over channels (k_dwconv_ln, vocoder.hip:20-54).
-// C = 4 * BT channels.
-__global__ void __launch_bounds__(BT) k_dwconv_ln(const uint16_t *w, const float *bias, const float *x, const float *hist,
-                                                  int C, const float *lw, const float *lb, float eps, float *y) {
-    __shared__ float red[8];
-    const int t = blockIdx.x;
-    float v[4], s = 0.f;
+// The ConvNeXt block's front (vocoder.hip:20-54 semantics): a causal depthwise conv over DWK time
+// steps, then LayerNorm over the C channels of each row. One wave per output row and no LDS: lane
+// l owns the MG groups of four channels 4 l + 256 m, so each of its loads is a 16-byte piece of a
+// row that the wave reads whole (the depthwise weights tap-major, [DWK][C] f16, 8 bytes per group),
+// and the row's mean and variance are two wave reductions in registers. Rows before t = 0 come from
+// the DWK - 1 history rows; the block's threads then carry the next chunk's history into hnext.
+template <int MG>
+__global__ void __launch_bounds__(BT) k_dw_ln(const float *x, const float *hist, const uint16_t *wt, const float *bias,
+                                              const float *lw, const float *lb, float eps, int R, float *y, float *hnext) {
+    constexpr int DWK = 7, C = 256 * MG;
+    const int l = threadIdx.x & 63, t = blockIdx.x * (BT / 64) + (threadIdx.x >> 6);
+    if (t < R) {
+        f32x4_t xv[DWK][MG];
+        u32x2_t wv[DWK][MG];
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        const int c = threadIdx.x + k * BT;
-        float acc = gld(bias + c);
-        for (int j = 0; j < 7; ++j) {
-            const int tt = t - 6 + j;
-            const float xv = tt >= 0 ? gld(x + static_cast<size_t>(tt) * C + c) : gld(hist + static_cast<size_t>(6 + tt) * C + c);
-            acc = fmaf(h2f(gld(w + c * 7 + j)), xv, acc);
+        for (int j = 0; j < DWK; ++j) {
+            const int tt = t - (DWK - 1) + j;
+            const float *row = tt >= 0 ? x + static_cast<size_t>(tt) * C : hist + static_cast<size_t>(DWK - 1 + tt) * C;
+#pragma unroll
+            for (int m = 0; m < MG; ++m) {
+                const int c = 4 * l + 256 * m;
+                xv[j][m] = ld4(row + c);
+                wv[j][m] = gld(reinterpret_cast<const u32x2_t *>(wt + static_cast<size_t>(j) * C + c));
+            }
         }
-        v[k] = acc;
-        s += acc;
-    }
-    s = wave_sum(s);
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
-    __syncthreads();
-    const float mean = (red[0] + red[1] + red[2] + red[3]) / static_cast<float>(C);
-    float ss = 0.f;
+        f32x4_t acc[MG];
+        float s = 0.f;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        const float d = v[k] - mean;
-        ss = fmaf(d, d, ss);
-    }
-    ss = wave_sum(ss);
-    if ((threadIdx.x & 63) == 0) red[4 + (threadIdx.x >> 6)] = ss;
-    __syncthreads();
-    const float inv = rsqrtf((red[4] + red[5] + red[6] + red[7]) / static_cast<float>(C) + eps);
+        for (int m = 0; m < MG; ++m) {
+            acc[m] = ld4(bias + 4 * l + 256 * m);
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        const int c = threadIdx.x + k * BT;
-        gst(y + static_cast<size_t>(t) * C + c, (v[k] - mean) * inv * gld(lw + c) + gld(lb + c));
+            for (int j = 0; j < DWK; ++j) {
+                const u32x2_t w = wv[j][m];
+                const float wf[4] = {h2f(static_cast<uint16_t>(w.x)), h2f(static_cast<uint16_t>(w.x >> 16)),
+                                     h2f(static_cast<uint16_t>(w.y)), h2f(static_cast<uint16_t>(w.y >> 16))};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc[m][e] = fmaf(wf[e], xv[j][m][e], acc[m][e]);
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e) s += acc[m][e];
+        }
+        const float mean = wave_sum(s) / static_cast<float>(C);
+        float ss = 0.f;
+#pragma unroll
+        for (int m = 0; m < MG; ++m)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                acc[m][e] -= mean;
+                ss = fmaf(acc[m][e], acc[m][e], ss);
+            }
+        const float inv = rsqrtf(wave_sum(ss) / static_cast<float>(C) + eps);
+#pragma unroll
+        for (int m = 0; m < MG; ++m) {
+            const int c = 4 * l + 256 * m;
+            const f32x4_t g = ld4(lw + c), b = ld4(lb + c);
+            st4(y + static_cast<size_t>(t) * C + c, acc[m] * inv * g + b);
+        }
     }
+    carry_rows(hist, x, C, R, DWK - 1, C, hnext);
 }
 
-// RoPE on q and k of row t at position pos0 + t; k and v appended to the ring caches
-// (k_rope_append, vocoder.hip:57-84). Row layout [q | k | v], nh heads of hd.
-__global__ void __launch_bounds__(BT) k_rope_append(float *qkv, int nh, int hd, int pos0, int ring, const float *invf,
-                                                    float *kc, float *vc) {
-    const int t = blockIdx.x, pos = pos0 + t, slot = pos % ring, HDT = nh * hd, half = hd / 2;
-    float *row = qkv + static_cast<size_t>(t) * 3 * HDT;
-    for (int i = threadIdx.x; i < nh * half; i += BT) {
-        const int h = i / half, p = i % half;
+// Sliding-window causal attention of the codec transformer (k_attention, vocoder.hip:87-122
+// semantics) with RoPE (theta from invf, rotate-half) and the K/V ring append folded in. A block
+// takes RT query rows of one head: it stages in LDS the roped keys and the values of every
+// position those rows see (positions of this chunk straight from the q|k|v rows, roped here;
+// earlier ones from the ring, stored roped), then each wave runs RT/4 rows: lane j scores keys
+// j and j + 64 of the row's window, softmax by two wave reductions, and lane d sums p_j V[j][d]
+// with p_j read from lane j (readlane). The block also writes its rows' roped k and v to the ring
+// for later chunks: ring >= window + chunk, so no slot written here is one this launch reads.
+template <int HD>
+__global__ void __launch_bounds__(BT) k_window_attention(const float *qkv, int nh, int T, int pos0, int window, int ring,
+                                                         const float *invf, float *kc, float *vc, float *out) {
+    constexpr int RT = 16, HALF = HD / 2, KS = HD + 1, DPL = HD / 64;   // K rows padded: lanes j read rows j
+    extern __shared__ float sm[];
+    const int HDT = nh * HD, ld = 3 * HDT, h = blockIdx.y;
+    const int t0 = blockIdx.x * RT, t1 = min(T, t0 + RT);
+    const int kp0 = max(0, pos0 + t0 - window + 1), nk = pos0 + t1 - kp0;
+    float *Ks = sm, *Vs = Ks + (window + RT - 1) * KS, *Qs = Vs + (window + RT - 1) * HD;
+    for (int e = threadIdx.x; e < nk * HALF; e += BT) {
+        const int r = e / HALF, i = e - r * HALF, p = kp0 + r;
+        float k0, k1, v0, v1;
+        if (p >= pos0) {
+            const float *row = qkv + static_cast<size_t>(p - pos0) * ld + h * HD;
+            const float a0 = gld(row + HDT + i), a1 = gld(row + HDT + i + HALF);
+            v0 = gld(row + 2 * HDT + i);
+            v1 = gld(row + 2 * HDT + i + HALF);
+            float sn, cs;
+            sincosf(static_cast<float>(p) * gld(invf + i), &sn, &cs);
+            k0 = a0 * cs - a1 * sn;
+            k1 = a1 * cs + a0 * sn;
+            if (p - pos0 >= t0 && p - pos0 < t1) {
+                const size_t o = static_cast<size_t>(p % ring) * HDT + h * HD + i;
+                gst(kc + o, k0);
+                gst(kc + o + HALF, k1);
+                gst(vc + o, v0);
+                gst(vc + o + HALF, v1);
+            }
+        } else {
+            const size_t o = static_cast<size_t>(p % ring) * HDT + h * HD + i;
+            k0 = gld(kc + o);
+            k1 = gld(kc + o + HALF);
+            v0 = gld(vc + o);
+            v1 = gld(vc + o + HALF);
+        }
+        Ks[r * KS + i] = k0;
+        Ks[r * KS + i + HALF] = k1;
+        Vs[r * HD + i] = v0;
+        Vs[r * HD + i + HALF] = v1;
+    }
+    for (int e = threadIdx.x; e < (t1 - t0) * HALF; e += BT) {
+        const int rr = e / HALF, i = e - rr * HALF, p = pos0 + t0 + rr;
+        const float *row = qkv + static_cast<size_t>(t0 + rr) * ld + h * HD;
+        const float a0 = gld(row + i), a1 = gld(row + i + HALF);
         float sn, cs;
-        sincosf(static_cast<float>(pos) * gld(invf + p), &sn, &cs);
-        float *q = row + h * hd, *k = row + HDT + h * hd;
-        const float q0 = q[p], q1 = q[p + half], k0 = k[p], k1 = k[p + half];
-        q[p] = q0 * cs - q1 * sn;
-        q[p + half] = q1 * cs + q0 * sn;
-        const float r0 = k0 * cs - k1 * sn, r1 = k1 * cs + k0 * sn;
-        gst(kc + static_cast<size_t>(slot) * HDT + h * hd + p, r0);
-        gst(kc + static_cast<size_t>(slot) * HDT + h * hd + p + half, r1);
+        sincosf(static_cast<float>(p) * gld(invf + i), &sn, &cs);
+        Qs[rr * HD + i] = a0 * cs - a1 * sn;
+        Qs[rr * HD + i + HALF] = a1 * cs + a0 * sn;
     }
-    for (int i = threadIdx.x; i < HDT; i += BT) gst(vc + static_cast<size_t>(slot) * HDT + i, row[2 * HDT + i]);
-}
-
-// Sliding-window causal attention: keys max(0, pos - window + 1) .. pos from the rings
-// (k_attention, vocoder.hip:87-122). 128 threads, window <= 128, hd <= 128.
-__global__ void __launch_bounds__(128) k_window_attn(const float *qkv, int nh, int hd, int pos0, int window, int ring,
-                                                     const float *kc, const float *vc, float *out) {
-    __shared__ float sc[128], red[4];
-    const int t = blockIdx.x, h = blockIdx.y, pos = pos0 + t, HDT = nh * hd;
-    const int k0 = max(0, pos - window + 1), n = pos - k0 + 1;
-    const float *q = qkv + static_cast<size_t>(t) * 3 * HDT + h * hd;
-    const int j = threadIdx.x, wv = j >> 6;
-    float s = -INFINITY;
-    if (j < n) {
-        const float *k = kc + static_cast<size_t>((k0 + j) % ring) * HDT + h * hd;
-        float d = 0.f;
-        for (int i = 0; i < hd; ++i) d = fmaf(gld(q + i), gld(k + i), d);
-        s = d * rsqrtf(static_cast<float>(hd));
-    }
-    float m = wave_max(s);
-    if ((j & 63) == 0) red[wv] = m;
     __syncthreads();
-    m = fmaxf(red[0], red[1]);
-    const float e = j < n ? expf(s - m) : 0.f;
-    float sum = wave_sum(e);
-    __syncthreads();
-    if ((j & 63) == 0) red[2 + wv] = sum;
-    __syncthreads();
-    sum = red[2] + red[3];
-    sc[j] = e / sum;
-    __syncthreads();
-    if (j < hd) {
-        float acc = 0.f;
-        for (int i = 0; i < n; ++i) acc = fmaf(sc[i], gld(vc + static_cast<size_t>((k0 + i) % ring) * HDT + h * hd + j), acc);
-        gst(out + static_cast<size_t>(t) * HDT + h * hd + j, acc);
+    const int wv = threadIdx.x >> 6, l = threadIdx.x & 63;
+    const float scale = rsqrtf(static_cast<float>(HD));
+    for (int k = 0; k < RT / 4; ++k) {
+        const int rr = wv * (RT / 4) + k, t = t0 + rr;
+        if (t >= t1) break;
+        const int pos = pos0 + t, klo = max(0, pos - window + 1), n = pos - klo + 1, rb = klo - kp0;
+        const float *q = Qs + rr * HD;
+        float s[2] = {-INFINITY, -INFINITY};
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int j = l + 64 * u;
+            if (j < n) {
+                const float *kr = Ks + (rb + j) * KS;
+                float d = 0.f;
+#pragma unroll 16
+                for (int i = 0; i < HD; ++i) d = fmaf(q[i], kr[i], d);
+                s[u] = d * scale;
+            }
+        }
+        const float m = wave_max(fmaxf(s[0], s[1]));
+        float p[2];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) p[u] = l + 64 * u < n ? expf(s[u] - m) : 0.f;
+        const float inv = 1.f / wave_sum(p[0] + p[1]);
+        float acc[DPL] = {};
+        for (int j = 0; j < n; ++j) {
+            const float pj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p[j >> 6]), j & 63));
+            const float *vr = Vs + (rb + j) * HD + l;
+#pragma unroll
+            for (int d = 0; d < DPL; ++d) acc[d] = fmaf(pj, vr[64 * d], acc[d]);
+        }
+#pragma unroll
+        for (int d = 0; d < DPL; ++d) gst(out + static_cast<size_t>(t) * HDT + h * HD + l + 64 * d, acc[d] * inv);
     }
 }
 
@@ -199,6 +237,14 @@ __global__ void k_relayout_tconv(const uint16_t *w, int Cin, int Cout, int k, in
     r /= kk;
     const int co = static_cast<int>(r % Cout), p = static_cast<int>(r / Cout);
     gst(out + i, gld(w + (static_cast<size_t>(ci) * Cout + co) * k + p + (kk - 1 - j) * s));
+}
+
+// Depthwise conv weights [C][1][K] -> tap-major [K][C] (k_dw_ln reads a tap's channels at once).
+__global__ void k_tap_major(const uint16_t *w, int C, int K, uint16_t *out) {
+    const int i = blockIdx.x * BT + threadIdx.x;
+    if (i >= C * K) return;
+    const int j = i / C, c = i - j * C;
+    gst(out + i, gld(w + static_cast<size_t>(c) * K + j));
 }
 
 __global__ void k_snake_prep(const float *alpha, const float *beta, int n, float *sa, float *sb) {
@@ -228,9 +274,9 @@ struct TLayer {
 };
 
 struct ConvNeXt {
-    const uint16_t *dw;
+    const uint16_t *dwt;               // depthwise weights, tap-major [7][C]
     const float *dw_b, *ln_w, *ln_b, *gamma;
-    float *hist, *hist2;
+    float *hist, *hist2;               // the depthwise conv's 6 history rows (pair: read one, write the other)
     Conv pw1, pw2;
 };
 
@@ -258,11 +304,21 @@ struct navi_vocoder {
     float *pcm16 = nullptr;            // [rows][16] output of the padded final conv
     float *invf = nullptr;
     uint32_t *flag = nullptr;
-    // buffers
+    // activations of one chunk (time-major rows)
     int32_t *d_codes = nullptr;
-    float *e = nullptr, *h = nullptr, *a = nullptr, *x = nullptr, *n = nullptr, *qkv = nullptr, *att = nullptr,
-          *gu = nullptr, *u = nullptr, *A = nullptr, *B = nullptr, *G = nullptr, *d = nullptr, *pcm = nullptr;
-    float *P[4] = {}, *Q[4] = {}, *ZP[4] = {};
+    float *lat = nullptr;              // RVQ latent [T][CD]
+    float *pre = nullptr;              // pre_conv output [T][L]
+    float *xs = nullptr, *xn = nullptr;   // transformer residual stream and its RMSNorm [T][VH]
+    float *qkv = nullptr, *att = nullptr, *gu = nullptr;
+    float *post = nullptr;             // transformer output projection [T][L]
+    float *upx[2] = {};                // upsampling stages' residual streams [R][L]
+    float *lnx = nullptr;              // ConvNeXt depthwise + LayerNorm output [R][L]
+    float *pwh = nullptr;              // ConvNeXt hidden [R][4L]
+    float *dec_in = nullptr;           // Snake(dec0 output), block 0's input [R][DD]
+    float *pcm = nullptr;
+    // per decoder block: the residual stream, its Snake (the next conv's input) and the Snake of
+    // each unit's first conv output
+    float *res[4] = {}, *res_s[4] = {}, *mid_s[4] = {};
     float *part = nullptr;             // K-split partial sums (conv_splits)
     size_t part_floats = 0;
     hipEvent_t ev0 = nullptr, ev1 = nullptr;
@@ -303,6 +359,10 @@ void launch_k(const ConvArgs &a, int pro, int epi, dim3 grid, hipStream_t s) {
     NAVI_CONV(PRO_NONE, EPI_PARTIAL)
     NAVI_CONV(PRO_SILU_GATE, EPI_SCALE_RESIDUAL)
     NAVI_CONV(PRO_SILU_GATE, EPI_PARTIAL)
+    if constexpr (K == 1) {
+        NAVI_CONV(PRO_RVQ, EPI_BIAS)
+        NAVI_CONV(PRO_RVQ, EPI_PARTIAL)
+    }
 #undef NAVI_CONV
 }
 
@@ -382,22 +442,27 @@ navi_status launch_generic(navi_vocoder &v, const Conv &c, ConvArgs &a, int pro,
     return NAVI_OK;
 }
 
-// Runs one conv over T input rows; updates its history afterwards. z (optional): also write
-// Snake(y) with the Snake parameters of zc, the conv that consumes this output.
+// Runs one conv over T input rows. A causal conv reads its history and writes the next chunk's
+// into the other buffer of its pair (the pair then swaps). z (optional): also write Snake(y) with
+// the Snake parameters of zc, the conv that consumes this output. PRO_RVQ takes no x: its rows
+// are gathered from the codebooks by the chunk's codes.
 navi_status run_conv(navi_vocoder &v, Conv &c, int pro, int epi, const float *x, int T, int ldx, float *y, int ldy,
                      const float *res, const float *scale, char *err, size_t errlen, float *z = nullptr,
                      const Conv *zc = nullptr) {
-    hipStream_t s = device_state().stream;
     ConvArgs a{};
     a.x = x; a.hist = c.hist; a.w = c.w; a.bias = c.bias; a.res = res; a.scale = scale;
     a.y = y; a.z = z; a.flag = v.flag; a.ldx = ldx; a.ldy = ldy; a.T = T; a.Cin = c.Cin; a.Cout = c.Cout;
     a.dil = c.dil; a.phases = c.phases; a.lpad = (c.K - 1) * c.dil;   // causal
+    a.hnext = c.H > 0 ? c.hist2 : nullptr;
+    if (pro == PRO_RVQ) {
+        a.codes = v.d_codes; a.cb0 = v.cb_first; a.cbr = v.cb_rest; a.nq = v.p.n_q; a.cbsize = v.p.codebook_size;
+    }
     if (z) {
         a.za = zc->sa;
         a.zb = zc->sb;
     }
     if (conv_is_c96(c)) {
-        if (!launch_c96(c, a, pro, epi, T, s)) {
+        if (!launch_c96(c, a, pro, epi, T, device_state().stream)) {
             set_err(err, errlen, "vocoder: no 96-channel conv kernel for K=%d Cout=%d epilogue %d", c.K, c.Cout, epi);
             return NAVI_ERR_UNSUPPORTED;
         }
@@ -405,13 +470,13 @@ navi_status run_conv(navi_vocoder &v, Conv &c, int pro, int epi, const float *x,
         const navi_status st = launch_generic(v, c, a, pro, epi, T, err, errlen);
         if (st != NAVI_OK) return st;
     }
-    if (c.H > 0) {
-        const size_t nh = static_cast<size_t>(c.H) * c.Cin;
-        hipLaunchKernelGGL(k_hist_update, dim3(static_cast<unsigned>((nh + BT - 1) / BT)), dim3(BT), 0, s, c.hist, x, T, c.H,
-                           c.Cin, ldx, c.hist2);
-        std::swap(c.hist, c.hist2);
-    }
+    if (c.H > 0) std::swap(c.hist, c.hist2);
     return NAVI_OK;
+}
+
+size_t attention_lds(int window, int head_dim) {
+    constexpr int RT = 16;
+    return (static_cast<size_t>(window + RT - 1) * (2 * head_dim + 1) + static_cast<size_t>(RT) * head_dim) * sizeof(float);
 }
 
 #define VOC_TRY(expr)                         \
@@ -420,71 +485,76 @@ navi_status run_conv(navi_vocoder &v, Conv &c, int pro, int epi, const float *x,
         if (s_ != NAVI_OK) return s_;         \
     } while (0)
 
+// One chunk of T frames: codes (already in v.d_codes) -> T * samples_per_frame PCM samples in v.pcm
+// (the stage order of decode_chunk, vocoder.hip:261-343, which is the model's).
 navi_status decode_chunk(navi_vocoder &v, int T, char *err, size_t errlen) {
     hipStream_t s = device_state().stream;
     const navi_vocoder_params &p = v.p;
-    const int VH = v.VH, L = v.L, HDT = v.HDT, FF = p.xf.ff, CD = v.CD;
-    hipLaunchKernelGGL(k_rvq, dim3(T), dim3(BT), 0, s, v.d_codes, p.n_q, v.cb_first, v.cb_rest, CD / 2, p.codebook_size, v.e);
-    VOC_TRY(run_conv(v, v.rvq_proj, PRO_NONE, EPI_BIAS, v.e, T, CD, v.h, CD, nullptr, nullptr, err, errlen));
-    VOC_TRY(run_conv(v, v.pre_conv, PRO_NONE, EPI_BIAS, v.h, T, CD, v.a, L, nullptr, nullptr, err, errlen));
-    VOC_TRY(run_conv(v, v.in_proj, PRO_NONE, EPI_BIAS, v.a, T, L, v.x, VH, nullptr, nullptr, err, errlen));
+    const int VH = v.VH, L = v.L, HDT = v.HDT, FF = p.xf.ff, CD = v.CD, nh = p.xf.n_head;
+    // RVQ front end and its two output projections, one conv gathering its rows from the codebooks
+    VOC_TRY(run_conv(v, v.rvq_proj, PRO_RVQ, EPI_BIAS, nullptr, T, CD, v.lat, CD, nullptr, nullptr, err, errlen));
+    VOC_TRY(run_conv(v, v.pre_conv, PRO_NONE, EPI_BIAS, v.lat, T, CD, v.pre, L, nullptr, nullptr, err, errlen));
+    VOC_TRY(run_conv(v, v.in_proj, PRO_NONE, EPI_BIAS, v.pre, T, L, v.xs, VH, nullptr, nullptr, err, errlen));
+    const dim3 att_grid((T + 15) / 16, nh);
+    const size_t att_lds = attention_lds(p.sliding_window, p.xf.head_dim);
     for (TLayer &ly : v.layers) {
-        hipLaunchKernelGGL(k_rmsnorm, dim3(T), dim3(BT), 0, s, v.x, ly.ln1, VH, p.xf.rms_eps, v.n);
-        VOC_TRY(run_conv(v, ly.qkv, PRO_NONE, EPI_BIAS, v.n, T, VH, v.qkv, 3 * HDT, nullptr, nullptr, err, errlen));
-        hipLaunchKernelGGL(k_rope_append, dim3(T), dim3(BT), 0, s, v.qkv, p.xf.n_head, p.xf.head_dim, v.pos0, v.ring, v.invf,
-                           ly.kc, ly.vc);
-        hipLaunchKernelGGL(k_window_attn, dim3(T, p.xf.n_head), dim3(128), 0, s, v.qkv, p.xf.n_head, p.xf.head_dim, v.pos0,
-                           p.sliding_window, v.ring, ly.kc, ly.vc, v.att);
-        VOC_TRY(run_conv(v, ly.o, PRO_NONE, EPI_SCALE_RESIDUAL, v.att, T, HDT, v.x, VH, v.x, ly.attn_scale, err, errlen));
-        hipLaunchKernelGGL(k_rmsnorm, dim3(T), dim3(BT), 0, s, v.x, ly.ln2, VH, p.xf.rms_eps, v.n);
-        VOC_TRY(run_conv(v, ly.gu, PRO_NONE, EPI_BIAS, v.n, T, VH, v.gu, 2 * FF, nullptr, nullptr, err, errlen));
-        VOC_TRY(run_conv(v, ly.down, PRO_SILU_GATE, EPI_SCALE_RESIDUAL, v.gu, T, 2 * FF, v.x, VH, v.x, ly.mlp_scale, err,
+        hipLaunchKernelGGL(k_rmsnorm, dim3(T), dim3(BT), 0, s, v.xs, ly.ln1, VH, p.xf.rms_eps, v.xn);
+        VOC_TRY(run_conv(v, ly.qkv, PRO_NONE, EPI_BIAS, v.xn, T, VH, v.qkv, 3 * HDT, nullptr, nullptr, err, errlen));
+        if (p.xf.head_dim == 64)
+            hipLaunchKernelGGL(k_window_attention<64>, att_grid, dim3(BT), att_lds, s, v.qkv, nh, T, v.pos0, p.sliding_window,
+                               v.ring, v.invf, ly.kc, ly.vc, v.att);
+        else
+            hipLaunchKernelGGL(k_window_attention<128>, att_grid, dim3(BT), att_lds, s, v.qkv, nh, T, v.pos0,
+                               p.sliding_window, v.ring, v.invf, ly.kc, ly.vc, v.att);
+        VOC_TRY(run_conv(v, ly.o, PRO_NONE, EPI_SCALE_RESIDUAL, v.att, T, HDT, v.xs, VH, v.xs, ly.attn_scale, err, errlen));
+        hipLaunchKernelGGL(k_rmsnorm, dim3(T), dim3(BT), 0, s, v.xs, ly.ln2, VH, p.xf.rms_eps, v.xn);
+        VOC_TRY(run_conv(v, ly.gu, PRO_NONE, EPI_BIAS, v.xn, T, VH, v.gu, 2 * FF, nullptr, nullptr, err, errlen));
+        VOC_TRY(run_conv(v, ly.down, PRO_SILU_GATE, EPI_SCALE_RESIDUAL, v.gu, T, 2 * FF, v.xs, VH, v.xs, ly.mlp_scale, err,
                          errlen));
     }
-    hipLaunchKernelGGL(k_rmsnorm, dim3(T), dim3(BT), 0, s, v.x, v.final_norm, VH, p.xf.rms_eps, v.n);
-    VOC_TRY(run_conv(v, v.out_proj, PRO_NONE, EPI_BIAS, v.n, T, VH, v.u, L, nullptr, nullptr, err, errlen));
-    int R = T;
-    const float *src = v.u;
+    hipLaunchKernelGGL(k_rmsnorm, dim3(T), dim3(BT), 0, s, v.xs, v.final_norm, VH, p.xf.rms_eps, v.xn);
+    VOC_TRY(run_conv(v, v.out_proj, PRO_NONE, EPI_BIAS, v.xn, T, VH, v.post, L, nullptr, nullptr, err, errlen));
+    // two upsampling stages: transposed conv, then the ConvNeXt block in place on its output
+    int rows = T;
+    const float *stage_in = v.post;
     for (int j = 0; j < 2; ++j) {
-        float *dst = j == 0 ? v.A : v.B, *tmp = j == 0 ? v.B : v.A;
-        VOC_TRY(run_conv(v, v.up_conv[j], PRO_NONE, EPI_BIAS, src, R, L, dst, L, nullptr, nullptr, err, errlen));
-        R *= p.upsampling_ratios[j];
+        float *up = v.upx[j];
+        VOC_TRY(run_conv(v, v.up_conv[j], PRO_NONE, EPI_BIAS, stage_in, rows, L, up, L, nullptr, nullptr, err, errlen));
+        rows *= p.upsampling_ratios[j];
         ConvNeXt &cx = v.cnx[j];
-        hipLaunchKernelGGL(k_dwconv_ln, dim3(R), dim3(BT), 0, s, cx.dw, cx.dw_b, dst, cx.hist, L, cx.ln_w, cx.ln_b, 1e-6f, tmp);
-        const size_t nh = static_cast<size_t>(6) * L;
-        hipLaunchKernelGGL(k_hist_update, dim3(static_cast<unsigned>((nh + BT - 1) / BT)), dim3(BT), 0, s, cx.hist, dst, R, 6,
-                           L, L, cx.hist2);
+        hipLaunchKernelGGL(k_dw_ln<4>, dim3((rows + 3) / 4), dim3(BT), 0, s, up, cx.hist, cx.dwt, cx.dw_b, cx.ln_w, cx.ln_b,
+                           1e-6f, rows, v.lnx, cx.hist2);
         std::swap(cx.hist, cx.hist2);
-        VOC_TRY(run_conv(v, cx.pw1, PRO_NONE, EPI_GELU, tmp, R, L, v.G, 4 * L, nullptr, nullptr, err, errlen));
-        VOC_TRY(run_conv(v, cx.pw2, PRO_NONE, EPI_SCALE_RESIDUAL, v.G, R, 4 * L, dst, L, dst, cx.gamma, err, errlen));
-        src = dst;
+        VOC_TRY(run_conv(v, cx.pw1, PRO_NONE, EPI_GELU, v.lnx, rows, L, v.pwh, 4 * L, nullptr, nullptr, err, errlen));
+        VOC_TRY(run_conv(v, cx.pw2, PRO_NONE, EPI_SCALE_RESIDUAL, v.pwh, rows, 4 * L, up, L, up, cx.gamma, err, errlen));
+        stage_in = up;
     }
     // The Snake that starts every conv of the decoder blocks is applied once per element by the
-    // conv that produces its input (z output): dec0 -> block 0 up, up -> unit 0 conv1, conv1 ->
-    // conv2, conv2 -> next conv1 / next block's up / the final conv. P holds the residual stream,
-    // ZP its Snake for the next consumer, Q the Snake of conv1's output (conv1's raw output is not
-    // needed).
-    VOC_TRY(run_conv(v, v.dec0, PRO_NONE, EPI_BIAS, src, R, L, nullptr, v.DD, nullptr, nullptr, err, errlen, v.d,
+    // conv that produces its input (z output): dec0 -> block 0's transposed conv, that conv ->
+    // unit 0's first conv, a first conv -> its second, a second conv -> the next unit's first /
+    // the next block's transposed conv / the final conv. Only the Snake of a first conv's output
+    // is kept (its raw output is not read again).
+    VOC_TRY(run_conv(v, v.dec0, PRO_NONE, EPI_BIAS, stage_in, rows, L, nullptr, v.DD, nullptr, nullptr, err, errlen, v.dec_in,
                      &v.blocks[0].up));
-    const float *in = v.d;
-    int width = v.DD;
+    const float *blk_in = v.dec_in;
+    int ch = v.DD;
     for (int b = 0; b < 4; ++b) {
         Block &bk = v.blocks[b];
-        VOC_TRY(run_conv(v, bk.up, PRO_NONE, EPI_BIAS, in, R, width, v.P[b], bk.Cout, nullptr, nullptr, err, errlen, v.ZP[b],
-                         &bk.u[0].c1));
-        R *= bk.rate;
-        width = bk.Cout;
+        VOC_TRY(run_conv(v, bk.up, PRO_NONE, EPI_BIAS, blk_in, rows, ch, v.res[b], bk.Cout, nullptr, nullptr, err, errlen,
+                         v.res_s[b], &bk.u[0].c1));
+        rows *= bk.rate;
+        ch = bk.Cout;
         for (int k = 0; k < 3; ++k) {
             const Conv *next = k < 2 ? &bk.u[k + 1].c1 : b < 3 ? &v.blocks[b + 1].up : &v.final_conv;
-            VOC_TRY(run_conv(v, bk.u[k].c1, PRO_NONE, EPI_BIAS, v.ZP[b], R, width, nullptr, width, nullptr, nullptr, err,
-                             errlen, v.Q[b], &bk.u[k].c2));
-            VOC_TRY(run_conv(v, bk.u[k].c2, PRO_NONE, EPI_RESIDUAL, v.Q[b], R, width, v.P[b], width, v.P[b], nullptr, err,
-                             errlen, v.ZP[b], next));
+            VOC_TRY(run_conv(v, bk.u[k].c1, PRO_NONE, EPI_BIAS, v.res_s[b], rows, ch, nullptr, ch, nullptr, nullptr, err,
+                             errlen, v.mid_s[b], &bk.u[k].c2));
+            VOC_TRY(run_conv(v, bk.u[k].c2, PRO_NONE, EPI_RESIDUAL, v.mid_s[b], rows, ch, v.res[b], ch, v.res[b], nullptr, err,
+                             errlen, v.res_s[b], next));
         }
-        in = v.ZP[b];
+        blk_in = v.res_s[b];
     }
-    VOC_TRY(run_conv(v, v.final_conv, PRO_NONE, EPI_CLAMP, in, R, width, v.pcm16, 16, nullptr, nullptr, err, errlen));
-    hipLaunchKernelGGL(k_take_col0, dim3((R + BT - 1) / BT), dim3(BT), 0, s, v.pcm16, R, 16, v.pcm);
+    VOC_TRY(run_conv(v, v.final_conv, PRO_NONE, EPI_CLAMP, blk_in, rows, ch, v.pcm16, 16, nullptr, nullptr, err, errlen));
+    hipLaunchKernelGGL(k_take_col0, dim3((rows + BT - 1) / BT), dim3(BT), 0, s, v.pcm16, rows, 16, v.pcm);
     v.pos0 += T;
     NAVI_TRY_HIP(hipGetLastError(), err, errlen);
     return NAVI_OK;
@@ -539,7 +609,8 @@ navi_status navi_vocoder_create(const navi_vocoder_params *p, const navi_tensor_
     const int VH = xf.hidden, L = p->latent_dim, CD = p->codebook_dim, DD = p->decoder_dim, HDT = xf.n_head * xf.head_dim;
     int spf = p->upsampling_ratios[0] * p->upsampling_ratios[1];
     for (int b = 0; b < 4; ++b) spf *= p->upsample_rates[b];
-    bool ok = xf.n_head == xf.n_kv_head && xf.head_dim <= 128 && xf.head_dim % 2 == 0 && VH % 64 == 0 && L == 4 * BT &&
+    bool ok = xf.n_head == xf.n_kv_head && (xf.head_dim == 64 || xf.head_dim == 128) &&
+              attention_lds(p->sliding_window, xf.head_dim) <= 64 * 1024 && p->n_q <= 16 && VH % 64 == 0 && L == 4 * BT &&
               CD % 64 == 0 && DD % 64 == 0 && HDT % 64 == 0 && xf.ff % 64 == 0 && p->sliding_window >= 1 &&
               p->sliding_window <= 128 && spf == p->samples_per_frame && p->n_semantic == 1 && p->n_q >= 2 &&
               max_chunk_frames >= 1 && max_chunk_frames <= 4096;
@@ -698,7 +769,14 @@ navi_status navi_vocoder_create(const navi_vocoder_params *p, const navi_tensor_
         c.Cin = L; c.Cout = L; c.K = 1; c.phases = r;
         if ((st = tconv(w, L, L, r, r, c.w)) != NAVI_OK) return fail(st);
         ConvNeXt &cx = v->cnx[j];
-        VB(uint16_t, up + "1.dwconv.conv.weight", NAVI_DT_F16, L, 1, 7, cx.dw);
+        const uint16_t *dw = nullptr;
+        VB(uint16_t, up + "1.dwconv.conv.weight", NAVI_DT_F16, L, 1, 7, dw);
+        {
+            uint16_t *t_ = nullptr;
+            VA(t_, static_cast<size_t>(7) * L);
+            hipLaunchKernelGGL(k_tap_major, dim3((7 * L + BT - 1) / BT), dim3(BT), 0, s, dw, L, 7, t_);
+            cx.dwt = t_;
+        }
         VB(float, up + "1.dwconv.conv.bias", NAVI_DT_F32, L, 0, 0, cx.dw_b);
         VB(float, up + "1.norm.weight", NAVI_DT_F32, L, 0, 0, cx.ln_w);
         VB(float, up + "1.norm.bias", NAVI_DT_F32, L, 0, 0, cx.ln_b);
@@ -752,9 +830,9 @@ navi_status navi_vocoder_create(const navi_vocoder_params *p, const navi_tensor_
                 return fail(st);
         }
         rows *= bk.rate;
-        VA(v->P[b], rows * C * bk.Cout);
-        VA(v->Q[b], rows * C * bk.Cout);
-        VA(v->ZP[b], rows * C * bk.Cout);
+        VA(v->res[b], rows * C * bk.Cout);
+        VA(v->res_s[b], rows * C * bk.Cout);
+        VA(v->mid_s[b], rows * C * bk.Cout);
         width = bk.Cout;
     }
     {
@@ -784,20 +862,20 @@ navi_status navi_vocoder_create(const navi_vocoder_params *p, const navi_tensor_
     VA(v->invf, 64);
     VA(v->flag, 1);
     VA(v->d_codes, C * p->n_q);
-    VA(v->e, C * CD);
-    VA(v->h, C * CD);
-    VA(v->a, C * L);
-    VA(v->x, C * VH);
-    VA(v->n, C * VH);
+    VA(v->lat, C * CD);
+    VA(v->pre, C * L);
+    VA(v->xs, C * VH);
+    VA(v->xn, C * VH);
     VA(v->qkv, C * 3 * HDT);
     VA(v->att, C * HDT);
     VA(v->gu, C * 2 * xf.ff);
-    VA(v->u, C * L);
+    VA(v->post, C * L);
     const size_t up_rows = C * p->upsampling_ratios[0] * p->upsampling_ratios[1];
-    VA(v->A, up_rows * L);
-    VA(v->B, up_rows * L);
-    VA(v->G, up_rows * 4 * L);
-    VA(v->d, up_rows * DD);
+    VA(v->upx[0], C * p->upsampling_ratios[0] * L);
+    VA(v->upx[1], up_rows * L);
+    VA(v->lnx, up_rows * L);
+    VA(v->pwh, up_rows * 4 * L);
+    VA(v->dec_in, up_rows * DD);
     VA(v->pcm, C * p->samples_per_frame);
     VA(v->pcm16, C * p->samples_per_frame * 16);
     {
