@@ -40,7 +40,7 @@ typedef enum {
     NAVI_ERR_CANCELLED = 7       /* the PCM consumer stopped the request (navi_synth's callback) */
 } navi_status;
 
-/* ---- device (runtime/device/device.h:100-123) ---------------------------- */
+/* ---- device (runtime/device/device.h:43-66) ------------------------------ */
 
 typedef struct {
     int32_t index;
@@ -64,7 +64,7 @@ void *navi_device_stream(void);
 navi_status navi_device_synchronize(void);
 const char *navi_build_arch(void);    /* the offload arch the kernels were built for */
 
-/* ---- device memory (DeviceWeights arena, device_weights.cpp:245-299; Impl::alloc) */
+/* ---- device memory (DeviceWeights arena, device_weights.cpp:18-76; Impl::alloc) */
 
 navi_status navi_mem_alloc(void **dptr, size_t bytes);   /* zero-filled */
 navi_status navi_mem_free(void *dptr);
@@ -200,7 +200,7 @@ typedef struct {                       /* talker.h:26-32 Prompt: device rows own
     int32_t n_prefill, n_trailing;
 } navi_prompt;
 
-/* Talker::create (talker.hip:197-265): binds the talker's weights by name (text embedding,
+/* Talker::create (talker.hip:200-274): binds the talker's weights by name (text embedding,
  * text projection, layers, final norm, codec head, codec embedding), allocates the KV cache
  * (max_positions rows per layer, f16 [max_positions][kv_dim]) and the prompt/prefill work
  * buffers for up to max_prompt_tokens rows. */
@@ -218,15 +218,15 @@ navi_status navi_talker_build_prompt(navi_talker *t, const int32_t *ids, int32_t
  * 0..n_rows-1; writes KV rows 0..n_rows-1, keeps the last row's post-norm hidden and its
  * logits, and sets the cache's n_used to n_rows. */
 navi_status navi_talker_prefill(navi_talker *t, const float *d_rows, int32_t n_rows, char *err, size_t errlen);
-/* Talker::kv (talker.h:48): the cache as the view navi_frame_run takes; *n_used (may be NULL)
+/* Talker::kv (talker.h:57): the cache as the view navi_frame_run takes; *n_used (may be NULL)
  * is the number of rows the last prefill wrote. The pointer arrays live as long as t. */
 navi_status navi_talker_kv(navi_talker *t, navi_kv_view *out, int32_t *n_used);
 const float *navi_talker_hidden(const navi_talker *t);   /* Talker::d_hidden: f32[hidden] */
 const float *navi_talker_logits(const navi_talker *t);   /* Talker::d_logits: f32[vocab] */
 double navi_talker_last_ms(const navi_talker *t);         /* Talker::last_ms: device time of the last prefill */
 
-/* ---- linear layer (Talker::Impl::gemm, talker.hip:160-190; k_gemm_skinny / k_conv<K=1>,
- * kernels.h:255-330) ---------------------------------------------------------------------
+/* ---- linear layer (Talker::Impl::gemm, talker.hip:158-187; k_gemm_skinny / k_conv<K=1>,
+ * kernels.h:73-330) -----------------------------------------------------------------------
  * d_y[m][n] = act(bias[n] + sum_k d_x[m][k] * w[n][k]) + residual[m][n] for m < M, n < N.
  * d_x f32 rows with stride ldx, w f16 [N][K] row-major (nn.Linear layout), d_y f32 rows with
  * stride ldy. bias, residual may be NULL; residual may alias d_y. act: 0 none, 1 SiLU.
@@ -267,20 +267,33 @@ typedef struct {                       /* the codec decoder fields of params.h (
     int32_t samples_per_frame;         /* 1920 = the product of the ratios and rates */
 } navi_vocoder_params;
 
-/* Vocoder::create (vocoder.hip:465-600): binds the codec.decoder.* tensors by name, prepares
+/* Vocoder::create (vocoder.hip:427-602): binds the codec.decoder.* tensors by name, prepares
  * the device-side copies the kernels read (concatenated projections and codebooks, tap-major
  * conv weights, phase-split transposed convs, exp'd Snake parameters) and the streaming state
  * for chunks of up to max_chunk_frames frames. */
 navi_status navi_vocoder_create(const navi_vocoder_params *p, const navi_tensor_ref *tensors, int32_t n_tensors,
                                 int32_t max_chunk_frames, navi_vocoder **out, char *err, size_t errlen);
 void navi_vocoder_destroy(navi_vocoder *v);
-/* Vocoder::reset (vocoder.hip:611-623): a new utterance (clears the causal histories, position 0). */
+/* Vocoder::reset (vocoder.hip:604-615): a new utterance (clears the causal histories, position 0). */
 navi_status navi_vocoder_reset(navi_vocoder *v);
-/* Vocoder::decode (vocoder.hip:625-643): codes host i32 [n_frames][n_q] in [0, codebook_size),
+/* Vocoder::decode (vocoder.hip:617-636): codes host i32 [n_frames][n_q] in [0, codebook_size),
  * continuing the utterance; writes n_frames * samples_per_frame samples to host pcm (where
  * the reference appends to a vector). Decodes in chunks of max_chunk_frames; synchronous. */
 navi_status navi_vocoder_decode(navi_vocoder *v, const int32_t *codes, int32_t n_frames, float *pcm, char *err,
                                 size_t errlen);
+/* Vocoder::set_stage_hook (vocoder.h:46-48; vocoder.hip:180-185, 638): fn (NULL = off) is called
+ * after every stage of a chunk with the stage's name (the reference's names: "rvq", "pre_conv",
+ * "in_proj", "norm1_<l>", "qkv_<l>" (before RoPE), "attnraw<l>", "xattn_<l>", "layer<l>",
+ * "pre_transformer", "up<j>_t", "up<j>_ln", "up<j>_cnx", "dec0", "dec<b>_b1".."dec<b>_b4", "pcm")
+ * and its device buffer f32 [rows][cols], after the stream has drained; the buffer is valid
+ * during the call. For debugging: every stage then synchronizes. */
+typedef void (*navi_stage_fn)(void *user, const char *name, const float *d_buf, int32_t rows, int32_t cols);
+navi_status navi_vocoder_set_stage_hook(navi_vocoder *v, navi_stage_fn fn, void *user);
+/* vocoder_owns_tensor (vocoder.hip:413-425): whether DeviceWeights::upload may skip a tensor
+ * because the vocoder reads it from the file itself. Always 0 here: navi_vocoder_create makes
+ * its re-laid-out copies on the device from the arena, so the arena must hold every
+ * codec.decoder.* tensor. */
+int32_t navi_vocoder_owns_tensor(const char *name);
 int32_t navi_vocoder_samples_per_frame(const navi_vocoder *v);   /* Vocoder::samples_per_frame */
 int32_t navi_vocoder_max_chunk_frames(const navi_vocoder *v);    /* Vocoder::max_chunk_frames */
 double navi_vocoder_last_ms(const navi_vocoder *v);              /* Vocoder::last_ms: device time of the last decode */

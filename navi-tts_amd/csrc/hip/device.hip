@@ -1,6 +1,6 @@
 // Device selection and device memory behind the C ABI.
 // Device::open (runtime/device/device.cpp:77-108) and the DeviceWeights arena /
-// Impl::alloc helpers (device_weights.cpp:245-299, frame.hip:604-610) go through here.
+// Impl::alloc helpers (device_weights.cpp:18-76, frame.hip:604-610) go through here.
 #include "host_util.h"
 
 #include <cstring>

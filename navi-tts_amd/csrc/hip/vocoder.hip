@@ -319,6 +319,9 @@ struct navi_vocoder {
     // per decoder block: the residual stream, its Snake (the next conv's input) and the Snake of
     // each unit's first conv output
     float *res[4] = {}, *res_s[4] = {}, *mid_s[4] = {};
+    float *dec_raw = nullptr;          // dec0's output before its Snake: written only for the stage hook
+    navi_stage_fn hook = nullptr;      // debugging: called after every stage of a chunk
+    void *hook_user = nullptr;
     float *part = nullptr;             // K-split partial sums (conv_splits)
     size_t part_floats = 0;
     hipEvent_t ev0 = nullptr, ev1 = nullptr;
@@ -485,6 +488,16 @@ size_t attention_lds(int window, int head_dim) {
         if (s_ != NAVI_OK) return s_;         \
     } while (0)
 
+// The stage hook (Vocoder::set_stage_hook, vocoder.h:46-48): the device buffer of a finished stage,
+// after the stream has drained. The stage names are the reference's (vocoder.hip:267-341), which
+// its tools compare by.
+navi_status snap(navi_vocoder &v, const std::string &name, const float *buf, int rows, int cols, char *err, size_t errlen) {
+    if (!v.hook) return NAVI_OK;
+    NAVI_TRY_HIP(hipStreamSynchronize(device_state().stream), err, errlen);
+    v.hook(v.hook_user, name.c_str(), buf, rows, cols);
+    return NAVI_OK;
+}
+
 // One chunk of T frames: codes (already in v.d_codes) -> T * samples_per_frame PCM samples in v.pcm
 // (the stage order of decode_chunk, vocoder.hip:261-343, which is the model's).
 navi_status decode_chunk(navi_vocoder &v, int T, char *err, size_t errlen) {
@@ -493,27 +506,38 @@ navi_status decode_chunk(navi_vocoder &v, int T, char *err, size_t errlen) {
     const int VH = v.VH, L = v.L, HDT = v.HDT, FF = p.xf.ff, CD = v.CD, nh = p.xf.n_head;
     // RVQ front end and its two output projections, one conv gathering its rows from the codebooks
     VOC_TRY(run_conv(v, v.rvq_proj, PRO_RVQ, EPI_BIAS, nullptr, T, CD, v.lat, CD, nullptr, nullptr, err, errlen));
+    VOC_TRY(snap(v, "rvq", v.lat, T, CD, err, errlen));
     VOC_TRY(run_conv(v, v.pre_conv, PRO_NONE, EPI_BIAS, v.lat, T, CD, v.pre, L, nullptr, nullptr, err, errlen));
+    VOC_TRY(snap(v, "pre_conv", v.pre, T, L, err, errlen));
     VOC_TRY(run_conv(v, v.in_proj, PRO_NONE, EPI_BIAS, v.pre, T, L, v.xs, VH, nullptr, nullptr, err, errlen));
+    VOC_TRY(snap(v, "in_proj", v.xs, T, VH, err, errlen));
     const dim3 att_grid((T + 15) / 16, nh);
     const size_t att_lds = attention_lds(p.sliding_window, p.xf.head_dim);
-    for (TLayer &ly : v.layers) {
+    for (size_t li = 0; li < v.layers.size(); ++li) {
+        TLayer &ly = v.layers[li];
+        const std::string ls = std::to_string(li);
         hipLaunchKernelGGL(k_rmsnorm, dim3(T), dim3(BT), 0, s, v.xs, ly.ln1, VH, p.xf.rms_eps, v.xn);
+        VOC_TRY(snap(v, "norm1_" + ls, v.xn, T, VH, err, errlen));
         VOC_TRY(run_conv(v, ly.qkv, PRO_NONE, EPI_BIAS, v.xn, T, VH, v.qkv, 3 * HDT, nullptr, nullptr, err, errlen));
+        VOC_TRY(snap(v, "qkv_" + ls, v.qkv, T, 3 * HDT, err, errlen));
         if (p.xf.head_dim == 64)
             hipLaunchKernelGGL(k_window_attention<64>, att_grid, dim3(BT), att_lds, s, v.qkv, nh, T, v.pos0, p.sliding_window,
                                v.ring, v.invf, ly.kc, ly.vc, v.att);
         else
             hipLaunchKernelGGL(k_window_attention<128>, att_grid, dim3(BT), att_lds, s, v.qkv, nh, T, v.pos0,
                                p.sliding_window, v.ring, v.invf, ly.kc, ly.vc, v.att);
+        VOC_TRY(snap(v, "attnraw" + ls, v.att, T, HDT, err, errlen));
         VOC_TRY(run_conv(v, ly.o, PRO_NONE, EPI_SCALE_RESIDUAL, v.att, T, HDT, v.xs, VH, v.xs, ly.attn_scale, err, errlen));
+        VOC_TRY(snap(v, "xattn_" + ls, v.xs, T, VH, err, errlen));
         hipLaunchKernelGGL(k_rmsnorm, dim3(T), dim3(BT), 0, s, v.xs, ly.ln2, VH, p.xf.rms_eps, v.xn);
         VOC_TRY(run_conv(v, ly.gu, PRO_NONE, EPI_BIAS, v.xn, T, VH, v.gu, 2 * FF, nullptr, nullptr, err, errlen));
         VOC_TRY(run_conv(v, ly.down, PRO_SILU_GATE, EPI_SCALE_RESIDUAL, v.gu, T, 2 * FF, v.xs, VH, v.xs, ly.mlp_scale, err,
                          errlen));
+        VOC_TRY(snap(v, "layer" + ls, v.xs, T, VH, err, errlen));
     }
     hipLaunchKernelGGL(k_rmsnorm, dim3(T), dim3(BT), 0, s, v.xs, v.final_norm, VH, p.xf.rms_eps, v.xn);
     VOC_TRY(run_conv(v, v.out_proj, PRO_NONE, EPI_BIAS, v.xn, T, VH, v.post, L, nullptr, nullptr, err, errlen));
+    VOC_TRY(snap(v, "pre_transformer", v.post, T, L, err, errlen));
     // two upsampling stages: transposed conv, then the ConvNeXt block in place on its output
     int rows = T;
     const float *stage_in = v.post;
@@ -521,12 +545,16 @@ navi_status decode_chunk(navi_vocoder &v, int T, char *err, size_t errlen) {
         float *up = v.upx[j];
         VOC_TRY(run_conv(v, v.up_conv[j], PRO_NONE, EPI_BIAS, stage_in, rows, L, up, L, nullptr, nullptr, err, errlen));
         rows *= p.upsampling_ratios[j];
+        const std::string js = "up" + std::to_string(j);
+        VOC_TRY(snap(v, js + "_t", up, rows, L, err, errlen));
         ConvNeXt &cx = v.cnx[j];
         hipLaunchKernelGGL(k_dw_ln<4>, dim3((rows + 3) / 4), dim3(BT), 0, s, up, cx.hist, cx.dwt, cx.dw_b, cx.ln_w, cx.ln_b,
                            1e-6f, rows, v.lnx, cx.hist2);
         std::swap(cx.hist, cx.hist2);
+        VOC_TRY(snap(v, js + "_ln", v.lnx, rows, L, err, errlen));
         VOC_TRY(run_conv(v, cx.pw1, PRO_NONE, EPI_GELU, v.lnx, rows, L, v.pwh, 4 * L, nullptr, nullptr, err, errlen));
         VOC_TRY(run_conv(v, cx.pw2, PRO_NONE, EPI_SCALE_RESIDUAL, v.pwh, rows, 4 * L, up, L, up, cx.gamma, err, errlen));
+        VOC_TRY(snap(v, js + "_cnx", up, rows, L, err, errlen));
         stage_in = up;
     }
     // The Snake that starts every conv of the decoder blocks is applied once per element by the
@@ -534,8 +562,9 @@ navi_status decode_chunk(navi_vocoder &v, int T, char *err, size_t errlen) {
     // unit 0's first conv, a first conv -> its second, a second conv -> the next unit's first /
     // the next block's transposed conv / the final conv. Only the Snake of a first conv's output
     // is kept (its raw output is not read again).
-    VOC_TRY(run_conv(v, v.dec0, PRO_NONE, EPI_BIAS, stage_in, rows, L, nullptr, v.DD, nullptr, nullptr, err, errlen, v.dec_in,
-                     &v.blocks[0].up));
+    VOC_TRY(run_conv(v, v.dec0, PRO_NONE, EPI_BIAS, stage_in, rows, L, v.hook ? v.dec_raw : nullptr, v.DD, nullptr, nullptr, err,
+                     errlen, v.dec_in, &v.blocks[0].up));
+    VOC_TRY(snap(v, "dec0", v.dec_raw, rows, v.DD, err, errlen));
     const float *blk_in = v.dec_in;
     int ch = v.DD;
     for (int b = 0; b < 4; ++b) {
@@ -544,17 +573,21 @@ navi_status decode_chunk(navi_vocoder &v, int T, char *err, size_t errlen) {
                          v.res_s[b], &bk.u[0].c1));
         rows *= bk.rate;
         ch = bk.Cout;
+        const std::string bs = "dec" + std::to_string(b + 1) + "_b";
+        VOC_TRY(snap(v, bs + "1", v.res[b], rows, ch, err, errlen));
         for (int k = 0; k < 3; ++k) {
             const Conv *next = k < 2 ? &bk.u[k + 1].c1 : b < 3 ? &v.blocks[b + 1].up : &v.final_conv;
             VOC_TRY(run_conv(v, bk.u[k].c1, PRO_NONE, EPI_BIAS, v.res_s[b], rows, ch, nullptr, ch, nullptr, nullptr, err,
                              errlen, v.mid_s[b], &bk.u[k].c2));
             VOC_TRY(run_conv(v, bk.u[k].c2, PRO_NONE, EPI_RESIDUAL, v.mid_s[b], rows, ch, v.res[b], ch, v.res[b], nullptr, err,
                              errlen, v.res_s[b], next));
+            VOC_TRY(snap(v, bs + std::to_string(2 + k), v.res[b], rows, ch, err, errlen));
         }
         blk_in = v.res_s[b];
     }
     VOC_TRY(run_conv(v, v.final_conv, PRO_NONE, EPI_CLAMP, blk_in, rows, ch, v.pcm16, 16, nullptr, nullptr, err, errlen));
     hipLaunchKernelGGL(k_take_col0, dim3((rows + BT - 1) / BT), dim3(BT), 0, s, v.pcm16, rows, 16, v.pcm);
+    VOC_TRY(snap(v, "pcm", v.pcm, rows, 1, err, errlen));
     v.pos0 += T;
     NAVI_TRY_HIP(hipGetLastError(), err, errlen);
     return NAVI_OK;
@@ -876,6 +909,7 @@ navi_status navi_vocoder_create(const navi_vocoder_params *p, const navi_tensor_
     VA(v->lnx, up_rows * L);
     VA(v->pwh, up_rows * 4 * L);
     VA(v->dec_in, up_rows * DD);
+    VA(v->dec_raw, up_rows * DD);
     VA(v->pcm, C * p->samples_per_frame);
     VA(v->pcm16, C * p->samples_per_frame * 16);
     {
@@ -974,6 +1008,18 @@ navi_status navi_vocoder_decode(navi_vocoder *v, const int32_t *codes, int32_t n
         return NAVI_ERR_INVALID;
     }
     return NAVI_OK;
+}
+
+navi_status navi_vocoder_set_stage_hook(navi_vocoder *v, navi_stage_fn fn, void *user) {
+    if (!v) return NAVI_ERR_INVALID;
+    v->hook = fn;
+    v->hook_user = user;
+    return NAVI_OK;
+}
+
+int32_t navi_vocoder_owns_tensor(const char *name) {
+    (void) name;
+    return 0;   // every codec tensor is read from the weight arena; the re-laid-out copies are made on the device
 }
 
 int32_t navi_vocoder_samples_per_frame(const navi_vocoder *v) { return v ? v->p.samples_per_frame : 0; }

@@ -1,5 +1,5 @@
 // The reference's C++ request interface over this library's C ABI: navi::qwen3tts::Graph with
-// the signatures of model/qwen3tts/graph.h:23-84, so the HTTP server's paths
+// the signatures of model/qwen3tts/graph.h:23-79, so the HTTP server's paths
 // (runtime/server/server.cpp:401-437 speak / speak_stream, 770-788 warm_up) call it as they call
 // the reference. Header-only (C++20 for std::span, as the reference): the shared library keeps
 // exporting plain C.

@@ -3,7 +3,7 @@
 This is plumbing: it loads the in-tree libnavi_amd.so (and fails loudly when it
 is missing), declares the C structs, and wraps the handles the way the
 reference's C++ classes wrap their Impl: `DeviceWeights` (one device arena per
-`.navi`, device_weights.cpp:245-299), `KvCache` (talker.h:20-24) and `Frame`
+`.navi`, device_weights.cpp:18-76), `KvCache` (talker.h:20-24) and `Frame`
 (frame.h:46-71). Nothing here computes; every operation is a C ABI call.
 """
 from __future__ import annotations
@@ -32,6 +32,7 @@ EXPORTS = [
     "navi_talker_hidden", "navi_talker_logits", "navi_talker_last_ms", "navi_linear", "navi_linear_noalloc",
     "navi_vocoder_create", "navi_vocoder_destroy", "navi_vocoder_reset", "navi_vocoder_decode",
     "navi_vocoder_samples_per_frame", "navi_vocoder_max_chunk_frames", "navi_vocoder_last_ms", "navi_synth",
+    "navi_vocoder_set_stage_hook", "navi_vocoder_owns_tensor",
     "navi_streams_create", "navi_streams_destroy", "navi_streams_reset", "navi_streams_run", "navi_streams_step_out",
     "navi_streams_max_streams", "navi_streams_last_ms", "navi_streams_set_taps", "navi_streams_set_graphs",
     "navi_speaker_mel", "navi_speaker_create", "navi_speaker_destroy", "navi_speaker_embed_mel", "navi_speaker_embed",
@@ -131,6 +132,7 @@ class SynthStats(C.Structure):
 
 
 PCM_CALLBACK = C.CFUNCTYPE(C.c_int32, C.POINTER(C.c_float), C.c_int32, C.c_void_p)
+STAGE_CALLBACK = C.CFUNCTYPE(None, C.c_void_p, C.c_char_p, C.c_void_p, C.c_int32, C.c_int32)
 
 
 class Prompt(C.Structure):
@@ -204,6 +206,8 @@ def lib() -> C.CDLL:
     for f in ("navi_vocoder_samples_per_frame", "navi_vocoder_max_chunk_frames"):
         getattr(L, f).argtypes = [C.c_void_p]
     L.navi_vocoder_last_ms.argtypes = [C.c_void_p]
+    L.navi_vocoder_set_stage_hook.argtypes = [C.c_void_p, STAGE_CALLBACK, C.c_void_p]
+    L.navi_vocoder_owns_tensor.argtypes = [C.c_char_p]
     L.navi_vocoder_last_ms.restype = C.c_double
     L.navi_speaker_mel.argtypes = [C.POINTER(SpeakerParams), C.c_void_p, C.c_int64, C.c_void_p, C.c_int64,
                                    C.POINTER(C.c_int32), E, C.c_size_t]
@@ -306,7 +310,7 @@ ARENA_ALIGN = 256
 
 class DeviceWeights:
     """One device arena holding every selected tensor of a `.navi`
-    (DeviceWeights::upload, device_weights.cpp:245-299: 256-byte aligned, file order,
+    (DeviceWeights::upload, device_weights.cpp:18-76: 256-byte aligned, file order,
     `groups` placed adjacently)."""
 
     def __init__(self, path, select=None, groups=()):
@@ -742,6 +746,18 @@ class Vocoder:
 
     def last_ms(self) -> float:
         return lib().navi_vocoder_last_ms(self.h)
+
+    def set_stage_hook(self, fn):
+        """Vocoder::set_stage_hook: fn(name, host f32 [rows][cols]) after every stage (None = off)."""
+        if fn is None:
+            self._hook = None
+            _check(lib().navi_vocoder_set_stage_hook(self.h, STAGE_CALLBACK(), None), what="navi_vocoder_set_stage_hook")
+            return
+
+        def tramp(_user, name, d_buf, rows, cols):
+            fn(name.decode(), download(d_buf, np.float32, rows * cols).reshape(rows, cols))
+        self._hook = STAGE_CALLBACK(tramp)
+        _check(lib().navi_vocoder_set_stage_hook(self.h, self._hook, None), what="navi_vocoder_set_stage_hook")
 
 
 # ---- speaker encoder -------------------------------------------------------------------

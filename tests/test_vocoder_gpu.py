@@ -79,3 +79,44 @@ def test_bad_code_is_an_error(codec):
     with pytest.raises(abi.NaviError) as e:
         v.decode(codes)
     assert e.value.status == abi.NAVI_ERR_INVALID
+
+
+def test_stage_hook_stages_match_oracle(codec):
+    """Vocoder::set_stage_hook (vocoder.h:46-48): every stage of a chunk reaches the hook under the
+    reference's stage names, in the model's order; the stages compare one by one with the oracle's
+    intermediates (rel-RMS, the SNR bar's equivalent), and "pcm" is exactly what decode returns."""
+    abi, W, ora = codec
+    codes = np.random.default_rng(3).integers(0, 2048, (8, 16))
+    v = abi.Vocoder(W, max_chunk_frames=8)
+    got = {}
+    names = []
+
+    def hook(name, arr):
+        names.append(name)
+        got[name] = arr.copy()
+    v.set_stage_hook(hook)
+    pcm = v.decode(codes)
+    v.set_stage_hook(None)
+    L = len([n for n in names if n.startswith("layer")])
+    want_order = (["rvq", "pre_conv", "in_proj"]
+                  + sum([[f"norm1_{l}", f"qkv_{l}", f"attnraw{l}", f"xattn_{l}", f"layer{l}"] for l in range(L)], [])
+                  + ["pre_transformer"] + sum([[f"up{j}_t", f"up{j}_ln", f"up{j}_cnx"] for j in range(2)], [])
+                  + ["dec0"] + sum([[f"dec{b}_b{k}" for k in range(1, 5)] for b in range(1, 5)], []) + ["pcm"])
+    log(f"stage hook: {len(names)} stages, {L} transformer layers")
+    assert names == want_order
+    np.testing.assert_array_equal(got["pcm"][:, 0], pcm)
+    ostages = ora.stages(codes)
+    pairs = [("rvq", "rvq"), ("pre_conv", "pre_conv"), (f"layer{L - 1}", f"layer{L - 1}"),
+             ("pre_transformer", "pre_transformer"), ("up0_cnx", "up0"), ("up1_cnx", "up1"), ("dec0", "dec0")]
+    pairs += [(f"dec{b}_b4", f"block{b}") for b in range(1, 5)]
+    for dn, on in pairs:
+        a = np.asarray(got[dn], np.float64)
+        b = ostages[on].numpy().astype(np.float64)
+        assert a.shape == b.shape, (dn, a.shape, b.shape)
+        rel = np.sqrt(np.sum((a - b) ** 2) / max(np.sum(b ** 2), 1e-300))
+        log(f"  {dn:16s} vs oracle {on:16s}: rel-rms {rel:.2e}")
+        assert rel < 1e-3
+    # no hook: the same PCM, no callbacks
+    v.reset()
+    names.clear()
+    assert np.array_equal(v.decode(codes), pcm) and not names
