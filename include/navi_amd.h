@@ -62,6 +62,10 @@ navi_status navi_device_open(navi_device_info *out, char *err, size_t errlen);
 /* The library stream (hipStream_t) for callers that enqueue their own work. */
 void *navi_device_stream(void);
 navi_status navi_device_synchronize(void);
+/* Device::~Device (device.cpp:117-119): waits for the library stream and destroys it. Destroy
+ * every handle first. A host calls it before the process exits, while the HIP runtime (and any
+ * tool attached to it) is still up; a later call that needs the device opens it again. */
+navi_status navi_device_close(void);
 const char *navi_build_arch(void);    /* the offload arch the kernels were built for */
 
 /* ---- device memory (DeviceWeights arena, device_weights.cpp:18-76; Impl::alloc) */

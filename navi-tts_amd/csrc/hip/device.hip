@@ -88,6 +88,16 @@ navi_status navi_device_open(navi_device_info *out, char *err, size_t errlen) {
 
 void *navi_device_stream(void) { return device_state().stream; }
 
+navi_status navi_device_close(void) {
+    DeviceState &s = device_state();
+    if (!s.open) return NAVI_OK;
+    const hipError_t e = hipStreamSynchronize(s.stream);
+    const hipError_t e2 = hipStreamDestroy(s.stream);
+    s.stream = nullptr;
+    s.open = false;
+    return e == hipSuccess && e2 == hipSuccess ? NAVI_OK : NAVI_ERR_HIP;
+}
+
 navi_status navi_device_synchronize(void) {
     if (!device_state().open) return NAVI_OK;
     return hipStreamSynchronize(device_state().stream) == hipSuccess ? NAVI_OK : NAVI_ERR_HIP;

@@ -8,7 +8,9 @@ reference's C++ classes wrap their Impl: `DeviceWeights` (one device arena per
 """
 from __future__ import annotations
 
+import atexit
 import ctypes as C
+import weakref
 from pathlib import Path
 
 import numpy as np
@@ -22,7 +24,7 @@ LIB_PATH = Path(__file__).resolve().parent.parent / "lib" / "libnavi_amd.so"
 
 # The exported entry points include/navi_amd.h declares (checked by the CPU tests).
 EXPORTS = [
-    "navi_device_open", "navi_device_stream", "navi_device_synchronize", "navi_build_arch",
+    "navi_device_open", "navi_device_stream", "navi_device_synchronize", "navi_device_close", "navi_build_arch",
     "navi_mem_alloc", "navi_mem_free", "navi_mem_h2d", "navi_mem_d2h", "navi_mem_d2d", "navi_mem_zero",
     "navi_frame_create", "navi_frame_destroy", "navi_frame_reset", "navi_frame_run", "navi_frame_run_many", "navi_frame_step_out",
     "navi_frame_grid_blocks", "navi_frame_occupancy_per_mp", "navi_frame_set_taps", "navi_frame_tap_hidden",
@@ -253,6 +255,33 @@ def _check(st: int, err: C.Array | None = None, what: str = ""):
         raise NaviError(st, msg or what)
 
 
+# Every live handle and device buffer, released before the process exits (below).
+_live = weakref.WeakSet()
+
+
+def _track(obj):
+    _live.add(obj)
+    return obj
+
+
+@atexit.register
+def _release_all():
+    """Destroys every live handle, frees every device buffer and closes the library's device
+    (navi_device_close) while the interpreter shuts down: nothing of the library's is left for
+    the C runtime's exit handlers, which run after any tool attached to HIP (a profiler) has
+    finalised."""
+    if _lib is None:
+        return
+    objs = list(_live)
+    for o in objs:
+        if not isinstance(o, DeviceBuffer):
+            o.close()
+    for o in objs:
+        if isinstance(o, DeviceBuffer):
+            o.free()
+    _lib.navi_device_close()
+
+
 def device_open() -> DeviceInfo:
     info = DeviceInfo()
     err = C.create_string_buffer(256)
@@ -268,6 +297,7 @@ class DeviceBuffer:
         p = C.c_void_p()
         _check(lib().navi_mem_alloc(C.byref(p), self.nbytes), what="navi_mem_alloc")
         self.ptr = p.value
+        _track(self)
 
     def upload(self, arr: np.ndarray, offset: int = 0):
         a = np.ascontiguousarray(arr)
@@ -427,6 +457,7 @@ class Frame:
         _check(lib().navi_frame_create(C.byref(self.params), refs, len(refs), C.byref(opt), C.byref(h), err, 256), err)
         self.h = h.value
         self.hidden = self.params.talker.hidden
+        _track(self)
 
     def close(self):
         if self.h:
@@ -529,6 +560,7 @@ class Streams:
         self.h = h.value
         self.max_streams = max_streams
         self.hidden = self.params.talker.hidden
+        _track(self)
 
     def close(self):
         if self.h:
@@ -623,6 +655,7 @@ class Talker:
         v, n = KvView(), C.c_int32()
         _check(lib().navi_talker_kv(self.h, C.byref(v), C.byref(n)), what="navi_talker_kv")
         self.kv = TalkerKv(v, n.value)
+        _track(self)
 
     def close(self):
         if self.h:
@@ -722,6 +755,7 @@ class Vocoder:
         self.h = h.value
         self.samples_per_frame = lib().navi_vocoder_samples_per_frame(self.h)
         self.n_q = self.params.n_q
+        _track(self)
 
     def close(self):
         if self.h:
@@ -792,6 +826,7 @@ class Speaker:
         err = C.create_string_buffer(256)
         _check(lib().navi_speaker_create(C.byref(self.params), refs, len(refs), max_seconds, C.byref(h), err, 256), err)
         self.h = h.value
+        _track(self)
 
     def close(self):
         if self.h:
