@@ -74,9 +74,19 @@ def build_hip(jobs: int = 8) -> Path:
     return out
 
 
+def build_bench() -> Path:
+    """The hop-latency microbenchmark of the frame kernel's exchange primitive (a standalone program)."""
+    LIB.mkdir(parents=True, exist_ok=True)
+    out = LIB / "hop_latency"
+    _run([HIPCC, "-O3", "-std=c++17", f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+          "-o", str(out), str(PKG / "csrc" / "bench" / "hop_latency.hip")])
+    return out
+
+
 def build_all() -> None:
     build_randinit()
     build_hip()
+    build_bench()
 
 
 if __name__ == "__main__":

@@ -290,6 +290,36 @@ def test_frame_loop_matches_single_frames(sess):
     np.testing.assert_array_equal(sess.frame.step_out(), step_single)
 
 
+def test_frame_loop_matches_oracle_greedy(sess):
+    """navi_frame_run_many against the oracle directly (not only against single device frames):
+    8 greedy frames from the prefill, run as one on-device loop, give the oracle's codes frame for
+    frame, and the last step embedding is the oracle's bit for bit."""
+    import torch
+    from oracle import sampler as osamp
+    n = 8
+    s = sess.abi.Sampling.greedy(min_frames=n)
+    so = osamp.Sampling(temperature=0.0, cp_temperature=0.0, repetition_penalty=1.05, min_frames=n)
+    sess.frame.reset()
+    pad = sess.d_trail.ptr + 4 * 1024 * sess.n_trail
+    codes, eos, _ = sess.frame.run_many(sess.kv, sess.n_prefill - 1, sess.d_trail.ptr, sess.n_trail, pad, s, 4, 0, n,
+                                        skip_first=True, d_hidden=sess.d_hidden.ptr, d_logits=sess.d_logits.ptr)
+    assert not eos and codes.shape == (n, 16)
+    kvo = [(k.clone(), v.clone()) for k, v in sess.kv_o]
+    sess.ora.reset()
+    want, step = [], None
+    with torch.no_grad():
+        for i in range(n):
+            if i == 0:
+                c, step = sess.ora.frame(so, 4, 0, sess.trailing_host(0), hidden=sess.hidden, logits=sess.logits)
+            else:
+                c, step = sess.ora.frame(so, 4, i, sess.trailing_host(i), kv=kvo, n_past=sess.n_prefill + i - 1,
+                                         step_in=step)
+            want.append(c)
+    log(f"loop vs oracle: {n} frames, first {want[0][:4]}, last {want[-1][:4]}")
+    assert [list(c) for c in codes] == want
+    np.testing.assert_array_equal(sess.frame.step_out(), step)
+
+
 def test_frame_loop_stops_at_eos(sess):
     """A frame that samples EOS ends the loop on the device; it is the last row returned."""
     s = sess.abi.Sampling.greedy(min_frames=0)

@@ -75,3 +75,47 @@ def test_synth_reports_frame_errors(full_small):
     with pytest.raises(abi.NaviError) as e:
         abi.synth(talker, frame, voc, ids=ids, speaker=spk, max_frames=40, sampling=abi.Sampling.make(min_frames=40))
     assert "KV cache full" in str(e.value)
+
+
+def test_synth_matches_oracle_greedy(full_small):
+    """A whole request against the oracle (Graph::synth, graph.cpp:52-111, restated on the CPU):
+    prompt rows -> prefill -> greedy frames -> the codec decoder, streamed by navi_synth in batches
+    of 2 then 4 frames. The oracle runs the same request frame by frame and decodes its codes in
+    one shot; the PCM must reach the vocoder bar (SNR >= 40 dB), which also requires every code to
+    be the oracle's (one different code changes its frame's audio completely)."""
+    import torch
+    from navi_amd import abi
+    from oracle import sampler as osamp
+    from oracle.model import Oracle
+    from oracle.vocoder import Vocoder as OVoc
+    abi.device_open()
+    W = abi.DeviceWeights(full_small, select=lambda t: t.dtype != 4)
+    talker = abi.Talker(W, max_prompt_tokens=128, max_positions=256)
+    frame = abi.Frame(W)
+    voc = abi.Vocoder(W, max_chunk_frames=16)
+    ids = _ids(W.kv, 14, 21)
+    spk = np.random.default_rng(22).standard_normal(1024).astype(np.float32)
+    n = 12
+    st, pcm, sizes = abi.synth(talker, frame, voc, ids=ids, speaker=spk, seed=3, max_frames=n,
+                               sampling=abi.Sampling.greedy(min_frames=n), vocoder_batch=4, first_batch=2)
+    assert st.n_frames == n and sizes == [2 * 1920] + [4 * 1920] * 2 + [2 * 1920]
+    ora = Oracle(full_small)
+    pre, trail, pad = ora.build_prompt(ids, "english", spk)
+    kvo = ora.new_kv(64)
+    hid, lg = ora.prefill(pre, kvo)
+    so = osamp.Sampling(temperature=0.0, cp_temperature=0.0, repetition_penalty=1.05, min_frames=n)
+    ora.reset()
+    codes, step = [], None
+    with torch.no_grad():
+        for i in range(n):
+            th = trail[i] if i < trail.shape[0] else pad
+            if i == 0:
+                c, step = ora.frame(so, 3, 0, th, hidden=hid, logits=lg)
+            else:
+                c, step = ora.frame(so, 3, i, th, kv=kvo, n_past=pre.shape[0] + i - 1, step_in=step)
+            codes.append(c)
+    want = OVoc(full_small).decode(np.array(codes))
+    err = pcm.astype(np.float64) - want
+    snr = 10 * np.log10(np.sum(want.astype(np.float64) ** 2) / max(np.sum(err ** 2), 1e-300))
+    log(f"synth vs oracle request: {n} frames, first codes {codes[0][:4]}, PCM SNR {snr:.1f} dB")
+    assert pcm.shape == want.shape and snr >= 40.0
