@@ -149,11 +149,13 @@ def multistream(W, kv: dict, abi, steps: int = 12, warmup: int = 3, n_streams: i
                             "achieved_gbs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}}
 
 
-def streaming_and_vocoder(W, kv: dict, abi) -> dict:
+def streaming_and_vocoder(W, kv: dict, abi, parts=("prefill", "streaming", "vocoder")) -> dict:
     """BASELINE configs[2] (streaming utterance) through navi_synth and configs[3] (vocoder),
     plus the prefill times. The 128 text ids are prefilled with the prompt (130 rows: the
     reference layout's 10 rows + the first 120 trailing text rows; the last 8 text rows and
-    tts_eos stream as trailing rows), so the context grows to ~370 as the config states."""
+    tts_eos stream as trailing rows), so the context grows to ~370 as the config states.
+    `parts` selects what runs (a profiler run of one part)."""
+    prefill_roofline = prefill_roofline_for(kv)
     rng = np.random.default_rng(SEED)
     talker = abi.Talker(W, max_prompt_tokens=256, max_positions=512)
     frame = abi.Frame(W)
@@ -175,46 +177,89 @@ def streaming_and_vocoder(W, kv: dict, abi) -> dict:
     abi.lib().navi_mem_d2d(trail.ptr, pr.trailing + 4 * 1024 * 120, 4 * 1024 * (pr.n_trailing - 120))
     pad = abi.DeviceBuffer(4 * 1024)
     abi.lib().navi_mem_d2d(pad.ptr, pr.tts_pad, 4 * 1024)
+    out = {}
     pre_ms = {}
-    for n in (pr.n_prefill, n_pre):
+    for n in ((pr.n_prefill, n_pre) if "prefill" in parts else ()):
         t = []
         for _ in range(5):
             talker.prefill(rows.ptr, n)
             t.append(talker.last_ms())
         pre_ms[n] = float(np.median(t))
+    if "prefill" in parts:
+        out["prefill_ms"] = {"rows_10": round(pre_ms[pr.n_prefill], 3), "rows_130": round(pre_ms[n_pre], 3)}
+        out["prefill_roofline"] = {"bound": "hbm (weights once per prefill); MFMA work x2 for the hi/lo split",
+                                   "rows_10": prefill_roofline(pr.n_prefill, pre_ms[pr.n_prefill]),
+                                   "rows_130": prefill_roofline(n_pre, pre_ms[n_pre])}
+    if "streaming" in parts:
+        out["streaming"] = streaming(W, abi, talker, frame, rows, n_pre, trail, pr, pad, build_ms)
+    if "vocoder" in parts:
+        out["vocoder"] = vocoder_block(W, kv, abi, rng)
+    return out
+
+
+def prefill_roofline_for(kv: dict):
+    def prefill_roofline(T, ms):
+        """The prefill reads the talker weights once (the algorithmic bytes: layers + norms + head)
+        and does 2 x T x (layer MACs) + the head's row on the matrix cores (x2 for the hi/lo split
+        of the activations, which the matrix cores also execute)."""
+        H, Fd = kv["talker.hidden_size"], kv["talker.intermediate_size"]
+        Q = kv["talker.num_attention_heads"] * kv["talker.head_dim"]
+        KV = kv["talker.num_key_value_heads"] * kv["talker.head_dim"]
+        L = kv["talker.num_hidden_layers"]
+        macs = T * L * (H * (Q + 2 * KV) + Q * H + 3 * H * Fd) + H * kv["talker.vocab_size"]
+        b = algorithmic_bytes(kv, 0)
+        wbytes = b["talker"] + T * b["kv"]           # weights once + the T rows of K/V written
+        gbs = wbytes / (ms * 1e-3) / 1e9
+        tfl = 2 * 2 * macs / (ms * 1e-3) / 1e12
+        return {"rows": T, "ms": round(ms, 3), "bytes": int(wbytes), "achieved_gbs": round(gbs, 1),
+                "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "mfma_tflops": round(tfl, 2),
+                "mfma_frac": round(tfl / 2500.0, 5)}
+    return prefill_roofline
+
+
+def streaming(W, abi, talker, frame, rows, n_pre, trail, pr, pad, build_ms) -> dict:
+    """the 240-frame streaming utterance through navi_synth."""
     voc = abi.Vocoder(W, max_chunk_frames=32)
     s = abi.Sampling.make(min_frames=240)
     prompt = (rows.ptr, n_pre, trail.ptr, pr.n_trailing - 120, pad.ptr)
-    abi.synth(talker, frame, voc, prompt=prompt, seed=2, max_frames=16, sampling=s, vocoder_batch=16, first_batch=4)
+    # warm-up: the first batch and two full batches (both history parities of both chunk sizes)
+    abi.synth(talker, frame, voc, prompt=prompt, seed=2, max_frames=52, sampling=s, vocoder_batch=16, first_batch=4)
+    abi.synth(talker, frame, voc, prompt=prompt, seed=2, max_frames=52, sampling=s, vocoder_batch=16, first_batch=4)
     st, pcm, _ = abi.synth(talker, frame, voc, prompt=prompt, seed=2, max_frames=240, sampling=s, vocoder_batch=16,
                            first_batch=4)
+    return {"config": "configs[2]: 128 text ids prefilled (130 rows), speaker N(0,1), 240 frames, "
+                      "top-k 50, T 0.9, seed 2, first vocoder batch 4 then 16",
+            "ttfa_ms": round(st.ttfa_ms, 2), "prompt_build_ms": round(build_ms, 3),
+            # the reference's TTFA starts at the request, before the prompt rows exist
+            "ttfa_with_prompt_build_ms": round(st.ttfa_ms + build_ms, 2),
+            "rtf": round(st.rtf, 4), "total_ms": round(st.total_ms, 1),
+            "frames_ms_per_frame": round(st.frames_ms / max(st.n_frames, 1), 4),
+            "vocoder_ms": round(st.vocoder_ms, 2), "n_frames": st.n_frames, "audio_s": round(st.audio_s, 2)}
+
+
+def vocoder_block(W, kv: dict, abi, rng) -> dict:
+    """240 frames of codes U[0, 2048) in 16-frame chunks and as one block."""
     codes = rng.integers(0, 2048, (240, 16))
     v16 = abi.Vocoder(W, max_chunk_frames=16)
     v240 = abi.Vocoder(W, max_chunk_frames=240)
-    v16.decode(codes[:16])
-    v240.decode(codes[:16])
-    v16.reset()
-    v240.reset()
-    v16.decode(codes)
-    ms16 = v16.last_ms() / 240
+    # warm-up: every chunk size and history parity the timed decodes use (their graphs are captured)
+    v16.decode(codes[:32])
     v240.decode(codes)
-    ms240 = v240.last_ms() / 240
+    v240.decode(codes)
+    t16, t240 = [], []
+    for _ in range(3):
+        v16.reset()
+        v16.decode(codes)
+        t16.append(v16.last_ms() / 240)
+        v240.reset()
+        v240.decode(codes)
+        t240.append(v240.last_ms() / 240)
+    ms16, ms240 = float(np.median(t16)), float(np.median(t240))
     fl = vocoder_flops_per_frame(kv)
-    return {
-        "prefill_ms": {"rows_10": round(pre_ms[pr.n_prefill], 3), "rows_130": round(pre_ms[n_pre], 3)},
-        "streaming": {"config": "configs[2]: 128 text ids prefilled (130 rows), speaker N(0,1), 240 frames, "
-                                "top-k 50, T 0.9, seed 2, first vocoder batch 4 then 16",
-                      "ttfa_ms": round(st.ttfa_ms, 2), "prompt_build_ms": round(build_ms, 3),
-                      # the reference's TTFA starts at the request, before the prompt rows exist
-                      "ttfa_with_prompt_build_ms": round(st.ttfa_ms + build_ms, 2),
-                      "rtf": round(st.rtf, 4), "total_ms": round(st.total_ms, 1),
-                      "frames_ms_per_frame": round(st.frames_ms / max(st.n_frames, 1), 4),
-                      "vocoder_ms": round(st.vocoder_ms, 2), "n_frames": st.n_frames, "audio_s": round(st.audio_s, 2)},
-        "vocoder": {"config": "configs[3]: codes U[0,2048), 240 frames", "ms_per_frame_chunk16": round(ms16, 4),
-                    "ms_per_frame_block240": round(ms240, 4), "gflop_per_frame": round(fl / 1e9, 3),
-                    "tflops_block240": round(fl / (ms240 * 1e-3) / 1e12, 2),
-                    "mfma_frac_block240": round(fl / (ms240 * 1e-3) / 2.5e15, 5)},
-    }
+    return {"config": "configs[3]: codes U[0,2048), 240 frames", "ms_per_frame_chunk16": round(ms16, 4),
+            "ms_per_frame_block240": round(ms240, 4), "gflop_per_frame": round(fl / 1e9, 3),
+            "tflops_block240": round(fl / (ms240 * 1e-3) / 1e12, 2),
+            "mfma_frac_block240": round(fl / (ms240 * 1e-3) / 2.5e15, 5)}
 
 
 def speaker_flops_per_frame(kv: dict) -> float:
@@ -304,6 +349,8 @@ def main():
     ap.add_argument("--blob", default="", help="path for the random-init blob (default /dev/shm)")
     ap.add_argument("--keep-blob", action="store_true")
     ap.add_argument("--no-streaming", action="store_true", help="skip the prefill / streaming / vocoder extras")
+    ap.add_argument("--only", choices=("prefill", "streaming", "vocoder", "multistream", "speaker"), default="",
+                    help="run only this part (for a profiler run) and print its JSON instead of the bench line")
     ap.add_argument("--copy-calibration", type=float, default=0.0, metavar="GIB",
                     help="only run the counter-calibration copy kernel over GIB GiB and exit")
     args = ap.parse_args()
@@ -323,6 +370,18 @@ def main():
         make_blob(path)
         info = abi.device_open()
         W = abi.DeviceWeights(path, select=lambda t: t.dtype != 4)
+        if args.only:
+            kvd = W.kv
+            print(f"[bench] only {args.only}", flush=True, file=sys.stderr)
+            if args.only == "multistream":
+                part = multistream(W, kvd, abi)
+            elif args.only == "speaker":
+                part = speaker_encoder(W, kvd, abi)
+            else:
+                part = streaming_and_vocoder(W, kvd, abi, parts=(args.only,))
+            abi.lib().navi_device_synchronize()
+            print(json.dumps(part), flush=True)
+            return
         frame = abi.Frame(W)
         kvd = W.kv
         n_layer = kvd["talker.num_hidden_layers"]

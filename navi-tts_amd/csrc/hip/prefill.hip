@@ -566,6 +566,9 @@ struct navi_talker {
     float *prefill = nullptr, *trailing = nullptr, *pad_row = nullptr, *hidden = nullptr, *logits = nullptr;
     hipEvent_t ev0 = nullptr, ev1 = nullptr;
     double last_ms = 0;
+    // each row count's layer launches captured once as a HIP graph and replayed
+    std::vector<std::pair<int, hipGraphExec_t>> graphs;
+    bool use_graphs = true;
     std::vector<void *> owned;
 
     template <class T>
@@ -579,6 +582,7 @@ struct navi_talker {
     }
 
     ~navi_talker() {
+        for (auto &g : graphs) (void) hipGraphExecDestroy(g.second);
         if (ev0) (void) hipEventDestroy(ev0);
         if (ev1) (void) hipEventDestroy(ev1);
         for (void *p : owned) (void) hipFree(p);
@@ -832,6 +836,49 @@ navi_status navi_talker_build_prompt(navi_talker *t, const int32_t *ids, int32_t
     return NAVI_OK;
 }
 
+} // extern "C"
+
+namespace {
+
+// The prefill's kernels for T rows already in t.x: six launches per layer (q|k|v with the RMSNorm
+// fused -> q/k norms + RoPE + K/V store -> attention -> o (+ residual) -> gate|up with the RMSNorm
+// and SwiGLU fused -> down (+ residual); every projection one whole-K MFMA kernel, rows.h), then
+// the last row's final RMSNorm (the post-norm hidden the frame takes) and the codec head.
+void prefill_layers(navi_talker &t, int T, hipStream_t s) {
+    const int H = t.H, QKVW = t.QD + 2 * t.KVD;
+    const float scale = 1.f / std::sqrt(static_cast<float>(HD));
+    const size_t att_lds = static_cast<size_t>(2) * T * sizeof(float);
+    for (int l = 0; l < t.L; ++l) {
+        const LayerW &w = t.layers[l];
+        rows::launch_rows(rows::EPI_PLAIN, true, t.x, H, T, H, w.ln1, t.eps, w.wq, t.QD, w.wk, t.KVD, w.wv, t.KVD, t.part,
+                          QKVW, t.flag, s);
+        hipLaunchKernelGGL(k_qkv_finish, dim3(T), dim3(BT), QKVW * sizeof(float), s, t.part, 1, T, t.NQ, t.NKV, w.qn,
+                           w.kn, t.eps, t.invf, 0, t.q, t.kk[l], t.vv[l]);
+        if (T <= SHORT_KEYS)
+            hipLaunchKernelGGL(k_attn_prefill_short, dim3(T, t.NKV), dim3(BT), 0, s, t.q, t.kk[l], t.vv[l], t.NQ, t.NKV,
+                               0, scale, t.att);
+        else
+            hipLaunchKernelGGL(k_attn_prefill, dim3(T, t.NKV), dim3(BT), att_lds, s, t.q, t.kk[l], t.vv[l], t.NQ,
+                               t.NKV, 0, scale, t.att);
+        rows::launch_rows(rows::EPI_RESID, false, t.att, t.QD, T, t.QD, nullptr, 0.f, w.wo, H, nullptr, 0, nullptr, 0, t.x,
+                          H, t.flag, s);
+        rows::launch_rows(rows::EPI_SWIGLU, true, t.x, H, T, H, w.ln2, t.eps, w.wg, t.F, w.wu, t.F, nullptr, 0, t.h, t.F,
+                          t.flag, s);
+        rows::launch_rows(rows::EPI_RESID, false, t.h, t.F, T, t.F, nullptr, 0.f, w.wd, H, nullptr, 0, nullptr, 0, t.x, H,
+                          t.flag, s);
+    }
+    // the last row: final RMSNorm (the post-norm hidden the frame takes), then the codec head
+    float *last = t.xn + static_cast<size_t>(T - 1) * H;
+    hipLaunchKernelGGL(k_resid_norm, dim3(1), dim3(BT), 0, s, nullptr, 0, t.x + static_cast<size_t>(T - 1) * H,
+                       t.x + static_cast<size_t>(T - 1) * H, t.final_norm, t.eps, last, 1, H);
+    rows::launch_rows(rows::EPI_PLAIN, false, last, H, 1, H, nullptr, 0.f, t.head, t.V, nullptr, 0, nullptr, 0, t.logits, t.V,
+                      t.flag, s);
+}
+
+} // namespace
+
+extern "C" {
+
 navi_status navi_talker_prefill(navi_talker *t, const float *d_rows, int32_t n_rows, char *err, size_t errlen) {
     if (!t || !d_rows) {
         set_err(err, errlen, "talker: null argument");
@@ -841,43 +888,34 @@ navi_status navi_talker_prefill(navi_talker *t, const float *d_rows, int32_t n_r
         set_err(err, errlen, "talker: prefill of %d rows exceeds the prompt buffers or the KV cache", n_rows);
         return NAVI_ERR_INVALID;
     }
-    const int T = n_rows, H = t->H, QKVW = t->QD + 2 * t->KVD;
+    const int T = n_rows, H = t->H;
     hipStream_t s = device_state().stream;
     NAVI_TRY_HIP(hipMemsetAsync(t->flag, 0, 4, s), err, errlen);
     NAVI_TRY_HIP(hipEventRecord(t->ev0, s), err, errlen);
-    // Six launches per layer: q|k|v (RMSNorm fused) -> q/k norms + RoPE + K/V store -> attention
-    // -> o (+ residual) -> gate|up (RMSNorm and SwiGLU fused) -> down (+ residual); every
-    // projection one whole-K MFMA kernel (rows.h), no split-K partials.
     NAVI_TRY_HIP(hipMemcpyAsync(t->x, d_rows, static_cast<size_t>(T) * H * sizeof(float), hipMemcpyDeviceToDevice, s), err,
                  errlen);
-    const float scale = 1.f / std::sqrt(static_cast<float>(HD));
-    const size_t att_lds = static_cast<size_t>(2) * T * sizeof(float);
-    for (int l = 0; l < t->L; ++l) {
-        const LayerW &w = t->layers[l];
-        rows::launch_rows(rows::EPI_PLAIN, true, t->x, H, T, H, w.ln1, t->eps, w.wq, t->QD, w.wk, t->KVD, w.wv, t->KVD, t->part,
-                          QKVW, t->flag, s);
-        hipLaunchKernelGGL(k_qkv_finish, dim3(T), dim3(BT), QKVW * sizeof(float), s, t->part, 1, T, t->NQ, t->NKV, w.qn,
-                           w.kn, t->eps, t->invf, 0, t->q, t->kk[l], t->vv[l]);
-        if (T <= SHORT_KEYS)
-            hipLaunchKernelGGL(k_attn_prefill_short, dim3(T, t->NKV), dim3(BT), 0, s, t->q, t->kk[l], t->vv[l], t->NQ, t->NKV,
-                               0, scale, t->att);
-        else
-            hipLaunchKernelGGL(k_attn_prefill, dim3(T, t->NKV), dim3(BT), att_lds, s, t->q, t->kk[l], t->vv[l], t->NQ,
-                               t->NKV, 0, scale, t->att);
-        rows::launch_rows(rows::EPI_RESID, false, t->att, t->QD, T, t->QD, nullptr, 0.f, w.wo, H, nullptr, 0, nullptr, 0, t->x,
-                          H, t->flag, s);
-        rows::launch_rows(rows::EPI_SWIGLU, true, t->x, H, T, H, w.ln2, t->eps, w.wg, t->F, w.wu, t->F, nullptr, 0, t->h, t->F,
-                          t->flag, s);
-        rows::launch_rows(rows::EPI_RESID, false, t->h, t->F, T, t->F, nullptr, 0.f, w.wd, H, nullptr, 0, nullptr, 0, t->x, H,
-                          t->flag, s);
+    // The layers and the head: a launch sequence that depends only on T (every buffer is the
+    // handle's), so it is captured once per row count as a HIP graph and replayed.
+    if (t->use_graphs) {
+        hipGraphExec_t ex = nullptr;
+        for (auto &g : t->graphs)
+            if (g.first == T) ex = g.second;
+        if (!ex) {
+            NAVI_TRY_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal), err, errlen);
+            prefill_layers(*t, T, s);
+            hipGraph_t graph = nullptr;
+            NAVI_TRY_HIP(hipStreamEndCapture(s, &graph), err, errlen);
+            const hipError_t ei = hipGraphInstantiateWithFlags(&ex, graph, 0);
+            (void) hipGraphDestroy(graph);
+            NAVI_TRY_HIP(ei, err, errlen);
+            t->graphs.push_back({T, ex});
+        }
+        NAVI_TRY_HIP(hipGraphLaunch(ex, s), err, errlen);
+    } else {
+        prefill_layers(*t, T, s);
     }
-    // the last row: final RMSNorm (the post-norm hidden the frame takes), then the codec head
-    float *last = t->xn + static_cast<size_t>(T - 1) * H;
-    hipLaunchKernelGGL(k_resid_norm, dim3(1), dim3(BT), 0, s, nullptr, 0, t->x + static_cast<size_t>(T - 1) * H,
-                       t->x + static_cast<size_t>(T - 1) * H, t->final_norm, t->eps, last, 1, H);
-    NAVI_TRY_HIP(hipMemcpyAsync(t->hidden, last, H * 4, hipMemcpyDeviceToDevice, s), err, errlen);
-    rows::launch_rows(rows::EPI_PLAIN, false, last, H, 1, H, nullptr, 0.f, t->head, t->V, nullptr, 0, nullptr, 0, t->logits, t->V,
-                      t->flag, s);
+    NAVI_TRY_HIP(hipMemcpyAsync(t->hidden, t->xn + static_cast<size_t>(T - 1) * H, H * 4, hipMemcpyDeviceToDevice, s), err,
+                 errlen);
     NAVI_TRY_HIP(hipGetLastError(), err, errlen);
     NAVI_TRY_HIP(hipEventRecord(t->ev1, s), err, errlen);
     NAVI_TRY_HIP(hipEventSynchronize(t->ev1), err, errlen);
@@ -887,6 +925,12 @@ navi_status navi_talker_prefill(navi_talker *t, const float *d_rows, int32_t n_r
     const navi_status st = check_flag(*t, "prefill", err, errlen);
     if (st != NAVI_OK) return st;
     t->n_used = T;
+    return NAVI_OK;
+}
+
+navi_status navi_talker_set_graphs(navi_talker *t, int32_t enabled) {
+    if (!t) return NAVI_ERR_INVALID;
+    t->use_graphs = enabled != 0;
     return NAVI_OK;
 }
 

@@ -131,10 +131,11 @@ __global__ void __launch_bounds__(BT) k_dw_ln(const float *x, const float *hist,
 // with p_j read from lane j (readlane). The block also writes its rows' roped k and v to the ring
 // for later chunks: ring >= window + chunk, so no slot written here is one this launch reads.
 template <int HD>
-__global__ void __launch_bounds__(BT) k_window_attention(const float *qkv, int nh, int T, int pos0, int window, int ring,
+__global__ void __launch_bounds__(BT) k_window_attention(const float *qkv, int nh, int T, const int *pos0p, int window, int ring,
                                                          const float *invf, float *kc, float *vc, float *out) {
     constexpr int RT = 16, HALF = HD / 2, KS = HD + 1, DPL = HD / 64;   // K rows padded: lanes j read rows j
     extern __shared__ float sm[];
+    const int pos0 = gld(pos0p);                 // the chunk's first position (device-side: graph replays)
     const int HDT = nh * HD, ld = 3 * HDT, h = blockIdx.y;
     const int t0 = blockIdx.x * RT, t1 = min(T, t0 + RT);
     const int kp0 = max(0, pos0 + t0 - window + 1), nk = pos0 + t1 - kp0;
@@ -216,6 +217,11 @@ __global__ void __launch_bounds__(BT) k_window_attention(const float *qkv, int n
     }
 }
 
+// The utterance position after a chunk of T frames (the last kernel of a chunk).
+__global__ void k_advance_pos(int *pos0, int T) {
+    if (threadIdx.x == 0) gst(pos0, gld(pos0) + T);
+}
+
 // pcm[t] = y[t][0]: the last conv runs on the matrix cores with its one output channel padded to
 // a 16-column tile (15 zero weight rows); this keeps column 0.
 __global__ void __launch_bounds__(BT) k_take_col0(const float *y, int T, int ld, float *pcm) {
@@ -264,7 +270,8 @@ struct Conv {
     const float *sa = nullptr, *sb = nullptr;
     int Cin = 0, Cout = 0, K = 1, dil = 1, phases = 1, H = 0;
     int S = 1;                         // input-channel splits (fixed at create: conv_splits)
-    float *hist = nullptr, *hist2 = nullptr;
+    // the history pair: a chunk reads hbuf[parity] and writes the next chunk's into hbuf[parity ^ 1]
+    float *hbuf[2] = {};
 };
 
 struct TLayer {
@@ -276,7 +283,7 @@ struct TLayer {
 struct ConvNeXt {
     const uint16_t *dwt;               // depthwise weights, tap-major [7][C]
     const float *dw_b, *ln_w, *ln_b, *gamma;
-    float *hist, *hist2;               // the depthwise conv's 6 history rows (pair: read one, write the other)
+    float *hbuf[2];                    // the depthwise conv's 6 history rows (pair, as Conv::hbuf)
     Conv pw1, pw2;
 };
 
@@ -291,7 +298,12 @@ using namespace navi_amd::vc;
 
 struct navi_vocoder {
     navi_vocoder_params p{};
-    int cmax = 0, ring = 0, pos0 = 0, VH = 0, HDT = 0, L = 0, CD = 0, DD = 0;
+    int cmax = 0, ring = 0, VH = 0, HDT = 0, L = 0, CD = 0, DD = 0;
+    int parity = 0;                    // which buffer of every history pair the next chunk reads
+    int *d_pos0 = nullptr;             // the next chunk's first position (device)
+    // each chunk size's launch sequence captured once per history parity and replayed
+    std::vector<std::pair<std::pair<int, int>, hipGraphExec_t>> graphs;
+    bool use_graphs = true;
     const uint16_t *cb_first = nullptr;
     uint16_t *cb_rest = nullptr;
     Conv rvq_proj, pre_conv, in_proj, out_proj, dec0;
@@ -339,6 +351,7 @@ struct navi_vocoder {
     }
 
     ~navi_vocoder() {
+        for (auto &g : graphs) (void) hipGraphExecDestroy(g.second);
         if (ev0) (void) hipEventDestroy(ev0);
         if (ev1) (void) hipEventDestroy(ev1);
         for (void *v : owned) (void) hipFree(v);
@@ -453,10 +466,10 @@ navi_status run_conv(navi_vocoder &v, Conv &c, int pro, int epi, const float *x,
                      const float *res, const float *scale, char *err, size_t errlen, float *z = nullptr,
                      const Conv *zc = nullptr) {
     ConvArgs a{};
-    a.x = x; a.hist = c.hist; a.w = c.w; a.bias = c.bias; a.res = res; a.scale = scale;
+    a.x = x; a.hist = c.hbuf[v.parity]; a.w = c.w; a.bias = c.bias; a.res = res; a.scale = scale;
     a.y = y; a.z = z; a.flag = v.flag; a.ldx = ldx; a.ldy = ldy; a.T = T; a.Cin = c.Cin; a.Cout = c.Cout;
     a.dil = c.dil; a.phases = c.phases; a.lpad = (c.K - 1) * c.dil;   // causal
-    a.hnext = c.H > 0 ? c.hist2 : nullptr;
+    a.hnext = c.H > 0 ? c.hbuf[v.parity ^ 1] : nullptr;
     if (pro == PRO_RVQ) {
         a.codes = v.d_codes; a.cb0 = v.cb_first; a.cbr = v.cb_rest; a.nq = v.p.n_q; a.cbsize = v.p.codebook_size;
     }
@@ -473,7 +486,6 @@ navi_status run_conv(navi_vocoder &v, Conv &c, int pro, int epi, const float *x,
         const navi_status st = launch_generic(v, c, a, pro, epi, T, err, errlen);
         if (st != NAVI_OK) return st;
     }
-    if (c.H > 0) std::swap(c.hist, c.hist2);
     return NAVI_OK;
 }
 
@@ -521,10 +533,10 @@ navi_status decode_chunk(navi_vocoder &v, int T, char *err, size_t errlen) {
         VOC_TRY(run_conv(v, ly.qkv, PRO_NONE, EPI_BIAS, v.xn, T, VH, v.qkv, 3 * HDT, nullptr, nullptr, err, errlen));
         VOC_TRY(snap(v, "qkv_" + ls, v.qkv, T, 3 * HDT, err, errlen));
         if (p.xf.head_dim == 64)
-            hipLaunchKernelGGL(k_window_attention<64>, att_grid, dim3(BT), att_lds, s, v.qkv, nh, T, v.pos0, p.sliding_window,
-                               v.ring, v.invf, ly.kc, ly.vc, v.att);
+            hipLaunchKernelGGL(k_window_attention<64>, att_grid, dim3(BT), att_lds, s, v.qkv, nh, T, v.d_pos0,
+                               p.sliding_window, v.ring, v.invf, ly.kc, ly.vc, v.att);
         else
-            hipLaunchKernelGGL(k_window_attention<128>, att_grid, dim3(BT), att_lds, s, v.qkv, nh, T, v.pos0,
+            hipLaunchKernelGGL(k_window_attention<128>, att_grid, dim3(BT), att_lds, s, v.qkv, nh, T, v.d_pos0,
                                p.sliding_window, v.ring, v.invf, ly.kc, ly.vc, v.att);
         VOC_TRY(snap(v, "attnraw" + ls, v.att, T, HDT, err, errlen));
         VOC_TRY(run_conv(v, ly.o, PRO_NONE, EPI_SCALE_RESIDUAL, v.att, T, HDT, v.xs, VH, v.xs, ly.attn_scale, err, errlen));
@@ -548,9 +560,8 @@ navi_status decode_chunk(navi_vocoder &v, int T, char *err, size_t errlen) {
         const std::string js = "up" + std::to_string(j);
         VOC_TRY(snap(v, js + "_t", up, rows, L, err, errlen));
         ConvNeXt &cx = v.cnx[j];
-        hipLaunchKernelGGL(k_dw_ln<4>, dim3((rows + 3) / 4), dim3(BT), 0, s, up, cx.hist, cx.dwt, cx.dw_b, cx.ln_w, cx.ln_b,
-                           1e-6f, rows, v.lnx, cx.hist2);
-        std::swap(cx.hist, cx.hist2);
+        hipLaunchKernelGGL(k_dw_ln<4>, dim3((rows + 3) / 4), dim3(BT), 0, s, up, cx.hbuf[v.parity], cx.dwt, cx.dw_b, cx.ln_w,
+                           cx.ln_b, 1e-6f, rows, v.lnx, cx.hbuf[v.parity ^ 1]);
         VOC_TRY(snap(v, js + "_ln", v.lnx, rows, L, err, errlen));
         VOC_TRY(run_conv(v, cx.pw1, PRO_NONE, EPI_GELU, v.lnx, rows, L, v.pwh, 4 * L, nullptr, nullptr, err, errlen));
         VOC_TRY(run_conv(v, cx.pw2, PRO_NONE, EPI_SCALE_RESIDUAL, v.pwh, rows, 4 * L, up, L, up, cx.gamma, err, errlen));
@@ -588,8 +599,41 @@ navi_status decode_chunk(navi_vocoder &v, int T, char *err, size_t errlen) {
     VOC_TRY(run_conv(v, v.final_conv, PRO_NONE, EPI_CLAMP, blk_in, rows, ch, v.pcm16, 16, nullptr, nullptr, err, errlen));
     hipLaunchKernelGGL(k_take_col0, dim3((rows + BT - 1) / BT), dim3(BT), 0, s, v.pcm16, rows, 16, v.pcm);
     VOC_TRY(snap(v, "pcm", v.pcm, rows, 1, err, errlen));
-    v.pos0 += T;
+    hipLaunchKernelGGL(k_advance_pos, dim3(1), dim3(64), 0, s, v.d_pos0, T);
     NAVI_TRY_HIP(hipGetLastError(), err, errlen);
+    return NAVI_OK;
+}
+
+// A chunk: its launch sequence depends only on T and the history parity (every pointer and split
+// count is fixed at create, the position lives on the device), so it is captured once per
+// (T, parity) as a HIP graph and replayed; with the stage hook on, it runs eagerly.
+navi_status run_chunk(navi_vocoder &v, int T, char *err, size_t errlen) {
+    hipStream_t s = device_state().stream;
+    if (!v.use_graphs || v.hook) {
+        VOC_TRY(decode_chunk(v, T, err, errlen));
+    } else {
+        const std::pair<int, int> key{T, v.parity};
+        hipGraphExec_t ex = nullptr;
+        for (auto &g : v.graphs)
+            if (g.first == key) ex = g.second;
+        if (!ex) {
+            NAVI_TRY_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal), err, errlen);
+            const navi_status st = decode_chunk(v, T, err, errlen);
+            hipGraph_t graph = nullptr;
+            const hipError_t ec = hipStreamEndCapture(s, &graph);
+            if (st != NAVI_OK) {
+                if (graph) (void) hipGraphDestroy(graph);
+                return st;
+            }
+            NAVI_TRY_HIP(ec, err, errlen);
+            const hipError_t ei = hipGraphInstantiateWithFlags(&ex, graph, 0);
+            (void) hipGraphDestroy(graph);
+            NAVI_TRY_HIP(ei, err, errlen);
+            v.graphs.push_back({key, ex});
+        }
+        NAVI_TRY_HIP(hipGraphLaunch(ex, s), err, errlen);
+    }
+    v.parity ^= 1;
     return NAVI_OK;
 }
 
@@ -710,8 +754,8 @@ navi_status navi_vocoder_create(const navi_vocoder_params *p, const navi_tensor_
     auto hist = [&](Conv &c) -> navi_status {
         c.H = (c.K - 1) * c.dil;
         if (c.H == 0) return NAVI_OK;
-        navi_status s_ = v->alloc(c.hist, static_cast<size_t>(c.H) * c.Cin, err, errlen);
-        if (s_ == NAVI_OK) s_ = v->alloc(c.hist2, static_cast<size_t>(c.H) * c.Cin, err, errlen);
+        navi_status s_ = v->alloc(c.hbuf[0], static_cast<size_t>(c.H) * c.Cin, err, errlen);
+        if (s_ == NAVI_OK) s_ = v->alloc(c.hbuf[1], static_cast<size_t>(c.H) * c.Cin, err, errlen);
         return s_;
     };
     // RVQ front end: codebooks (rest concatenated) and the two output projections as one [CD][CD]
@@ -820,8 +864,8 @@ navi_status navi_vocoder_create(const navi_vocoder_params *p, const navi_tensor_
         VB(float, up + "1.pwconv2.bias", NAVI_DT_F32, L, 0, 0, cx.pw2.bias);
         cx.pw1.Cin = L; cx.pw1.Cout = 4 * L;
         cx.pw2.Cin = 4 * L; cx.pw2.Cout = L;
-        VA(cx.hist, static_cast<size_t>(6) * L);
-        VA(cx.hist2, static_cast<size_t>(6) * L);
+        VA(cx.hbuf[0], static_cast<size_t>(6) * L);
+        VA(cx.hbuf[1], static_cast<size_t>(6) * L);
     }
     {
         const uint16_t *w = nullptr;
@@ -894,6 +938,7 @@ navi_status navi_vocoder_create(const navi_vocoder_params *p, const navi_tensor_
     for (int i = 0; i < xf.head_dim / 2; ++i) invf[i] = static_cast<float>(1.0 / std::pow(xf.rope_theta, (2.0 * i) / xf.head_dim));
     VA(v->invf, 64);
     VA(v->flag, 1);
+    VA(v->d_pos0, 1);
     VA(v->d_codes, C * p->n_q);
     VA(v->lat, C * CD);
     VA(v->pre, C * L);
@@ -959,11 +1004,11 @@ void navi_vocoder_destroy(navi_vocoder *v) {
 navi_status navi_vocoder_reset(navi_vocoder *v) {
     if (!v) return NAVI_ERR_INVALID;
     hipStream_t s = device_state().stream;
-    v->pos0 = 0;
     auto zero = [&](float *ptr, size_t n) { return !ptr || hipMemsetAsync(ptr, 0, n * sizeof(float), s) == hipSuccess; };
-    auto zc = [&](Conv &c) { return zero(c.hist, static_cast<size_t>(c.H) * c.Cin) && zero(c.hist2, static_cast<size_t>(c.H) * c.Cin); };
+    auto zc = [&](Conv &c) { return zero(c.hbuf[0], static_cast<size_t>(c.H) * c.Cin) && zero(c.hbuf[1], static_cast<size_t>(c.H) * c.Cin); };
     bool ok = zc(v->pre_conv) && zc(v->dec0) && zc(v->final_conv);
-    for (int j = 0; j < 2; ++j) ok = ok && zero(v->cnx[j].hist, 6 * static_cast<size_t>(v->L)) && zero(v->cnx[j].hist2, 6 * static_cast<size_t>(v->L));
+    ok = ok && hipMemsetAsync(v->d_pos0, 0, sizeof(int), s) == hipSuccess;
+    for (int j = 0; j < 2; ++j) ok = ok && zero(v->cnx[j].hbuf[0], 6 * static_cast<size_t>(v->L)) && zero(v->cnx[j].hbuf[1], 6 * static_cast<size_t>(v->L));
     for (Block &b : v->blocks) {
         ok = ok && zc(b.up);
         for (Unit &u : b.u) ok = ok && zc(u.c1);
@@ -991,7 +1036,7 @@ navi_status navi_vocoder_decode(navi_vocoder *v, const int32_t *codes, int32_t n
         const int T = std::min(v->cmax, n_frames - f0);
         NAVI_TRY_HIP(hipMemcpyAsync(v->d_codes, codes + static_cast<size_t>(f0) * nq, static_cast<size_t>(T) * nq * 4,
                                     hipMemcpyHostToDevice, s), err, errlen);
-        const navi_status st = decode_chunk(*v, T, err, errlen);
+        const navi_status st = run_chunk(*v, T, err, errlen);
         if (st != NAVI_OK) return st;
         NAVI_TRY_HIP(hipMemcpyAsync(pcm + static_cast<size_t>(f0) * spf, v->pcm, static_cast<size_t>(T) * spf * 4,
                                     hipMemcpyDeviceToHost, s), err, errlen);
@@ -1007,6 +1052,12 @@ navi_status navi_vocoder_decode(navi_vocoder *v, const int32_t *codes, int32_t n
         set_err(err, errlen, "vocoder: an activation is outside the f16 range (|x| >= 65504 or NaN)");
         return NAVI_ERR_INVALID;
     }
+    return NAVI_OK;
+}
+
+navi_status navi_vocoder_set_graphs(navi_vocoder *v, int32_t enabled) {
+    if (!v) return NAVI_ERR_INVALID;
+    v->use_graphs = enabled != 0;
     return NAVI_OK;
 }
 

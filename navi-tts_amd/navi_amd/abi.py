@@ -31,10 +31,10 @@ EXPORTS = [
     "navi_frame_tap_logits", "navi_frame_tap_cp_logits", "navi_frame_set_profile", "navi_frame_profile",
     "navi_frame_set_epoch", "navi_frame_epoch", "navi_frame_set_spin_cap",
     "navi_talker_create", "navi_talker_destroy", "navi_talker_build_prompt", "navi_talker_prefill", "navi_talker_kv",
-    "navi_talker_hidden", "navi_talker_logits", "navi_talker_last_ms", "navi_linear", "navi_linear_noalloc",
+    "navi_talker_hidden", "navi_talker_logits", "navi_talker_last_ms", "navi_talker_set_graphs", "navi_linear", "navi_linear_noalloc",
     "navi_vocoder_create", "navi_vocoder_destroy", "navi_vocoder_reset", "navi_vocoder_decode",
     "navi_vocoder_samples_per_frame", "navi_vocoder_max_chunk_frames", "navi_vocoder_last_ms", "navi_synth",
-    "navi_vocoder_set_stage_hook", "navi_vocoder_owns_tensor",
+    "navi_vocoder_set_stage_hook", "navi_vocoder_owns_tensor", "navi_vocoder_set_graphs",
     "navi_streams_create", "navi_streams_destroy", "navi_streams_reset", "navi_streams_run", "navi_streams_step_out",
     "navi_streams_max_streams", "navi_streams_last_ms", "navi_streams_set_taps", "navi_streams_set_graphs",
     "navi_speaker_mel", "navi_speaker_create", "navi_speaker_destroy", "navi_speaker_embed_mel", "navi_speaker_embed",
@@ -186,6 +186,7 @@ def lib() -> C.CDLL:
     for f in ("navi_frame_tap_hidden", "navi_frame_tap_logits", "navi_frame_tap_cp_logits"):
         getattr(L, f).argtypes = [C.c_void_p]
         getattr(L, f).restype = C.c_void_p
+    L.navi_talker_set_graphs.argtypes = [C.c_void_p, C.c_int32]
     L.navi_talker_create.argtypes = [C.POINTER(ModelParams), C.POINTER(TensorRef), C.c_int32, C.c_int32, C.c_int32,
                                      C.POINTER(C.c_void_p), E, C.c_size_t]
     L.navi_talker_destroy.argtypes = [C.c_void_p]
@@ -210,6 +211,7 @@ def lib() -> C.CDLL:
     L.navi_vocoder_last_ms.argtypes = [C.c_void_p]
     L.navi_vocoder_set_stage_hook.argtypes = [C.c_void_p, STAGE_CALLBACK, C.c_void_p]
     L.navi_vocoder_owns_tensor.argtypes = [C.c_char_p]
+    L.navi_vocoder_set_graphs.argtypes = [C.c_void_p, C.c_int32]
     L.navi_vocoder_last_ms.restype = C.c_double
     L.navi_speaker_mel.argtypes = [C.POINTER(SpeakerParams), C.c_void_p, C.c_int64, C.c_void_p, C.c_int64,
                                    C.POINTER(C.c_int32), E, C.c_size_t]
@@ -668,6 +670,9 @@ class Talker:
         except Exception:
             pass
 
+    def set_graphs(self, on: bool):
+        _check(lib().navi_talker_set_graphs(self.h, 1 if on else 0), what="navi_talker_set_graphs")
+
     def language_id(self, language: str) -> int:
         if language in ("", "auto"):
             return -1
@@ -780,6 +785,9 @@ class Vocoder:
 
     def last_ms(self) -> float:
         return lib().navi_vocoder_last_ms(self.h)
+
+    def set_graphs(self, on: bool):
+        _check(lib().navi_vocoder_set_graphs(self.h, 1 if on else 0), what="navi_vocoder_set_graphs")
 
     def set_stage_hook(self, fn):
         """Vocoder::set_stage_hook: fn(name, host f32 [rows][cols]) after every stage (None = off)."""

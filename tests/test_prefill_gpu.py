@@ -199,3 +199,34 @@ def test_device_prompt_prefill_frames_match_oracle(abi, side):
         assert r.ok, r.error
         log(f"  frame {i}: gpu {list(r.codes)[:6]}... oracle {c[:6]}...")
         assert list(r.codes) == c
+
+
+@pytest.mark.parametrize("T", [10, 130])
+def test_prefill_graph_replays_match_eager(abi, side, T):
+    """Prefills replayed from the captured graph (the default) give bit for bit the hidden, logits
+    and K/V rows of prefills whose kernels the host launches one by one; three replays, each
+    with an eager prefill of other rows and a synchronisation in between."""
+    rng = np.random.default_rng(100 + T)
+    rows = rng.standard_normal((T, 1024)).astype(np.float32)
+    other = rng.standard_normal((T, 1024)).astype(np.float32)
+    d, d2 = abi.DeviceBuffer(rows.nbytes), abi.DeviceBuffer(other.nbytes)
+    d.upload(rows)
+    d2.upload(other)
+
+    def run(graphs, buf):
+        side.talker.set_graphs(graphs)
+        side.talker.prefill(buf.ptr, T)
+        hid, lg = side.talker.hidden_logits()
+        kv = [side.talker.kv.read(l, T) for l in range(side.ora.tp.n_layer)]
+        return hid.copy(), lg.copy(), kv
+    want = run(False, d)
+    for rep in range(3):
+        got = run(True, d)
+        np.testing.assert_array_equal(got[0], want[0])
+        np.testing.assert_array_equal(got[1], want[1])
+        for (gk, gv), (wk, wv) in zip(got[2], want[2]):
+            np.testing.assert_array_equal(gk, wk)
+            np.testing.assert_array_equal(gv, wv)
+        run(False, d2)                                   # eager work between the replays
+    side.talker.set_graphs(True)
+    log(f"prefill T={T}: 3 graph replays == eager")
