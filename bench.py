@@ -222,7 +222,7 @@ def streaming(W, abi, talker, frame, rows, n_pre, trail, pr, pad, build_ms) -> d
     voc = abi.Vocoder(W, max_chunk_frames=32)
     s = abi.Sampling.make(min_frames=240)
     prompt = (rows.ptr, n_pre, trail.ptr, pr.n_trailing - 120, pad.ptr)
-    # warm-up: the first batch and two full batches (both history parities of both chunk sizes)
+    # warm-up: the first batch and full batches of both chunk sizes
     abi.synth(talker, frame, voc, prompt=prompt, seed=2, max_frames=52, sampling=s, vocoder_batch=16, first_batch=4)
     abi.synth(talker, frame, voc, prompt=prompt, seed=2, max_frames=52, sampling=s, vocoder_batch=16, first_batch=4)
     st, pcm, _ = abi.synth(talker, frame, voc, prompt=prompt, seed=2, max_frames=240, sampling=s, vocoder_batch=16,
@@ -242,7 +242,7 @@ def vocoder_block(W, kv: dict, abi, rng) -> dict:
     codes = rng.integers(0, 2048, (240, 16))
     v16 = abi.Vocoder(W, max_chunk_frames=16)
     v240 = abi.Vocoder(W, max_chunk_frames=240)
-    # warm-up: every chunk size and history parity the timed decodes use (their graphs are captured)
+    # warm-up: both chunk sizes
     v16.decode(codes[:32])
     v240.decode(codes)
     v240.decode(codes)

@@ -222,9 +222,9 @@ navi_status navi_talker_build_prompt(navi_talker *t, const int32_t *ids, int32_t
  * 0..n_rows-1; writes KV rows 0..n_rows-1, keeps the last row's post-norm hidden and its
  * logits, and sets the cache's n_used to n_rows. */
 navi_status navi_talker_prefill(navi_talker *t, const float *d_rows, int32_t n_rows, char *err, size_t errlen);
-/* The prefill's layers for each row count are captured once as a HIP graph and replayed (on by
- * default); enabled = 0 launches every kernel from the host. Results are identical either way.
- * No reference counterpart. */
+/* enabled != 0: the prefill's layers for each row count are captured once as a HIP graph and
+ * replayed; 0 (the default): every kernel is launched from the host (on MI355X the replays measured
+ * no faster). Results are identical either way. No reference counterpart. */
 navi_status navi_talker_set_graphs(navi_talker *t, int32_t enabled);
 /* Talker::kv (talker.h:57): the cache as the view navi_frame_run takes; *n_used (may be NULL)
  * is the number of rows the last prefill wrote. The pointer arrays live as long as t. */
@@ -297,9 +297,10 @@ navi_status navi_vocoder_decode(navi_vocoder *v, const int32_t *codes, int32_t n
  * during the call. For debugging: every stage then synchronizes. */
 typedef void (*navi_stage_fn)(void *user, const char *name, const float *d_buf, int32_t rows, int32_t cols);
 navi_status navi_vocoder_set_stage_hook(navi_vocoder *v, navi_stage_fn fn, void *user);
-/* Each chunk size's launch sequence is captured once per history parity as a HIP graph and
- * replayed (on by default; the stage hook always runs eagerly). enabled = 0 launches every kernel
- * from the host instead; the PCM is identical either way. No reference counterpart. */
+/* enabled != 0: each chunk size's launch sequence is captured once per history parity as a HIP
+ * graph and replayed (the stage hook always runs eagerly); 0 (the default): every kernel is
+ * launched from the host (on MI355X the replays measured no faster). The PCM is identical either
+ * way. No reference counterpart. */
 navi_status navi_vocoder_set_graphs(navi_vocoder *v, int32_t enabled);
 /* vocoder_owns_tensor (vocoder.hip:413-425): whether DeviceWeights::upload may skip a tensor
  * because the vocoder reads it from the file itself. Always 0 here: navi_vocoder_create makes

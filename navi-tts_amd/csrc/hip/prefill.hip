@@ -568,7 +568,7 @@ struct navi_talker {
     double last_ms = 0;
     // each row count's layer launches captured once as a HIP graph and replayed
     std::vector<std::pair<int, hipGraphExec_t>> graphs;
-    bool use_graphs = true;
+    bool use_graphs = false;           // off by default: replays measured no faster than launches
     std::vector<void *> owned;
 
     template <class T>
@@ -895,7 +895,8 @@ navi_status navi_talker_prefill(navi_talker *t, const float *d_rows, int32_t n_r
     NAVI_TRY_HIP(hipMemcpyAsync(t->x, d_rows, static_cast<size_t>(T) * H * sizeof(float), hipMemcpyDeviceToDevice, s), err,
                  errlen);
     // The layers and the head: a launch sequence that depends only on T (every buffer is the
-    // handle's), so it is captured once per row count as a HIP graph and replayed.
+    // handle's), so it can be captured once per row count as a HIP graph and replayed
+    // (navi_talker_set_graphs; off by default, measured no faster than host launches).
     if (t->use_graphs) {
         hipGraphExec_t ex = nullptr;
         for (auto &g : t->graphs)

@@ -303,7 +303,7 @@ struct navi_vocoder {
     int *d_pos0 = nullptr;             // the next chunk's first position (device)
     // each chunk size's launch sequence captured once per history parity and replayed
     std::vector<std::pair<std::pair<int, int>, hipGraphExec_t>> graphs;
-    bool use_graphs = true;
+    bool use_graphs = false;           // off by default: replays measured no faster than launches
     const uint16_t *cb_first = nullptr;
     uint16_t *cb_rest = nullptr;
     Conv rvq_proj, pre_conv, in_proj, out_proj, dec0;
@@ -605,8 +605,10 @@ navi_status decode_chunk(navi_vocoder &v, int T, char *err, size_t errlen) {
 }
 
 // A chunk: its launch sequence depends only on T and the history parity (every pointer and split
-// count is fixed at create, the position lives on the device), so it is captured once per
-// (T, parity) as a HIP graph and replayed; with the stage hook on, it runs eagerly.
+// count is fixed at create, the position lives on the device), so it can be captured once per
+// (T, parity) as a HIP graph and replayed (navi_vocoder_set_graphs). Off by default: on MI355X the
+// replays measured no faster than host launches (each kernel's own latency, not the launch gap,
+// bounds a chunk). With the stage hook on, a chunk always runs eagerly.
 navi_status run_chunk(navi_vocoder &v, int T, char *err, size_t errlen) {
     hipStream_t s = device_state().stream;
     if (!v.use_graphs || v.hook) {

@@ -203,7 +203,7 @@ def test_device_prompt_prefill_frames_match_oracle(abi, side):
 
 @pytest.mark.parametrize("T", [10, 130])
 def test_prefill_graph_replays_match_eager(abi, side, T):
-    """Prefills replayed from the captured graph (the default) give bit for bit the hidden, logits
+    """Prefills replayed from the captured graph (navi_talker_set_graphs) give bit for bit the hidden, logits
     and K/V rows of prefills whose kernels the host launches one by one; three replays, each
     with an eager prefill of other rows and a synchronisation in between."""
     rng = np.random.default_rng(100 + T)
@@ -228,5 +228,5 @@ def test_prefill_graph_replays_match_eager(abi, side, T):
             np.testing.assert_array_equal(gk, wk)
             np.testing.assert_array_equal(gv, wv)
         run(False, d2)                                   # eager work between the replays
-    side.talker.set_graphs(True)
+    side.talker.set_graphs(False)
     log(f"prefill T={T}: 3 graph replays == eager")

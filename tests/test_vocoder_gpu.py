@@ -123,7 +123,7 @@ def test_stage_hook_stages_match_oracle(codec):
 
 
 def test_graph_replays_match_eager(codec):
-    """Chunks replayed from captured HIP graphs (the default) give the PCM of chunks whose kernels
+    """Chunks replayed from captured HIP graphs (navi_vocoder_set_graphs) give the PCM of chunks whose kernels
     the host launches one by one: a stream of 4 then 16-frame chunks (both history parities, a
     partial last chunk), replayed several times with resets and eager decodes in between; every
     replay is compared with the eager result."""
@@ -143,4 +143,5 @@ def test_graph_replays_match_eager(codec):
         v.set_graphs(False)                     # eager work between the replays
         assert np.array_equal(stream(), eager)
         v.set_graphs(True)
+    v.set_graphs(False)
     log(f"vocoder graph replays == eager over 45 frames (4 + 16 + 16 + 9), 3 rounds")
