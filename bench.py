@@ -35,7 +35,8 @@ SEED = 1
 
 
 def algorithmic_bytes(kv: dict, n_past: int) -> dict:
-    """Bytes one frame must read at least once (BASELINE.md / SURVEY 8d accounting)."""
+    """Bytes one frame must read at least once: every weight of the talker, the K/V rows of the
+    context, and the code predictor's layers and heads once per position."""
     def layer_bytes(ns):
         H, F = kv[f"{ns}.hidden_size"], kv[f"{ns}.intermediate_size"]
         Q = kv[f"{ns}.num_attention_heads"] * kv[f"{ns}.head_dim"]
@@ -359,7 +360,7 @@ def main():
         return
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
-              "(the batch-1 frame is a chain of dependent phases; see DESIGN.md, 'More than one GPU')", file=sys.stderr)
+              "(the batch-1 frame is a chain of dependent phases; the path shards by stream, one process per GPU)", file=sys.stderr)
         sys.exit(2)
 
     from navi_amd import abi

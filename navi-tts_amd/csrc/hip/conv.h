@@ -15,6 +15,7 @@ constexpr int CCH = 64;                  // input channels staged per step
 constexpr int LDW = CCH + 8;             // padded LDS row (halves)
 
 typedef _Float16 half8v __attribute__((ext_vector_type(8)));
+typedef _Float16 half4v __attribute__((ext_vector_type(4)));
 
 // Prologues (applied to the input as it is staged): SILU_GATE silu(x[ci]) * x[Cin + ci]; ADD2 x + x2;
 // RVQ: the input rows are not read from x but gathered from the codebooks by the frame's codes.
@@ -173,42 +174,63 @@ __global__ void __launch_bounds__(BT) k_conv_mfma(ConvArgs a) {
     f32x4_t acc[MT];
 #pragma unroll
     for (int i = 0; i < MT; ++i) acc[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    // Staging of the time window of one channel chunk: a thread owns IT float4s of it, always
-    // the same 4 channels (BT is a multiple of the chunk's float4 count, 8 or 16). A chunk's
-    // loads (inputs, weights) are all issued at once, and the next chunk's go out before this
-    // chunk's MFMAs, so no load waits on another.
-    constexpr int IT = (WROWS * (CCH / 4) + BT - 1) / BT;
+    // Staging of the time window of one channel chunk: a thread owns the same 4 channels c4 of every
+    // chunk and rows rr0 + 16 it of the window (IT of them). Where each of those rows comes from (a
+    // row of x, of the history, or zeros) is the same for every chunk, so it is worked out once:
+    // off[it] is the element offset of the row's channel 0 in x (bit it of xm) or in hist (hm); for
+    // PRO_RVQ off[it] is the frame index. A chunk's loads (inputs, weights) are all issued at once,
+    // and the next chunk's go out before this chunk's MFMAs, so no load waits on another.
+    constexpr int Q4 = CCH / 4, RPI = BT / Q4;               // float4s per staged row, rows per item step
+    constexpr int IT = (WROWS + RPI - 1) / RPI;
     constexpr bool TWO = PRO == PRO_SILU_GATE || PRO == PRO_ADD2;   // a second operand per element
+    static_assert(BT % Q4 == 0, "every item step covers whole rows");
+    const int c4 = (static_cast<int>(threadIdx.x) % Q4) * 4, rr0 = static_cast<int>(threadIdx.x) / Q4;
+    int off[IT];
+    uint32_t xm = 0, hm = 0;
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
+        const int r = rr0 + RPI * it;
+        int t = t0 - a.lpad + r;
+        if (a.reflect) t = t < 0 ? -t : t >= a.T ? 2 * (a.T - 1) - t : t;
+        off[it] = 0;
+        if (r < rows) {
+            if (t >= 0 && t < a.T) {
+                off[it] = PRO == PRO_RVQ ? t : t * a.ldx;
+                xm |= 1u << it;
+            } else if (t < 0 && a.hist && PRO != PRO_RVQ) {
+                off[it] = (H + t) * a.Cin;
+                hm |= 1u << it;
+            }
+        }
+    }
     f32x4_t av[IT], au[TWO ? IT : 1];
     u32x4_t bq[K][CCH / 32];
     auto load_tap = [&](int j, int ci0) {
         const int cc = min(CCH, ce - ci0);
 #pragma unroll
-        for (int s = 0; s < CCH / 32; ++s)
-            if (s * 32 < cc)
-                bq[j][s] = __builtin_nontemporal_load((const NAVI_GLOBAL u32x4_t *) (wbase + static_cast<size_t>(j) * a.Cin + ci0 + s * 32));
+        for (int s = 0; s < CCH / 32; ++s)   // past the chunk's channels: zeros (the staged A is zero there too)
+            bq[j][s] = s * 32 < cc ? __builtin_nontemporal_load((const NAVI_GLOBAL u32x4_t *) (wbase + static_cast<size_t>(j) * a.Cin + ci0 + s * 32))
+                                   : u32x4_t{0u, 0u, 0u, 0u};
     };
     auto load_a = [&](int ci0) {
-        const int q4 = min(CCH, ce - ci0) >> 2;
-        const int ci = ci0 + (threadIdx.x % q4) * 4;
+        const bool in = c4 < ce - ci0;                      // this thread's channels are inside the chunk
+        const int ci = ci0 + c4;
 #pragma unroll
         for (int it = 0; it < IT; ++it) {
-            const int r = (threadIdx.x + it * BT) / q4;
-            int t = t0 - a.lpad + r;
-            if (a.reflect) t = t < 0 ? -t : t >= a.T ? 2 * (a.T - 1) - t : t;
             av[it] = f32x4_t{0.f, 0.f, 0.f, 0.f};
             if (TWO) au[it] = av[it];
-            if (r < rows) {
+            if (!in) continue;
+            if ((xm >> it) & 1u) {
                 if (PRO == PRO_RVQ) {
-                    if (t >= 0 && t < a.T) av[it] = rvq_row4(a, t, ci);
-                } else if (t >= 0 && t < a.T) {
-                    const float *row = a.x + static_cast<size_t>(t) * a.ldx;
+                    av[it] = rvq_row4(a, off[it], ci);
+                } else {
+                    const float *row = a.x + off[it];
                     av[it] = *(const NAVI_GLOBAL f32x4_t *) (row + ci);
                     if (PRO == PRO_SILU_GATE) au[it] = *(const NAVI_GLOBAL f32x4_t *) (row + a.Cin + ci);
-                    if (PRO == PRO_ADD2) au[it] = *(const NAVI_GLOBAL f32x4_t *) (a.x2 + static_cast<size_t>(t) * a.ldx + ci);
-                } else if (t < 0 && a.hist) {
-                    av[it] = *(const NAVI_GLOBAL f32x4_t *) (a.hist + static_cast<size_t>(H + t) * a.Cin + ci);
+                    if (PRO == PRO_ADD2) au[it] = *(const NAVI_GLOBAL f32x4_t *) (a.x2 + off[it] + ci);
                 }
+            } else if ((hm >> it) & 1u) {
+                av[it] = *(const NAVI_GLOBAL f32x4_t *) (a.hist + off[it] + ci);
             }
         }
     };
@@ -220,50 +242,46 @@ __global__ void __launch_bounds__(BT) k_conv_mfma(ConvArgs a) {
         load_a(cb);
     }
     for (int ci0 = cb; ci0 < ce; ci0 += CCH) {
-        const int cc = min(CCH, ce - ci0);                  // multiple of 32
         const bool more = ci0 + CCH < ce;
         __syncthreads();                                    // the previous chunk's readers are done
-        {
-            const int q4 = cc >> 2, c = (threadIdx.x % q4) * 4;
 #pragma unroll
-            for (int it = 0; it < IT; ++it) {
-                const int r = (threadIdx.x + it * BT) / q4;
-                int t = t0 - a.lpad + r;
-                if (a.reflect) t = t < 0 ? -t : t >= a.T ? 2 * (a.T - 1) - t : t;
-                if (r >= rows) continue;
-                f32x4_t v = av[it];
-                if (PRO == PRO_SILU_GATE && t >= 0 && t < a.T) {
+        for (int it = 0; it < IT; ++it) {
+            const int r = rr0 + RPI * it;
+            if (r >= rows) continue;
+            f32x4_t v = av[it];
+            if (PRO == PRO_SILU_GATE && ((xm >> it) & 1u)) {
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) v[e] = silu(v[e]) * au[it][e];
-                }
-                if (PRO == PRO_ADD2) v += au[it];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    bad |= !(fabsf(v[e]) < 65504.f);
-                    const _Float16 h = static_cast<_Float16>(v[e]);
-                    whi[r][c + e] = h;
-                    wlo[r][c + e] = static_cast<_Float16>(v[e] - static_cast<float>(h));
-                }
+                for (int e = 0; e < 4; ++e) v[e] = silu(v[e]) * au[it][e];
             }
+            if (PRO == PRO_ADD2) v += au[it];
+            half4v h, o;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                bad |= !(fabsf(v[e]) < 65504.f);
+                h[e] = static_cast<_Float16>(v[e]);
+                o[e] = static_cast<_Float16>(v[e] - static_cast<float>(h[e]));
+            }
+            *reinterpret_cast<half4v *>(&whi[r][c4]) = h;
+            *reinterpret_cast<half4v *>(&wlo[r][c4]) = o;
         }
         __syncthreads();
         if (more) load_a(ci0 + CCH);
         if (live) {
 #pragma unroll
             for (int j = 0; j < K; ++j) {
+                // a partial chunk's missing channels hold zeros in A and B: no branch here, so the
+                // accumulators stay in place across the unrolled steps
 #pragma unroll
                 for (int s = 0; s < CCH / 32; ++s) {
-                    if (s * 32 < cc) {
-                        half8v b;
-                        __builtin_memcpy(&b, &bq[j][s], 16);
+                    half8v b;
+                    __builtin_memcpy(&b, &bq[j][s], 16);
 #pragma unroll
-                        for (int i = 0; i < MT; ++i) {
-                            const int wr = i * 16 + (l & 15) + j * a.dil;
-                            const half8v h = *reinterpret_cast<const half8v *>(&whi[wr][s * 32 + (l >> 4) * 8]);
-                            const half8v o = *reinterpret_cast<const half8v *>(&wlo[wr][s * 32 + (l >> 4) * 8]);
-                            acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(h, b, acc[i], 0, 0, 0);
-                            acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(o, b, acc[i], 0, 0, 0);
-                        }
+                    for (int i = 0; i < MT; ++i) {
+                        const int wr = i * 16 + (l & 15) + j * a.dil;
+                        const half8v h = *reinterpret_cast<const half8v *>(&whi[wr][s * 32 + (l >> 4) * 8]);
+                        const half8v o = *reinterpret_cast<const half8v *>(&wlo[wr][s * 32 + (l >> 4) * 8]);
+                        acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(h, b, acc[i], 0, 0, 0);
+                        acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(o, b, acc[i], 0, 0, 0);
                     }
                 }
                 if (more) load_tap(j, ci0 + CCH);           // tap j's registers are free again

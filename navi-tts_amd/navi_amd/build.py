@@ -19,7 +19,8 @@ OBJ = PKG / "lib" / "obj"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
-# -packed-fp32-ops: no v_pk_*_f32 in any HIP code (build rules).
+# -packed-fp32-ops: no packed FP32 instructions (v_pk_*_f32) in any HIP code: some of their forms have
+# given silently wrong results on this pool's MI355X boxes.
 HIP_FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-Wall", "-Wno-unused-function",
              "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
              "-I", str(ROOT / "include"), "-I", str(PKG / "csrc" / "hip")]
