@@ -29,6 +29,7 @@ struct RowArgs {
     uint32_t *flag;                   // set when an activation is outside the f16 range
     int lda, M, K, n1, n2, F, ldy;    // F: SWIGLU gate rows [0, F), up rows [F, 2F) of the combined W
     float eps;
+    const float *rs;                  // RESID: per-column scale of the added product (a layer scale), or null
 };
 
 namespace {
@@ -168,8 +169,9 @@ __global__ void __launch_bounds__(NWV * WAVE) k_rows(RowArgs a) {
         }
         // RESID: the four residual values are loaded before the first store (a load after a
         // store to the same buffer would wait for it: four memory round trips instead of one)
-        float old[4] = {0.f, 0.f, 0.f, 0.f};
+        float old[4] = {0.f, 0.f, 0.f, 0.f}, rsc = 1.f;
         if constexpr (EPI == EPI_RESID) {
+            if (a.rs) rsc = a.rs[nb];
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int m = m0 + 16 * i + 4 * kq + r;
@@ -188,7 +190,7 @@ __global__ void __launch_bounds__(NWV * WAVE) k_rows(RowArgs a) {
                 const float g = v[0][r] * sc, u = v[NT - 1][r] * sc;
                 *dst = g / (1.f + expf(-g)) * u;
             } else {
-                *dst = old[r] + v[0][r];
+                *dst = a.rs ? v[0][r] * rsc + old[r] : old[r] + v[0][r];
             }
         }
     }
@@ -244,6 +246,40 @@ void launch_rows(int epi, bool norm, const float *A, int lda, int M, int K, cons
     case 3: launch_rows_mt<3>(epi, norm, grid, ra, s); break;
     default: launch_rows_mt<4>(epi, norm, grid, ra, s); break;
     }
+}
+
+// The codec decoder's transformer layers (vocoder.hip): q|k|v and gate|up over K = 512 with the
+// RMSNorm fused (SwiGLU on gate|up), o and down over K = 1024 adding into the residual stream with
+// the per-column layer scale rs. One split of K over the waves per shape, whatever the row count
+// (MT and the column groups do not change a column's sums), so the output of a row does not
+// depend on how many rows a chunk has. false: a shape these kernels do not take.
+bool launch_rows_xf(int epi, bool norm, const float *A, int lda, int M, int K, const float *ln, float eps, const uint16_t *w0,
+                    int n0, const uint16_t *w1, int n1, float *y, int ldy, const float *rs, uint32_t *flag, hipStream_t s) {
+    const int F = epi == EPI_SWIGLU ? n0 : 0, N = epi == EPI_SWIGLU ? n0 : n0 + n1;
+    RowArgs ra{A, ln, w0, w1, nullptr, y, flag, lda, M, K, n0, n0 + n1, F, ldy, eps, rs};
+    if (M < 1 || N % 16 != 0) return false;
+    const int mt = M <= 16 ? 1 : M <= 32 ? 2 : M <= 48 ? 3 : 4;
+    const dim3 g1(N / 16, (M + 16 * mt - 1) / (16 * mt));
+    if (K == 512 && norm && (epi == EPI_PLAIN || epi == EPI_SWIGLU)) {
+        if (M > 64) {
+            if (epi == EPI_PLAIN && N % 64 == 0) return launch_wide<2, EPI_PLAIN, true, 8, 2, 4>(M, N, ra, s);
+            if (epi == EPI_SWIGLU && N % 32 == 0) return launch_wide<2, EPI_SWIGLU, true, 8, 2, 2>(M, N, ra, s);
+        }
+#define NAVI_XF(MT_)                                                                                      \
+        if (mt == MT_) {                                                                                  \
+            if (epi == EPI_PLAIN) hipLaunchKernelGGL((k_rows<MT_, EPI_PLAIN, true, 8, 2>), g1, dim3(8 * WAVE), 0, s, ra); \
+            else hipLaunchKernelGGL((k_rows<MT_, EPI_SWIGLU, true, 8, 2>), g1, dim3(8 * WAVE), 0, s, ra); \
+            return true;                                                                                  \
+        }
+        NAVI_XF(1) NAVI_XF(2) NAVI_XF(3) NAVI_XF(4)
+#undef NAVI_XF
+    }
+    if (K == 1024 && !norm && epi == EPI_RESID) {
+        if (M > 64 && N % 32 == 0) return launch_wide<1, EPI_RESID, false, 16, 2, 2>(M, N, ra, s);
+        hipLaunchKernelGGL((k_rows<1, EPI_RESID, false, 16, 2>), dim3(N / 16, (M + 15) / 16), dim3(16 * WAVE), 0, s, ra);
+        return true;
+    }
+    return false;
 }
 
 } // namespace

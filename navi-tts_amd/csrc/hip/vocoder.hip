@@ -33,6 +33,7 @@
 //    into the other, so no launch exists only to update it.
 #include "conv.h"
 #include "dev_common.h"
+#include "rows.h"
 #include "host_util.h"
 
 #include <algorithm>
@@ -124,61 +125,93 @@ __global__ void __launch_bounds__(BT) k_dw_ln(const float *x, const float *hist,
 
 // Sliding-window causal attention of the codec transformer (k_attention, vocoder.hip:87-122
 // semantics) with RoPE (theta from invf, rotate-half) and the K/V ring append folded in. A block
-// takes RT query rows of one head: it stages in LDS the roped keys and the values of every
+// takes RT query rows of one head (16, or 4 for chunks of up to 32 frames, so that a short chunk
+// still spreads over many blocks; a row's result does not depend on RT): it stages in LDS the roped keys and the values of every
 // position those rows see (positions of this chunk straight from the q|k|v rows, roped here;
 // earlier ones from the ring, stored roped), then each wave runs RT/4 rows: lane j scores keys
 // j and j + 64 of the row's window, softmax by two wave reductions, and lane d sums p_j V[j][d]
 // with p_j read from lane j (readlane). The block also writes its rows' roped k and v to the ring
 // for later chunks: ring >= window + chunk, so no slot written here is one this launch reads.
-template <int HD>
+template <int HD, int RT>
 __global__ void __launch_bounds__(BT) k_window_attention(const float *qkv, int nh, int T, const int *pos0p, int window, int ring,
                                                          const float *invf, float *kc, float *vc, float *out) {
-    constexpr int RT = 16, HALF = HD / 2, KS = HD + 1, DPL = HD / 64;   // K rows padded: lanes j read rows j
+    constexpr int HALF = HD / 2, KS = HD + 1, DPL = HD / 64;   // K rows padded: lanes j read rows j
+    static_assert(RT % 4 == 0 && RT <= 16, "RT / 4 rows per wave; the LDS is sized for 16");
     extern __shared__ float sm[];
     const int pos0 = gld(pos0p);                 // the chunk's first position (device-side: graph replays)
     const int HDT = nh * HD, ld = 3 * HDT, h = blockIdx.y;
     const int t0 = blockIdx.x * RT, t1 = min(T, t0 + RT);
     const int kp0 = max(0, pos0 + t0 - window + 1), nk = pos0 + t1 - kp0;
     float *Ks = sm, *Vs = Ks + (window + RT - 1) * KS, *Qs = Vs + (window + RT - 1) * HD;
-    for (int e = threadIdx.x; e < nk * HALF; e += BT) {
-        const int r = e / HALF, i = e - r * HALF, p = kp0 + r;
-        float k0, k1, v0, v1;
-        if (p >= pos0) {
-            const float *row = qkv + static_cast<size_t>(p - pos0) * ld + h * HD;
-            const float a0 = gld(row + HDT + i), a1 = gld(row + HDT + i + HALF);
-            v0 = gld(row + 2 * HDT + i);
-            v1 = gld(row + 2 * HDT + i + HALF);
-            float sn, cs;
-            sincosf(static_cast<float>(p) * gld(invf + i), &sn, &cs);
-            k0 = a0 * cs - a1 * sn;
-            k1 = a1 * cs + a0 * sn;
-            if (p - pos0 >= t0 && p - pos0 < t1) {
+    // Staging: a thread takes 4 dimensions i..i+3 of a row and their rotate-half partners i+HALF..,
+    // so every load is a float4; a batch of NB rows' loads is issued before any of them is used
+    // (one memory latency per batch instead of one per element).
+    constexpr int Q = HALF / 4, MAXE = (128 + RT - 1) * Q, NIT = (MAXE + BT - 1) / BT, NB = NIT < 5 ? NIT : 5;
+    const int ne = nk * Q;
+    for (int b0 = 0; b0 < NIT && b0 * BT < ne; b0 += NB) {
+        f32x4_t ka[NB], kb[NB], va[NB], vb[NB];
+#pragma unroll
+        for (int u = 0; u < NB; ++u) {
+            const int e = static_cast<int>(threadIdx.x) + (b0 + u) * BT;
+            if (b0 + u >= NIT || e >= ne) continue;
+            const int r = e / Q, i = (e - r * Q) * 4, p = kp0 + r;
+            if (p >= pos0) {
+                const float *row = qkv + static_cast<size_t>(p - pos0) * ld + h * HD;
+                ka[u] = ld4(row + HDT + i);
+                kb[u] = ld4(row + HDT + i + HALF);
+                va[u] = ld4(row + 2 * HDT + i);
+                vb[u] = ld4(row + 2 * HDT + i + HALF);
+            } else {
                 const size_t o = static_cast<size_t>(p % ring) * HDT + h * HD + i;
-                gst(kc + o, k0);
-                gst(kc + o + HALF, k1);
-                gst(vc + o, v0);
-                gst(vc + o + HALF, v1);
+                ka[u] = ld4(kc + o);
+                kb[u] = ld4(kc + o + HALF);
+                va[u] = ld4(vc + o);
+                vb[u] = ld4(vc + o + HALF);
             }
-        } else {
-            const size_t o = static_cast<size_t>(p % ring) * HDT + h * HD + i;
-            k0 = gld(kc + o);
-            k1 = gld(kc + o + HALF);
-            v0 = gld(vc + o);
-            v1 = gld(vc + o + HALF);
         }
-        Ks[r * KS + i] = k0;
-        Ks[r * KS + i + HALF] = k1;
-        Vs[r * HD + i] = v0;
-        Vs[r * HD + i + HALF] = v1;
+#pragma unroll
+        for (int u = 0; u < NB; ++u) {
+            const int e = static_cast<int>(threadIdx.x) + (b0 + u) * BT;
+            if (b0 + u >= NIT || e >= ne) continue;
+            const int r = e / Q, i = (e - r * Q) * 4, p = kp0 + r;
+            f32x4_t k0 = ka[u], k1 = kb[u];
+            if (p >= pos0) {
+                const f32x4_t f = ld4(invf + i);
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    float sn, cs;
+                    sincosf(static_cast<float>(p) * f[c], &sn, &cs);
+                    k0[c] = ka[u][c] * cs - kb[u][c] * sn;
+                    k1[c] = kb[u][c] * cs + ka[u][c] * sn;
+                }
+                if (p - pos0 >= t0 && p - pos0 < t1) {      // this tile's own rows go to the ring
+                    const size_t o = static_cast<size_t>(p % ring) * HDT + h * HD + i;
+                    st4(kc + o, k0);
+                    st4(kc + o + HALF, k1);
+                    st4(vc + o, va[u]);
+                    st4(vc + o + HALF, vb[u]);
+                }
+            }
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                Ks[r * KS + i + c] = k0[c];
+                Ks[r * KS + i + HALF + c] = k1[c];
+                Vs[r * HD + i + c] = va[u][c];
+                Vs[r * HD + i + HALF + c] = vb[u][c];
+            }
+        }
     }
-    for (int e = threadIdx.x; e < (t1 - t0) * HALF; e += BT) {
-        const int rr = e / HALF, i = e - rr * HALF, p = pos0 + t0 + rr;
+    for (int e = threadIdx.x; e < (t1 - t0) * Q; e += BT) {
+        const int rr = e / Q, i = (e - rr * Q) * 4, p = pos0 + t0 + rr;
         const float *row = qkv + static_cast<size_t>(t0 + rr) * ld + h * HD;
-        const float a0 = gld(row + i), a1 = gld(row + i + HALF);
-        float sn, cs;
-        sincosf(static_cast<float>(p) * gld(invf + i), &sn, &cs);
-        Qs[rr * HD + i] = a0 * cs - a1 * sn;
-        Qs[rr * HD + i + HALF] = a1 * cs + a0 * sn;
+        const f32x4_t a0 = ld4(row + i), a1 = ld4(row + i + HALF), f = ld4(invf + i);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            float sn, cs;
+            sincosf(static_cast<float>(p) * f[c], &sn, &cs);
+            Qs[rr * HD + i + c] = a0[c] * cs - a1[c] * sn;
+            Qs[rr * HD + i + HALF + c] = a1[c] * cs + a0[c] * sn;
+        }
     }
     __syncthreads();
     const int wv = threadIdx.x >> 6, l = threadIdx.x & 63;
@@ -205,12 +238,29 @@ __global__ void __launch_bounds__(BT) k_window_attention(const float *qkv, int n
 #pragma unroll
         for (int u = 0; u < 2; ++u) p[u] = l + 64 * u < n ? expf(s[u] - m) : 0.f;
         const float inv = 1.f / wave_sum(p[0] + p[1]);
+        // sum over the keys in key order; the V rows of 8 keys are read before their 8 products,
+        // so one LDS latency covers 8 keys
         float acc[DPL] = {};
-        for (int j = 0; j < n; ++j) {
-            const float pj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p[j >> 6]), j & 63));
-            const float *vr = Vs + (rb + j) * HD + l;
+        auto pk = [&](int j) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p[j >> 6]), j & 63)); };
+        const float *vb = Vs + rb * HD + l;
+        int j = 0;
+        for (; j + 8 <= n; j += 8) {
+            float vv[8][DPL];
 #pragma unroll
-            for (int d = 0; d < DPL; ++d) acc[d] = fmaf(pj, vr[64 * d], acc[d]);
+            for (int u = 0; u < 8; ++u)
+#pragma unroll
+                for (int d = 0; d < DPL; ++d) vv[u][d] = vb[(j + u) * HD + 64 * d];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const float pj = pk(j + u);
+#pragma unroll
+                for (int d = 0; d < DPL; ++d) acc[d] = fmaf(pj, vv[u][d], acc[d]);
+            }
+        }
+        for (; j < n; ++j) {
+            const float pj = pk(j);
+#pragma unroll
+            for (int d = 0; d < DPL; ++d) acc[d] = fmaf(pj, vb[j * HD + 64 * d], acc[d]);
         }
 #pragma unroll
         for (int d = 0; d < DPL; ++d) gst(out + static_cast<size_t>(t) * HDT + h * HD + l + 64 * d, acc[d] * inv);
@@ -510,6 +560,18 @@ navi_status snap(navi_vocoder &v, const std::string &name, const float *buf, int
     return NAVI_OK;
 }
 
+// A transformer projection of the chunk on the row-projection kernels (rows.h): RMSNorm, SwiGLU
+// and the layer-scaled residual add fused in, whole K per block, no split-K partials.
+navi_status xf_rows(int epi, bool norm, const float *A, int lda, int M, int K, const float *ln, float eps, const uint16_t *w0,
+                    int n0, const uint16_t *w1, int n1, float *y, int ldy, const float *rs, uint32_t *flag, char *err,
+                    size_t errlen) {
+    if (!rows::launch_rows_xf(epi, norm, A, lda, M, K, ln, eps, w0, n0, w1, n1, y, ldy, rs, flag, device_state().stream)) {
+        set_err(err, errlen, "vocoder: no row-projection kernel for K=%d N=%d (epilogue %d)", K, n0 + n1, epi);
+        return NAVI_ERR_UNSUPPORTED;
+    }
+    return NAVI_OK;
+}
+
 // One chunk of T frames: codes (already in v.d_codes) -> T * samples_per_frame PCM samples in v.pcm
 // (the stage order of decode_chunk, vocoder.hip:261-343, which is the model's).
 navi_status decode_chunk(navi_vocoder &v, int T, char *err, size_t errlen) {
@@ -523,28 +585,36 @@ navi_status decode_chunk(navi_vocoder &v, int T, char *err, size_t errlen) {
     VOC_TRY(snap(v, "pre_conv", v.pre, T, L, err, errlen));
     VOC_TRY(run_conv(v, v.in_proj, PRO_NONE, EPI_BIAS, v.pre, T, L, v.xs, VH, nullptr, nullptr, err, errlen));
     VOC_TRY(snap(v, "in_proj", v.xs, T, VH, err, errlen));
-    const dim3 att_grid((T + 15) / 16, nh);
     const size_t att_lds = attention_lds(p.sliding_window, p.xf.head_dim);
     for (size_t li = 0; li < v.layers.size(); ++li) {
         TLayer &ly = v.layers[li];
         const std::string ls = std::to_string(li);
-        hipLaunchKernelGGL(k_rmsnorm, dim3(T), dim3(BT), 0, s, v.xs, ly.ln1, VH, p.xf.rms_eps, v.xn);
-        VOC_TRY(snap(v, "norm1_" + ls, v.xn, T, VH, err, errlen));
-        VOC_TRY(run_conv(v, ly.qkv, PRO_NONE, EPI_BIAS, v.xn, T, VH, v.qkv, 3 * HDT, nullptr, nullptr, err, errlen));
+        if (v.hook) {                 // the normed rows are a stage of their own only for the hook
+            hipLaunchKernelGGL(k_rmsnorm, dim3(T), dim3(BT), 0, s, v.xs, ly.ln1, VH, p.xf.rms_eps, v.xn);
+            VOC_TRY(snap(v, "norm1_" + ls, v.xn, T, VH, err, errlen));
+        }
+        VOC_TRY(xf_rows(rows::EPI_PLAIN, true, v.xs, VH, T, VH, ly.ln1, p.xf.rms_eps, ly.qkv.w, 3 * HDT, nullptr, 0, v.qkv,
+                        3 * HDT, nullptr, v.flag, err, errlen));
         VOC_TRY(snap(v, "qkv_" + ls, v.qkv, T, 3 * HDT, err, errlen));
-        if (p.xf.head_dim == 64)
-            hipLaunchKernelGGL(k_window_attention<64>, att_grid, dim3(BT), att_lds, s, v.qkv, nh, T, v.d_pos0,
-                               p.sliding_window, v.ring, v.invf, ly.kc, ly.vc, v.att);
-        else
-            hipLaunchKernelGGL(k_window_attention<128>, att_grid, dim3(BT), att_lds, s, v.qkv, nh, T, v.d_pos0,
-                               p.sliding_window, v.ring, v.invf, ly.kc, ly.vc, v.att);
+#define NAVI_ATT(HD_, RT_)                                                                                              \
+        hipLaunchKernelGGL((k_window_attention<HD_, RT_>), dim3((T + RT_ - 1) / RT_, nh), dim3(BT), att_lds, s, v.qkv, nh, T, \
+                           v.d_pos0, p.sliding_window, v.ring, v.invf, ly.kc, ly.vc, v.att)
+        if (p.xf.head_dim == 64) {
+            if (T <= 32) NAVI_ATT(64, 4);
+            else NAVI_ATT(64, 16);
+        } else {
+            if (T <= 32) NAVI_ATT(128, 4);
+            else NAVI_ATT(128, 16);
+        }
+#undef NAVI_ATT
         VOC_TRY(snap(v, "attnraw" + ls, v.att, T, HDT, err, errlen));
-        VOC_TRY(run_conv(v, ly.o, PRO_NONE, EPI_SCALE_RESIDUAL, v.att, T, HDT, v.xs, VH, v.xs, ly.attn_scale, err, errlen));
+        VOC_TRY(xf_rows(rows::EPI_RESID, false, v.att, HDT, T, HDT, nullptr, 0.f, ly.o.w, VH, nullptr, 0, v.xs, VH,
+                        ly.attn_scale, v.flag, err, errlen));
         VOC_TRY(snap(v, "xattn_" + ls, v.xs, T, VH, err, errlen));
-        hipLaunchKernelGGL(k_rmsnorm, dim3(T), dim3(BT), 0, s, v.xs, ly.ln2, VH, p.xf.rms_eps, v.xn);
-        VOC_TRY(run_conv(v, ly.gu, PRO_NONE, EPI_BIAS, v.xn, T, VH, v.gu, 2 * FF, nullptr, nullptr, err, errlen));
-        VOC_TRY(run_conv(v, ly.down, PRO_SILU_GATE, EPI_SCALE_RESIDUAL, v.gu, T, 2 * FF, v.xs, VH, v.xs, ly.mlp_scale, err,
-                         errlen));
+        VOC_TRY(xf_rows(rows::EPI_SWIGLU, true, v.xs, VH, T, VH, ly.ln2, p.xf.rms_eps, ly.gu.w, FF,
+                        ly.gu.w + static_cast<size_t>(FF) * VH, FF, v.gu, FF, nullptr, v.flag, err, errlen));
+        VOC_TRY(xf_rows(rows::EPI_RESID, false, v.gu, FF, T, FF, nullptr, 0.f, ly.down.w, VH, nullptr, 0, v.xs, VH,
+                        ly.mlp_scale, v.flag, err, errlen));
         VOC_TRY(snap(v, "layer" + ls, v.xs, T, VH, err, errlen));
     }
     hipLaunchKernelGGL(k_rmsnorm, dim3(T), dim3(BT), 0, s, v.xs, v.final_norm, VH, p.xf.rms_eps, v.xn);
@@ -689,7 +759,8 @@ navi_status navi_vocoder_create(const navi_vocoder_params *p, const navi_tensor_
     int spf = p->upsampling_ratios[0] * p->upsampling_ratios[1];
     for (int b = 0; b < 4; ++b) spf *= p->upsample_rates[b];
     bool ok = xf.n_head == xf.n_kv_head && (xf.head_dim == 64 || xf.head_dim == 128) &&
-              attention_lds(p->sliding_window, xf.head_dim) <= 64 * 1024 && p->n_q <= 16 && VH % 64 == 0 && L == 4 * BT &&
+              attention_lds(p->sliding_window, xf.head_dim) <= 64 * 1024 && p->n_q <= 16 && VH == 512 && HDT == 1024 &&
+              xf.ff == 1024 && L == 4 * BT &&
               CD % 64 == 0 && DD % 64 == 0 && HDT % 64 == 0 && xf.ff % 64 == 0 && p->sliding_window >= 1 &&
               p->sliding_window <= 128 && spf == p->samples_per_frame && p->n_semantic == 1 && p->n_q >= 2 &&
               max_chunk_frames >= 1 && max_chunk_frames <= 4096;
