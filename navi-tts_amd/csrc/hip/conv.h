@@ -326,6 +326,143 @@ __global__ void __launch_bounds__(BT) k_conv_mfma(ConvArgs a) {
     if (a.hnext) carry_rows(a.hist, a.x, a.ldx, a.T, H, a.Cin, a.hnext);
 }
 
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+// The wide implicit-GEMM conv for the decoder's big causal convs (K = 7 or 1, one phase, no
+// prologue, no K split): v_mfma_f32_32x32x16_f16, whose operands cover twice the products of a
+// 16x16x32 step per LDS read. A block computes BM rows x 64 output channels; per chunk of 32 input
+// channels it stages in LDS the time window (BM + (K-1) dil rows, f16 hi + lo) and the weights of
+// every tap for its 64 channels, so each operand is read from memory once per block and from LDS by
+// the waves that use it. BM = 128: wave w owns rows 32w..32w+31 and both 32-column tiles (every A
+// read feeds two MFMAs); BM = 64: waves in 2 x 2, one 32 x 32 tile each (twice the blocks for short
+// chunks). Per output the sum runs over chunks, taps, 16-channel steps, hi then lo, in an order
+// that does not depend on BM or T. The next chunk's loads are in flight during this chunk's MFMAs.
+// Lane layout of the 32x32x16 step (checked on the device): lane l holds A[l % 32][8 (l / 32) ..]
+// and B[8 (l / 32) ..][l % 32]; accumulator r of lane l is row 8 (r / 4) + 4 (l / 32) + r % 4,
+// column l % 32.
+template <int K, int BM, int EPI>
+__global__ void __launch_bounds__(BT) k_conv_wide(ConvArgs a) {
+    constexpr int CC = 32, LDA = CC + 8, BN = 64;           // channels per chunk, LDS row (halves), block columns
+    constexpr int MAXWR = BM + (K - 1) * 9;                 // window rows at dilation <= 9
+    constexpr int NCT = BM == 128 ? 2 : 1;                  // 32-column tiles per wave
+    __shared__ __align__(16) _Float16 ahi[MAXWR * LDA];
+    __shared__ __align__(16) _Float16 alo[MAXWR * LDA];
+    __shared__ __align__(16) _Float16 bw[K * BN * LDA];
+    const int wv = threadIdx.x >> 6, l = threadIdx.x & 63;
+    const int wr = BM == 128 ? 32 * wv : 32 * (wv >> 1), wc = BM == 128 ? 0 : 32 * (wv & 1);
+    const int n0 = blockIdx.x * BN, t0 = blockIdx.y * BM;
+    const int H = (K - 1) * a.dil, rows = BM + H;
+    // A staging: 8 float4 per window row, thread -> rows (tid / 8) + 32 it, channels 4 (tid % 8);
+    // each row's source (x, history or zeros) fixed for the launch
+    constexpr int RPI = BT / (CC / 4), ITA = (MAXWR + RPI - 1) / RPI;
+    const int c4 = (static_cast<int>(threadIdx.x) % (CC / 4)) * 4, rr0 = static_cast<int>(threadIdx.x) / (CC / 4);
+    int aoff[ITA];
+    uint32_t xm = 0, hm = 0;
+#pragma unroll
+    for (int it = 0; it < ITA; ++it) {
+        const int r = rr0 + RPI * it, t = t0 - a.lpad + r;
+        aoff[it] = 0;
+        if (r < rows) {
+            if (t >= 0 && t < a.T) {
+                aoff[it] = t * a.ldx + c4;
+                xm |= 1u << it;
+            } else if (t < 0 && a.hist) {
+                aoff[it] = (H + t) * a.Cin + c4;
+                hm |= 1u << it;
+            }
+        }
+    }
+    // B staging: the 64 B of channels [ci0, ci0 + 32) of (column, tap), in four 16 B pieces
+    constexpr int NBI = BN * K * 4, ITB = (NBI + BT - 1) / BT;
+    int boff[ITB], bl[ITB];
+#pragma unroll
+    for (int it = 0; it < ITB; ++it) {
+        const int e = static_cast<int>(threadIdx.x) + BT * it, q = e & 3, ct = e >> 2, col = ct / K, tap = ct - col * K;
+        boff[it] = ((n0 + col) * K + tap) * a.Cin + 8 * q;
+        bl[it] = (tap * BN + col) * LDA + 8 * q;
+    }
+    f32x4_t av[ITA];
+    u32x4_t bv[ITB];
+    auto load = [&](int ci0) {
+#pragma unroll
+        for (int it = 0; it < ITA; ++it) {
+            av[it] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+            if ((xm >> it) & 1u) av[it] = *(const NAVI_GLOBAL f32x4_t *) (a.x + aoff[it] + ci0);
+            else if ((hm >> it) & 1u) av[it] = *(const NAVI_GLOBAL f32x4_t *) (a.hist + aoff[it] + ci0);
+        }
+#pragma unroll
+        for (int it = 0; it < ITB; ++it)
+            if (ITB * BT == NBI || static_cast<int>(threadIdx.x) + BT * it < NBI)
+                bv[it] = __builtin_nontemporal_load((const NAVI_GLOBAL u32x4_t *) (a.w + boff[it] + ci0));
+    };
+    f32x16_t acc[NCT];
+#pragma unroll
+    for (int c = 0; c < NCT; ++c)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[c][r] = 0.f;
+    bool bad = false;
+    load(0);
+    for (int ci0 = 0; ci0 < a.Cin; ci0 += CC) {
+        __syncthreads();                                    // the previous chunk's readers are done
+#pragma unroll
+        for (int it = 0; it < ITA; ++it) {
+            const int r = rr0 + RPI * it;
+            if (r >= rows) continue;
+            half4v h, o;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                bad |= !(fabsf(av[it][e]) < 65504.f);
+                h[e] = static_cast<_Float16>(av[it][e]);
+                o[e] = static_cast<_Float16>(av[it][e] - static_cast<float>(h[e]));
+            }
+            *reinterpret_cast<half4v *>(&ahi[r * LDA + c4]) = h;
+            *reinterpret_cast<half4v *>(&alo[r * LDA + c4]) = o;
+        }
+#pragma unroll
+        for (int it = 0; it < ITB; ++it)
+            if (ITB * BT == NBI || static_cast<int>(threadIdx.x) + BT * it < NBI)
+                *reinterpret_cast<u32x4_t *>(&bw[bl[it]]) = bv[it];
+        __syncthreads();
+        if (ci0 + CC < a.Cin) load(ci0 + CC);
+#pragma unroll
+        for (int j = 0; j < K; ++j) {
+#pragma unroll
+            for (int ks = 0; ks < CC / 16; ++ks) {
+                const int ar = (wr + (l & 31) + j * a.dil) * LDA + 16 * ks + 8 * (l >> 5);
+                const half8v h = *reinterpret_cast<const half8v *>(&ahi[ar]);
+                const half8v o = *reinterpret_cast<const half8v *>(&alo[ar]);
+#pragma unroll
+                for (int c = 0; c < NCT; ++c) {
+                    const half8v b = *reinterpret_cast<const half8v *>(&bw[(j * BN + wc + 32 * c + (l & 31)) * LDA + 16 * ks + 8 * (l >> 5)]);
+                    acc[c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(h, b, acc[c], 0, 0, 0);
+                    acc[c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(o, b, acc[c], 0, 0, 0);
+                }
+            }
+        }
+    }
+    if (bad) gst(a.flag, 1u);
+    // every load of the epilogue first (column operands, residuals), then the stores
+    EpiCol cc[NCT];
+#pragma unroll
+    for (int c = 0; c < NCT; ++c) cc[c] = epi_col(a, EPI, n0 + wc + 32 * c + (l & 31));
+    float res[NCT][16];
+#pragma unroll
+    for (int c = 0; c < NCT; ++c)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int t = t0 + wr + 8 * (r / 4) + 4 * (l >> 5) + (r & 3), co = n0 + wc + 32 * c + (l & 31);
+            res[c][r] = epi_has_res(EPI) && t < a.T ? gld(a.res + static_cast<size_t>(t) * a.ldy + co) : 0.f;
+        }
+#pragma unroll
+    for (int c = 0; c < NCT; ++c)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int t = t0 + wr + 8 * (r / 4) + 4 * (l >> 5) + (r & 3), co = n0 + wc + 32 * c + (l & 31);
+            if (t < a.T) conv_store(a, EPI, static_cast<size_t>(t) * a.ldy + co, cc[c], acc[c][r], res[c][r]);
+        }
+    if (a.hnext) carry_rows(a.hist, a.x, a.ldx, a.T, H, a.Cin, a.hnext);
+}
+
 // The 96-channel convs (the codec decoder's last block and its final conv): a block covers
 // RB = 64 MT rows and every output channel (Cout = 16 NCT). The whole input window (the rows plus
 // the (K-1) dil causal halo, all 96 channels, f16 hi + lo) is staged in LDS once, and so is each

@@ -320,6 +320,7 @@ struct Conv {
     const float *sa = nullptr, *sb = nullptr;
     int Cin = 0, Cout = 0, K = 1, dil = 1, phases = 1, H = 0;
     int S = 1;                         // input-channel splits (fixed at create: conv_splits)
+    bool wide = false;                 // runs on k_conv_wide (fixed at create: conv_takes_wide)
     // the history pair: a chunk reads hbuf[parity] and writes the next chunk's into hbuf[parity ^ 1]
     float *hbuf[2] = {};
 };
@@ -456,6 +457,30 @@ bool launch_c96(const Conv &c, const ConvArgs &a, int pro, int epi, int T, hipSt
     return false;
 }
 
+// The decoder blocks' causal convs (K 7 or 1, one phase, 32 | Cin, 64 | Cout, at least 32 rows per
+// frame) run on k_conv_wide, with no K split. Decided at create from the conv's shape and place,
+// so every chunking of the codes runs the same kernel and sums in the same order.
+bool conv_takes_wide(const Conv &c, int rows_per_frame) {
+    return c.phases == 1 && (c.K == 7 || c.K == 1) && c.dil <= 9 && c.Cin % 32 == 0 && c.Cout % 64 == 0 && rows_per_frame >= 32 &&
+           !conv_is_c96(c);
+}
+
+bool launch_wide_conv(const Conv &c, const ConvArgs &a, int pro, int epi, int T, hipStream_t s) {
+    if (pro != PRO_NONE) return false;
+    const int nb = c.Cout / 64;
+    const bool big = static_cast<long>((T + 127) / 128) * nb >= 512;   // enough 128-row tiles to fill the chip twice
+#define NAVI_WIDE(K_, E_)                                                                                              \
+    if (c.K == K_ && epi == E_) {                                                                                      \
+        if (big) hipLaunchKernelGGL((k_conv_wide<K_, 128, E_>), dim3(nb, (T + 127) / 128), dim3(BT), 0, s, a);       \
+        else hipLaunchKernelGGL((k_conv_wide<K_, 64, E_>), dim3(nb, (T + 63) / 64), dim3(BT), 0, s, a);               \
+        return true;                                                                                                   \
+    }
+    NAVI_WIDE(7, EPI_BIAS)
+    NAVI_WIDE(1, EPI_RESIDUAL)
+#undef NAVI_WIDE
+    return false;
+}
+
 // Input-channel splits of a conv over T rows: when the output tiles alone would leave most of the
 // 256 CUs idle, the channel chunks are spread over up to S blocks per tile (at least 2 chunks each)
 // and summed by k_conv_finish.
@@ -527,7 +552,12 @@ navi_status run_conv(navi_vocoder &v, Conv &c, int pro, int epi, const float *x,
         a.za = zc->sa;
         a.zb = zc->sb;
     }
-    if (conv_is_c96(c)) {
+    if (c.wide) {
+        if (!launch_wide_conv(c, a, pro, epi, T, device_state().stream)) {
+            set_err(err, errlen, "vocoder: no wide conv kernel for K=%d epilogue %d", c.K, epi);
+            return NAVI_ERR_UNSUPPORTED;
+        }
+    } else if (conv_is_c96(c)) {
         if (!launch_c96(c, a, pro, epi, T, device_state().stream)) {
             set_err(err, errlen, "vocoder: no 96-channel conv kernel for K=%d Cout=%d epilogue %d", c.K, c.Cout, epi);
             return NAVI_ERR_UNSUPPORTED;
@@ -1036,7 +1066,8 @@ navi_status navi_vocoder_create(const navi_vocoder_params *p, const navi_tensor_
         size_t need = 0;
         const int Cn = static_cast<int>(std::min<size_t>(C, 16)), Cf = static_cast<int>(C);
         auto upd = [&](Conv &c, int rows_per_frame) {
-            c.S = conv_splits(c, Cn * rows_per_frame);
+            c.wide = conv_takes_wide(c, rows_per_frame);
+            c.S = c.wide ? 1 : conv_splits(c, Cn * rows_per_frame);
             if (c.S > 1) need = std::max(need, static_cast<size_t>(c.S) * Cf * rows_per_frame * c.phases * c.Cout);
         };
         upd(v->rvq_proj, 1); upd(v->pre_conv, 1); upd(v->in_proj, 1); upd(v->out_proj, 1);
