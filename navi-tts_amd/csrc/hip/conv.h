@@ -328,29 +328,31 @@ __global__ void __launch_bounds__(BT) k_conv_mfma(ConvArgs a) {
 
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
-// The wide implicit-GEMM conv for the decoder's big causal convs (K = 7 or 1, one phase, no
-// prologue, no K split): v_mfma_f32_32x32x16_f16, whose operands cover twice the products of a
-// 16x16x32 step per LDS read. A block computes BM rows x 64 output channels; per chunk of 32 input
-// channels it stages in LDS the time window (BM + (K-1) dil rows, f16 hi + lo) and the weights of
-// every tap for its 64 channels, so each operand is read from memory once per block and from LDS by
-// the waves that use it. BM = 128: wave w owns rows 32w..32w+31 and both 32-column tiles (every A
-// read feeds two MFMAs); BM = 64: waves in 2 x 2, one 32 x 32 tile each (twice the blocks for short
-// chunks). Per output the sum runs over chunks, taps, 16-channel steps, hi then lo, in an order
-// that does not depend on BM or T. The next chunk's loads are in flight during this chunk's MFMAs.
+// The wide implicit-GEMM conv for the decoder blocks' causal convs (K = 7, 2 or 1, any number of
+// transposed-conv phases, no prologue, no K split): v_mfma_f32_32x32x16_f16, whose operands cover
+// twice the products of a 16x16x32 step per LDS read. A block computes BM rows x BN output channels
+// of one phase (blockIdx.z); per chunk of 32 input channels it stages in LDS the time window
+// (BM + (K-1) dil rows, f16 hi + lo) and the weights of every tap for its BN channels, so each
+// operand is read from memory once per block and from LDS by the waves that use it. BM = 128:
+// wave w owns rows 32w..32w+31 and all BN / 32 column tiles (every A read feeds BN / 32 MFMAs);
+// BM = 64: waves in 2 x 2, BN / 2 columns each (twice the blocks for short chunks). Per output the
+// sum runs over chunks, taps, 16-channel steps, hi then lo, in an order that does not depend on BM,
+// BN or T. The next chunk's loads are in flight during this chunk's MFMAs.
 // Lane layout of the 32x32x16 step (checked on the device): lane l holds A[l % 32][8 (l / 32) ..]
 // and B[8 (l / 32) ..][l % 32]; accumulator r of lane l is row 8 (r / 4) + 4 (l / 32) + r % 4,
 // column l % 32.
-template <int K, int BM, int EPI>
+template <int K, int BM, int BN, int EPI>
 __global__ void __launch_bounds__(BT) k_conv_wide(ConvArgs a) {
-    constexpr int CC = 32, LDA = CC + 8, BN = 64;           // channels per chunk, LDS row (halves), block columns
+    constexpr int CC = 32, LDA = CC + 8;                    // channels per chunk, LDS row (halves)
     constexpr int MAXWR = BM + (K - 1) * 9;                 // window rows at dilation <= 9
-    constexpr int NCT = BM == 128 ? 2 : 1;                  // 32-column tiles per wave
+    constexpr int NCT = BM == 128 ? BN / 32 : BN / 64;      // 32-column tiles per wave
+    static_assert(BN % 32 == 0 && (BM == 128 || (BM == 64 && BN % 64 == 0)), "tile shape");
     __shared__ __align__(16) _Float16 ahi[MAXWR * LDA];
     __shared__ __align__(16) _Float16 alo[MAXWR * LDA];
     __shared__ __align__(16) _Float16 bw[K * BN * LDA];
     const int wv = threadIdx.x >> 6, l = threadIdx.x & 63;
-    const int wr = BM == 128 ? 32 * wv : 32 * (wv >> 1), wc = BM == 128 ? 0 : 32 * (wv & 1);
-    const int n0 = blockIdx.x * BN, t0 = blockIdx.y * BM;
+    const int wr = BM == 128 ? 32 * wv : 32 * (wv >> 1), wc = BM == 128 ? 0 : (BN / 2) * (wv & 1);
+    const int n0 = blockIdx.x * BN, t0 = blockIdx.y * BM, phase = blockIdx.z;
     const int H = (K - 1) * a.dil, rows = BM + H;
     // A staging: 8 float4 per window row, thread -> rows (tid / 8) + 32 it, channels 4 (tid % 8);
     // each row's source (x, history or zeros) fixed for the launch
@@ -378,7 +380,7 @@ __global__ void __launch_bounds__(BT) k_conv_wide(ConvArgs a) {
 #pragma unroll
     for (int it = 0; it < ITB; ++it) {
         const int e = static_cast<int>(threadIdx.x) + BT * it, q = e & 3, ct = e >> 2, col = ct / K, tap = ct - col * K;
-        boff[it] = ((n0 + col) * K + tap) * a.Cin + 8 * q;
+        boff[it] = ((phase * a.Cout + n0 + col) * K + tap) * a.Cin + 8 * q;
         bl[it] = (tap * BN + col) * LDA + 8 * q;
     }
     f32x4_t av[ITA];
@@ -451,14 +453,15 @@ __global__ void __launch_bounds__(BT) k_conv_wide(ConvArgs a) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             const int t = t0 + wr + 8 * (r / 4) + 4 * (l >> 5) + (r & 3), co = n0 + wc + 32 * c + (l & 31);
-            res[c][r] = epi_has_res(EPI) && t < a.T ? gld(a.res + static_cast<size_t>(t) * a.ldy + co) : 0.f;
+            res[c][r] = epi_has_res(EPI) && t < a.T
+                            ? gld(a.res + (static_cast<size_t>(t) * a.phases + phase) * a.ldy + co) : 0.f;
         }
 #pragma unroll
     for (int c = 0; c < NCT; ++c)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             const int t = t0 + wr + 8 * (r / 4) + 4 * (l >> 5) + (r & 3), co = n0 + wc + 32 * c + (l & 31);
-            if (t < a.T) conv_store(a, EPI, static_cast<size_t>(t) * a.ldy + co, cc[c], acc[c][r], res[c][r]);
+            if (t < a.T) conv_store(a, EPI, (static_cast<size_t>(t) * a.phases + phase) * a.ldy + co, cc[c], acc[c][r], res[c][r]);
         }
     if (a.hnext) carry_rows(a.hist, a.x, a.ldx, a.T, H, a.Cin, a.hnext);
 }

@@ -457,25 +457,41 @@ bool launch_c96(const Conv &c, const ConvArgs &a, int pro, int epi, int T, hipSt
     return false;
 }
 
-// The decoder blocks' causal convs (K 7 or 1, one phase, 32 | Cin, 64 | Cout, at least 32 rows per
-// frame) run on k_conv_wide, with no K split. Decided at create from the conv's shape and place,
-// so every chunking of the codes runs the same kernel and sums in the same order.
+// The decoder blocks' causal convs (K 7, 2 or 1, any phases, 32 | Cin, 64 | Cout or Cout = 96 but
+// not the 96-channel k7, at least 32 input rows per frame) run on k_conv_wide, with no K split. Decided at create from the
+// conv's shape and place, so every chunking of the codes runs the same kernel and sums in the same
+// order.
 bool conv_takes_wide(const Conv &c, int rows_per_frame) {
-    return c.phases == 1 && (c.K == 7 || c.K == 1) && c.dil <= 9 && c.Cin % 32 == 0 && c.Cout % 64 == 0 && rows_per_frame >= 32 &&
-           !conv_is_c96(c);
+    if (c.Cout == 96 && c.K == 7) return false;      // k_conv_c96: measured faster for the last block's k7
+    return (c.K == 7 || c.K == 2 || c.K == 1) && c.dil <= 9 && c.Cin % 32 == 0 && (c.Cout % 64 == 0 || c.Cout == 96) &&
+           rows_per_frame >= 32;
 }
 
 bool launch_wide_conv(const Conv &c, const ConvArgs &a, int pro, int epi, int T, hipStream_t s) {
     if (pro != PRO_NONE) return false;
+    const int P = c.phases;
+    if (c.Cout == 96) {
+        const dim3 g(1, (T + 127) / 128, P);
+#define NAVI_W96(K_, E_)                                                                                           \
+        if (c.K == K_ && epi == E_) {                                                                              \
+            hipLaunchKernelGGL((k_conv_wide<K_, 128, 96, E_>), g, dim3(BT), 0, s, a);                             \
+            return true;                                                                                           \
+        }
+        NAVI_W96(2, EPI_BIAS)
+        NAVI_W96(1, EPI_RESIDUAL)
+#undef NAVI_W96
+        return false;
+    }
     const int nb = c.Cout / 64;
-    const bool big = static_cast<long>((T + 127) / 128) * nb >= 512;   // enough 128-row tiles to fill the chip twice
-#define NAVI_WIDE(K_, E_)                                                                                              \
-    if (c.K == K_ && epi == E_) {                                                                                      \
-        if (big) hipLaunchKernelGGL((k_conv_wide<K_, 128, E_>), dim3(nb, (T + 127) / 128), dim3(BT), 0, s, a);       \
-        else hipLaunchKernelGGL((k_conv_wide<K_, 64, E_>), dim3(nb, (T + 63) / 64), dim3(BT), 0, s, a);               \
-        return true;                                                                                                   \
+    const bool big = static_cast<long>((T + 127) / 128) * nb * P >= 512;   // enough 128-row tiles to fill the chip twice
+#define NAVI_WIDE(K_, E_)                                                                                          \
+    if (c.K == K_ && epi == E_) {                                                                                  \
+        if (big) hipLaunchKernelGGL((k_conv_wide<K_, 128, 64, E_>), dim3(nb, (T + 127) / 128, P), dim3(BT), 0, s, a); \
+        else hipLaunchKernelGGL((k_conv_wide<K_, 64, 64, E_>), dim3(nb, (T + 63) / 64, P), dim3(BT), 0, s, a);       \
+        return true;                                                                                               \
     }
     NAVI_WIDE(7, EPI_BIAS)
+    NAVI_WIDE(2, EPI_BIAS)
     NAVI_WIDE(1, EPI_RESIDUAL)
 #undef NAVI_WIDE
     return false;
