@@ -17,9 +17,8 @@ constexpr int LDW = CCH + 8;             // padded LDS row (halves)
 typedef _Float16 half8v __attribute__((ext_vector_type(8)));
 typedef _Float16 half4v __attribute__((ext_vector_type(4)));
 
-// Prologues (applied to the input as it is staged): SILU_GATE silu(x[ci]) * x[Cin + ci]; ADD2 x + x2;
-// RVQ: the input rows are not read from x but gathered from the codebooks by the frame's codes.
-enum Pro { PRO_NONE = 0, PRO_SILU_GATE = 2, PRO_ADD2 = 3, PRO_RVQ = 4 };
+// Prologues (applied to the input as it is staged): SILU_GATE silu(x[ci]) * x[Cin + ci]; ADD2 x + x2.
+enum Pro { PRO_NONE = 0, PRO_SILU_GATE = 2, PRO_ADD2 = 3 };
 // Epilogues after the bias: RELU_TANH is tanh(max(v, 0)); PARTIAL stores split-K partial sums.
 enum Epi { EPI_BIAS = 0, EPI_GELU = 1, EPI_RESIDUAL = 2, EPI_SCALE_RESIDUAL = 3, EPI_CLAMP = 4, EPI_PARTIAL = 5,
            EPI_RELU = 6, EPI_SIGMOID = 7, EPI_RELU_TANH = 8 };
@@ -43,8 +42,8 @@ struct ConvArgs {
     // When set: the causal history the next chunk reads (the last (K-1) dil rows of [hist ; x]),
     // written by this launch into the other buffer of the conv's history pair.
     float *hnext;
-    // PRO_RVQ: codes [T][nq]; input channel ci < Cin/2 of frame t is cb0[code 0][ci], channel
-    // Cin/2 + c the sum over q = 1..nq-1 of cbr[q-1][code q][c] (codebooks [cbsize][Cin/2] f16).
+    // RVQ rows (rvq_row4): codes [T][nq]; input channel ci < Cin/2 of frame t is cb0[code 0][ci],
+    // channel Cin/2 + c the sum over q = 1..nq-1 of cbr[q-1][code q][c] (codebooks [cbsize][Cin/2] f16).
     const int32_t *codes;
     const uint16_t *cb0, *cbr;
     int nq, cbsize;
@@ -127,8 +126,8 @@ __device__ __forceinline__ void carry_rows(const float *hist, const float *x, in
     }
 }
 
-// Four input channels ci..ci+3 of the RVQ front end at frame t (PRO_RVQ): the semantic codebook's
-// row, or the rest codebooks' rows summed in f32 in codebook order (k_rvq, vocoder.hip:125-143).
+// Four input channels ci..ci+3 of the RVQ front end at frame t: the semantic codebook's row, or
+// the rest codebooks' rows summed in f32 in codebook order (k_rvq, vocoder.hip:125-143).
 // All the row loads of the sum are issued before the first add.
 __device__ __forceinline__ f32x4_t rvq_row4(const ConvArgs &a, int t, int ci) {
     const int half = a.Cin >> 1;
@@ -177,8 +176,8 @@ __global__ void __launch_bounds__(BT) k_conv_mfma(ConvArgs a) {
     // Staging of the time window of one channel chunk: a thread owns the same 4 channels c4 of every
     // chunk and rows rr0 + 16 it of the window (IT of them). Where each of those rows comes from (a
     // row of x, of the history, or zeros) is the same for every chunk, so it is worked out once:
-    // off[it] is the element offset of the row's channel 0 in x (bit it of xm) or in hist (hm); for
-    // PRO_RVQ off[it] is the frame index. A chunk's loads (inputs, weights) are all issued at once,
+    // off[it] is the element offset of the row's channel 0 in x (bit it of xm) or in hist (hm). A
+    // chunk's loads (inputs, weights) are all issued at once,
     // and the next chunk's go out before this chunk's MFMAs, so no load waits on another.
     constexpr int Q4 = CCH / 4, RPI = BT / Q4;               // float4s per staged row, rows per item step
     constexpr int IT = (WROWS + RPI - 1) / RPI;
@@ -195,9 +194,9 @@ __global__ void __launch_bounds__(BT) k_conv_mfma(ConvArgs a) {
         off[it] = 0;
         if (r < rows) {
             if (t >= 0 && t < a.T) {
-                off[it] = PRO == PRO_RVQ ? t : t * a.ldx;
+                off[it] = t * a.ldx;
                 xm |= 1u << it;
-            } else if (t < 0 && a.hist && PRO != PRO_RVQ) {
+            } else if (t < 0 && a.hist) {
                 off[it] = (H + t) * a.Cin;
                 hm |= 1u << it;
             }
@@ -221,14 +220,10 @@ __global__ void __launch_bounds__(BT) k_conv_mfma(ConvArgs a) {
             if (TWO) au[it] = av[it];
             if (!in) continue;
             if ((xm >> it) & 1u) {
-                if (PRO == PRO_RVQ) {
-                    av[it] = rvq_row4(a, off[it], ci);
-                } else {
-                    const float *row = a.x + off[it];
-                    av[it] = *(const NAVI_GLOBAL f32x4_t *) (row + ci);
-                    if (PRO == PRO_SILU_GATE) au[it] = *(const NAVI_GLOBAL f32x4_t *) (row + a.Cin + ci);
-                    if (PRO == PRO_ADD2) au[it] = *(const NAVI_GLOBAL f32x4_t *) (a.x2 + off[it] + ci);
-                }
+                const float *row = a.x + off[it];
+                av[it] = *(const NAVI_GLOBAL f32x4_t *) (row + ci);
+                if (PRO == PRO_SILU_GATE) au[it] = *(const NAVI_GLOBAL f32x4_t *) (row + a.Cin + ci);
+                if (PRO == PRO_ADD2) au[it] = *(const NAVI_GLOBAL f32x4_t *) (a.x2 + off[it] + ci);
             } else if ((hm >> it) & 1u) {
                 av[it] = *(const NAVI_GLOBAL f32x4_t *) (a.hist + off[it] + ci);
             }

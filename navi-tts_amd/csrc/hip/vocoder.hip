@@ -19,13 +19,16 @@
 //  * Few output tiles (short chunks, narrow layers): the input channels are split over up to
 //    S blocks per tile and the partial sums added in split order by a finish kernel, so a
 //    16-frame chunk still spreads over the 256 CUs.
-//  * The last decoder block's 96-channel convs and the final conv run on k_conv_c96: a block
-//    stages its whole input window and each tap's weights in LDS and covers every output
-//    channel, reading the input ~1.4x instead of ~3.7x.
-//  * The RVQ front end is the first conv's prologue (its input rows are gathered from the
-//    codebooks while being staged); RoPE and the K/V ring append are folded into the windowed
-//    attention kernel; the ConvNeXt depthwise conv + LayerNorm runs one wave per row with
-//    register-only reductions.
+//  * The decoder blocks' convs (k7, k1 and the transposed convs' phases) run on k_conv_wide
+//    (conv.h): v_mfma_f32_32x32x16_f16 on 128- or 64-row x 64- or 96-column tiles, the time
+//    window and every tap's weights staged in LDS per 32-channel chunk, no K split. The last
+//    block's 96-channel k7 and the final conv run on k_conv_c96 (whole input window and each
+//    tap's weights in LDS, every output channel in one block).
+//  * The transformer's projections run on the fused row kernels of rows.h (RMSNorm, SwiGLU and
+//    the layer-scaled residual add inside; 5 launches per layer). RoPE and the K/V ring append
+//    are folded into the windowed attention kernel; the RVQ rows are gathered by one small
+//    kernel; the ConvNeXt depthwise conv + LayerNorm runs one wave per row with register-only
+//    reductions.
 //  * Streaming state: each causal conv keeps its last (K-1)*dil input rows (the history the
 //    next chunk's first rows read), the ConvNeXt depthwise conv its last 6, the attention its
 //    K/V in a ring of >= window + chunk positions: chunked decoding equals one-shot decoding.
@@ -267,6 +270,17 @@ __global__ void __launch_bounds__(BT) k_window_attention(const float *qkv, int n
     }
 }
 
+// The RVQ front end's input rows (k_rvq, vocoder.hip:125-143): channel ci < CD/2 of frame t is the
+// semantic codebook's row for code 0, the rest the other codebooks' rows summed in codebook order;
+// one float4 per thread, all of its codebook loads issued before the sum. A kernel of its own: as
+// the first conv's prologue every one of that conv's column blocks repeated the gathers.
+__global__ void __launch_bounds__(BT) k_rvq_rows(ConvArgs a, float *out) {
+    const int q4 = a.Cin / 4, i = blockIdx.x * BT + threadIdx.x;
+    if (i >= a.T * q4) return;
+    const int t = i / q4, ci = (i - t * q4) * 4;
+    st4(out + static_cast<size_t>(t) * a.Cin + ci, rvq_row4(a, t, ci));
+}
+
 // The utterance position after a chunk of T frames (the last kernel of a chunk).
 __global__ void k_advance_pos(int *pos0, int T) {
     if (threadIdx.x == 0) gst(pos0, gld(pos0) + T);
@@ -369,6 +383,7 @@ struct navi_vocoder {
     uint32_t *flag = nullptr;
     // activations of one chunk (time-major rows)
     int32_t *d_codes = nullptr;
+    float *lat_in = nullptr;           // RVQ rows gathered from the codebooks [T][CD]
     float *lat = nullptr;              // RVQ latent [T][CD]
     float *pre = nullptr;              // pre_conv output [T][L]
     float *xs = nullptr, *xn = nullptr;   // transformer residual stream and its RMSNorm [T][VH]
@@ -426,10 +441,6 @@ void launch_k(const ConvArgs &a, int pro, int epi, dim3 grid, hipStream_t s) {
     NAVI_CONV(PRO_NONE, EPI_PARTIAL)
     NAVI_CONV(PRO_SILU_GATE, EPI_SCALE_RESIDUAL)
     NAVI_CONV(PRO_SILU_GATE, EPI_PARTIAL)
-    if constexpr (K == 1) {
-        NAVI_CONV(PRO_RVQ, EPI_BIAS)
-        NAVI_CONV(PRO_RVQ, EPI_PARTIAL)
-    }
 #undef NAVI_CONV
 }
 
@@ -551,8 +562,7 @@ navi_status launch_generic(navi_vocoder &v, const Conv &c, ConvArgs &a, int pro,
 
 // Runs one conv over T input rows. A causal conv reads its history and writes the next chunk's
 // into the other buffer of its pair (the pair then swaps). z (optional): also write Snake(y) with
-// the Snake parameters of zc, the conv that consumes this output. PRO_RVQ takes no x: its rows
-// are gathered from the codebooks by the chunk's codes.
+// the Snake parameters of zc, the conv that consumes this output.
 navi_status run_conv(navi_vocoder &v, Conv &c, int pro, int epi, const float *x, int T, int ldx, float *y, int ldy,
                      const float *res, const float *scale, char *err, size_t errlen, float *z = nullptr,
                      const Conv *zc = nullptr) {
@@ -561,9 +571,6 @@ navi_status run_conv(navi_vocoder &v, Conv &c, int pro, int epi, const float *x,
     a.y = y; a.z = z; a.flag = v.flag; a.ldx = ldx; a.ldy = ldy; a.T = T; a.Cin = c.Cin; a.Cout = c.Cout;
     a.dil = c.dil; a.phases = c.phases; a.lpad = (c.K - 1) * c.dil;   // causal
     a.hnext = c.H > 0 ? c.hbuf[v.parity ^ 1] : nullptr;
-    if (pro == PRO_RVQ) {
-        a.codes = v.d_codes; a.cb0 = v.cb_first; a.cbr = v.cb_rest; a.nq = v.p.n_q; a.cbsize = v.p.codebook_size;
-    }
     if (z) {
         a.za = zc->sa;
         a.zb = zc->sb;
@@ -625,7 +632,13 @@ navi_status decode_chunk(navi_vocoder &v, int T, char *err, size_t errlen) {
     const navi_vocoder_params &p = v.p;
     const int VH = v.VH, L = v.L, HDT = v.HDT, FF = p.xf.ff, CD = v.CD, nh = p.xf.n_head;
     // RVQ front end and its two output projections, one conv gathering its rows from the codebooks
-    VOC_TRY(run_conv(v, v.rvq_proj, PRO_RVQ, EPI_BIAS, nullptr, T, CD, v.lat, CD, nullptr, nullptr, err, errlen));
+    {
+        ConvArgs ra{};
+        ra.codes = v.d_codes; ra.cb0 = v.cb_first; ra.cbr = v.cb_rest; ra.nq = p.n_q; ra.cbsize = p.codebook_size;
+        ra.T = T; ra.Cin = CD;
+        hipLaunchKernelGGL(k_rvq_rows, dim3((T * (CD / 4) + BT - 1) / BT), dim3(BT), 0, s, ra, v.lat_in);
+    }
+    VOC_TRY(run_conv(v, v.rvq_proj, PRO_NONE, EPI_BIAS, v.lat_in, T, CD, v.lat, CD, nullptr, nullptr, err, errlen));
     VOC_TRY(snap(v, "rvq", v.lat, T, CD, err, errlen));
     VOC_TRY(run_conv(v, v.pre_conv, PRO_NONE, EPI_BIAS, v.lat, T, CD, v.pre, L, nullptr, nullptr, err, errlen));
     VOC_TRY(snap(v, "pre_conv", v.pre, T, L, err, errlen));
@@ -1059,6 +1072,7 @@ navi_status navi_vocoder_create(const navi_vocoder_params *p, const navi_tensor_
     VA(v->flag, 1);
     VA(v->d_pos0, 1);
     VA(v->d_codes, C * p->n_q);
+    VA(v->lat_in, C * CD);
     VA(v->lat, C * CD);
     VA(v->pre, C * L);
     VA(v->xs, C * VH);
