@@ -336,9 +336,10 @@ typedef float f32x16_t __attribute__((ext_vector_type(16)));
 // Lane layout of the 32x32x16 step (checked on the device): lane l holds A[l % 32][8 (l / 32) ..]
 // and B[8 (l / 32) ..][l % 32]; accumulator r of lane l is row 8 (r / 4) + 4 (l / 32) + r % 4,
 // column l % 32.
-template <int K, int BM, int BN, int EPI>
+template <int K, int BM, int BN, int EPI, int CC = 32>
 __global__ void __launch_bounds__(BT) k_conv_wide(ConvArgs a) {
-    constexpr int CC = 32, LDA = CC + 8;                    // channels per chunk, LDS row (halves)
+    constexpr int LDA = CC + 8;                             // LDS row (halves)
+    static_assert(CC == 32 || CC == 16, "channels per chunk");
     constexpr int MAXWR = BM + (K - 1) * 9;                 // window rows at dilation <= 9
     constexpr int NCT = BM == 128 ? BN / 32 : BN / 64;      // 32-column tiles per wave
     static_assert(BN % 32 == 0 && (BM == 128 || (BM == 64 && BN % 64 == 0)), "tile shape");
@@ -369,12 +370,12 @@ __global__ void __launch_bounds__(BT) k_conv_wide(ConvArgs a) {
             }
         }
     }
-    // B staging: the 64 B of channels [ci0, ci0 + 32) of (column, tap), in four 16 B pieces
-    constexpr int NBI = BN * K * 4, ITB = (NBI + BT - 1) / BT;
+    // B staging: channels [ci0, ci0 + CC) of (column, tap), in CC / 8 pieces of 16 B
+    constexpr int QB = CC / 8, NBI = BN * K * QB, ITB = (NBI + BT - 1) / BT;
     int boff[ITB], bl[ITB];
 #pragma unroll
     for (int it = 0; it < ITB; ++it) {
-        const int e = static_cast<int>(threadIdx.x) + BT * it, q = e & 3, ct = e >> 2, col = ct / K, tap = ct - col * K;
+        const int e = static_cast<int>(threadIdx.x) + BT * it, q = e % QB, ct = e / QB, col = ct / K, tap = ct - col * K;
         boff[it] = ((phase * a.Cout + n0 + col) * K + tap) * a.Cin + 8 * q;
         bl[it] = (tap * BN + col) * LDA + 8 * q;
     }

@@ -473,7 +473,6 @@ bool launch_c96(const Conv &c, const ConvArgs &a, int pro, int epi, int T, hipSt
 // conv's shape and place, so every chunking of the codes runs the same kernel and sums in the same
 // order.
 bool conv_takes_wide(const Conv &c, int rows_per_frame) {
-    if (c.Cout == 96 && c.K == 7) return false;      // k_conv_c96: measured faster for the last block's k7
     return (c.K == 7 || c.K == 2 || c.K == 1) && c.dil <= 9 && c.Cin % 32 == 0 && (c.Cout % 64 == 0 || c.Cout == 96) &&
            rows_per_frame >= 32;
 }
@@ -487,6 +486,10 @@ bool launch_wide_conv(const Conv &c, const ConvArgs &a, int pro, int epi, int T,
         if (c.K == K_ && epi == E_) {                                                                              \
             hipLaunchKernelGGL((k_conv_wide<K_, 128, 96, E_>), g, dim3(BT), 0, s, a);                             \
             return true;                                                                                           \
+        }
+        if (c.K == 7 && epi == EPI_BIAS) {
+            hipLaunchKernelGGL((k_conv_wide<7, 128, 96, EPI_BIAS, 16>), g, dim3(BT), 0, s, a);
+            return true;
         }
         NAVI_W96(2, EPI_BIAS)
         NAVI_W96(1, EPI_RESIDUAL)
