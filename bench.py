@@ -68,11 +68,29 @@ def copy_calibration(gib: float, reps: int):
     print(json.dumps({"copy_calibration": {"bytes_read": 4 * n, "bytes_written": 4 * n, "dispatches": reps}}), flush=True)
 
 
+FRAME_SOURCES = ("frame.hip", "sampler.h", "dev_common.h", "host_util.h")
+
+
+def frame_source_digest() -> str:
+    """sha1 over the sources k_frame is compiled from: the counter run behind the traffic figure is
+    valid only for the kernel those sources build."""
+    import hashlib
+    h = hashlib.sha1()
+    for name in FRAME_SOURCES:
+        h.update((ROOT / "navi-tts_amd" / "csrc" / "hip" / name).read_bytes())
+    return h.hexdigest()
+
+
 def measured_traffic():
-    """HBM bytes per k_frame launch from the committed counter runs (None when absent)."""
+    """HBM bytes per k_frame launch from the committed counter runs: None when the file is absent or
+    was measured on other kernel sources than the ones built now (its `frame_sources_sha1`)."""
     if not TRAFFIC_FILE.exists():
         return None
     t = json.loads(TRAFFIC_FILE.read_text())
+    if t.get("frame_sources_sha1") != frame_source_digest():
+        print("[bench] profiles/k_frame_n256_traffic.json was measured on other k_frame sources: traffic null",
+              file=sys.stderr)
+        return None
     return int(t["frame_bytes_per_launch"])
 
 
