@@ -7,9 +7,11 @@
 // same seeds, same sampling rules, same step assembly, so stream i computes what navi_frame_run
 // computes for it alone, up to the summation order of the projections. MI355X design:
 //
-//  * Projections: the prefill's split-K MFMA linear (activations as f16 hi + lo pairs, f16
-//    weights) with M = n streams (code-predictor positions 0 and 1: 2n rows). Every weight byte
-//    streams from HBM once per step for all streams, so the weights cost 3.3 GB per step whatever n.
+//  * Projections: the whole-K MFMA row kernels of rows.h (activations as f16 hi + lo pairs, f16
+//    weights) with M = n streams (code-predictor positions 0 and 1: 2n rows), the RMSNorm, SwiGLU
+//    and residual add fused in. Every weight byte streams from HBM once per step for all streams
+//    (twice for the residual projections above 16 rows), so the weights cost ~3.3 GB per step
+//    whatever n. The step (610 launches) is captured once as a HIP graph and replayed.
 //  * Talker attention: split-KV decode attention, one block per (stream, kv head, key range); the
 //    two q heads of a GQA group share the K/V loads (one key per thread for the scores, eight
 //    keys' V rows in flight per wave); a combine kernel merges the ranges' (max, sum, vector).
