@@ -75,13 +75,18 @@ def build_hip(jobs: int = 8) -> Path:
     return out
 
 
-def build_bench() -> Path:
-    """The hop-latency microbenchmark of the frame kernel's exchange primitive (a standalone program)."""
+def build_bench() -> list[Path]:
+    """The microbenchmarks behind the design's latency figures (standalone programs): the frame
+    kernel's exchange hop, and the dependent-launch floor of the row-projection chains."""
     LIB.mkdir(parents=True, exist_ok=True)
-    out = LIB / "hop_latency"
-    _run([HIPCC, "-O3", "-std=c++17", f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-          "-o", str(out), str(PKG / "csrc" / "bench" / "hop_latency.hip")])
-    return out
+    outs = []
+    for name in ("hop_latency", "launch_floor"):
+        out = LIB / name
+        _run([HIPCC, "-O3", "-std=c++17", f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+              "-I", str(ROOT / "include"), "-I", str(PKG / "csrc" / "hip"),
+              "-o", str(out), str(PKG / "csrc" / "bench" / (name + ".hip"))])
+        outs.append(out)
+    return outs
 
 
 def build_all() -> None:
