@@ -589,6 +589,208 @@ __global__ void __launch_bounds__(BT) k_conv_c96(ConvArgs a) {
     if (a.hnext) carry_rows(a.hist, a.x, a.ldx, a.T, H, CIN, a.hnext);
 }
 
+// One residual unit of the codec decoder's last block (96 channels) in one kernel: the Snake'd
+// residual stream x -> k7 conv (dilation dil) + bias -> Snake with the k1's parameters -> k1 conv
+// + bias + the residual -> y, and y's Snake with the next conv's parameters -> z. The k7 part is
+// k_conv_wide<7, 128, 96, EPI_BIAS, 16>'s (same staging, same order of sums); its output tile
+// (128 rows x 96 channels) goes through the Snake into LDS as f16 hi + lo, where the k1 reads it
+// as its A operand, with the k1's weights staged once per block: the intermediate never goes to
+// memory and the unit is one launch. The k1 sums 16-channel steps in channel order, hi then lo,
+// as the separate k1 launch did, so the output is the two-launch path's.
+struct UnitArgs {
+    const float *x, *hist;              // k7 input rows [T][96] and its history [6 dil][96]
+    float *hnext;                       // the next chunk's k7 history (the other buffer of its pair)
+    const uint16_t *w7, *w1;            // [96][7][96] and [96][96] f16
+    const float *b7, *b1;               // [96]
+    const float *za_mid, *zb_mid;       // the Snake on the k1's input
+    const float *res;                   // the residual stream [T][96]
+    float *y;                           // the unit's output [T][96] (may be res itself), or null
+    float *z;                           // Snake(y) with (za, zb): the next conv's input
+    const float *za, *zb;
+    uint32_t *flag;
+    int T, dil;
+};
+
+__global__ void __launch_bounds__(BT) k_unit96(UnitArgs u) {
+    constexpr int C = 96, K = 7, BM = 128, CC = 16, LDA = CC + 8, NCT = 3;
+    constexpr int MAXWR = BM + (K - 1) * 9, LDM = C + 8;
+    constexpr int A_BYTES = MAXWR * LDA * 2 * 2, B_BYTES = K * C * LDA * 2;           // k7 staging
+    constexpr int M_BYTES = BM * LDM * 2 * 2, W_BYTES = C * LDM * 2;                  // k1 operands
+    constexpr int SMEM = (A_BYTES + B_BYTES > M_BYTES + W_BYTES ? A_BYTES + B_BYTES : M_BYTES + W_BYTES);
+    __shared__ __align__(16) unsigned char smem[SMEM];
+    _Float16 *ahi = reinterpret_cast<_Float16 *>(smem), *alo = ahi + MAXWR * LDA, *bw = alo + MAXWR * LDA;
+    _Float16 *mhi = reinterpret_cast<_Float16 *>(smem), *mlo = mhi + BM * LDM, *w1s = mlo + BM * LDM;
+    const int wv = threadIdx.x >> 6, l = threadIdx.x & 63, wr = 32 * wv;
+    const int t0 = blockIdx.x * BM;
+    const int H = (K - 1) * u.dil, rows = BM + H, lpad = H;
+    // the k1's weights: loaded now, staged in LDS after the k7 (18 KB, 16 B per thread per step)
+    constexpr int W1Q = C * C / 8, ITW = (W1Q + BT - 1) / BT;
+    u32x4_t w1r[ITW];
+#pragma unroll
+    for (int it = 0; it < ITW; ++it) {
+        const int e = static_cast<int>(threadIdx.x) + BT * it;
+        if (e < W1Q) w1r[it] = *(const NAVI_GLOBAL u32x4_t *) (u.w1 + static_cast<size_t>(e) * 8);
+    }
+    // ---- k7: as k_conv_wide<7, 128, 96, EPI_BIAS, 16> ----
+    constexpr int RPI = BT / (CC / 4), ITA = (MAXWR + RPI - 1) / RPI;
+    const int c4 = (static_cast<int>(threadIdx.x) % (CC / 4)) * 4, rr0 = static_cast<int>(threadIdx.x) / (CC / 4);
+    int aoff[ITA];
+    uint32_t xm = 0, hm = 0;
+#pragma unroll
+    for (int it = 0; it < ITA; ++it) {
+        const int r = rr0 + RPI * it, t = t0 - lpad + r;
+        aoff[it] = 0;
+        if (r < rows) {
+            if (t >= 0 && t < u.T) {
+                aoff[it] = t * C + c4;
+                xm |= 1u << it;
+            } else if (t < 0 && u.hist) {
+                aoff[it] = (H + t) * C + c4;
+                hm |= 1u << it;
+            }
+        }
+    }
+    constexpr int QB = CC / 8, NBI = C * K * QB, ITB = (NBI + BT - 1) / BT;
+    int boff[ITB], bl[ITB];
+#pragma unroll
+    for (int it = 0; it < ITB; ++it) {
+        const int e = static_cast<int>(threadIdx.x) + BT * it, q = e % QB, ct = e / QB, col = ct / K, tap = ct - col * K;
+        boff[it] = (col * K + tap) * C + 8 * q;
+        bl[it] = (tap * C + col) * LDA + 8 * q;
+    }
+    f32x4_t av[ITA];
+    u32x4_t bv[ITB];
+    auto load = [&](int ci0) {
+#pragma unroll
+        for (int it = 0; it < ITA; ++it) {
+            av[it] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+            if ((xm >> it) & 1u) av[it] = *(const NAVI_GLOBAL f32x4_t *) (u.x + aoff[it] + ci0);
+            else if ((hm >> it) & 1u) av[it] = *(const NAVI_GLOBAL f32x4_t *) (u.hist + aoff[it] + ci0);
+        }
+#pragma unroll
+        for (int it = 0; it < ITB; ++it)
+            if (ITB * BT == NBI || static_cast<int>(threadIdx.x) + BT * it < NBI)
+                bv[it] = __builtin_nontemporal_load((const NAVI_GLOBAL u32x4_t *) (u.w7 + boff[it] + ci0));
+    };
+    f32x16_t acc[NCT];
+#pragma unroll
+    for (int c = 0; c < NCT; ++c)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[c][r] = 0.f;
+    bool bad = false;
+    load(0);
+    for (int ci0 = 0; ci0 < C; ci0 += CC) {
+        __syncthreads();
+#pragma unroll
+        for (int it = 0; it < ITA; ++it) {
+            const int r = rr0 + RPI * it;
+            if (r >= rows) continue;
+            half4v h, o;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                bad |= !(fabsf(av[it][e]) < 65504.f);
+                h[e] = static_cast<_Float16>(av[it][e]);
+                o[e] = static_cast<_Float16>(av[it][e] - static_cast<float>(h[e]));
+            }
+            *reinterpret_cast<half4v *>(&ahi[r * LDA + c4]) = h;
+            *reinterpret_cast<half4v *>(&alo[r * LDA + c4]) = o;
+        }
+#pragma unroll
+        for (int it = 0; it < ITB; ++it)
+            if (ITB * BT == NBI || static_cast<int>(threadIdx.x) + BT * it < NBI)
+                *reinterpret_cast<u32x4_t *>(&bw[bl[it]]) = bv[it];
+        __syncthreads();
+        if (ci0 + CC < C) load(ci0 + CC);
+#pragma unroll
+        for (int j = 0; j < K; ++j) {
+            const int ar = (wr + (l & 31) + j * u.dil) * LDA + 8 * (l >> 5);
+            const half8v h = *reinterpret_cast<const half8v *>(&ahi[ar]);
+            const half8v o = *reinterpret_cast<const half8v *>(&alo[ar]);
+#pragma unroll
+            for (int c = 0; c < NCT; ++c) {
+                const half8v b = *reinterpret_cast<const half8v *>(&bw[(j * C + 32 * c + (l & 31)) * LDA + 8 * (l >> 5)]);
+                acc[c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(h, b, acc[c], 0, 0, 0);
+                acc[c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(o, b, acc[c], 0, 0, 0);
+            }
+        }
+    }
+    // ---- the k7's output through the k1's Snake into LDS (hi + lo), the k1's weights beside it ----
+    float b7c[NCT], zam[NCT], zbm[NCT];
+#pragma unroll
+    for (int c = 0; c < NCT; ++c) {
+        const int co = 32 * c + (l & 31);
+        b7c[c] = gld(u.b7 + co);
+        zam[c] = gld(u.za_mid + co);
+        zbm[c] = gld(u.zb_mid + co);
+    }
+    __syncthreads();                                        // every wave is done with the k7 staging
+#pragma unroll
+    for (int c = 0; c < NCT; ++c)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int row = wr + 8 * (r / 4) + 4 * (l >> 5) + (r & 3), co = 32 * c + (l & 31);
+            const float m = snake(acc[c][r] + b7c[c], zam[c], zbm[c]);
+            if (t0 + row < u.T) bad |= !(fabsf(m) < 65504.f);
+            const _Float16 h = static_cast<_Float16>(m);
+            mhi[row * LDM + co] = h;
+            mlo[row * LDM + co] = static_cast<_Float16>(m - static_cast<float>(h));
+        }
+#pragma unroll
+    for (int it = 0; it < ITW; ++it) {
+        const int e = static_cast<int>(threadIdx.x) + BT * it;
+        if (e < W1Q) {
+            const int col = e / (C / 8), q = e - col * (C / 8);
+            *reinterpret_cast<u32x4_t *>(&w1s[col * LDM + 8 * q]) = w1r[it];
+        }
+    }
+    if (bad) gst(u.flag, 1u);
+    __syncthreads();
+    // ---- k1 over the 96 channels: 16-channel steps in order, hi then lo ----
+    f32x16_t acc1[NCT];
+#pragma unroll
+    for (int c = 0; c < NCT; ++c)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc1[c][r] = 0.f;
+#pragma unroll
+    for (int ks = 0; ks < C / 16; ++ks) {
+        const int ar = (wr + (l & 31)) * LDM + 16 * ks + 8 * (l >> 5);
+        const half8v h = *reinterpret_cast<const half8v *>(&mhi[ar]);
+        const half8v o = *reinterpret_cast<const half8v *>(&mlo[ar]);
+#pragma unroll
+        for (int c = 0; c < NCT; ++c) {
+            const half8v b = *reinterpret_cast<const half8v *>(&w1s[(32 * c + (l & 31)) * LDM + 16 * ks + 8 * (l >> 5)]);
+            acc1[c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(h, b, acc1[c], 0, 0, 0);
+            acc1[c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(o, b, acc1[c], 0, 0, 0);
+        }
+    }
+    // ---- epilogue: every load first (column operands, residuals), then the stores ----
+    float b1c[NCT], zac[NCT], zbc[NCT], rs[NCT][16];
+#pragma unroll
+    for (int c = 0; c < NCT; ++c) {
+        const int co = 32 * c + (l & 31);
+        b1c[c] = gld(u.b1 + co);
+        zac[c] = gld(u.za + co);
+        zbc[c] = gld(u.zb + co);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int t = t0 + wr + 8 * (r / 4) + 4 * (l >> 5) + (r & 3);
+            rs[c][r] = t < u.T ? gld(u.res + static_cast<size_t>(t) * C + co) : 0.f;
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < NCT; ++c)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int t = t0 + wr + 8 * (r / 4) + 4 * (l >> 5) + (r & 3), co = 32 * c + (l & 31);
+            if (t >= u.T) continue;
+            const float v = (acc1[c][r] + b1c[c]) + rs[c][r];
+            const size_t o = static_cast<size_t>(t) * C + co;
+            if (u.y) gst(u.y + o, v);
+            gst(u.z + o, snake(v, zac[c], zbc[c]));
+        }
+    if (u.hnext) carry_rows(u.hist, u.x, C, u.T, H, C, u.hnext);
+}
+
 // Sum of the K-split partials in split order, then the epilogue (EPI_PARTIAL's second half).
 // (kernels in an unnamed namespace: every including file gets its own)
 __global__ void __launch_bounds__(BT) k_conv_finish(ConvArgs a, int splits, int epi) {

@@ -511,6 +511,21 @@ bool launch_wide_conv(const Conv &c, const ConvArgs &a, int pro, int epi, int T,
     return false;
 }
 
+// A residual unit of the last decoder block (96 channels: k7 then k1, one phase each) runs as one
+// kernel, k_unit96 (conv.h): the k7's Snake'd output stays in LDS as the k1's input.
+bool unit_fused(const Unit &u) {
+    return u.c1.Cin == 96 && u.c1.Cout == 96 && u.c1.K == 7 && u.c1.phases == 1 && u.c1.dil <= 9 && u.c2.Cin == 96 &&
+           u.c2.Cout == 96 && u.c2.K == 1 && u.c2.phases == 1;
+}
+
+void launch_unit96(navi_vocoder &v, Unit &u, const float *x, int T, const float *res, float *y, float *z, const Conv &next) {
+    UnitArgs a{};
+    a.x = x; a.hist = u.c1.hbuf[v.parity]; a.hnext = u.c1.H > 0 ? u.c1.hbuf[v.parity ^ 1] : nullptr;
+    a.w7 = u.c1.w; a.w1 = u.c2.w; a.b7 = u.c1.bias; a.b1 = u.c2.bias; a.za_mid = u.c2.sa; a.zb_mid = u.c2.sb;
+    a.res = res; a.y = y; a.z = z; a.za = next.sa; a.zb = next.sb; a.flag = v.flag; a.T = T; a.dil = u.c1.dil;
+    hipLaunchKernelGGL(k_unit96, dim3((T + 127) / 128), dim3(BT), 0, device_state().stream, a);
+}
+
 // Input-channel splits of a conv over T rows: when the output tiles alone would leave most of the
 // 256 CUs idle, the channel chunks are spread over up to S blocks per tile (at least 2 chunks each)
 // and summed by k_conv_finish.
@@ -718,15 +733,27 @@ navi_status decode_chunk(navi_vocoder &v, int T, char *err, size_t errlen) {
         ch = bk.Cout;
         const std::string bs = "dec" + std::to_string(b + 1) + "_b";
         VOC_TRY(snap(v, bs + "1", v.res[b], rows, ch, err, errlen));
+        float *unit_in = v.res_s[b];           // the Snake'd residual stream a unit reads
         for (int k = 0; k < 3; ++k) {
             const Conv *next = k < 2 ? &bk.u[k + 1].c1 : b < 3 ? &v.blocks[b + 1].up : &v.final_conv;
-            VOC_TRY(run_conv(v, bk.u[k].c1, PRO_NONE, EPI_BIAS, v.res_s[b], rows, ch, nullptr, ch, nullptr, nullptr, err,
-                             errlen, v.mid_s[b], &bk.u[k].c2));
-            VOC_TRY(run_conv(v, bk.u[k].c2, PRO_NONE, EPI_RESIDUAL, v.mid_s[b], rows, ch, v.res[b], ch, v.res[b], nullptr, err,
-                             errlen, v.res_s[b], next));
+            // the last unit's raw output is read by nothing but the stage hook (the next stage
+            // takes its Snake'd copy)
+            float *y = k < 2 || v.hook ? v.res[b] : nullptr;
+            if (unit_fused(bk.u[k])) {
+                // one launch reads unit_in (its k7 window reaches into the neighbouring blocks'
+                // rows) while it writes the Snake'd output, so that goes to the other buffer
+                float *unit_out = unit_in == v.res_s[b] ? v.mid_s[b] : v.res_s[b];
+                launch_unit96(v, bk.u[k], unit_in, rows, v.res[b], y, unit_out, *next);
+                unit_in = unit_out;
+            } else {
+                VOC_TRY(run_conv(v, bk.u[k].c1, PRO_NONE, EPI_BIAS, v.res_s[b], rows, ch, nullptr, ch, nullptr, nullptr, err,
+                                 errlen, v.mid_s[b], &bk.u[k].c2));
+                VOC_TRY(run_conv(v, bk.u[k].c2, PRO_NONE, EPI_RESIDUAL, v.mid_s[b], rows, ch, y, ch, v.res[b], nullptr, err,
+                                 errlen, v.res_s[b], next));
+            }
             VOC_TRY(snap(v, bs + std::to_string(2 + k), v.res[b], rows, ch, err, errlen));
         }
-        blk_in = v.res_s[b];
+        blk_in = unit_in;
     }
     VOC_TRY(run_conv(v, v.final_conv, PRO_NONE, EPI_CLAMP, blk_in, rows, ch, v.pcm16, 16, nullptr, nullptr, err, errlen));
     hipLaunchKernelGGL(k_take_col0, dim3((rows + BT - 1) / BT), dim3(BT), 0, s, v.pcm16, rows, 16, v.pcm);
