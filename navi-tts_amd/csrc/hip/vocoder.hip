@@ -439,16 +439,15 @@ void launch_k(const ConvArgs &a, int pro, int epi, dim3 grid, hipStream_t s) {
     NAVI_CONV(PRO_NONE, EPI_SCALE_RESIDUAL)
     NAVI_CONV(PRO_NONE, EPI_CLAMP)
     NAVI_CONV(PRO_NONE, EPI_PARTIAL)
-    NAVI_CONV(PRO_SILU_GATE, EPI_SCALE_RESIDUAL)
-    NAVI_CONV(PRO_SILU_GATE, EPI_PARTIAL)
 #undef NAVI_CONV
 }
 
 int conv_mt(int T) { return T <= 16 ? 1 : 4; }
 
-// The 96-channel convs of the last decoder block (k7 and k1) and the final 96 -> 16 conv run on
-// k_conv_c96 (input window and weights staged in LDS, every output channel in one block). Chosen
-// by the conv's shape only, so every chunking of the codes runs the same kernel.
+// The final 96 -> 16 conv (one output channel padded to a 16-column tile) runs on k_conv_c96
+// (input window and weights staged in LDS, every output channel in one block); the last block's
+// own 96-channel convs take k_conv_wide / k_unit96 first. Chosen by the conv's shape only, so
+// every chunking of the codes runs the same kernel.
 bool conv_is_c96(const Conv &c) {
     return c.phases == 1 && c.S == 1 && c.dil <= 9 && (c.K == 7 || c.K == 1) && c.Cin == 96 && (c.Cout == 96 || c.Cout == 16);
 }
@@ -461,8 +460,6 @@ bool launch_c96(const Conv &c, const ConvArgs &a, int pro, int epi, int T, hipSt
         hipLaunchKernelGGL((k_conv_c96<K_, NCT_, 2, E_>), grid, dim3(BT), 0, s, a);             \
         return true;                                                                            \
     }
-    NAVI_C96(7, 6, EPI_BIAS)
-    NAVI_C96(1, 6, EPI_RESIDUAL)
     NAVI_C96(7, 1, EPI_CLAMP)
 #undef NAVI_C96
     return false;
