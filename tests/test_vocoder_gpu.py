@@ -60,6 +60,22 @@ def test_chunked_equals_one_shot(codec):
     assert d1 <= 1e-5 and d2 <= 1e-5
 
 
+def test_tile_shapes_do_not_change_the_pcm(codec):
+    """The decoder blocks' convs pick 128- or 64-row tiles by the chunk's row count (k_conv_wide: the
+    192-channel block takes 128-row tiles at 40 frames, 64-row tiles at 16) and the transformer's row
+    kernels more row tiles per block for more rows: a column's sums keep their order in every case,
+    so 40 frames decoded as one block and as 16-frame chunks (16 + 16 + 8) give the same PCM bit for bit. (Both handles hold at least 16
+    frames, so their input-channel split counts, fixed at create from a 16-frame chunk, agree.)"""
+    abi, W, _ = codec
+    codes = np.random.default_rng(5).integers(0, 2048, (40, 16))
+    one = abi.Vocoder(W, max_chunk_frames=40)
+    block = one.decode(codes)
+    small = abi.Vocoder(W, max_chunk_frames=16)
+    chunks = small.decode(codes)
+    log(f"40-frame block vs 16-frame chunks: max diff {np.abs(block - chunks).max():.2e}")
+    assert np.array_equal(block, chunks)
+
+
 def test_reset_restarts_the_utterance(codec):
     abi, W, _ = codec
     codes = np.random.default_rng(2).integers(0, 2048, (6, 16))
