@@ -281,6 +281,16 @@ __global__ void __launch_bounds__(BT) k_rvq_rows(ConvArgs a, float *out) {
     st4(out + static_cast<size_t>(t) * a.Cin + ci, rvq_row4(a, t, ci));
 }
 
+// Zeroes span blockIdx.x ({pointer, 32-bit words}): reset's one launch over every history buffer.
+struct ZeroSpan {
+    uint32_t *p;
+    uint32_t n;
+};
+__global__ void __launch_bounds__(BT) k_zero_spans(const ZeroSpan *spans) {
+    const ZeroSpan z = spans[blockIdx.x];
+    for (uint32_t i = threadIdx.x; i < z.n; i += BT) gst(z.p + i, 0u);
+}
+
 // The utterance position after a chunk of T frames (the last kernel of a chunk).
 __global__ void k_advance_pos(int *pos0, int T) {
     if (threadIdx.x == 0) gst(pos0, gld(pos0) + T);
@@ -366,6 +376,10 @@ struct navi_vocoder {
     int cmax = 0, ring = 0, VH = 0, HDT = 0, L = 0, CD = 0, DD = 0;
     int parity = 0;                    // which buffer of every history pair the next chunk reads
     int *d_pos0 = nullptr;             // the next chunk's first position (device)
+    // what reset clears (every causal history buffer and the position): one fill kernel over
+    // these spans instead of a memset per buffer
+    ZeroSpan *d_spans = nullptr;
+    int n_spans = 0;
     // each chunk size's launch sequence captured once per history parity and replayed
     std::vector<std::pair<std::pair<int, int>, hipGraphExec_t>> graphs;
     bool use_graphs = false;           // off by default: replays measured no faster than launches
@@ -1145,6 +1159,32 @@ navi_status navi_vocoder_create(const navi_vocoder_params *p, const navi_tensor_
         v->part_floats = need;
         VA(v->part, need);
     }
+    {
+        std::vector<ZeroSpan> spans;
+        auto add = [&](void *ptr, size_t words) {
+            if (ptr && words) spans.push_back({static_cast<uint32_t *>(ptr), static_cast<uint32_t>(words)});
+        };
+        auto addc = [&](Conv &c) {
+            add(c.hbuf[0], static_cast<size_t>(c.H) * c.Cin);
+            add(c.hbuf[1], static_cast<size_t>(c.H) * c.Cin);
+        };
+        addc(v->pre_conv); addc(v->dec0); addc(v->final_conv);
+        for (int j = 0; j < 2; ++j) {
+            add(v->cnx[j].hbuf[0], 6 * static_cast<size_t>(v->L));
+            add(v->cnx[j].hbuf[1], 6 * static_cast<size_t>(v->L));
+        }
+        for (Block &b : v->blocks) {
+            addc(b.up);
+            for (Unit &u : b.u) addc(u.c1);
+        }
+        add(v->d_pos0, 1);
+        VA(v->d_spans, spans.size());
+        v->n_spans = static_cast<int>(spans.size());
+        if (hipMemcpyAsync(v->d_spans, spans.data(), spans.size() * sizeof(ZeroSpan), hipMemcpyHostToDevice, s) != hipSuccess) {
+            set_err(err, errlen, "vocoder: span table copy failed");
+            return fail(NAVI_ERR_HIP);
+        }
+    }
 #undef VB
 #undef VA
     if (hipMemcpyAsync(v->invf, invf, sizeof invf, hipMemcpyHostToDevice, s) != hipSuccess || hipEventCreate(&v->ev0) != hipSuccess ||
@@ -1165,17 +1205,10 @@ void navi_vocoder_destroy(navi_vocoder *v) {
 navi_status navi_vocoder_reset(navi_vocoder *v) {
     if (!v) return NAVI_ERR_INVALID;
     hipStream_t s = device_state().stream;
-    auto zero = [&](float *ptr, size_t n) { return !ptr || hipMemsetAsync(ptr, 0, n * sizeof(float), s) == hipSuccess; };
-    auto zc = [&](Conv &c) { return zero(c.hbuf[0], static_cast<size_t>(c.H) * c.Cin) && zero(c.hbuf[1], static_cast<size_t>(c.H) * c.Cin); };
-    bool ok = zc(v->pre_conv) && zc(v->dec0) && zc(v->final_conv);
-    ok = ok && hipMemsetAsync(v->d_pos0, 0, sizeof(int), s) == hipSuccess;
-    for (int j = 0; j < 2; ++j) ok = ok && zero(v->cnx[j].hbuf[0], 6 * static_cast<size_t>(v->L)) && zero(v->cnx[j].hbuf[1], 6 * static_cast<size_t>(v->L));
-    for (Block &b : v->blocks) {
-        ok = ok && zc(b.up);
-        for (Unit &u : b.u) ok = ok && zc(u.c1);
-    }
-    // the K/V rings need no clearing: attention reads only positions already written this utterance
-    return ok && hipStreamSynchronize(s) == hipSuccess ? NAVI_OK : NAVI_ERR_HIP;
+    // every causal history (conv, depthwise conv) and the position back to zero; the K/V rings need
+    // no clearing: attention reads only positions already written this utterance
+    hipLaunchKernelGGL(k_zero_spans, dim3(v->n_spans), dim3(BT), 0, s, v->d_spans);
+    return hipGetLastError() == hipSuccess && hipStreamSynchronize(s) == hipSuccess ? NAVI_OK : NAVI_ERR_HIP;
 }
 
 navi_status navi_vocoder_decode(navi_vocoder *v, const int32_t *codes, int32_t n_frames, float *pcm, char *err,
