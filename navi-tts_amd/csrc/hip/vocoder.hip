@@ -1207,8 +1207,9 @@ navi_status navi_vocoder_reset(navi_vocoder *v) {
     hipStream_t s = device_state().stream;
     // every causal history (conv, depthwise conv) and the position back to zero; the K/V rings need
     // no clearing: attention reads only positions already written this utterance
+    // (asynchronous, as Vocoder::reset's memsets are: the next decode is queued behind it on the stream)
     hipLaunchKernelGGL(k_zero_spans, dim3(v->n_spans), dim3(BT), 0, s, v->d_spans);
-    return hipGetLastError() == hipSuccess && hipStreamSynchronize(s) == hipSuccess ? NAVI_OK : NAVI_ERR_HIP;
+    return hipGetLastError() == hipSuccess ? NAVI_OK : NAVI_ERR_HIP;
 }
 
 navi_status navi_vocoder_decode(navi_vocoder *v, const int32_t *codes, int32_t n_frames, float *pcm, char *err,
