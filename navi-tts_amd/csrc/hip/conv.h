@@ -589,51 +589,49 @@ __global__ void __launch_bounds__(BT) k_conv_c96(ConvArgs a) {
     if (a.hnext) carry_rows(a.hist, a.x, a.ldx, a.T, H, CIN, a.hnext);
 }
 
-// One residual unit of the codec decoder's last block (96 channels) in one kernel: the Snake'd
-// residual stream x -> k7 conv (dilation dil) + bias -> Snake with the k1's parameters -> k1 conv
-// + bias + the residual -> y, and y's Snake with the next conv's parameters -> z. The k7 part is
-// k_conv_wide<7, 128, 96, EPI_BIAS, 16>'s (same staging, same order of sums); its output tile
-// (128 rows x 96 channels) goes through the Snake into LDS as f16 hi + lo, where the k1 reads it
-// as its A operand, with the k1's weights staged once per block: the intermediate never goes to
-// memory and the unit is one launch. The k1 sums 16-channel steps in channel order, hi then lo,
-// as the separate k1 launch did, so the output is the two-launch path's.
+// One residual unit of the codec decoder's narrow blocks (C = 96 or 192 channels) in one kernel:
+// the Snake'd residual stream x -> k7 conv (dilation dil) + bias -> Snake with the k1's parameters
+// -> k1 conv + bias + the residual -> y, and y's Snake with the next conv's parameters -> z. A block
+// owns BM rows and all C output channels (C = 96: 128 rows, waves 4 x 1; C = 192: 64 rows, waves
+// 2 x 2; each wave 32 rows x 96 columns). The k7 stages its time window and every tap's weights per
+// CC7-channel chunk as k_conv_wide does; its output tile goes through the Snake into LDS as f16 hi
+// + lo, where the k1 reads it as its A operand while the k1's weights are staged 32 channels at a
+// time, the next piece in flight during the MFMAs: the intermediate never goes to memory and the
+// unit is one launch. Per output the k7 sums chunks, taps, 16-channel steps, hi then lo, and the
+// k1 16-channel steps in channel order, hi then lo, whatever the chunk's row count.
 struct UnitArgs {
-    const float *x, *hist;              // k7 input rows [T][96] and its history [6 dil][96]
+    const float *x, *hist;              // k7 input rows [T][C] and its history [6 dil][C]
     float *hnext;                       // the next chunk's k7 history (the other buffer of its pair)
-    const uint16_t *w7, *w1;            // [96][7][96] and [96][96] f16
-    const float *b7, *b1;               // [96]
+    const uint16_t *w7, *w1;            // [C][7][C] and [C][C] f16
+    const float *b7, *b1;               // [C]
     const float *za_mid, *zb_mid;       // the Snake on the k1's input
-    const float *res;                   // the residual stream [T][96]
-    float *y;                           // the unit's output [T][96] (may be res itself), or null
-    float *z;                           // Snake(y) with (za, zb): the next conv's input
+    const float *res;                   // the residual stream [T][C]
+    float *y;                           // the unit's output [T][C] (may be res itself), or null
+    float *z;                           // Snake(y) with (za, zb): the next conv's input; not x
     const float *za, *zb;
     uint32_t *flag;
     int T, dil;
 };
 
-__global__ void __launch_bounds__(BT) k_unit96(UnitArgs u) {
-    constexpr int C = 96, K = 7, BM = 128, CC = 16, LDA = CC + 8, NCT = 3;
-    constexpr int MAXWR = BM + (K - 1) * 9, LDM = C + 8;
+template <int C, int BM, int CC7>
+__global__ void __launch_bounds__(BT) k_unit(UnitArgs u) {
+    constexpr int K = 7, LDA = CC7 + 8, NCT = 3;
+    constexpr int WRW = BM / 32, WCW = 4 / WRW;             // waves along rows, along columns
+    static_assert(WRW * WCW == 4 && C == WCW * 32 * NCT, "each wave 32 rows x 96 columns");
+    constexpr int MAXWR = BM + (K - 1) * 9, LDM = C + 8, CC1 = 32, LDW = CC1 + 8;
     constexpr int A_BYTES = MAXWR * LDA * 2 * 2, B_BYTES = K * C * LDA * 2;           // k7 staging
-    constexpr int M_BYTES = BM * LDM * 2 * 2, W_BYTES = C * LDM * 2;                  // k1 operands
+    constexpr int M_BYTES = BM * LDM * 2 * 2, W_BYTES = C * LDW * 2;                  // k1 operands
     constexpr int SMEM = (A_BYTES + B_BYTES > M_BYTES + W_BYTES ? A_BYTES + B_BYTES : M_BYTES + W_BYTES);
     __shared__ __align__(16) unsigned char smem[SMEM];
     _Float16 *ahi = reinterpret_cast<_Float16 *>(smem), *alo = ahi + MAXWR * LDA, *bw = alo + MAXWR * LDA;
     _Float16 *mhi = reinterpret_cast<_Float16 *>(smem), *mlo = mhi + BM * LDM, *w1s = mlo + BM * LDM;
-    const int wv = threadIdx.x >> 6, l = threadIdx.x & 63, wr = 32 * wv;
+    const int wv = threadIdx.x >> 6, l = threadIdx.x & 63;
+    const int wr = 32 * (wv % WRW), wc = 32 * NCT * (wv / WRW);
     const int t0 = blockIdx.x * BM;
     const int H = (K - 1) * u.dil, rows = BM + H, lpad = H;
-    // the k1's weights: loaded now, staged in LDS after the k7 (18 KB, 16 B per thread per step)
-    constexpr int W1Q = C * C / 8, ITW = (W1Q + BT - 1) / BT;
-    u32x4_t w1r[ITW];
-#pragma unroll
-    for (int it = 0; it < ITW; ++it) {
-        const int e = static_cast<int>(threadIdx.x) + BT * it;
-        if (e < W1Q) w1r[it] = *(const NAVI_GLOBAL u32x4_t *) (u.w1 + static_cast<size_t>(e) * 8);
-    }
-    // ---- k7: as k_conv_wide<7, 128, 96, EPI_BIAS, 16> ----
-    constexpr int RPI = BT / (CC / 4), ITA = (MAXWR + RPI - 1) / RPI;
-    const int c4 = (static_cast<int>(threadIdx.x) % (CC / 4)) * 4, rr0 = static_cast<int>(threadIdx.x) / (CC / 4);
+    // ---- k7: the staging and step order of k_conv_wide ----
+    constexpr int RPI = BT / (CC7 / 4), ITA = (MAXWR + RPI - 1) / RPI;
+    const int c4 = (static_cast<int>(threadIdx.x) % (CC7 / 4)) * 4, rr0 = static_cast<int>(threadIdx.x) / (CC7 / 4);
     int aoff[ITA];
     uint32_t xm = 0, hm = 0;
 #pragma unroll
@@ -650,7 +648,7 @@ __global__ void __launch_bounds__(BT) k_unit96(UnitArgs u) {
             }
         }
     }
-    constexpr int QB = CC / 8, NBI = C * K * QB, ITB = (NBI + BT - 1) / BT;
+    constexpr int QB = CC7 / 8, NBI = C * K * QB, ITB = (NBI + BT - 1) / BT;
     int boff[ITB], bl[ITB];
 #pragma unroll
     for (int it = 0; it < ITB; ++it) {
@@ -672,6 +670,16 @@ __global__ void __launch_bounds__(BT) k_unit96(UnitArgs u) {
             if (ITB * BT == NBI || static_cast<int>(threadIdx.x) + BT * it < NBI)
                 bv[it] = __builtin_nontemporal_load((const NAVI_GLOBAL u32x4_t *) (u.w7 + boff[it] + ci0));
     };
+    // the k1's weights, 32 input channels (CC1) at a time: [C][CC1] in 16-byte pieces
+    constexpr int W1Q = C * CC1 / 8, ITW = (W1Q + BT - 1) / BT;
+    u32x4_t w1r[ITW];
+    auto load_w1 = [&](int ci0) {
+#pragma unroll
+        for (int it = 0; it < ITW; ++it) {
+            const int e = static_cast<int>(threadIdx.x) + BT * it, col = e / (CC1 / 8), q = e - col * (CC1 / 8);
+            if (ITW * BT == W1Q || e < W1Q) w1r[it] = *(const NAVI_GLOBAL u32x4_t *) (u.w1 + static_cast<size_t>(col) * C + ci0 + 8 * q);
+        }
+    };
     f32x16_t acc[NCT];
 #pragma unroll
     for (int c = 0; c < NCT; ++c)
@@ -679,7 +687,7 @@ __global__ void __launch_bounds__(BT) k_unit96(UnitArgs u) {
         for (int r = 0; r < 16; ++r) acc[c][r] = 0.f;
     bool bad = false;
     load(0);
-    for (int ci0 = 0; ci0 < C; ci0 += CC) {
+    for (int ci0 = 0; ci0 < C; ci0 += CC7) {
         __syncthreads();
 #pragma unroll
         for (int it = 0; it < ITA; ++it) {
@@ -700,25 +708,29 @@ __global__ void __launch_bounds__(BT) k_unit96(UnitArgs u) {
             if (ITB * BT == NBI || static_cast<int>(threadIdx.x) + BT * it < NBI)
                 *reinterpret_cast<u32x4_t *>(&bw[bl[it]]) = bv[it];
         __syncthreads();
-        if (ci0 + CC < C) load(ci0 + CC);
+        if (ci0 + CC7 < C) load(ci0 + CC7);
+        else load_w1(0);                                    // the k1's first weight piece, during the last MFMAs
 #pragma unroll
         for (int j = 0; j < K; ++j) {
-            const int ar = (wr + (l & 31) + j * u.dil) * LDA + 8 * (l >> 5);
-            const half8v h = *reinterpret_cast<const half8v *>(&ahi[ar]);
-            const half8v o = *reinterpret_cast<const half8v *>(&alo[ar]);
 #pragma unroll
-            for (int c = 0; c < NCT; ++c) {
-                const half8v b = *reinterpret_cast<const half8v *>(&bw[(j * C + 32 * c + (l & 31)) * LDA + 8 * (l >> 5)]);
-                acc[c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(h, b, acc[c], 0, 0, 0);
-                acc[c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(o, b, acc[c], 0, 0, 0);
+            for (int ks = 0; ks < CC7 / 16; ++ks) {
+                const int ar = (wr + (l & 31) + j * u.dil) * LDA + 16 * ks + 8 * (l >> 5);
+                const half8v h = *reinterpret_cast<const half8v *>(&ahi[ar]);
+                const half8v o = *reinterpret_cast<const half8v *>(&alo[ar]);
+#pragma unroll
+                for (int c = 0; c < NCT; ++c) {
+                    const half8v b = *reinterpret_cast<const half8v *>(&bw[(j * C + wc + 32 * c + (l & 31)) * LDA + 16 * ks + 8 * (l >> 5)]);
+                    acc[c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(h, b, acc[c], 0, 0, 0);
+                    acc[c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(o, b, acc[c], 0, 0, 0);
+                }
             }
         }
     }
-    // ---- the k7's output through the k1's Snake into LDS (hi + lo), the k1's weights beside it ----
+    // ---- the k7's output through the k1's Snake into LDS as f16 hi + lo ----
     float b7c[NCT], zam[NCT], zbm[NCT];
 #pragma unroll
     for (int c = 0; c < NCT; ++c) {
-        const int co = 32 * c + (l & 31);
+        const int co = wc + 32 * c + (l & 31);
         b7c[c] = gld(u.b7 + co);
         zam[c] = gld(u.za_mid + co);
         zbm[c] = gld(u.zb_mid + co);
@@ -728,46 +740,47 @@ __global__ void __launch_bounds__(BT) k_unit96(UnitArgs u) {
     for (int c = 0; c < NCT; ++c)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-            const int row = wr + 8 * (r / 4) + 4 * (l >> 5) + (r & 3), co = 32 * c + (l & 31);
+            const int row = wr + 8 * (r / 4) + 4 * (l >> 5) + (r & 3), co = wc + 32 * c + (l & 31);
             const float m = snake(acc[c][r] + b7c[c], zam[c], zbm[c]);
             if (t0 + row < u.T) bad |= !(fabsf(m) < 65504.f);
             const _Float16 h = static_cast<_Float16>(m);
             mhi[row * LDM + co] = h;
             mlo[row * LDM + co] = static_cast<_Float16>(m - static_cast<float>(h));
         }
-#pragma unroll
-    for (int it = 0; it < ITW; ++it) {
-        const int e = static_cast<int>(threadIdx.x) + BT * it;
-        if (e < W1Q) {
-            const int col = e / (C / 8), q = e - col * (C / 8);
-            *reinterpret_cast<u32x4_t *>(&w1s[col * LDM + 8 * q]) = w1r[it];
-        }
-    }
     if (bad) gst(u.flag, 1u);
-    __syncthreads();
-    // ---- k1 over the 96 channels: 16-channel steps in order, hi then lo ----
+    // ---- k1: 32-channel weight pieces, 16-channel steps in channel order, hi then lo ----
     f32x16_t acc1[NCT];
 #pragma unroll
     for (int c = 0; c < NCT; ++c)
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc1[c][r] = 0.f;
+    for (int ci0 = 0; ci0 < C; ci0 += CC1) {
+        if (ci0 > 0) __syncthreads();                       // the previous piece's readers are done
 #pragma unroll
-    for (int ks = 0; ks < C / 16; ++ks) {
-        const int ar = (wr + (l & 31)) * LDM + 16 * ks + 8 * (l >> 5);
-        const half8v h = *reinterpret_cast<const half8v *>(&mhi[ar]);
-        const half8v o = *reinterpret_cast<const half8v *>(&mlo[ar]);
+        for (int it = 0; it < ITW; ++it) {
+            const int e = static_cast<int>(threadIdx.x) + BT * it, col = e / (CC1 / 8), q = e - col * (CC1 / 8);
+            if (ITW * BT == W1Q || e < W1Q) *reinterpret_cast<u32x4_t *>(&w1s[col * LDW + 8 * q]) = w1r[it];
+        }
+        __syncthreads();                                    // the piece (and, first time, the tile) in LDS
+        if (ci0 + CC1 < C) load_w1(ci0 + CC1);
 #pragma unroll
-        for (int c = 0; c < NCT; ++c) {
-            const half8v b = *reinterpret_cast<const half8v *>(&w1s[(32 * c + (l & 31)) * LDM + 16 * ks + 8 * (l >> 5)]);
-            acc1[c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(h, b, acc1[c], 0, 0, 0);
-            acc1[c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(o, b, acc1[c], 0, 0, 0);
+        for (int ks = 0; ks < CC1 / 16; ++ks) {
+            const int ar = (wr + (l & 31)) * LDM + ci0 + 16 * ks + 8 * (l >> 5);
+            const half8v h = *reinterpret_cast<const half8v *>(&mhi[ar]);
+            const half8v o = *reinterpret_cast<const half8v *>(&mlo[ar]);
+#pragma unroll
+            for (int c = 0; c < NCT; ++c) {
+                const half8v b = *reinterpret_cast<const half8v *>(&w1s[(wc + 32 * c + (l & 31)) * LDW + 16 * ks + 8 * (l >> 5)]);
+                acc1[c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(h, b, acc1[c], 0, 0, 0);
+                acc1[c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(o, b, acc1[c], 0, 0, 0);
+            }
         }
     }
     // ---- epilogue: every load first (column operands, residuals), then the stores ----
     float b1c[NCT], zac[NCT], zbc[NCT], rs[NCT][16];
 #pragma unroll
     for (int c = 0; c < NCT; ++c) {
-        const int co = 32 * c + (l & 31);
+        const int co = wc + 32 * c + (l & 31);
         b1c[c] = gld(u.b1 + co);
         zac[c] = gld(u.za + co);
         zbc[c] = gld(u.zb + co);
@@ -781,7 +794,7 @@ __global__ void __launch_bounds__(BT) k_unit96(UnitArgs u) {
     for (int c = 0; c < NCT; ++c)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-            const int t = t0 + wr + 8 * (r / 4) + 4 * (l >> 5) + (r & 3), co = 32 * c + (l & 31);
+            const int t = t0 + wr + 8 * (r / 4) + 4 * (l >> 5) + (r & 3), co = wc + 32 * c + (l & 31);
             if (t >= u.T) continue;
             const float v = (acc1[c][r] + b1c[c]) + rs[c][r];
             const size_t o = static_cast<size_t>(t) * C + co;

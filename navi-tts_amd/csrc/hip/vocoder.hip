@@ -460,7 +460,7 @@ int conv_mt(int T) { return T <= 16 ? 1 : 4; }
 
 // The final 96 -> 16 conv (one output channel padded to a 16-column tile) runs on k_conv_c96
 // (input window and weights staged in LDS, every output channel in one block); the last block's
-// own 96-channel convs take k_conv_wide / k_unit96 first. Chosen by the conv's shape only, so
+// own 96-channel convs take k_conv_wide / k_unit first. Chosen by the conv's shape only, so
 // every chunking of the codes runs the same kernel.
 bool conv_is_c96(const Conv &c) {
     return c.phases == 1 && c.S == 1 && c.dil <= 9 && (c.K == 7 || c.K == 1) && c.Cin == 96 && (c.Cout == 96 || c.Cout == 16);
@@ -523,18 +523,21 @@ bool launch_wide_conv(const Conv &c, const ConvArgs &a, int pro, int epi, int T,
 }
 
 // A residual unit of the last decoder block (96 channels: k7 then k1, one phase each) runs as one
-// kernel, k_unit96 (conv.h): the k7's Snake'd output stays in LDS as the k1's input.
+// kernel, k_unit (conv.h): the k7's Snake'd output stays in LDS as the k1's input. (The 192-channel
+// block's units on k_unit<192, 64> measured slower than its two k_conv_wide launches: 437-504 us
+// against 295 + 153 us per unit for 240 frames, 64 against 47 us in 16-frame chunks.)
 bool unit_fused(const Unit &u) {
-    return u.c1.Cin == 96 && u.c1.Cout == 96 && u.c1.K == 7 && u.c1.phases == 1 && u.c1.dil <= 9 && u.c2.Cin == 96 &&
-           u.c2.Cout == 96 && u.c2.K == 1 && u.c2.phases == 1;
+    const int C = u.c1.Cout;
+    return C == 96 && u.c1.Cin == C && u.c1.K == 7 && u.c1.phases == 1 && u.c1.dil <= 9 && u.c2.Cin == C && u.c2.Cout == C &&
+           u.c2.K == 1 && u.c2.phases == 1;
 }
 
-void launch_unit96(navi_vocoder &v, Unit &u, const float *x, int T, const float *res, float *y, float *z, const Conv &next) {
+void launch_unit(navi_vocoder &v, Unit &u, const float *x, int T, const float *res, float *y, float *z, const Conv &next) {
     UnitArgs a{};
     a.x = x; a.hist = u.c1.hbuf[v.parity]; a.hnext = u.c1.H > 0 ? u.c1.hbuf[v.parity ^ 1] : nullptr;
     a.w7 = u.c1.w; a.w1 = u.c2.w; a.b7 = u.c1.bias; a.b1 = u.c2.bias; a.za_mid = u.c2.sa; a.zb_mid = u.c2.sb;
     a.res = res; a.y = y; a.z = z; a.za = next.sa; a.zb = next.sb; a.flag = v.flag; a.T = T; a.dil = u.c1.dil;
-    hipLaunchKernelGGL(k_unit96, dim3((T + 127) / 128), dim3(BT), 0, device_state().stream, a);
+    hipLaunchKernelGGL((k_unit<96, 128, 16>), dim3((T + 127) / 128), dim3(BT), 0, device_state().stream, a);
 }
 
 // Input-channel splits of a conv over T rows: when the output tiles alone would leave most of the
@@ -754,7 +757,7 @@ navi_status decode_chunk(navi_vocoder &v, int T, char *err, size_t errlen) {
                 // one launch reads unit_in (its k7 window reaches into the neighbouring blocks'
                 // rows) while it writes the Snake'd output, so that goes to the other buffer
                 float *unit_out = unit_in == v.res_s[b] ? v.mid_s[b] : v.res_s[b];
-                launch_unit96(v, bk.u[k], unit_in, rows, v.res[b], y, unit_out, *next);
+                launch_unit(v, bk.u[k], unit_in, rows, v.res[b], y, unit_out, *next);
                 unit_in = unit_out;
             } else {
                 VOC_TRY(run_conv(v, bk.u[k].c1, PRO_NONE, EPI_BIAS, v.res_s[b], rows, ch, nullptr, ch, nullptr, nullptr, err,
