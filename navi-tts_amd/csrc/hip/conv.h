@@ -324,7 +324,7 @@ __global__ void __launch_bounds__(BT) k_conv_mfma(ConvArgs a) {
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
 // The wide implicit-GEMM conv for the decoder blocks' causal convs (K = 7, 2 or 1, any number of
-// transposed-conv phases, no prologue, no K split): v_mfma_f32_32x32x16_f16, whose operands cover
+// transposed-conv phases, no prologue): v_mfma_f32_32x32x16_f16, whose operands cover
 // twice the products of a 16x16x32 step per LDS read. A block computes BM rows x BN output channels
 // of one phase (blockIdx.z); per chunk of 32 input channels it stages in LDS the time window
 // (BM + (K-1) dil rows, f16 hi + lo) and the weights of every tap for its BN channels, so each
@@ -336,7 +336,13 @@ typedef float f32x16_t __attribute__((ext_vector_type(16)));
 // Lane layout of the 32x32x16 step (checked on the device): lane l holds A[l % 32][8 (l / 32) ..]
 // and B[8 (l / 32) ..][l % 32]; accumulator r of lane l is row 8 (r / 4) + 4 (l / 32) + r % 4,
 // column l % 32.
-template <int K, int BM, int BN, int EPI, int CC = 32>
+// Input-channel splits (a conv whose output tiles alone leave the CUs idle in short chunks): the
+// channels fall into S equal ranges of a.cps. SM = 1: block z = phase * S + s sums range s only and
+// writes it to a.part[s] (k_conv_finish adds the ranges in order and applies the epilogue);
+// SM = 2: one block sums every range, each from zero, and adds the range sums in the same order
+// itself, so a launch without partials gives the same bits as the split launch (the split count is
+// the conv's, whatever the chunk; only how it runs depends on the chunk's size). SM = 0: no split.
+template <int K, int BM, int BN, int EPI, int CC = 32, int SM = 0>
 __global__ void __launch_bounds__(BT) k_conv_wide(ConvArgs a) {
     constexpr int LDA = CC + 8;                             // LDS row (halves)
     static_assert(CC == 32 || CC == 16, "channels per chunk");
@@ -348,7 +354,9 @@ __global__ void __launch_bounds__(BT) k_conv_wide(ConvArgs a) {
     __shared__ __align__(16) _Float16 bw[K * BN * LDA];
     const int wv = threadIdx.x >> 6, l = threadIdx.x & 63;
     const int wr = BM == 128 ? 32 * wv : 32 * (wv >> 1), wc = BM == 128 ? 0 : (BN / 2) * (wv & 1);
-    const int n0 = blockIdx.x * BN, t0 = blockIdx.y * BM, phase = blockIdx.z;
+    const int S = SM == 1 ? static_cast<int>(gridDim.z) / a.phases : 1, sp = SM == 1 ? static_cast<int>(blockIdx.z) % S : 0;
+    const int n0 = blockIdx.x * BN, t0 = blockIdx.y * BM, phase = SM == 1 ? static_cast<int>(blockIdx.z) / S : blockIdx.z;
+    const int cbeg = SM == 1 ? sp * a.cps : 0, cend = SM == 1 ? min(a.Cin, cbeg + a.cps) : a.Cin;
     const int H = (K - 1) * a.dil, rows = BM + H;
     // A staging: 8 float4 per window row, thread -> rows (tid / 8) + 32 it, channels 4 (tid % 8);
     // each row's source (x, history or zeros) fixed for the launch
@@ -393,14 +401,26 @@ __global__ void __launch_bounds__(BT) k_conv_wide(ConvArgs a) {
             if (ITB * BT == NBI || static_cast<int>(threadIdx.x) + BT * it < NBI)
                 bv[it] = __builtin_nontemporal_load((const NAVI_GLOBAL u32x4_t *) (a.w + boff[it] + ci0));
     };
-    f32x16_t acc[NCT];
+    f32x16_t acc[NCT], racc[SM == 2 ? NCT : 1];
 #pragma unroll
     for (int c = 0; c < NCT; ++c)
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[c][r] = 0.f;
-    bool bad = false;
-    load(0);
-    for (int ci0 = 0; ci0 < a.Cin; ci0 += CC) {
+    bool bad = false, rfirst = true;
+    load(cbeg);
+    for (int ci0 = cbeg; ci0 < cend; ci0 += CC) {
+        if constexpr (SM == 2) {
+            if (ci0 > 0 && ci0 % a.cps == 0) {              // a range ends: fold its sum in, restart from zero
+#pragma unroll
+                for (int c = 0; c < NCT; ++c)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        racc[c][r] = rfirst ? acc[c][r] : racc[c][r] + acc[c][r];
+                        acc[c][r] = 0.f;
+                    }
+                rfirst = false;
+            }
+        }
         __syncthreads();                                    // the previous chunk's readers are done
 #pragma unroll
         for (int it = 0; it < ITA; ++it) {
@@ -421,7 +441,7 @@ __global__ void __launch_bounds__(BT) k_conv_wide(ConvArgs a) {
             if (ITB * BT == NBI || static_cast<int>(threadIdx.x) + BT * it < NBI)
                 *reinterpret_cast<u32x4_t *>(&bw[bl[it]]) = bv[it];
         __syncthreads();
-        if (ci0 + CC < a.Cin) load(ci0 + CC);
+        if (ci0 + CC < cend) load(ci0 + CC);
 #pragma unroll
         for (int j = 0; j < K; ++j) {
 #pragma unroll
@@ -439,6 +459,26 @@ __global__ void __launch_bounds__(BT) k_conv_wide(ConvArgs a) {
         }
     }
     if (bad) gst(a.flag, 1u);
+    if constexpr (SM == 2) {
+        if (!rfirst) {
+#pragma unroll
+            for (int c = 0; c < NCT; ++c)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[c][r] = racc[c][r] + acc[c][r];
+        }
+    }
+    if constexpr (SM == 1) {
+        float *part = a.part + static_cast<size_t>(sp) * a.T * a.phases * a.Cout;
+#pragma unroll
+        for (int c = 0; c < NCT; ++c)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int t = t0 + wr + 8 * (r / 4) + 4 * (l >> 5) + (r & 3), co = n0 + wc + 32 * c + (l & 31);
+                if (t < a.T) gst(part + (static_cast<size_t>(t) * a.phases + phase) * a.Cout + co, acc[c][r]);
+            }
+        if (a.hnext) carry_rows(a.hist, a.x, a.ldx, a.T, H, a.Cin, a.hnext);
+        return;
+    }
     // every load of the epilogue first (column operands, residuals), then the stores
     EpiCol cc[NCT];
 #pragma unroll

@@ -479,16 +479,37 @@ bool launch_c96(const Conv &c, const ConvArgs &a, int pro, int epi, int T, hipSt
     return false;
 }
 
-// The decoder blocks' causal convs (K 7, 2 or 1, any phases, 32 | Cin, 64 | Cout or Cout = 96 but
-// not the 96-channel k7, at least 32 input rows per frame) run on k_conv_wide, with no K split. Decided at create from the
-// conv's shape and place, so every chunking of the codes runs the same kernel and sums in the same
-// order.
+// The decoder blocks' causal convs (K 7, 2 or 1, any phases, 32 | Cin, 64 | Cout or Cout = 96,
+// at least 32 input rows per frame) run on k_conv_wide. Decided at create from the conv's shape and
+// place, so every chunking of the codes runs the same kernel and sums in the same order.
 bool conv_takes_wide(const Conv &c, int rows_per_frame) {
     return (c.K == 7 || c.K == 2 || c.K == 1) && c.dil <= 9 && c.Cin % 32 == 0 && (c.Cout % 64 == 0 || c.Cout == 96) &&
            rows_per_frame >= 32;
 }
 
-bool launch_wide_conv(const Conv &c, const ConvArgs &a, int pro, int epi, int T, hipStream_t s) {
+// Input-channel splits of a k_conv_wide conv (64-column tiles only), fixed at create: when the
+// 64-row tiles of a 16-frame chunk (rows16 input rows) would leave the 256 CUs idle, the channels
+// fall into S equal ranges of at least two 32-channel chunks each. A short chunk then runs S times
+// the blocks (partials summed by k_conv_finish), a long one the same sums in one block per tile.
+constexpr int WIDE_SPLIT_TILES = 256;
+int wide_splits(const Conv &c, int rows16) {
+    if (c.Cout % 64 != 0) return 1;
+    const int tiles = (c.Cout / 64) * ((rows16 + 63) / 64) * c.phases, chunks = c.Cin / 32;
+    int S = 1;
+    while (tiles * S < WIDE_SPLIT_TILES && chunks % (2 * S) == 0 && chunks / (2 * S) >= 2) S *= 2;
+    return S;
+}
+
+// Whether a launch over T rows runs the split blocks (fewer than WIDE_SPLIT_TILES 64-row tiles),
+// and the largest such T (the rows the split workspace has to hold).
+bool wide_split_run(const Conv &c, int T) {
+    return c.S > 1 && (c.Cout / 64) * ((T + 63) / 64) * c.phases < WIDE_SPLIT_TILES;
+}
+int wide_split_max_rows(const Conv &c) {
+    return c.S > 1 ? 64 * ((WIDE_SPLIT_TILES - 1) / ((c.Cout / 64) * c.phases)) : 0;
+}
+
+bool launch_wide_conv(const Conv &c, ConvArgs &a, int pro, int epi, int T, float *part, hipStream_t s) {
     if (pro != PRO_NONE) return false;
     const int P = c.phases;
     if (c.Cout == 96) {
@@ -508,16 +529,33 @@ bool launch_wide_conv(const Conv &c, const ConvArgs &a, int pro, int epi, int T,
         return false;
     }
     const int nb = c.Cout / 64;
-    const bool big = static_cast<long>((T + 127) / 128) * nb * P >= 512;   // enough 128-row tiles to fill the chip twice
-#define NAVI_WIDE(K_, E_)                                                                                          \
-    if (c.K == K_ && epi == E_) {                                                                                  \
-        if (big) hipLaunchKernelGGL((k_conv_wide<K_, 128, 64, E_>), dim3(nb, (T + 127) / 128, P), dim3(BT), 0, s, a); \
-        else hipLaunchKernelGGL((k_conv_wide<K_, 64, 64, E_>), dim3(nb, (T + 63) / 64, P), dim3(BT), 0, s, a);       \
-        return true;                                                                                               \
+    a.cps = c.Cin / c.S;
+    if (wide_split_run(c, T)) {
+        const bool known = (c.K == 7 && epi == EPI_BIAS) || (c.K == 2 && epi == EPI_BIAS) || (c.K == 1 && epi == EPI_RESIDUAL);
+        if (!known) return false;
+        a.part = part;
+        const dim3 g(nb, (T + 63) / 64, P * c.S);
+        if (c.K == 7) hipLaunchKernelGGL((k_conv_wide<7, 64, 64, EPI_PARTIAL, 32, 1>), g, dim3(BT), 0, s, a);
+        else if (c.K == 2) hipLaunchKernelGGL((k_conv_wide<2, 64, 64, EPI_PARTIAL, 32, 1>), g, dim3(BT), 0, s, a);
+        else hipLaunchKernelGGL((k_conv_wide<1, 64, 64, EPI_PARTIAL, 32, 1>), g, dim3(BT), 0, s, a);
+        const size_t n = static_cast<size_t>(T) * P * c.Cout;
+        hipLaunchKernelGGL(k_conv_finish, dim3(static_cast<unsigned>((n + BT - 1) / BT)), dim3(BT), 0, s, a, c.S, epi);
+        return true;
     }
-    NAVI_WIDE(7, EPI_BIAS)
-    NAVI_WIDE(2, EPI_BIAS)
-    NAVI_WIDE(1, EPI_RESIDUAL)
+    const bool big = static_cast<long>((T + 127) / 128) * nb * P >= 512;   // enough 128-row tiles to fill the chip twice
+#define NAVI_WIDE(K_, E_, SM_)                                                                                           \
+    if (big) hipLaunchKernelGGL((k_conv_wide<K_, 128, 64, E_, 32, SM_>), dim3(nb, (T + 127) / 128, P), dim3(BT), 0, s, a); \
+    else hipLaunchKernelGGL((k_conv_wide<K_, 64, 64, E_, 32, SM_>), dim3(nb, (T + 63) / 64, P), dim3(BT), 0, s, a);
+#define NAVI_WIDE_E(K_, E_)                          \
+    if (c.K == K_ && epi == E_) {                    \
+        if (c.S > 1) { NAVI_WIDE(K_, E_, 2) }        \
+        else { NAVI_WIDE(K_, E_, 0) }                \
+        return true;                                 \
+    }
+    NAVI_WIDE_E(7, EPI_BIAS)
+    NAVI_WIDE_E(2, EPI_BIAS)
+    NAVI_WIDE_E(1, EPI_RESIDUAL)
+#undef NAVI_WIDE_E
 #undef NAVI_WIDE
     return false;
 }
@@ -608,7 +646,11 @@ navi_status run_conv(navi_vocoder &v, Conv &c, int pro, int epi, const float *x,
         a.zb = zc->sb;
     }
     if (c.wide) {
-        if (!launch_wide_conv(c, a, pro, epi, T, device_state().stream)) {
+        if (wide_split_run(c, T) && static_cast<size_t>(c.S) * T * c.phases * c.Cout > v.part_floats) {
+            set_err(err, errlen, "vocoder: split workspace too small");
+            return NAVI_ERR_INVALID;
+        }
+        if (!launch_wide_conv(c, a, pro, epi, T, v.part, device_state().stream)) {
             set_err(err, errlen, "vocoder: no wide conv kernel for K=%d epilogue %d", c.K, epi);
             return NAVI_ERR_UNSUPPORTED;
         }
@@ -1141,8 +1183,10 @@ navi_status navi_vocoder_create(const navi_vocoder_params *p, const navi_tensor_
         const int Cn = static_cast<int>(std::min<size_t>(C, 16)), Cf = static_cast<int>(C);
         auto upd = [&](Conv &c, int rows_per_frame) {
             c.wide = conv_takes_wide(c, rows_per_frame);
-            c.S = c.wide ? 1 : conv_splits(c, Cn * rows_per_frame);
-            if (c.S > 1) need = std::max(need, static_cast<size_t>(c.S) * Cf * rows_per_frame * c.phases * c.Cout);
+            c.S = c.wide ? wide_splits(c, Cn * rows_per_frame) : conv_splits(c, Cn * rows_per_frame);
+            const size_t rows = c.wide ? std::min<size_t>(static_cast<size_t>(Cf) * rows_per_frame, wide_split_max_rows(c))
+                                       : static_cast<size_t>(Cf) * rows_per_frame;
+            if (c.S > 1) need = std::max(need, static_cast<size_t>(c.S) * rows * c.phases * c.Cout);
         };
         upd(v->rvq_proj, 1); upd(v->pre_conv, 1); upd(v->in_proj, 1); upd(v->out_proj, 1);
         for (TLayer &ly : v->layers) { upd(ly.qkv, 1); upd(ly.o, 1); upd(ly.gu, 1); upd(ly.down, 1); }

@@ -61,18 +61,20 @@ def test_chunked_equals_one_shot(codec):
 
 
 def test_tile_shapes_do_not_change_the_pcm(codec):
-    """The decoder blocks' convs pick 128- or 64-row tiles by the chunk's row count (k_conv_wide: the
-    192-channel block takes 128-row tiles at 40 frames, 64-row tiles at 16) and the transformer's row
-    kernels more row tiles per block for more rows: a column's sums keep their order in every case,
-    so 40 frames decoded as one block and as 16-frame chunks (16 + 16 + 8) give the same PCM bit for bit. (Both handles hold at least 16
-    frames, so their input-channel split counts, fixed at create from a 16-frame chunk, agree.)"""
+    """The decoder blocks' convs pick their tiles by the chunk's row count (k_conv_wide: 128- or
+    64-row tiles; the 768- and 384-channel convs, whose input channels are split in ranges fixed at
+    create, run the ranges as separate blocks with partials for short chunks and in one block for
+    long ones) and the transformer's row kernels more row tiles per block for more rows: a column's
+    sums keep their order in every case, so 64 frames decoded as one block and as 16-frame chunks
+    give the same PCM bit for bit. (Both handles hold at least 16 frames, so their split counts,
+    fixed at create from a 16-frame chunk, agree.)"""
     abi, W, _ = codec
-    codes = np.random.default_rng(5).integers(0, 2048, (40, 16))
-    one = abi.Vocoder(W, max_chunk_frames=40)
+    codes = np.random.default_rng(5).integers(0, 2048, (64, 16))
+    one = abi.Vocoder(W, max_chunk_frames=64)
     block = one.decode(codes)
     small = abi.Vocoder(W, max_chunk_frames=16)
     chunks = small.decode(codes)
-    log(f"40-frame block vs 16-frame chunks: max diff {np.abs(block - chunks).max():.2e}")
+    log(f"64-frame block vs 16-frame chunks: max diff {np.abs(block - chunks).max():.2e}")
     assert np.array_equal(block, chunks)
 
 
