@@ -49,10 +49,12 @@ namespace vc {
 
 using namespace cv;
 
+constexpr int ROW_PAD = 8;   // floats past a transformer activation row (navi_vocoder::lxs)
+
 // y[t] = RMSNorm(x[t]) * w over C channels.
-__global__ void __launch_bounds__(BT) k_rmsnorm(const float *x, const float *w, int C, float eps, float *y) {
+__global__ void __launch_bounds__(BT) k_rmsnorm(const float *x, int ldx, const float *w, int C, float eps, float *y) {
     __shared__ float red[4];
-    const float *row = x + static_cast<size_t>(blockIdx.x) * C;
+    const float *row = x + static_cast<size_t>(blockIdx.x) * ldx;
     float ss = 0.f;
     for (int c = threadIdx.x; c < C; c += BT) {
         const float v = gld(row + c);
@@ -137,7 +139,7 @@ __global__ void __launch_bounds__(BT) k_dw_ln(const float *x, const float *hist,
 // for later chunks: ring >= window + chunk, so no slot written here is one this launch reads.
 template <int HD, int RT>
 __global__ void __launch_bounds__(BT) k_window_attention(const float *qkv, int nh, int T, const int *pos0p, int window, int ring,
-                                                         const float *invf, float *kc, float *vc, float *out) {
+                                                         const float *invf, float *kc, float *vc, float *out, int ldo) {
     constexpr int HALF = HD / 2, KS = HD + 1, DPL = HD / 64;   // K rows padded: lanes j read rows j
     static_assert(RT % 4 == 0 && RT <= 16, "RT / 4 rows per wave; the LDS is sized for 16");
     extern __shared__ float sm[];
@@ -266,7 +268,7 @@ __global__ void __launch_bounds__(BT) k_window_attention(const float *qkv, int n
             for (int d = 0; d < DPL; ++d) acc[d] = fmaf(pj, vb[j * HD + 64 * d], acc[d]);
         }
 #pragma unroll
-        for (int d = 0; d < DPL; ++d) gst(out + static_cast<size_t>(t) * HDT + h * HD + l + 64 * d, acc[d] * inv);
+        for (int d = 0; d < DPL; ++d) gst(out + static_cast<size_t>(t) * ldo + h * HD + l + 64 * d, acc[d] * inv);
     }
 }
 
@@ -400,8 +402,13 @@ struct navi_vocoder {
     float *lat_in = nullptr;           // RVQ rows gathered from the codebooks [T][CD]
     float *lat = nullptr;              // RVQ latent [T][CD]
     float *pre = nullptr;              // pre_conv output [T][L]
-    float *xs = nullptr, *xn = nullptr;   // transformer residual stream and its RMSNorm [T][VH]
-    float *qkv = nullptr, *att = nullptr, *gu = nullptr;
+    float *xs = nullptr, *xn = nullptr;   // transformer residual stream [T][lxs] and its RMSNorm [T][VH]
+    float *qkv = nullptr, *att = nullptr, *gu = nullptr;   // att [T][latt], gu [T][lgu]
+    // Row strides of the transformer's projection inputs: ROW_PAD floats past the row, since
+    // strides that are multiples of 2-4 KB put the 16 rows of an MFMA operand load on the same
+    // memory channels (the 16-row projections measured 12-19 % faster padded)
+    int lxs = 0, latt = 0, lgu = 0;
+    float *snapbuf = nullptr;          // compact copy of a padded stage for the stage hook
     float *post = nullptr;             // transformer output projection [T][L]
     float *upx[2] = {};                // upsampling stages' residual streams [R][L]
     float *lnx = nullptr;              // ConvNeXt depthwise + LayerNorm output [R][L]
@@ -680,8 +687,15 @@ size_t attention_lds(int window, int head_dim) {
 // The stage hook (Vocoder::set_stage_hook, vocoder.h:46-48): the device buffer of a finished stage,
 // after the stream has drained. The stage names are the reference's (vocoder.hip:267-341), which
 // its tools compare by.
-navi_status snap(navi_vocoder &v, const std::string &name, const float *buf, int rows, int cols, char *err, size_t errlen) {
+navi_status snap(navi_vocoder &v, const std::string &name, const float *buf, int rows, int cols, char *err, size_t errlen,
+                 int ld = 0) {
     if (!v.hook) return NAVI_OK;
+    if (ld > cols) {                   // padded rows: the hook gets a compact copy
+        NAVI_TRY_HIP(hipMemcpy2DAsync(v.snapbuf, static_cast<size_t>(cols) * 4, buf, static_cast<size_t>(ld) * 4,
+                                      static_cast<size_t>(cols) * 4, rows, hipMemcpyDeviceToDevice, device_state().stream),
+                     err, errlen);
+        buf = v.snapbuf;
+    }
     NAVI_TRY_HIP(hipStreamSynchronize(device_state().stream), err, errlen);
     v.hook(v.hook_user, name.c_str(), buf, rows, cols);
     return NAVI_OK;
@@ -716,22 +730,22 @@ navi_status decode_chunk(navi_vocoder &v, int T, char *err, size_t errlen) {
     VOC_TRY(snap(v, "rvq", v.lat, T, CD, err, errlen));
     VOC_TRY(run_conv(v, v.pre_conv, PRO_NONE, EPI_BIAS, v.lat, T, CD, v.pre, L, nullptr, nullptr, err, errlen));
     VOC_TRY(snap(v, "pre_conv", v.pre, T, L, err, errlen));
-    VOC_TRY(run_conv(v, v.in_proj, PRO_NONE, EPI_BIAS, v.pre, T, L, v.xs, VH, nullptr, nullptr, err, errlen));
-    VOC_TRY(snap(v, "in_proj", v.xs, T, VH, err, errlen));
+    VOC_TRY(run_conv(v, v.in_proj, PRO_NONE, EPI_BIAS, v.pre, T, L, v.xs, v.lxs, nullptr, nullptr, err, errlen));
+    VOC_TRY(snap(v, "in_proj", v.xs, T, VH, err, errlen, v.lxs));
     const size_t att_lds = attention_lds(p.sliding_window, p.xf.head_dim);
     for (size_t li = 0; li < v.layers.size(); ++li) {
         TLayer &ly = v.layers[li];
         const std::string ls = std::to_string(li);
         if (v.hook) {                 // the normed rows are a stage of their own only for the hook
-            hipLaunchKernelGGL(k_rmsnorm, dim3(T), dim3(BT), 0, s, v.xs, ly.ln1, VH, p.xf.rms_eps, v.xn);
+            hipLaunchKernelGGL(k_rmsnorm, dim3(T), dim3(BT), 0, s, v.xs, v.lxs, ly.ln1, VH, p.xf.rms_eps, v.xn);
             VOC_TRY(snap(v, "norm1_" + ls, v.xn, T, VH, err, errlen));
         }
-        VOC_TRY(xf_rows(rows::EPI_PLAIN, true, v.xs, VH, T, VH, ly.ln1, p.xf.rms_eps, ly.qkv.w, 3 * HDT, nullptr, 0, v.qkv,
+        VOC_TRY(xf_rows(rows::EPI_PLAIN, true, v.xs, v.lxs, T, VH, ly.ln1, p.xf.rms_eps, ly.qkv.w, 3 * HDT, nullptr, 0, v.qkv,
                         3 * HDT, nullptr, v.flag, err, errlen));
         VOC_TRY(snap(v, "qkv_" + ls, v.qkv, T, 3 * HDT, err, errlen));
 #define NAVI_ATT(HD_, RT_)                                                                                              \
         hipLaunchKernelGGL((k_window_attention<HD_, RT_>), dim3((T + RT_ - 1) / RT_, nh), dim3(BT), att_lds, s, v.qkv, nh, T, \
-                           v.d_pos0, p.sliding_window, v.ring, v.invf, ly.kc, ly.vc, v.att)
+                           v.d_pos0, p.sliding_window, v.ring, v.invf, ly.kc, ly.vc, v.att, v.latt)
         if (p.xf.head_dim == 64) {
             if (T <= 32) NAVI_ATT(64, 4);
             else NAVI_ATT(64, 16);
@@ -740,17 +754,17 @@ navi_status decode_chunk(navi_vocoder &v, int T, char *err, size_t errlen) {
             else NAVI_ATT(128, 16);
         }
 #undef NAVI_ATT
-        VOC_TRY(snap(v, "attnraw" + ls, v.att, T, HDT, err, errlen));
-        VOC_TRY(xf_rows(rows::EPI_RESID, false, v.att, HDT, T, HDT, nullptr, 0.f, ly.o.w, VH, nullptr, 0, v.xs, VH,
+        VOC_TRY(snap(v, "attnraw" + ls, v.att, T, HDT, err, errlen, v.latt));
+        VOC_TRY(xf_rows(rows::EPI_RESID, false, v.att, v.latt, T, HDT, nullptr, 0.f, ly.o.w, VH, nullptr, 0, v.xs, v.lxs,
                         ly.attn_scale, v.flag, err, errlen));
-        VOC_TRY(snap(v, "xattn_" + ls, v.xs, T, VH, err, errlen));
-        VOC_TRY(xf_rows(rows::EPI_SWIGLU, true, v.xs, VH, T, VH, ly.ln2, p.xf.rms_eps, ly.gu.w, FF,
-                        ly.gu.w + static_cast<size_t>(FF) * VH, FF, v.gu, FF, nullptr, v.flag, err, errlen));
-        VOC_TRY(xf_rows(rows::EPI_RESID, false, v.gu, FF, T, FF, nullptr, 0.f, ly.down.w, VH, nullptr, 0, v.xs, VH,
+        VOC_TRY(snap(v, "xattn_" + ls, v.xs, T, VH, err, errlen, v.lxs));
+        VOC_TRY(xf_rows(rows::EPI_SWIGLU, true, v.xs, v.lxs, T, VH, ly.ln2, p.xf.rms_eps, ly.gu.w, FF,
+                        ly.gu.w + static_cast<size_t>(FF) * VH, FF, v.gu, v.lgu, nullptr, v.flag, err, errlen));
+        VOC_TRY(xf_rows(rows::EPI_RESID, false, v.gu, v.lgu, T, FF, nullptr, 0.f, ly.down.w, VH, nullptr, 0, v.xs, v.lxs,
                         ly.mlp_scale, v.flag, err, errlen));
-        VOC_TRY(snap(v, "layer" + ls, v.xs, T, VH, err, errlen));
+        VOC_TRY(snap(v, "layer" + ls, v.xs, T, VH, err, errlen, v.lxs));
     }
-    hipLaunchKernelGGL(k_rmsnorm, dim3(T), dim3(BT), 0, s, v.xs, v.final_norm, VH, p.xf.rms_eps, v.xn);
+    hipLaunchKernelGGL(k_rmsnorm, dim3(T), dim3(BT), 0, s, v.xs, v.lxs, v.final_norm, VH, p.xf.rms_eps, v.xn);
     VOC_TRY(run_conv(v, v.out_proj, PRO_NONE, EPI_BIAS, v.xn, T, VH, v.post, L, nullptr, nullptr, err, errlen));
     VOC_TRY(snap(v, "pre_transformer", v.post, T, L, err, errlen));
     // two upsampling stages: transposed conv, then the ConvNeXt block in place on its output
@@ -1161,11 +1175,15 @@ navi_status navi_vocoder_create(const navi_vocoder_params *p, const navi_tensor_
     VA(v->lat_in, C * CD);
     VA(v->lat, C * CD);
     VA(v->pre, C * L);
-    VA(v->xs, C * VH);
+    v->lxs = VH + ROW_PAD;
+    v->latt = HDT + ROW_PAD;
+    v->lgu = xf.ff + ROW_PAD;
+    VA(v->xs, C * v->lxs);
     VA(v->xn, C * VH);
     VA(v->qkv, C * 3 * HDT);
-    VA(v->att, C * HDT);
-    VA(v->gu, C * 2 * xf.ff);
+    VA(v->att, C * v->latt);
+    VA(v->gu, C * v->lgu);
+    VA(v->snapbuf, C * std::max(VH, HDT));
     VA(v->post, C * L);
     const size_t up_rows = C * p->upsampling_ratios[0] * p->upsampling_ratios[1];
     VA(v->upx[0], C * p->upsampling_ratios[0] * L);
