@@ -12,9 +12,11 @@
 //    and residual add fused in. Every weight byte streams from HBM once per step for all streams
 //    (twice for the residual projections above 16 rows), so the weights cost ~3.3 GB per step
 //    whatever n. The step (610 launches) is captured once as a HIP graph and replayed.
-//  * Talker attention: split-KV decode attention, one block per (stream, kv head, key range); the
-//    two q heads of a GQA group share the K/V loads (one key per thread for the scores, eight
-//    keys' V rows in flight per wave); a combine kernel merges the ranges' (max, sum, vector).
+//  * Talker attention: split-KV decode attention, one block per (stream, kv head, key range), with
+//    the q/k head norms, RoPE and the step's f16 K/V store folded in (the range holding the new key
+//    stores it); the two q heads of a GQA group share the K/V loads (16 lanes per key for the
+//    scores, the same keys' V rows in flight); a combine kernel merges the ranges' (max, sum,
+//    vector).
 //  * Code-predictor attention: one block per (stream, kv head) fuses the q/k head norms, RoPE, the
 //    f16 K/V store into the stream's cp cache and the attention over its <= 16 positions.
 //  * Sampling: block_sample (sampler.h, the frame kernel's sampler) with one block per stream.
@@ -52,59 +54,26 @@ struct StreamMeta {
     uint64_t talker_seed, cp_seed;
 };
 
-// ---- talker: q/k norms + RoPE + K/V store, per stream -----------------------------------
-
-// Row m of the [q | k | v] partials: per-head RMSNorm of q and k, RoPE at the stream's position,
-// q kept f32, k and v rounded to f16 into the stream's cache (norm_rope_store, frame.hip:311-346).
-__global__ void __launch_bounds__(BT) k_st_qkv_finish(const float *part, int S, int M, int nq, int nkv, const float *qn,
-                                                      const float *kn, float eps, const float *invf, const StreamMeta *meta,
-                                                      uint16_t *const *kcache, uint16_t *const *vcache, float *q) {
-    extern __shared__ float row[];
-    const int m = blockIdx.x, pos = meta[m].n_past;
-    const int QD = nq * HD, KVD = nkv * HD, W = QD + 2 * KVD;
-    const size_t stride = static_cast<size_t>(M) * W;
-    for (int i = threadIdx.x * 4; i < W; i += BT * 4) {
-        const f32x4_t v = sum_parts4(part, S, stride, static_cast<size_t>(m) * W + i);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) row[i + j] = v[j];
-    }
-    __syncthreads();
-    const int wv = threadIdx.x >> 6, l = threadIdx.x & 63;
-    float sn, cs;
-    sincosf(static_cast<float>(pos) * gld(invf + l), &sn, &cs);
-    for (int hh = wv; hh < nq + nkv; hh += NW) {
-        float *hp = row + hh * HD;
-        const float *nw = hh < nq ? qn : kn;
-        const float a0 = hp[l], a1 = hp[l + HD / 2];
-        const float sc = rsqrtf(wave_sum(fmaf(a0, a0, a1 * a1)) / static_cast<float>(HD) + eps);
-        const float x0 = a0 * sc * gld(nw + l), x1 = a1 * sc * gld(nw + l + HD / 2);
-        hp[l] = x0 * cs - x1 * sn;
-        hp[l + HD / 2] = x0 * sn + x1 * cs;
-    }
-    __syncthreads();
-    for (int i = threadIdx.x; i < QD; i += BT) gst(q + static_cast<size_t>(m) * QD + i, row[i]);
-    uint16_t *kc = kcache[m] + static_cast<size_t>(pos) * KVD, *vc = vcache[m] + static_cast<size_t>(pos) * KVD;
-    for (int i = threadIdx.x; i < KVD; i += BT) {
-        gst(kc + i, f2h(row[QD + i]));
-        gst(vc + i, f2h(row[QD + KVD + i]));
-    }
-}
-
 // ---- talker: split-KV decode attention ----------------------------------------------------
 
-// Block (m, g, s): keys [s * KPS, min(n, (s + 1) * KPS)) of stream m's cache, n = n_past + 1, for
-// the two q heads of kv group g. Writes per head (max, sum of e^(score - max), unnormalised
-// vector) to part[m][g][s][h] = {m, l, o[HD]}.
-__global__ void __launch_bounds__(BT) k_st_attn(const float *q, const StreamMeta *meta, uint16_t *const *kcache,
-                                                uint16_t *const *vcache, int nq, int nkv, int splits, float *part) {
-    __shared__ float qs[2][HD], sc[2][KPS], red[2][NW], opart[NW][4][2][HD];
+// Block (m, g, s): keys [s * KPS, min(n, (s + 1) * KPS)) of stream m, n = n_past + 1, for the two
+// q heads of kv group g, from the raw q|k|v row of the stream (part, the projection's output).
+// Waves 0 and 1 take q heads 2g and 2g + 1: per-head RMSNorm and RoPE at the stream's position
+// (norm_rope_store, frame.hip:311-346). The block whose range holds the step's own key (n_past)
+// also normalises and ropes its k (wave 2), rounds k and v (wave 3) to f16, stores them into the
+// stream's cache at n_past and uses those values for that key; every other key comes from the
+// cache. Writes per head (max, sum of e^(score - max), unnormalised vector) to
+// out[m][g][s][h] = {m, l, o[HD]}.
+__global__ void __launch_bounds__(BT) k_st_attn(const float *part, const StreamMeta *meta, uint16_t *const *kcache,
+                                                uint16_t *const *vcache, int nq, int nkv, int splits, const float *qn,
+                                                const float *kn, float eps, const float *invf, float *partials) {
+    __shared__ float qs[2][HD], nkv_[2][HD], sc[2][KPS], red[2][NW], opart[NW][4][2][HD];
     const int m = blockIdx.x, g = blockIdx.y, s = blockIdx.z;
-    const int n = meta[m].n_past + 1, j0 = s * KPS, j1 = min(n, j0 + KPS), cnt = max(0, j1 - j0);
-    const int QD = nq * HD, KVD = nkv * HD;
+    const int pos = meta[m].n_past, n = pos + 1, j0 = s * KPS, j1 = min(n, j0 + KPS), cnt = max(0, j1 - j0);
+    const bool own = pos >= j0 && pos < j0 + KPS;       // this range holds the step's own key
+    const int QD = nq * HD, KVD = nkv * HD, W = QD + 2 * KVD;
     const int wv = threadIdx.x >> 6, l = threadIdx.x & 63;
-    float *out = part + ((static_cast<size_t>(m) * nkv + g) * splits + s) * 2 * (HD + 2);
-    qs[threadIdx.x >> 7][threadIdx.x & (HD - 1)] = gld(q + static_cast<size_t>(m) * QD + g * 2 * HD + threadIdx.x);
-    __syncthreads();
+    float *out = partials + ((static_cast<size_t>(m) * nkv + g) * splits + s) * 2 * (HD + 2);
     const uint16_t *kb = kcache[m] + g * HD, *vb = vcache[m] + g * HD;
     u32x4_t vr[KPS / NW / 4];
     // Scores, 16 lanes per key: wave w takes keys 64w .. 64w + 63 of the range, four per load
@@ -113,27 +82,77 @@ __global__ void __launch_bounds__(BT) k_st_attn(const float *q, const StreamMeta
     // heads' scores in sc.
     {
         const int c = l & 15, r = l >> 4;
-        float q0[8], q1[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            q0[e] = qs[0][c * 8 + e];
-            q1[e] = qs[1][c * 8 + e];
-        }
         constexpr int KI = KPS / NW / 4;
         u32x4_t kr[KI];
 #pragma unroll
         for (int i = 0; i < KI; ++i) {
             const int jl = wv * (KPS / NW) + 4 * i + r;
-            kr[i] = jl < cnt ? *(const NAVI_GLOBAL u32x4_t *) (kb + static_cast<size_t>(j0 + jl) * KVD + c * 8)
-                             : u32x4_t{0u, 0u, 0u, 0u};
+            kr[i] = jl < cnt && j0 + jl != pos ? *(const NAVI_GLOBAL u32x4_t *) (kb + static_cast<size_t>(j0 + jl) * KVD + c * 8)
+                                               : u32x4_t{0u, 0u, 0u, 0u};
         }
         // the same keys' V chunks are loaded now too (they do not depend on the scores): one
         // memory latency per block instead of two
 #pragma unroll
         for (int i = 0; i < KI; ++i) {
             const int jl = wv * (KPS / NW) + 4 * i + r;
-            vr[i] = jl < cnt ? *(const NAVI_GLOBAL u32x4_t *) (vb + static_cast<size_t>(j0 + jl) * KVD + c * 8)
-                             : u32x4_t{0u, 0u, 0u, 0u};
+            vr[i] = jl < cnt && j0 + jl != pos ? *(const NAVI_GLOBAL u32x4_t *) (vb + static_cast<size_t>(j0 + jl) * KVD + c * 8)
+                                               : u32x4_t{0u, 0u, 0u, 0u};
+        }
+        // while those loads are in flight: q heads 2g, 2g + 1 and (own range) the step's k and v,
+        // lane l holding dims l and l + 64
+        if (wv < 2 || own) {
+            const float *row = part + static_cast<size_t>(m) * W;
+            const float *hp = wv < 2 ? row + (2 * g + wv) * HD : row + QD + (wv - 2) * KVD + g * HD;
+            const float a0 = gld(hp + l), a1 = gld(hp + l + HD / 2);
+            if (wv < 3) {
+                float sn, cs;
+                sincosf(static_cast<float>(pos) * gld(invf + l), &sn, &cs);
+                const float *nw = wv < 2 ? qn : kn;
+                const float scl = rsqrtf(wave_sum(fmaf(a0, a0, a1 * a1)) / static_cast<float>(HD) + eps);
+                const float x0 = a0 * scl * gld(nw + l), x1 = a1 * scl * gld(nw + l + HD / 2);
+                const float y0 = x0 * cs - x1 * sn, y1 = x0 * sn + x1 * cs;
+                if (wv < 2) {
+                    qs[wv][l] = y0;
+                    qs[wv][l + HD / 2] = y1;
+                } else {
+                    const uint16_t h0 = f2h(y0), h1 = f2h(y1);
+                    uint16_t *kd = kcache[m] + static_cast<size_t>(pos) * KVD + g * HD;
+                    gst(kd + l, h0);
+                    gst(kd + l + HD / 2, h1);
+                    nkv_[0][l] = h2f(h0);
+                    nkv_[0][l + HD / 2] = h2f(h1);
+                }
+            } else {
+                const uint16_t h0 = f2h(a0), h1 = f2h(a1);
+                uint16_t *vd = vcache[m] + static_cast<size_t>(pos) * KVD + g * HD;
+                gst(vd + l, h0);
+                gst(vd + l + HD / 2, h1);
+                nkv_[1][l] = h2f(h0);
+                nkv_[1][l + HD / 2] = h2f(h1);
+            }
+        }
+        __syncthreads();
+        float q0[8], q1[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            q0[e] = qs[0][c * 8 + e];
+            q1[e] = qs[1][c * 8 + e];
+        }
+        if (own) {                         // the step's own key: its chunk from LDS
+#pragma unroll
+            for (int i = 0; i < KI; ++i) {
+                const int jl = wv * (KPS / NW) + 4 * i + r;
+                if (j0 + jl == pos) {
+                    half8_t hk, hv;
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        hk[e] = static_cast<_Float16>(nkv_[0][c * 8 + e]);
+                        hv[e] = static_cast<_Float16>(nkv_[1][c * 8 + e]);
+                    }
+                    __builtin_memcpy(&kr[i], &hk, 16);
+                    __builtin_memcpy(&vr[i], &hv, 16);
+                }
+            }
         }
 #pragma unroll
         for (int i = 0; i < KI; ++i) {
@@ -431,7 +450,7 @@ using namespace navi_amd::ms;
 
 // The step's activations and split-K workspace, and the HIP stream it runs on.
 struct StreamWork {
-    float *x = nullptr, *xn = nullptr, *q = nullptr, *att = nullptr, *h = nullptr, *part = nullptr, *apart = nullptr;
+    float *x = nullptr, *xn = nullptr, *att = nullptr, *h = nullptr, *part = nullptr, *apart = nullptr;
     float *lg = nullptr;
     int lx = 0, la = 0, lf = 0;       // row strides of x, att and h (ROW_PAD floats past the row)
     hipStream_t st = nullptr;
@@ -542,7 +561,7 @@ void layer(navi_streams &h, StreamWork &g, const LayerW &w, float eps, int rows,
 navi_status run_group(navi_streams *h, StreamWork &g, int i0, int n, int zsplits, const float *step_in,
                       const float *d_trailing, const SampleArgs &sa, char *err, size_t errlen) {
     hipStream_t s = g.st;
-    const int H = h->H, QKVW = h->QD + 2 * h->KVD;
+    const int H = h->H;
     const float et = h->p.talker.rms_eps, ec = h->p.cp.rms_eps;
     const StreamMeta *meta = h->meta + i0;
     uint8_t *seen = h->seen + static_cast<size_t>(i0) * h->VT;
@@ -557,10 +576,8 @@ navi_status run_group(navi_streams *h, StreamWork &g, int i0, int n, int zsplits
         uint16_t *const *kt = h->ktab + static_cast<size_t>(l) * h->ms + i0;
         uint16_t *const *vt = h->vtab + static_cast<size_t>(l) * h->ms + i0;
         layer(*h, g, h->tl[l], et, n, [&]() {
-            hipLaunchKernelGGL(k_st_qkv_finish, dim3(n), dim3(BT), QKVW * sizeof(float), s, g.part, 1, n, h->NQ, h->NKV,
-                               h->tl[l].qn, h->tl[l].kn, et, h->invf_t, meta, kt, vt, g.q);
-            hipLaunchKernelGGL(k_st_attn, dim3(n, h->NKV, zsplits), dim3(BT), 0, s, g.q, meta, kt, vt, h->NQ, h->NKV, h->splits,
-                               g.apart);
+            hipLaunchKernelGGL(k_st_attn, dim3(n, h->NKV, zsplits), dim3(BT), 0, s, g.part, meta, kt, vt, h->NQ, h->NKV,
+                               h->splits, h->tl[l].qn, h->tl[l].kn, et, h->invf_t, g.apart);
             hipLaunchKernelGGL(k_st_attn_combine, dim3(n, h->NKV), dim3(BT), 0, s, g.apart, meta, h->NQ, h->NKV, h->splits,
                                g.att, g.la);
         });
@@ -675,7 +692,6 @@ navi_status navi_streams_create(const navi_model_params *p, const navi_tensor_re
     g.lf = h->F + ROW_PAD;
     SA(g.x, R * g.lx);
     SA(g.xn, R * H);
-    SA(g.q, static_cast<size_t>(max_streams) * h->QD);
     SA(g.att, R * g.la);
     SA(g.h, R * g.lf);
     SA(g.part, pf_need);
