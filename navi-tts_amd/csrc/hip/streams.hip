@@ -11,7 +11,7 @@
 //    weights) with M = n streams (code-predictor positions 0 and 1: 2n rows), the RMSNorm, SwiGLU
 //    and residual add fused in. Every weight byte streams from HBM once per step for all streams
 //    (twice for the residual projections above 16 rows), so the weights cost ~3.3 GB per step
-//    whatever n. The step (610 launches) is captured once as a HIP graph and replayed.
+//    whatever n. The step (582 launches) is captured once as a HIP graph and replayed.
 //  * Talker attention: split-KV decode attention, one block per (stream, kv head, key range), with
 //    the q/k head norms, RoPE and the step's f16 K/V store folded in (the range holding the new key
 //    stores it); the two q heads of a GQA group share the K/V loads (16 lanes per key for the
