@@ -11,6 +11,9 @@
 //   all-gather N, 8 copies : every block publishes N/256 words to 8 copies (one per XCD) and
 //                            gathers all N words from its own XCD's copy (k_frame's broadcast);
 //   all-gather N, 1 copy   : the same from a single copy;
+//   all-gather N, chunk polls: 8 copies, but every thread polls all words of its producer's chunk
+//                            until every tag matches, so the poll that succeeds delivers the data
+//                            (no sentinel round and no second read after a barrier);
 //   reduce-scatter 1024    : every block publishes 4 words to each of the 256 blocks (one copy)
 //                            and gathers the 1024 words addressed to it (the shape of a split
 //                            matvec whose partial sums go to the row owners);
@@ -103,8 +106,38 @@ __device__ bool wait_and_read(const uint64_t *base, int np, int stride, uint32_t
     return bad == 0;
 }
 
+// every thread polls its own PER contiguous words (producer t's whole chunk when CH == PER) until
+// every tag matches: the poll that succeeds delivers the data (no second read after a barrier)
+template <int N>
+__device__ bool wait_full(const uint64_t *base, uint32_t tag, uint32_t *fail, float *dst, int &bad) {
+    constexpr int PER = N / BT;
+    const uint64_t *p = base + threadIdx.x * PER;
+    uint64_t w[PER];
+#pragma unroll
+    for (int k = 0; k < PER; ++k) w[k] = peek(p + k);
+    unsigned long long s = 0;
+    for (;;) {
+        bool done = true;
+#pragma unroll
+        for (int k = 0; k < PER; ++k) done &= tag_of(w[k]) == tag;
+        if (done) break;
+        if (++s >= CAP || ((s & 63) == 0 && peek(reinterpret_cast<const uint64_t *>(fail)) != 0)) {
+            bad = 1;
+            break;
+        }
+#pragma unroll
+        for (int k = 0; k < PER; ++k)
+            if (tag_of(w[k]) != tag) w[k] = peek(p + k);
+    }
+#pragma unroll
+    for (int k = 0; k < PER; ++k) dst[threadIdx.x * PER + k] = __uint_as_float(static_cast<uint32_t>(w[k]));
+    __syncthreads();
+    if (bad && threadIdx.x == 0) __hip_atomic_store(fail, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return bad == 0;
+}
+
 // MODE 0: all-gather over the grid (N words, REPL copies); 1: reduce-scatter (1024 words per
-// block); 2: all-gather among the blocks of one XCD (1024 words).
+// block); 2: all-gather among the blocks of one XCD (1024 words); 3: MODE 0 with chunk polls.
 template <int MODE, int N, int REPL>
 __global__ void __launch_bounds__(BT, 1) k_hops(uint64_t *mb, size_t region, int rounds, uint32_t base_tag, uint32_t *fail,
                                                 int *xcc_of_block) {
@@ -125,6 +158,13 @@ __global__ void __launch_bounds__(BT, 1) k_hops(uint64_t *mb, size_t region, int
                 put(reg + static_cast<size_t>(rep) * N + b * CH + c, word(tag, acc + c));
             }
             if (!wait_and_read<N>(reg + static_cast<size_t>(REPL > 1 ? x % REPL : 0) * N, NB, CH, tag, fail, buf, bad)) return;
+        } else if (MODE == 3) {
+            constexpr int CH = N / NB;
+            for (int i = threadIdx.x; i < CH * REPL; i += BT) {
+                const int c = i % CH, rep = i / CH;
+                put(reg + static_cast<size_t>(rep) * N + b * CH + c, word(tag, acc + c));
+            }
+            if (!wait_full<N>(reg + static_cast<size_t>(REPL > 1 ? x % REPL : 0) * N, tag, fail, buf, bad)) return;
         } else if (MODE == 1) {
             // 4 words to every block d: slot d * 1024 + b * 4 .. + 3
             for (int i = threadIdx.x; i < NB * 4; i += BT) {
@@ -198,6 +238,8 @@ int main(int argc, char **argv) {
         {"all-gather 1024 words, 1 copy", reinterpret_cast<const void *>(k_hops<0, 1024, 1>)},
         {"all-gather 3072 words, 8 copies (per XCD)", reinterpret_cast<const void *>(k_hops<0, 3072, 8>)},
         {"all-gather 2048 words, 8 copies (per XCD)", reinterpret_cast<const void *>(k_hops<0, 2048, 8>)},
+        {"all-gather 1024 words, 8 copies, chunk polls", reinterpret_cast<const void *>(k_hops<3, 1024, 8>)},
+        {"all-gather 3072 words, 8 copies, chunk polls", reinterpret_cast<const void *>(k_hops<3, 3072, 8>)},
         {"reduce-scatter 1024 words (4 from each block)", reinterpret_cast<const void *>(k_hops<1, 1024, 1>)},
         {"XCD-local all-gather 1024 words (32 blocks)", reinterpret_cast<const void *>(k_hops<2, 1024, 1>)},
     };
