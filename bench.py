@@ -353,9 +353,26 @@ def cpu_baseline(path: Path, frames: int) -> dict:
     for i in range(frames):
         _, step = ora.frame(s, 2, i + 1, trail, kv=kvo, n_past=N_PAST, step_in=step)
     ms = (time.perf_counter() - t0) * 1e3 / frames
+    # the same restatement's prefill (10 prompt rows, N(0,1)) and codec decoder (8 frames of codes
+    # U[0, 2048) in one call), each timed once after one warm-up call
+    rows = rng.standard_normal((10, 1024)).astype(np.float32)
+    kvp = ora.new_kv(16)
+    ora.prefill(rows, kvp)
+    t0 = time.perf_counter()
+    ora.prefill(rows, kvp)
+    pre_ms = (time.perf_counter() - t0) * 1e3
+    from oracle.vocoder import Vocoder as OVoc
+    voc = OVoc(path)
+    codes = rng.integers(0, 2048, (8, 16))
+    voc.decode(codes[:2])
+    t0 = time.perf_counter()
+    voc.decode(codes)
+    voc_ms = (time.perf_counter() - t0) * 1e3 / len(codes)
     return {"value": round(ms, 2), "unit": "ms/frame", "cores": threads, "kind": "port", "cpu": host_cpu(),
+            "prefill_ms_rows_10": round(pre_ms, 1), "vocoder_ms_per_frame": round(voc_ms, 1),
             "sample": f"{frames} frames at n_past={N_PAST} after 1 warm-up frame, full 0.6B random-init model, "
-                      f"PyTorch f32 restatement (oracle/) with torch.set_num_threads({threads})"}
+                      f"PyTorch f32 restatement (oracle/) with torch.set_num_threads({threads}); "
+                      "a 10-row prefill and an 8-frame codec decode, each once after a warm-up call"}
 
 
 def main():
