@@ -129,7 +129,7 @@ struct Smem {
                 float big[2 * FF];  // att [T][QD] | h [T][FF]
                 struct { float lg[VT]; alignas(16) int idx[VT]; } samp;   // idx: the sampler's counters
             };
-            // this block's cp K/V (kv head blockIdx/2), whole frame, zero until written; K rows
+            // this block's cp K/V (kv head att_head() / 2), whole frame, zero until written; K rows
             // keep 16-byte chunk c at slot c ^ (row & 15)
             uint16_t ckv[2][MAX_CL][NCB][HD];
             float rope[2][NCB][HD / 2];      // cp RoPE cos / sin of positions 0..15, dim pairs
@@ -176,6 +176,17 @@ __device__ __forceinline__ int tid() { return static_cast<int>(threadIdx.x); }
 __device__ __forceinline__ int lane() { return static_cast<int>(threadIdx.x) & (WAVE - 1); }
 __device__ __forceinline__ int wave() { return static_cast<int>(threadIdx.x) / WAVE; }
 __device__ __forceinline__ int blk() { return static_cast<int>(blockIdx.x); }
+
+// Blocks are dispatched to the XCDs round-robin (block b on XCD b % 8), and kv group g's q|k|v
+// rows and its attention are kept on XCD g, so the q|k|v -> attention hop stays inside one L2:
+// the 32 blocks of XCD g (j = b / 8) compute q heads 2g and 2g + 1 (j < 16), k of group g
+// (16 <= j < 24) and v of group g (j >= 24), 16 rows each; q head h's attention blocks are the
+// blocks b with b % 8 == h / 2 and (b / 8) % 2 == h % 2.
+__device__ __forceinline__ int qkv_row0() {
+    const int x = blk() % NKV, j = blk() / NKV;
+    return j < 16 ? 2 * HD * x + 16 * j : j < 24 ? QD + HD * x + 16 * (j - 16) : QD + KVD + HD * x + 16 * (j - 24);
+}
+__device__ __forceinline__ int att_head() { return 2 * (blk() % NKV) + ((blk() / NKV) & 1); }
 
 // ---- block reductions (fixed order: every block gets bit-identical results) ----
 
@@ -384,7 +395,7 @@ __device__ __forceinline__ void xfrag(const float *x, int base, float (&xf)[NC][
 __device__ __forceinline__ uint4 ldw(const uint16_t *p, bool reuse) { return reuse ? ldg16(p) : ldg16_stream(p); }
 
 __device__ __forceinline__ void load_qkv(Regs &R, const LayerPtrs &L, bool reuse) {
-    const int rb = blk() * (QKV / NB);
+    const int rb = qkv_row0();
     const uint16_t *M;
     int base;
     if (rb < QD) { M = L.wq; base = rb; }
@@ -448,7 +459,7 @@ __device__ __forceinline__ void load_lm(Regs &R, const uint16_t *head) {
 
 template <int T>
 __device__ __forceinline__ void qkv_phase(const Args &a, const Regs &R, Smem &S, uint32_t tag, const float (&sc)[T]) {
-    const int row0 = blk() * (QKV / NB) + wave() * 4;
+    const int row0 = qkv_row0() + wave() * 4;
 #pragma unroll
     for (int t = 0; t < T; ++t) {
         float xf[2][8], d[4];
@@ -583,17 +594,18 @@ __device__ __forceinline__ void stage_kv(const uint16_t *Kc, const uint16_t *Vc,
     }
 }
 
-// Talker attention, spread over all 256 blocks: block b takes q head h = b % NH and range
+// Talker attention, spread over all 256 blocks: block b takes q head h = att_head() and range
 // r = b / NH of the cached keys (NR ranges of ceil(pos / NR) keys; the current key at pos goes
 // to the last range, whose even-head block also writes the new f16 K/V row). A block stages its
 // range's K/V rows in LDS by DMA while this step's q/k/v are in flight, normalises and rotates
 // q (and the current k), runs a per-wave online softmax over its keys and publishes the range's
-// partial (max, sum, unnormalised V sum) as one AP_W-word chunk. Block h (range 0) gathers the NR
-// partials of head h, combines them in range order and publishes the head's output. The ranges
-// of a head sit on one XCD (block h + NH r), so the partial hop stays within its L2.
+// partial (max, sum, unnormalised V sum) as one AP_W-word chunk. The range-0 block of head h
+// gathers the NR partials of head h, combines them in range order and publishes the head's
+// output. Every range of head h sits on XCD h / 2 with the blocks that produce its q|k|v, so
+// both the q|k|v hop and the partial hop stay within one L2.
 __device__ bool talker_attention(const Args &a, const Ctx &cx, float qkw, int il, uint32_t tag_qkv, uint32_t tag_ap,
                                  uint32_t tag_att, Smem &S) {
-    const int h = blk() % NH, r = blk() / NH, g = h / GRP, pos = a.n_past;
+    const int h = att_head(), r = blk() / NH, g = h / GRP, pos = a.n_past;
     const int R = (pos + NR - 1) / NR, j0 = min(pos, r * R), n = max(0, min(pos, j0 + R) - j0);   // n <= KCH
     const bool last = r == NR - 1;
     uint16_t *const Kbase = cx.kv[il], *const Vbase = cx.kv[MAX_TL + il];
@@ -757,12 +769,12 @@ __device__ bool talker_attention(const Args &a, const Ctx &cx, float qkw, int il
     return true;
 }
 
-// Code-predictor attention for q head h = blockIdx over T rows at positions p0..p0+T-1;
+// Code-predictor attention for q head h = att_head() (blocks 0..15) over T rows at positions p0..p0+T-1;
 // K/V of this block's kv head live in S.u.m.ckv for the whole frame (rows not yet written are
 // zero), RoPE cos/sin in S.u.m.rope (the frame's table of the 16 cp positions).
 template <int T>
 __device__ bool cp_attention(const Args &a, float qkw, int il, int p0, uint32_t tag_qkv, uint32_t tag_att, Smem &S) {
-    const int h = blk(), g = h / GRP;
+    const int h = att_head(), g = h / GRP;
     PROF_MARK(a, S);
     S.nw[tid()] = qkw;                                     // published by gather_head's barrier
     if (!gather_head<T>(a, h, g, tag_qkv, S)) return false;
