@@ -210,40 +210,42 @@ __global__ void __launch_bounds__(BT) k_swiglu(const float *part, int S, int M, 
     }
 }
 
-// Row m of [q | k | v] (partials, ldp = nq + 2 nkv heads * 128): per-head RMSNorm of q and k,
-// rotate-half RoPE at position pos0 + m, q kept f32, k and v rounded to f16 into the cache
-// (k_qk_norm_rope, talker.hip:46-82).
-__global__ void __launch_bounds__(BT) k_qkv_finish(const float *part, int S, int M, int nq, int nkv, const float *qn,
-                                                   const float *kn, float eps, const float *invf, int pos0, float *q,
-                                                   uint16_t *kc, uint16_t *vc) {
-    extern __shared__ float row[];
+// Row m of [q | k | v] (nq + 2 nkv heads of 128 in one row of the q|k|v projection): per-head
+// RMSNorm of q and k, rotate-half RoPE at position pos0 + m, q kept f32, k and v rounded to f16
+// into the cache (k_qk_norm_rope, talker.hip:46-82). One wave per head slice (q heads, then k,
+// then v; block (m, b) takes slices 4b .. 4b + 3), lane l holding dims l and l + 64: no LDS and no
+// barrier, so the launch is one load latency deep. The values start from 0 + x as the split-K sum
+// of one partial did (a -0 stays +0 in the cache).
+__global__ void __launch_bounds__(BT) k_qkv_finish(const float *qkv, int nq, int nkv, const float *qn, const float *kn,
+                                                   float eps, const float *invf, int pos0, float *q, uint16_t *kc,
+                                                   uint16_t *vc) {
     const int m = blockIdx.x, pos = pos0 + m;
+    const int hh = blockIdx.y * (BT / WAVE) + (threadIdx.x >> 6), l = threadIdx.x & 63;
+    if (hh >= nq + 2 * nkv) return;
     const int QD = nq * HD, KVD = nkv * HD, W = QD + 2 * KVD;
-    const size_t stride = static_cast<size_t>(M) * W;
-    for (int i = threadIdx.x * 4; i < W; i += BT * 4) {
-        const f32x4_t v = sum_parts4(part, S, stride, static_cast<size_t>(m) * W + i);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) row[i + j] = v[j];
+    const float *hp = qkv + static_cast<size_t>(m) * W + hh * HD;
+    const float a0 = 0.f + gld(hp + l), a1 = 0.f + gld(hp + l + HD / 2);
+    if (hh >= nq + nkv) {
+        uint16_t *vd = vc + static_cast<size_t>(pos) * KVD + (hh - nq - nkv) * HD;
+        gst(vd + l, f2h(a0));
+        gst(vd + l + HD / 2, f2h(a1));
+        return;
     }
-    __syncthreads();
-    const int wv = threadIdx.x >> 6, l = threadIdx.x & 63;
-    const float inv = gld(invf + l);
     float sn, cs;
-    sincosf(static_cast<float>(pos) * inv, &sn, &cs);
-    for (int hh = wv; hh < nq + nkv; hh += BT / WAVE) {
-        float *hp = row + hh * HD;
-        const float *nw = hh < nq ? qn : kn;
-        const float a0 = hp[l], a1 = hp[l + HD / 2];
-        const float sc = rsqrtf(wave_sum(fmaf(a0, a0, a1 * a1)) / static_cast<float>(HD) + eps);
-        const float x0 = a0 * sc * gld(nw + l), x1 = a1 * sc * gld(nw + l + HD / 2);
-        hp[l] = x0 * cs - x1 * sn;
-        hp[l + HD / 2] = x1 * cs + x0 * sn;
-    }
-    __syncthreads();
-    for (int i = threadIdx.x; i < QD; i += BT) gst(q + static_cast<size_t>(m) * QD + i, row[i]);
-    for (int i = threadIdx.x; i < KVD; i += BT) {
-        gst(kc + static_cast<size_t>(pos) * KVD + i, f2h(row[QD + i]));
-        gst(vc + static_cast<size_t>(pos) * KVD + i, f2h(row[QD + KVD + i]));
+    sincosf(static_cast<float>(pos) * gld(invf + l), &sn, &cs);
+    const float *nw = hh < nq ? qn : kn;
+    const float sc = rsqrtf(wave_sum(fmaf(a0, a0, a1 * a1)) / static_cast<float>(HD) + eps);
+    const float x0 = a0 * sc * gld(nw + l), x1 = a1 * sc * gld(nw + l + HD / 2);
+    const float y0 = x0 * cs - x1 * sn;
+    const float y1 = x1 * cs + x0 * sn;
+    if (hh < nq) {
+        float *qd = q + static_cast<size_t>(m) * QD + hh * HD;
+        gst(qd + l, y0);
+        gst(qd + l + HD / 2, y1);
+    } else {
+        uint16_t *kd = kc + static_cast<size_t>(pos) * KVD + (hh - nq) * HD;
+        gst(kd + l, f2h(y0));
+        gst(kd + l + HD / 2, f2h(y1));
     }
 }
 
@@ -860,8 +862,8 @@ void prefill_layers(navi_talker &t, int T, hipStream_t s) {
         const LayerW &w = t.layers[l];
         rows::launch_rows(rows::EPI_PLAIN, true, t.x, t.lx, T, H, w.ln1, t.eps, w.wq, t.QD, w.wk, t.KVD, w.wv, t.KVD, t.part,
                           QKVW, t.flag, s);
-        hipLaunchKernelGGL(k_qkv_finish, dim3(T), dim3(BT), QKVW * sizeof(float), s, t.part, 1, T, t.NQ, t.NKV, w.qn,
-                           w.kn, t.eps, t.invf, 0, t.q, t.kk[l], t.vv[l]);
+        hipLaunchKernelGGL(k_qkv_finish, dim3(T, (t.NQ + 2 * t.NKV + BT / WAVE - 1) / (BT / WAVE)), dim3(BT), 0, s, t.part,
+                           t.NQ, t.NKV, w.qn, w.kn, t.eps, t.invf, 0, t.q, t.kk[l], t.vv[l]);
         if (T <= SHORT_KEYS)
             hipLaunchKernelGGL(k_attn_prefill_short, dim3(T, t.NKV), dim3(BT), 0, s, t.q, t.kk[l], t.vv[l], t.NQ, t.NKV,
                                0, scale, t.att, t.la);
