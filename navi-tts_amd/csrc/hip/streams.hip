@@ -261,7 +261,7 @@ __global__ void __launch_bounds__(BT) k_st_cp_attn(const float *part, int S, int
                                                    const float *qn, const float *kn, float eps, const float *invf, int layer,
                                                    int n_layer, uint16_t *cpk, uint16_t *cpv, float *att, int lda) {
     __shared__ float vec[2][4][HD];          // [t][q0, q1, k, v]
-    __shared__ float kf[NCB][HD], vf[NCB][HD];
+    __shared__ float kf[NCB][HD + 4], vf[NCB][HD];   // K rows padded: the 4-lane score reads of 16 keys spread over the banks
     const int m = blockIdx.x, g = blockIdx.y;
     const int QD = nq * HD, KVD = nkv * HD, W = QD + 2 * KVD;
     const size_t stride = static_cast<size_t>(rows) * W;
@@ -275,11 +275,17 @@ __global__ void __launch_bounds__(BT) k_st_cp_attn(const float *part, int S, int
         for (int e = 0; e < 4; ++e) vec[t][vi][d + e] = v[e];
     }
     const size_t base = (static_cast<size_t>(m) * n_layer + layer) * NCB * KVD + g * HD;
-    // earlier positions of this stream's cp cache (written by earlier launches)
-    for (int i = threadIdx.x; i < p0 * HD; i += BT) {
+    // earlier positions of this stream's cp cache (written by earlier launches); rows past this
+    // launch's last position zero (the value sum below reads all NCB rows with weight 0)
+    for (int i = threadIdx.x; i < NCB * HD; i += BT) {
         const int j = i / HD, d = i % HD;
-        kf[j][d] = h2f(gld(cpk + base + static_cast<size_t>(j) * KVD + d));
-        vf[j][d] = h2f(gld(cpv + base + static_cast<size_t>(j) * KVD + d));
+        if (j < p0) {
+            kf[j][d] = h2f(gld(cpk + base + static_cast<size_t>(j) * KVD + d));
+            vf[j][d] = h2f(gld(cpv + base + static_cast<size_t>(j) * KVD + d));
+        } else if (j >= p0 + T) {
+            kf[j][d] = 0.f;
+            vf[j][d] = 0.f;
+        }
     }
     __syncthreads();
     // head norms + RoPE: one wave per (t, vector) of q0, q1, k
@@ -306,28 +312,42 @@ __global__ void __launch_bounds__(BT) k_st_cp_attn(const float *part, int S, int
         vf[p0 + t][d] = h2f(vh);
     }
     __syncthreads();
-    // attention: one wave per (t, head), lane j scores key j
+    // attention: one wave per (t, head). Scores: lanes 4j..4j+3 take key j, lane 4j + s dims
+    // 32s..32s+31 (one FMA chain), summed by two DPP steps. Value sum: lane l owns dims 2l, 2l+1
+    // over all NCB rows (rows past the key count are zero with weight 0), even and odd keys in
+    // two chains.
     for (int task = wv; task < T * 2; task += NW) {
         const int t = task / 2, hh = task % 2, n = p0 + t + 1;
-        float sl = -INFINITY;
-        if (l < n) {
-            float acc = 0.f;
-#pragma unroll 8
-            for (int d = 0; d < HD; ++d) acc = fmaf(kf[l][d], vec[t][hh][d], acc);
-            sl = acc * ATT_SCALE;
+        const int j = l >> 2, sq = l & 3;
+        float acc = 0.f;
+        {
+            const f32x4_t *kr = reinterpret_cast<const f32x4_t *>(&kf[j][sq * 32]);
+            const f32x4_t *qr = reinterpret_cast<const f32x4_t *>(&vec[t][hh][sq * 32]);
+#pragma unroll
+            for (int c = 0; c < 8; ++c) {
+                const f32x4_t kk = kr[c], qq = qr[c];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc = fmaf(kk[e], qq[e], acc);
+            }
         }
+        acc += dpp_mov<0xB1>(acc);       // quad_perm [1,0,3,2]
+        acc += dpp_mov<0x4E>(acc);       // quad_perm [2,3,0,1]: the 4 lanes of key j hold its dot
+        const float sl = j < n ? acc * ATT_SCALE : -INFINITY;
         const float mx = wave_max(sl);
-        const float e = l < n ? expf(sl - mx) : 0.f;
-        const float inv = 1.f / wave_sum(e);
-        float o0 = 0.f, o1 = 0.f;
-        for (int j = 0; j < n; ++j) {
-            const float p = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), j));
-            o0 = fmaf(p, vf[j][2 * l], o0);
-            o1 = fmaf(p, vf[j][2 * l + 1], o1);
+        const float e = j < n ? expf(sl - mx) : 0.f;
+        const float inv = 1.f / wave_sum(sq == 0 ? e : 0.f);
+        float o0 = 0.f, o1 = 0.f, q0 = 0.f, q1 = 0.f;
+#pragma unroll
+        for (int r = 0; r < NCB; r += 2) {
+            const float pa = lane_value(e, 4 * r), pb = lane_value(e, 4 * r + 4);
+            o0 = fmaf(pa, vf[r][2 * l], o0);
+            o1 = fmaf(pa, vf[r][2 * l + 1], o1);
+            q0 = fmaf(pb, vf[r + 1][2 * l], q0);
+            q1 = fmaf(pb, vf[r + 1][2 * l + 1], q1);
         }
         float *dst = att + static_cast<size_t>(m * T + t) * lda + (g * 2 + hh) * HD + 2 * l;
-        gst(dst, o0 * inv);
-        gst(dst + 1, o1 * inv);
+        gst(dst, (o0 + q0) * inv);
+        gst(dst + 1, (o1 + q1) * inv);
     }
 }
 
