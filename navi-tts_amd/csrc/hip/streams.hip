@@ -238,14 +238,53 @@ __global__ void __launch_bounds__(BT) k_st_attn_combine(const float *part, const
     const int m = blockIdx.x, g = blockIdx.y, hh = threadIdx.x >> 7, d = threadIdx.x & (HD - 1);
     const int used = (meta[m].n_past + 1 + KPS - 1) / KPS;
     const float *p = part + (static_cast<size_t>(m) * nkv + g) * splits * 2 * (HD + 2) + hh * (HD + 2);
-    float M = -INFINITY;
-    for (int s = 0; s < used; ++s) M = fmaxf(M, gld(p + s * 2 * (HD + 2)));
-    float num = 0.f, den = 0.f;
-    for (int s = 0; s < used; ++s) {
+    // the ranges' (max, sum, value) loads in batches of CB, every load of a batch in flight at
+    // once; the first batch (contexts up to CB * KPS keys) stays in registers for both passes
+    constexpr int CB = 8;
+    float mv[CB], lv[CB], ov[CB];
+#pragma unroll
+    for (int s = 0; s < CB; ++s) {
         const float *ps = p + s * 2 * (HD + 2);
-        const float w = expf(gld(ps) - M);
-        den = fmaf(gld(ps + 1), w, den);
-        num = fmaf(gld(ps + 2 + d), w, num);
+        mv[s] = s < used ? gld(ps) : -INFINITY;
+        lv[s] = s < used ? gld(ps + 1) : 0.f;
+        ov[s] = s < used ? gld(ps + 2 + d) : 0.f;
+    }
+    float M = -INFINITY;
+#pragma unroll
+    for (int s = 0; s < CB; ++s)
+        if (s < used) M = fmaxf(M, mv[s]);
+    for (int s0 = CB; s0 < used; s0 += CB) {
+        float mb[CB];
+#pragma unroll
+        for (int s = 0; s < CB; ++s) mb[s] = s0 + s < used ? gld(p + (s0 + s) * 2 * (HD + 2)) : -INFINITY;
+#pragma unroll
+        for (int s = 0; s < CB; ++s)
+            if (s0 + s < used) M = fmaxf(M, mb[s]);
+    }
+    float num = 0.f, den = 0.f;
+#pragma unroll
+    for (int s = 0; s < CB; ++s)
+        if (s < used) {
+            const float w = expf(mv[s] - M);
+            den = fmaf(lv[s], w, den);
+            num = fmaf(ov[s], w, num);
+        }
+    for (int s0 = CB; s0 < used; s0 += CB) {
+        float mb[CB], lb[CB], ob[CB];
+#pragma unroll
+        for (int s = 0; s < CB; ++s) {
+            const float *ps = p + (s0 + s) * 2 * (HD + 2);
+            mb[s] = s0 + s < used ? gld(ps) : -INFINITY;
+            lb[s] = s0 + s < used ? gld(ps + 1) : 0.f;
+            ob[s] = s0 + s < used ? gld(ps + 2 + d) : 0.f;
+        }
+#pragma unroll
+        for (int s = 0; s < CB; ++s)
+            if (s0 + s < used) {
+                const float w = expf(mb[s] - M);
+                den = fmaf(lb[s], w, den);
+                num = fmaf(ob[s], w, num);
+            }
     }
     gst(att + static_cast<size_t>(m) * lda + (g * 2 + hh) * HD + d, num / den);
 }
