@@ -128,7 +128,8 @@ __device__ __forceinline__ void carry_rows(const float *hist, const float *x, in
 
 // Four input channels ci..ci+3 of the RVQ front end at frame t: the semantic codebook's row, or
 // the rest codebooks' rows summed in f32 in codebook order (k_rvq, vocoder.hip:125-143).
-// All the row loads of the sum are issued before the first add.
+// Every code load first (indices clamped into the frame's row, so all of them run at once), then
+// every row load, then the sum: two memory latencies.
 __device__ __forceinline__ f32x4_t rvq_row4(const ConvArgs &a, int t, int ci) {
     const int half = a.Cin >> 1;
     const int32_t *code = a.codes + static_cast<size_t>(t) * a.nq;
@@ -138,11 +139,14 @@ __device__ __forceinline__ f32x4_t rvq_row4(const ConvArgs &a, int t, int ci) {
     };
     if (ci < half) return unpack(gld(reinterpret_cast<const u32x2_t *>(a.cb0 + static_cast<size_t>(gld(code)) * half + ci)));
     constexpr int MAXQ = 16;
+    int cq[MAXQ - 1];
+#pragma unroll
+    for (int q = 1; q < MAXQ; ++q) cq[q - 1] = gld(code + min(q, a.nq - 1));
     u32x2_t w[MAXQ - 1];
 #pragma unroll
     for (int q = 1; q < MAXQ; ++q)
         if (q < a.nq)
-            w[q - 1] = gld(reinterpret_cast<const u32x2_t *>(a.cbr + (static_cast<size_t>(q - 1) * a.cbsize + gld(code + q)) * half +
+            w[q - 1] = gld(reinterpret_cast<const u32x2_t *>(a.cbr + (static_cast<size_t>(q - 1) * a.cbsize + cq[q - 1]) * half +
                                                             (ci - half)));
     f32x4_t v = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
