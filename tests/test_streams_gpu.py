@@ -44,7 +44,8 @@ class Batch:
                 v = rng.standard_normal((n, kvd)).astype(np.float16)
                 kvo[l][0][:n] = torch.from_numpy(k.astype(np.float32))
                 kvo[l][1][:n] = torch.from_numpy(v.astype(np.float32))
-                kvd_.fill(l, k, v, 0)
+                if n:
+                    kvd_.fill(l, k, v, 0)
             self.kv_o.append(kvo)
             self.kv_d.append(kvd_)
         n = len(contexts)
@@ -63,11 +64,12 @@ def batch(small_blob):
     return Batch(small_blob, [37, 300, 1, 129, 256][:N_STREAMS])
 
 
-def test_greedy_streams_match_oracle(batch):
+def greedy_steps(b, steps, name):
+    """`steps` batched greedy steps of every stream of `b`, each checked against the oracle's
+    frame for that stream alone (teacher-forced on the device codes): taps within tolerance,
+    codes through the greedy gate, next step input bit-exact."""
     from oracle import sampler as osamp
-    b = batch
     n = len(b.n_past)
-    steps = 3
     s_gpu = b.abi.Sampling.greedy(min_frames=steps)
     s_ora = osamp.Sampling(temperature=0.0, top_k=50, repetition_penalty=1.05, cp_temperature=0.0, cp_top_k=50,
                            min_frames=steps)
@@ -100,7 +102,17 @@ def test_greedy_streams_match_oracle(batch):
             np.testing.assert_array_equal(dev_step[i], so)
             step_o[i] = so
             n_past[i] += 1
-    summarize_decisions("streams_5_greedy", record)
+    summarize_decisions(name, record)
+
+
+def test_greedy_streams_match_oracle(batch):
+    greedy_steps(batch, 3, "streams_5_greedy")
+
+
+def test_greedy_streams_from_an_empty_cache(small_blob):
+    """Streams whose caches start empty (n_past 0: the key range that holds the step's own key has
+    no cached key at all) beside short ones, stepped past the first cached keys."""
+    greedy_steps(Batch(small_blob, [0, 1, 2], seed=13), 3, "streams_ctx0_greedy")
 
 
 def test_sampled_streams_match_oracle_on_device_logits(batch):
