@@ -344,7 +344,11 @@ __global__ void __launch_bounds__(BT) k_attn_prefill(const float *q, const uint1
 // covers four whole 256-byte key rows, and every K and V chunk of the block is issued before the
 // first score: one memory latency per block where the loop above pays one per 32 keys of V.
 // Scores are summed over a key's 16 lanes by DPP; thread t owns key t for the softmax.
+// The score and value loops skip the key groups past the row's keys: per group of four keys when
+// every key of the launch falls in wave 0's range (FEW: prompts of up to 64 rows), per wave
+// otherwise (a per-group exit in the unrolled loops of the longer rows measured slower).
 constexpr int SHORT_KEYS = 256;
+template <bool FEW>
 __global__ void __launch_bounds__(BT) k_attn_prefill_short(const float *q, const uint16_t *kc, const uint16_t *vc, int nq,
                                                            int nkv, int pos0, float scale, float *out, int ldo) {
     constexpr int NWV = BT / WAVE, KW = SHORT_KEYS / NWV, KI = KW / 4;
@@ -376,6 +380,7 @@ __global__ void __launch_bounds__(BT) k_attn_prefill_short(const float *q, const
         }
 #pragma unroll
         for (int i = 0; i < KI; ++i) {
+            if (wv * KW + (FEW ? 4 * i : 0) >= n) break;  // this wave's remaining keys are past the row's
             uint4 k4;
             __builtin_memcpy(&k4, &kr[i], 16);
             float a0 = dot8(k4, q0, 0.f), a1 = dot8(k4, q1, 0.f);
@@ -414,6 +419,7 @@ __global__ void __launch_bounds__(BT) k_attn_prefill_short(const float *q, const
         for (int e = 0; e < 8; ++e) o0[e] = o1[e] = 0.f;
 #pragma unroll
         for (int i = 0; i < KI; ++i) {
+            if (wv * KW + (FEW ? 4 * i : 0) >= n) break;  // zero weights (and zero rows) from here on
             const int j = wv * KW + 4 * i + r;
             const float p0 = sc[0][j], p1 = sc[1][j];
             half8_t hv;
@@ -865,8 +871,8 @@ void prefill_layers(navi_talker &t, int T, hipStream_t s) {
         hipLaunchKernelGGL(k_qkv_finish, dim3(T, (t.NQ + 2 * t.NKV + BT / WAVE - 1) / (BT / WAVE)), dim3(BT), 0, s, t.part,
                            t.NQ, t.NKV, w.qn, w.kn, t.eps, t.invf, 0, t.q, t.kk[l], t.vv[l]);
         if (T <= SHORT_KEYS)
-            hipLaunchKernelGGL(k_attn_prefill_short, dim3(T, t.NKV), dim3(BT), 0, s, t.q, t.kk[l], t.vv[l], t.NQ, t.NKV,
-                               0, scale, t.att, t.la);
+            hipLaunchKernelGGL(T <= SHORT_KEYS / (BT / WAVE) ? k_attn_prefill_short<true> : k_attn_prefill_short<false>,
+                               dim3(T, t.NKV), dim3(BT), 0, s, t.q, t.kk[l], t.vv[l], t.NQ, t.NKV, 0, scale, t.att, t.la);
         else
             hipLaunchKernelGGL(k_attn_prefill, dim3(T, t.NKV), dim3(BT), att_lds, s, t.q, t.kk[l], t.vv[l], t.NQ,
                                t.NKV, 0, scale, t.att, t.la);
