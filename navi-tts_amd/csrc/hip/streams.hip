@@ -291,103 +291,136 @@ __global__ void __launch_bounds__(BT) k_st_attn_combine(const float *part, const
 
 // ---- code predictor: norms + RoPE + K/V store + attention, per (stream, kv head) -----------
 
-// Rows m * T + t (t < T) at cp positions p0 + t of stream m. The block sums the partials of its
-// group's columns (q heads 2g, 2g + 1, k and v of head g), normalises q and k per head, applies
-// RoPE, stores K/V in f16 into cpk/cpv [stream][layer][pos][kvd], then attends each row over
-// positions 0..p0 + t with the f16-rounded keys (the frame kernel's cp attention reads the same
-// f16 values from LDS).
-__global__ void __launch_bounds__(BT) k_st_cp_attn(const float *part, int S, int rows, int T, int p0, int nq, int nkv,
-                                                   const float *qn, const float *kn, float eps, const float *invf, int layer,
-                                                   int n_layer, uint16_t *cpk, uint16_t *cpv, float *att, int lda) {
-    __shared__ float vec[2][4][HD];          // [t][q0, q1, k, v]
-    __shared__ float kf[NCB][HD + 4], vf[NCB][HD];   // K rows padded: the 4-lane score reads of 16 keys spread over the banks
-    const int m = blockIdx.x, g = blockIdx.y;
+// Rows m * T + t (t < T <= 2) at cp positions p0 + t of stream m, per (stream, kv group g). Wave
+// w < 2 T takes row t = w / 2 and q head 2g + (w & 1) on its own, with no block barrier: it loads
+// its q row, the k and v rows of the launch's T rows and the cached keys and values of positions
+// 0..p0 - 1 straight into the layouts its loops use (every load in flight at once), normalises and
+// ropes q and the new keys per head, rounds the new keys and values to f16 (the head-2g wave of
+// row t stores row t's into cpk/cpv [stream][layer][pos][kvd]), moves them through its own LDS
+// slice into the score and value layouts, and attends row t over positions 0..p0 + t with the
+// f16-rounded keys (the frame kernel's cp attention reads the same f16 values). Scores: lanes
+// 4j..4j+3 take key j, lane 4j + s dims 32s..32s+31 in one FMA chain, summed by two DPP steps.
+// Value sum: lane l owns dims 2l, 2l+1 over all NCB rows (rows past the keys are zero with
+// weight 0), even and odd keys in two chains.
+__global__ void __launch_bounds__(BT) k_st_cp_attn(const float *part, int T, int p0, int nq, int nkv, const float *qn,
+                                                   const float *kn, float eps, const float *invf, int layer, int n_layer,
+                                                   uint16_t *cpk, uint16_t *cpv, float *att, int lda) {
+    __shared__ __align__(16) float lq[NW][HD], lk[NW][2][HD], lv[NW][2][HD];
+    const int m = blockIdx.x, g = blockIdx.y, w = threadIdx.x >> 6, l = threadIdx.x & 63;
+    if (w >= 2 * T) return;
+    const int t = w >> 1, hh = w & 1, n = p0 + t + 1, j = l >> 2, sq = l & 3;
     const int QD = nq * HD, KVD = nkv * HD, W = QD + 2 * KVD;
-    const size_t stride = static_cast<size_t>(rows) * W;
-    const int wv = threadIdx.x >> 6, l = threadIdx.x & 63;
-    // partial sums: (t, vector, dim) with 4 dims per thread
-    for (int i = threadIdx.x; i < T * 4 * (HD / 4); i += BT) {
-        const int t = i / (4 * (HD / 4)), r = i % (4 * (HD / 4)), vi = r / (HD / 4), d = (r % (HD / 4)) * 4;
-        const int col = vi < 2 ? (g * 2 + vi) * HD + d : vi == 2 ? QD + g * HD + d : QD + KVD + g * HD + d;
-        const f32x4_t v = sum_parts4(part, S, stride, static_cast<size_t>(m * T + t) * W + col);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) vec[t][vi][d + e] = v[e];
-    }
     const size_t base = (static_cast<size_t>(m) * n_layer + layer) * NCB * KVD + g * HD;
-    // earlier positions of this stream's cp cache (written by earlier launches); rows past this
-    // launch's last position zero (the value sum below reads all NCB rows with weight 0)
-    for (int i = threadIdx.x; i < NCB * HD; i += BT) {
-        const int j = i / HD, d = i % HD;
-        if (j < p0) {
-            kf[j][d] = h2f(gld(cpk + base + static_cast<size_t>(j) * KVD + d));
-            vf[j][d] = h2f(gld(cpv + base + static_cast<size_t>(j) * KVD + d));
-        } else if (j >= p0 + T) {
-            kf[j][d] = 0.f;
-            vf[j][d] = 0.f;
+    // every load first: q, the T new k / v rows (lane l: dims l, l + 64), the cached keys (lane
+    // 4j + s: 32 dims of key j) and values (lane l: dims 2l, 2l+1 of every row), weights, RoPE
+    const float *qr = part + static_cast<size_t>(m * T + t) * W + (g * 2 + hh) * HD;
+    const float qa = 0.f + gld(qr + l), qb = 0.f + gld(qr + l + HD / 2);
+    float ka[2] = {}, kb[2] = {}, va[2] = {}, vb[2] = {};
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+        if (u < T) {
+            const float *r = part + static_cast<size_t>(m * T + u) * W + QD + g * HD;
+            ka[u] = 0.f + gld(r + l);
+            kb[u] = 0.f + gld(r + l + HD / 2);
+            va[u] = 0.f + gld(r + KVD + l);
+            vb[u] = 0.f + gld(r + KVD + l + HD / 2);
         }
-    }
-    __syncthreads();
-    // head norms + RoPE: one wave per (t, vector) of q0, q1, k
-    for (int task = wv; task < T * 3; task += NW) {
-        const int t = task / 3, vi = task % 3;
-        float *hp = vec[t][vi];
-        const float *nw = vi < 2 ? qn : kn;
+    u32x4_t kc[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+        kc[c] = j < p0 ? *(const NAVI_GLOBAL u32x4_t *) (cpk + base + static_cast<size_t>(j) * KVD + 32 * sq + 8 * c)
+                       : u32x4_t{0u, 0u, 0u, 0u};
+    uint32_t vcw[NCB];
+#pragma unroll
+    for (int r = 0; r < NCB; ++r)
+        vcw[r] = r < p0 ? *(const NAVI_GLOBAL uint32_t *) (cpv + base + static_cast<size_t>(r) * KVD + 2 * l) : 0u;
+    const float qn0 = gld(qn + l), qn1 = gld(qn + l + HD / 2), kn0 = gld(kn + l), kn1 = gld(kn + l + HD / 2);
+    const float inv_f = gld(invf + l);
+    // q of row t, then the new keys and values of rows 0..T-1, into this wave's LDS slice
+    {
         float sn, cs;
-        sincosf(static_cast<float>(p0 + t) * gld(invf + l), &sn, &cs);
-        const float a0 = hp[l], a1 = hp[l + HD / 2];
-        const float scl = rsqrtf(wave_sum(fmaf(a0, a0, a1 * a1)) / static_cast<float>(HD) + eps);
-        const float x0 = a0 * scl * gld(nw + l), x1 = a1 * scl * gld(nw + l + HD / 2);
-        hp[l] = x0 * cs - x1 * sn;
-        hp[l + HD / 2] = x0 * sn + x1 * cs;
+        sincosf(static_cast<float>(p0 + t) * inv_f, &sn, &cs);
+        const float scl = rsqrtf(wave_sum(fmaf(qa, qa, qb * qb)) / static_cast<float>(HD) + eps);
+        const float x0 = qa * scl * qn0, x1 = qb * scl * qn1;
+        lq[w][l] = x0 * cs - x1 * sn;
+        lq[w][l + HD / 2] = x0 * sn + x1 * cs;
     }
-    __syncthreads();
-    // the new keys/values: f16 into the cache and (f16-rounded) into LDS
-    for (int i = threadIdx.x; i < T * HD; i += BT) {
-        const int t = i / HD, d = i % HD;
-        const uint16_t kh = f2h(vec[t][2][d]), vh = f2h(vec[t][3][d]);
-        gst(cpk + base + static_cast<size_t>(p0 + t) * KVD + d, kh);
-        gst(cpv + base + static_cast<size_t>(p0 + t) * KVD + d, vh);
-        kf[p0 + t][d] = h2f(kh);
-        vf[p0 + t][d] = h2f(vh);
-    }
-    __syncthreads();
-    // attention: one wave per (t, head). Scores: lanes 4j..4j+3 take key j, lane 4j + s dims
-    // 32s..32s+31 (one FMA chain), summed by two DPP steps. Value sum: lane l owns dims 2l, 2l+1
-    // over all NCB rows (rows past the key count are zero with weight 0), even and odd keys in
-    // two chains.
-    for (int task = wv; task < T * 2; task += NW) {
-        const int t = task / 2, hh = task % 2, n = p0 + t + 1;
-        const int j = l >> 2, sq = l & 3;
-        float acc = 0.f;
-        {
-            const f32x4_t *kr = reinterpret_cast<const f32x4_t *>(&kf[j][sq * 32]);
-            const f32x4_t *qr = reinterpret_cast<const f32x4_t *>(&vec[t][hh][sq * 32]);
 #pragma unroll
-            for (int c = 0; c < 8; ++c) {
-                const f32x4_t kk = kr[c], qq = qr[c];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) acc = fmaf(kk[e], qq[e], acc);
+    for (int u = 0; u < 2; ++u)
+        if (u < T) {
+            float sn, cs;
+            sincosf(static_cast<float>(p0 + u) * inv_f, &sn, &cs);
+            const float scl = rsqrtf(wave_sum(fmaf(ka[u], ka[u], kb[u] * kb[u])) / static_cast<float>(HD) + eps);
+            const float x0 = ka[u] * scl * kn0, x1 = kb[u] * scl * kn1;
+            const uint16_t k0 = f2h(x0 * cs - x1 * sn), k1 = f2h(x0 * sn + x1 * cs), v0 = f2h(va[u]), v1 = f2h(vb[u]);
+            if (hh == 0 && u == t) {
+                const size_t o = base + static_cast<size_t>(p0 + u) * KVD;
+                gst(cpk + o + l, k0);
+                gst(cpk + o + l + HD / 2, k1);
+                gst(cpv + o + l, v0);
+                gst(cpv + o + l + HD / 2, v1);
             }
+            lk[w][u][l] = h2f(k0);
+            lk[w][u][l + HD / 2] = h2f(k1);
+            lv[w][u][l] = h2f(v0);
+            lv[w][u][l + HD / 2] = h2f(v1);
         }
-        acc += dpp_mov<0xB1>(acc);       // quad_perm [1,0,3,2]
-        acc += dpp_mov<0x4E>(acc);       // quad_perm [2,3,0,1]: the 4 lanes of key j hold its dot
-        const float sl = j < n ? acc * ATT_SCALE : -INFINITY;
-        const float mx = wave_max(sl);
-        const float e = j < n ? expf(sl - mx) : 0.f;
-        const float inv = 1.f / wave_sum(sq == 0 ? e : 0.f);
-        float o0 = 0.f, o1 = 0.f, q0 = 0.f, q1 = 0.f;
+    // scores (this wave's LDS writes above are visible to its own later reads)
+    float acc = 0.f;
+    {
+        const f32x4_t *qv = reinterpret_cast<const f32x4_t *>(&lq[w][sq * 32]);
+        const int u = j - p0;
+        const f32x4_t *kn4 = reinterpret_cast<const f32x4_t *>(&lk[w][u >= 0 && u < T ? u : 0][sq * 32]);
 #pragma unroll
-        for (int r = 0; r < NCB; r += 2) {
-            const float pa = lane_value(e, 4 * r), pb = lane_value(e, 4 * r + 4);
-            o0 = fmaf(pa, vf[r][2 * l], o0);
-            o1 = fmaf(pa, vf[r][2 * l + 1], o1);
-            q0 = fmaf(pb, vf[r + 1][2 * l], q0);
-            q1 = fmaf(pb, vf[r + 1][2 * l + 1], q1);
+        for (int c = 0; c < 8; ++c) {
+            f32x4_t kk;
+            if (j < p0) {
+                const uint32_t wd0 = kc[c >> 1][2 * (c & 1)], wd1 = kc[c >> 1][2 * (c & 1) + 1];
+                kk = f32x4_t{h2f(static_cast<uint16_t>(wd0)), h2f(static_cast<uint16_t>(wd0 >> 16)),
+                             h2f(static_cast<uint16_t>(wd1)), h2f(static_cast<uint16_t>(wd1 >> 16))};
+            } else if (u < T) {
+                kk = kn4[c];
+            } else {
+                kk = f32x4_t{0.f, 0.f, 0.f, 0.f};
+            }
+            const f32x4_t qq = qv[c];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc = fmaf(kk[e], qq[e], acc);
         }
-        float *dst = att + static_cast<size_t>(m * T + t) * lda + (g * 2 + hh) * HD + 2 * l;
-        gst(dst, (o0 + q0) * inv);
-        gst(dst + 1, (o1 + q1) * inv);
     }
+    acc += dpp_mov<0xB1>(acc);       // quad_perm [1,0,3,2]
+    acc += dpp_mov<0x4E>(acc);       // quad_perm [2,3,0,1]: the 4 lanes of key j hold its dot
+    const float sl = j < n ? acc * ATT_SCALE : -INFINITY;
+    const float mx = wave_max(sl);
+    const float e = j < n ? expf(sl - mx) : 0.f;
+    const float inv = 1.f / wave_sum(sq == 0 ? e : 0.f);
+    float o0 = 0.f, o1 = 0.f, q0 = 0.f, q1 = 0.f;
+    auto vrow = [&](int r, float &a, float &b) {
+        if (r < p0) {
+            a = h2f(static_cast<uint16_t>(vcw[r]));
+            b = h2f(static_cast<uint16_t>(vcw[r] >> 16));
+        } else if (r - p0 < T) {
+            a = lv[w][r - p0][2 * l];
+            b = lv[w][r - p0][2 * l + 1];
+        } else {
+            a = 0.f;
+            b = 0.f;
+        }
+    };
+#pragma unroll
+    for (int r = 0; r < NCB; r += 2) {
+        const float pa = lane_value(e, 4 * r), pb = lane_value(e, 4 * r + 4);
+        float a0, a1, b0, b1;
+        vrow(r, a0, a1);
+        vrow(r + 1, b0, b1);
+        o0 = fmaf(pa, a0, o0);
+        o1 = fmaf(pa, a1, o1);
+        q0 = fmaf(pb, b0, q0);
+        q1 = fmaf(pb, b1, q1);
+    }
+    float *dst = att + static_cast<size_t>(m * T + t) * lda + (g * 2 + hh) * HD + 2 * l;
+    gst(dst, (o0 + q0) * inv);
+    gst(dst + 1, (o1 + q1) * inv);
 }
 
 // ---- sampling, one block per stream --------------------------------------------------------
@@ -659,7 +692,7 @@ navi_status run_group(navi_streams *h, StreamWork &g, int i0, int n, int zsplits
         const int T = pos == 1 ? 2 : 1, p0 = pos == 1 ? 0 : pos, rows = n * T;
         for (int l = 0; l < h->CL; ++l) {
             layer(*h, g, h->cl[l], ec, rows, [&]() {
-                hipLaunchKernelGGL(k_st_cp_attn, dim3(n, h->NKV), dim3(BT), 0, s, g.part, 1, rows, T, p0, h->NQ, h->NKV,
+                hipLaunchKernelGGL(k_st_cp_attn, dim3(n, h->NKV), dim3(2 * T * WAVE), 0, s, g.part, T, p0, h->NQ, h->NKV,
                                    h->cl[l].qn, h->cl[l].kn, ec, h->invf_c, l, h->CL, cpk, cpv, g.att, g.la);
             });
         }
