@@ -153,6 +153,18 @@ __global__ void __launch_bounds__(BT) k_window_attention(const float *qkv, int n
     // (one memory latency per batch instead of one per element).
     constexpr int Q = HALF / 4, MAXE = (128 + RT - 1) * Q, NIT = (MAXE + BT - 1) / BT, NB = NIT < 5 ? NIT : 5;
     const int ne = nk * Q;
+    // this thread's q element (at most one: RT * Q <= BT), loaded before the K/V staging so the two
+    // loads share one memory latency
+    static_assert(RT * Q <= BT, "one q element per thread");
+    const int eq = static_cast<int>(threadIdx.x), rq = eq / Q, iq = (eq - rq * Q) * 4;
+    const bool has_q = eq < (t1 - t0) * Q;
+    f32x4_t qa0{}, qa1{}, qf{};
+    if (has_q) {
+        const float *row = qkv + static_cast<size_t>(t0 + rq) * ld + h * HD;
+        qa0 = ld4(row + iq);
+        qa1 = ld4(row + iq + HALF);
+        qf = ld4(invf + iq);
+    }
     for (int b0 = 0; b0 < NIT && b0 * BT < ne; b0 += NB) {
         f32x4_t ka[NB], kb[NB], va[NB], vb[NB];
 #pragma unroll
@@ -206,16 +218,14 @@ __global__ void __launch_bounds__(BT) k_window_attention(const float *qkv, int n
             }
         }
     }
-    for (int e = threadIdx.x; e < (t1 - t0) * Q; e += BT) {
-        const int rr = e / Q, i = (e - rr * Q) * 4, p = pos0 + t0 + rr;
-        const float *row = qkv + static_cast<size_t>(t0 + rr) * ld + h * HD;
-        const f32x4_t a0 = ld4(row + i), a1 = ld4(row + i + HALF), f = ld4(invf + i);
+    if (has_q) {
+        const int p = pos0 + t0 + rq;
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
             float sn, cs;
-            sincosf(static_cast<float>(p) * f[c], &sn, &cs);
-            Qs[rr * HD + i + c] = a0[c] * cs - a1[c] * sn;
-            Qs[rr * HD + i + HALF + c] = a1[c] * cs + a0[c] * sn;
+            sincosf(static_cast<float>(p) * qf[c], &sn, &cs);
+            Qs[rq * HD + iq + c] = qa0[c] * cs - qa1[c] * sn;
+            Qs[rq * HD + iq + HALF + c] = qa1[c] * cs + qa0[c] * sn;
         }
     }
     __syncthreads();
