@@ -214,8 +214,8 @@ __global__ void __launch_bounds__(BT) k_swiglu(const float *part, int S, int M, 
 // RMSNorm of q and k, rotate-half RoPE at position pos0 + m, q kept f32, k and v rounded to f16
 // into the cache (k_qk_norm_rope, talker.hip:46-82). One wave per head slice (q heads, then k,
 // then v; block (m, b) takes slices 4b .. 4b + 3), lane l holding dims l and l + 64: no LDS and no
-// barrier, so the launch is one load latency deep. The values start from 0 + x as the split-K sum
-// of one partial did (a -0 stays +0 in the cache).
+// barrier, so the launch is one load latency deep. The values are 0 + x, as the split-K sum of
+// one partial was, so a -0 partial is stored as +0 exactly as before.
 __global__ void __launch_bounds__(BT) k_qkv_finish(const float *qkv, int nq, int nkv, const float *qn, const float *kn,
                                                    float eps, const float *invf, int pos0, float *q, uint16_t *kc,
                                                    uint16_t *vc) {
