@@ -313,8 +313,8 @@ __global__ void __launch_bounds__(BT) k_st_cp_attn(const float *part, int T, int
     const size_t base = (static_cast<size_t>(m) * n_layer + layer) * NCB * KVD + g * HD;
     // every load first: q, the T new k / v rows (lane l: dims l, l + 64), the cached keys (lane
     // 4j + s: 32 dims of key j) and values (lane l: dims 2l, 2l+1 of every row), weights, RoPE.
-    // The q|k|v values are 0 + x, the sum of one split-K partial as the projection's finish gave
-    // them (a -0 becomes +0), so the results match that path bit for bit.
+    // The q|k|v values are taken as 0 + x (a -0 becomes +0), the value a sum over one partial
+    // gives, so the stored keys and values keep the bits they had when the rows were summed here.
     const float *qr = part + static_cast<size_t>(m * T + t) * W + (g * 2 + hh) * HD;
     const float qa = 0.f + gld(qr + l), qb = 0.f + gld(qr + l + HD / 2);
     float ka[2] = {}, kb[2] = {}, va[2] = {}, vb[2] = {};
