@@ -91,10 +91,14 @@ def build_bench() -> list[Path]:
 
 
 def build_all() -> None:
+    """The product: the HIP library and the random-init tool (the microbenchmarks are built on
+    demand, `python -m navi_amd.build bench`)."""
     build_randinit()
     build_hip()
-    build_bench()
 
 
 if __name__ == "__main__":
-    build_all()
+    if sys.argv[1:] == ["bench"]:
+        build_bench()
+    else:
+        build_all()

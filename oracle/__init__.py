@@ -28,10 +28,14 @@ Pinning (tests/test_oracle_*.py, tests/test_blob.py):
   softmax; suppression / EOS gate / penalty special cases;
 * model: decoder layer vs transformers' Qwen3DecoderLayer (random weights, non-unit norms), with a
   planted-mistake control; prefill == sequential decode; RoPE and RMSNorm closed forms; the
-  assembly order; prompt layout vs the reference's fixtures (row counts, speaker row);
+  assembly order; prompt layout vs the reference's fixtures (row counts, speaker row); the text
+  projection (fc1 -> SiLU -> fc2) vs transformers' Qwen3OmniMoeTalkerResizeMLP, with
+  planted-mistake controls;
 * vocoder: SnakeBeta, the residual unit, ConvNeXt and the sliding-window transformer layer vs
   transformers' Qwen3-Omni code2wav modules; causal and transposed convs vs brute-force loops;
-  the RVQ front end vs an explicit sum; causality of the whole decoder;
+  the RVQ front end vs transformers' MimiSplitResidualVectorQuantizer.decode (one semantic
+  codebook + the summed acoustic ones, each set through its own 1x1 output projection), with
+  planted-mistake controls; causality of the whole decoder;
 * speaker: the log-mel vs the reference's own fixture (speaker_mels.npy, first 2 s of
   voice_1.wav); the "same" reflect conv vs torch.nn.Conv1d(padding_mode="reflect");
   weighted statistics vs numpy.average; the whole network on a time-constant mel vs its closed

@@ -11,6 +11,7 @@ Test infrastructure (see oracle/__init__.py). Restates, in PyTorch f32 on the CP
 * `Oracle.talker_step` - frame.hip:537-550 (talker phases of k_frame);
 * `Oracle.code_predictor` - frame.hip:554-575 (16 positions, lm_head[pos-1], cp KV per frame);
 * `Oracle.assemble_step` - frame.hip:503-513 (f32 adds in the kernel's order);
+* `text_projection`   - talker.hip:333-335 (fc1 -> SiLU -> fc2, both with bias);
 * `Oracle.build_prompt` - talker.hip:283-352 (10-row prefill layout, trailing rows, tts_pad);
 * `Oracle.prefill`    - talker.hip:354-399;
 * `Oracle.frame`      - one frame: run_first / run of frame.hip:787-810 with Impl::launch's seeds (653-659).
@@ -103,6 +104,18 @@ def load_layers(blob: NaviBlob, prefix: str, n: int) -> list[LayerW]:
 
 def linear(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
     return torch.nn.functional.linear(x, w)
+
+
+def silu(a: torch.Tensor) -> torch.Tensor:
+    return a / (1.0 + torch.exp(-a))
+
+
+def text_projection(rows: torch.Tensor, w1: torch.Tensor, b1: torch.Tensor, w2: torch.Tensor,
+                    b2: torch.Tensor) -> torch.Tensor:
+    """talker.hip:333-335: fc2(SiLU(fc1(rows) + b1)) + b2 (the gemm's EPI_SILU epilogue on fc1,
+    kernels.h:262-350); f32 products, bias and activation in f64, rounded to f32 per stage."""
+    a = silu(linear(rows, w1).double() + b1.double()).float()
+    return (linear(a, w2).double() + b2.double()).float()
 
 
 def decoder_layer(P: Xf, w: LayerW, x: torch.Tensor, kc: torch.Tensor, vc: torch.Tensor, pos0: int,
@@ -270,11 +283,9 @@ class Oracle:
         table = b.array("talker.model.text_embedding.weight")
         rows = torch.from_numpy(table[np.asarray(tids)].astype(F32))
         t = lambda name: torch.from_numpy(b.f32(name))
-        a = (linear(rows, t("talker.text_projection.linear_fc1.weight")).double()
-             + t("talker.text_projection.linear_fc1.bias").double())
-        a = (a / (1.0 + torch.exp(-a))).float()
-        proj = (linear(a, t("talker.text_projection.linear_fc2.weight")).double()
-                + t("talker.text_projection.linear_fc2.bias").double()).float().numpy()
+        tp = "talker.text_projection."
+        proj = text_projection(rows, t(tp + "linear_fc1.weight"), t(tp + "linear_fc1.bias"),
+                               t(tp + "linear_fc2.weight"), t(tp + "linear_fc2.bias")).numpy()
         if language in ("", "auto"):
             cids = [kv["talker.codec_nothink_id"], kv["talker.codec_think_bos_id"], kv["talker.codec_think_eos_id"]]
         else:

@@ -45,14 +45,21 @@ def _row_err(dev, ora):
     return float(np.abs(dev[fin] - ora[fin]).max())
 
 
+# A flip (device code != oracle code) is admitted only where the oracle's own scores put the device's
+# code within NEAR_TIE of their maximum. The bound is fixed, independent of the measured row error:
+# 2e-3 is 1.5x the largest logit error measured on any greedy row (1.27e-3, configs[0] at 24 frames),
+# so a device that reorders two scores further apart than any error it has shown fails. Each test
+# also caps the number of flips it admits (summarize_decisions' max_flips).
+NEAR_TIE = 2e-3
+
+
 def check_greedy_frame(i, codes, dbg, record, dev_logits, dev_cp_logits):
     """The greedy gate for the 16 decisions of frame i (teacher-forced oracle, so one flip does not
     end the comparison). For each position p:
     * the device's code is the argmax of the device's OWN scores (its logits taps, modified by the
       oracle's sampler rules for cb0): given identical logits, the decision is bit-exact;
-    * it equals the oracle's code, unless the oracle's own scores put the device's code within
-      2 x err_p of their maximum, where err_p = max |device - oracle| over that very row: only then
-      can that row's measured logit error reorder the two (a per-decision bound, not a fixed one).
+    * it equals the oracle's code, unless the oracle's own scores put the device's code within the
+      fixed NEAR_TIE of their maximum.
     Every decision goes into `record` (dicts: frame, pos, dev, ora, gap, err, margin)."""
     dev_scores = [dbg["modify"](dev_logits)] + [np.asarray(x, np.float64) for x in dev_cp_logits]
     ora_scores = [np.asarray(dbg["cb0_scores"], np.float64)] + [np.asarray(x, np.float64) for x in dbg["cp_logits"]]
@@ -67,12 +74,13 @@ def check_greedy_frame(i, codes, dbg, record, dev_logits, dev_cp_logits):
         assert dc == own, f"frame {i} position {p}: device code {dc} is not the argmax {own} of its own scores"
         if dc != oc:
             log(f"  frame {i} position {p}: device {dc} oracle {oc}, oracle gap {gap:.2e}, row error {err:.2e}")
-            assert gap <= 2.0 * err, (f"frame {i} position {p}: device {dc} vs oracle {oc}: gap {gap:.3e} exceeds "
-                                      f"2 x the row's logit error {err:.3e}")
+            assert gap <= NEAR_TIE, (f"frame {i} position {p}: device {dc} vs oracle {oc}: the oracle's gap {gap:.3e} "
+                                     f"exceeds the near-tie bound {NEAR_TIE:.0e}")
 
 
-def summarize_decisions(name, record):
-    """Logs the decision count and writes the record to $NAVI_DECISION_LOG/<name>.json when set."""
+def summarize_decisions(name, record, max_flips=0):
+    """Logs the decision count, writes the record to $NAVI_DECISION_LOG/<name>.json when set, and
+    fails when more than `max_flips` decisions differ from the oracle's."""
     flips = [r for r in record if r["dev"] != r["ora"]]
     n = len(record)
     closest = min(record, key=lambda r: r["margin"]) if record else None
@@ -88,4 +96,5 @@ def summarize_decisions(name, record):
                        "max_row_err": max((r["err"] for r in record), default=0.0),
                        "min_margin": closest["margin"] if closest else None,
                        "margins_below_1e-3": sum(1 for r in record if r["margin"] < 1e-3)}, f, indent=1)
+    assert len(flips) <= max_flips, f"{name}: {len(flips)} greedy decisions differ from the oracle (cap {max_flips})"
     return flips

@@ -8,8 +8,9 @@ and is compared with the oracle doing the same on the CPU: the prefill's hidden 
 within 2e-2 max abs and cosine > 0.9995; every frame's logits within 2e-2; every one of the
 24 x 16 greedy decisions gated by gpu_util.check_greedy_frame: the device's code is the argmax of
 its own logits (bit-exact given identical logits) and the oracle's code, unless the oracle's scores
-put the device's code within 2 x that row's measured logit error of their maximum. The oracle is
-teacher-forced with the device's codes, so such a flip does not end the comparison. The decision
+put the device's code within the fixed near-tie bound 2e-3 of their maximum, at most 2 such flips
+in the 384 decisions. The oracle is teacher-forced with the device's codes, so such a flip does
+not end the comparison. The decision
 record (count, flips, row errors, margins) is written when NAVI_DECISION_LOG names a directory.
 """
 import numpy as np
@@ -84,5 +85,5 @@ def test_config0_greedy_end_to_end(full_blob):
             f"{r.us:.0f} us")
         assert lg_err < 2e-2
         check_greedy_frame(i, codes, dbg, record, tlg, tcp)
-    summarize_decisions("config0_greedy_24_frames", record)
+    summarize_decisions("config0_greedy_24_frames", record, max_flips=2)
     log(f"config0: mean device {np.mean(us[1:]):.0f} us/frame (talker frames)")

@@ -70,7 +70,7 @@ def test_greedy_32_streams_at_context_1024(batch32):
             n_past[i] += 1
         log(f"  worst over streams: hidden {worst[0]:.2e}/{worst[1]:.7f} logits {worst[2]:.2e}/{worst[3]:.7f} "
             f"cp {worst[4]:.2e}/{worst[5]:.7f}")
-    summarize_decisions("streams_32_ctx1024_greedy", record)
+    summarize_decisions("streams_32_ctx1024_greedy", record, max_flips=2)
 
 
 def test_sampled_32_streams_match_oracle_on_device_logits(batch32):

@@ -102,7 +102,7 @@ def greedy_steps(b, steps, name):
             np.testing.assert_array_equal(dev_step[i], so)
             step_o[i] = so
             n_past[i] += 1
-    summarize_decisions(name, record)
+    summarize_decisions(name, record, max_flips=1)
 
 
 def test_greedy_streams_match_oracle(batch):
