@@ -163,3 +163,34 @@ def test_graph_replays_match_eager(codec):
         v.set_graphs(True)
     v.set_graphs(False)
     log(f"vocoder graph replays == eager over 45 frames (4 + 16 + 16 + 9), 3 rounds")
+
+
+def test_config3_240_frames_block_and_stream(codec):
+    """BASELINE configs[3] at its own size: 240 frames of uniform codes decoded as one 240-frame
+    block and as a stream of 4 then 16-frame chunks, both against the oracle's one-shot decode
+    (SNR >= 40 dB), and block == stream within 1e-5. Past frame 72 the pre-transformer's attention
+    drops keys older than its 72-position window (reference k_attention, vocoder.hip:86-117), and
+    with 16-frame chunks its K/V ring of next_pow2(72 + 16) = 128 slots (vocoder.hip:473-474)
+    wraps from frame 128 on, so both paths run here under the oracle's windowed mask."""
+    abi, W, ora = codec
+    codes = np.random.default_rng(7).integers(0, 2048, (240, 16))
+    want = ora.decode(codes)
+    block = abi.Vocoder(W, max_chunk_frames=240)
+    log("vocoder configs[3]: 240-frame block")
+    got_block = block.decode(codes)
+    stream = abi.Vocoder(W, max_chunk_frames=16)
+    log("vocoder configs[3]: 240 frames as 4 + 16 x 14 + 12")
+    parts = [stream.decode(codes[:4])]
+    for f in range(4, 240, 16):
+        parts.append(stream.decode(codes[f:f + 16]))
+    got_stream = np.concatenate(parts)
+    assert got_block.shape == got_stream.shape == want.shape == (240 * 1920,)
+    s_block, s_stream = snr_db(got_block, want), snr_db(got_stream, want)
+    # the windowed and wrapped region on its own: frames 128..239 (ring wrapped, keys truncated)
+    tail = slice(128 * 1920, 240 * 1920)
+    s_tail = snr_db(got_stream[tail], want[tail])
+    d = float(np.abs(got_block - got_stream).max())
+    log(f"  SNR block {s_block:.1f} dB, stream {s_stream:.1f} dB, stream frames 128-239 {s_tail:.1f} dB; "
+        f"block vs stream max diff {d:.2e}")
+    assert s_block >= 40.0 and s_stream >= 40.0 and s_tail >= 40.0
+    assert d <= 1e-5
