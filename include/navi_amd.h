@@ -245,8 +245,9 @@ navi_status navi_linear(const float *d_x, int32_t ldx, int32_t M, const uint16_t
                         const float *bias, const float *residual, int32_t act, float *d_y, int32_t ldy,
                         char *err, size_t errlen);
 /* navi_linear without any allocation. No counterpart in the reference: it is for callers that
- * cannot allocate device memory (code under HIP graph capture, serving loops or harnesses that
- * forbid hipMalloc). Same arguments, kernels and results (bit-identical) as navi_linear, but the
+ * cannot allocate device memory (serving loops or harnesses that forbid hipMalloc). It runs on
+ * the library stream and synchronizes it, so it does not belong in a graph the caller captures.
+ * Same arguments, kernels and results (bit-identical) as navi_linear, but the
  * split-K partials live in a fixed 8 MiB array of the library on each GPU (held until the process
  * ends) instead of a workspace the library allocates: S x M x N floats must fit in its
  * 2,097,088 floats (S, navi_linear's K-split count, is at most K / 256 and falls as the output

@@ -245,4 +245,60 @@ int navi_test_server_stream(navi_talker *t, navi_frame *f, navi_vocoder *v, navi
     return rep.put(out, out_len);
 }
 
+// Scenario "one request as the server streams it": the worker runs synth with the given sampling
+// into the bounded queue, the consumer drains it; the s16 samples it received (in order) and the
+// batch sizes go back to the caller for a comparison with the oracle's request. Returns 0, or 1
+// with the error text in err.
+int navi_test_server_stream_request(navi_talker *t, navi_frame *f, navi_vocoder *v, int32_t english_id,
+                                    const int32_t *ids, int32_t n_ids, const float *speaker, uint64_t seed,
+                                    int32_t max_frames, float temperature, float cp_temperature, int16_t *pcm_out,
+                                    int64_t pcm_cap, int64_t *n_pcm, int32_t *sizes_out, int32_t max_sizes,
+                                    int32_t *n_sizes, char *err, size_t errlen) {
+    try {
+        Graph g(t, f, v, nullptr, {{"english", english_id}});
+        SynthRequest sr;
+        sr.ids.assign(ids, ids + n_ids);
+        sr.speaker = std::span<const float>(speaker, 1024);
+        sr.seed = seed;
+        sr.max_frames = max_frames;
+        sr.sampling.temperature = temperature;
+        sr.sampling.cp_temperature = cp_temperature;
+        sr.sampling.min_frames = max_frames;
+        sr.first_batch = navi::qwen3tts::STREAM_FIRST_BATCH;
+        sr.vocoder_batch = navi::qwen3tts::STREAM_BATCH;
+        ChunkQueue q;
+        SynthStats st;
+        std::string error;
+        std::thread worker([&] { stream_worker(g, sr, q, st, error); });
+        bool done_at_first = true;
+        const bool audio = q.wait_first(done_at_first);
+        std::vector<int16_t> c;
+        int64_t n = 0;
+        int32_t k = 0;
+        bool overflow = false;
+        while (audio && q.pop(c)) {
+            if (n + static_cast<int64_t>(c.size()) > pcm_cap || k >= max_sizes) {
+                q.abort();
+                overflow = true;
+                break;
+            }
+            std::copy(c.begin(), c.end(), pcm_out + n);
+            n += static_cast<int64_t>(c.size());
+            sizes_out[k++] = static_cast<int32_t>(c.size());
+        }
+        worker.join();
+        *n_pcm = n;
+        *n_sizes = k;
+        if (overflow) error = "output buffer too small";
+        if (!error.empty()) {
+            std::snprintf(err, errlen, "%s", error.c_str());
+            return 1;
+        }
+        return 0;
+    } catch (const std::exception &e) {
+        std::snprintf(err, errlen, "%s", e.what());
+        return 1;
+    }
+}
+
 } // extern "C"

@@ -100,3 +100,70 @@ def test_python_on_pcm_exception_stops_the_request(graph):
                              vocoder_batch=8, first_batch=8)
     assert st.n_frames == 8 and sizes == [4 * 1920, 4 * 1920]
     assert np.array_equal(pcm, pcm2)
+
+
+def _to_s16(pcm):
+    """runtime/audio/wav.cpp:13-22: clamp to [-1, 1], scale by 32767, round to nearest (even)."""
+    return np.rint(np.clip(np.asarray(pcm, np.float32), -1.0, 1.0) * np.float32(32767.0)).astype(np.int16)
+
+
+def test_server_stream_matches_oracle_greedy(graph, scratch_dir):
+    """The server's streaming path (server.cpp:398-495: the worker's synth into the bounded s16
+    queue, drained by the consumer) against the oracle's request: greedy prompt -> prefill -> 40
+    frames -> the codec decoder in one shot, then the server's s16 conversion. The streamed s16
+    must reach SNR >= 40 dB against the oracle's s16, and the device vocoder fed the ORACLE's codes
+    in the server's batches (4, then 16) must give the streamed s16 sample for sample: the stream
+    carries exactly the oracle's codes."""
+    import torch
+    from oracle import sampler as osamp
+    from oracle.model import Oracle
+    from oracle.vocoder import Vocoder as OVoc
+    abi, W, talker, frame, voc, _ = graph
+    if not HARNESS.exists():
+        pytest.fail(f"{HARNESS} is not built (run __graft_entry__.build())")
+    lib = C.CDLL(str(HARNESS))
+    fn = lib.navi_test_server_stream_request
+    fn.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int32, C.c_void_p, C.c_int32, C.c_void_p, C.c_uint64,
+                   C.c_int32, C.c_float, C.c_float, C.c_void_p, C.c_int64, C.POINTER(C.c_int64), C.c_void_p,
+                   C.c_int32, C.POINTER(C.c_int32), C.c_char_p, C.c_size_t]
+    n = 40
+    ids = np.asarray(_ids(W.kv, 16, 31), np.int32)
+    spk = np.random.default_rng(32).standard_normal(1024).astype(np.float32)
+    pcm = np.zeros(n * 1920, np.int16)
+    sizes = np.zeros(16, np.int32)
+    n_pcm, n_sizes = C.c_int64(0), C.c_int32(0)
+    err = C.create_string_buffer(512)
+    log("server streaming path, greedy 40 frames, against the oracle's request")
+    rc = fn(talker.h, frame.h, voc.h, int(W.kv["talker.language.english"]), ids.ctypes.data, ids.size,
+            spk.ctypes.data, 6, n, 0.0, 0.0, pcm.ctypes.data, pcm.size, C.byref(n_pcm), sizes.ctypes.data,
+            sizes.size, C.byref(n_sizes), err, 512)
+    assert rc == 0, err.value.decode()
+    sizes = sizes[:n_sizes.value].tolist()
+    assert n_pcm.value == n * 1920 and sizes == [4 * 1920, 16 * 1920, 16 * 1920, 4 * 1920]
+
+    path = scratch_dir / "small_all_spk.navi"
+    ora = Oracle(path)
+    pre, trail, pad = ora.build_prompt(ids.tolist(), "english", spk)
+    kvo = ora.new_kv(128)
+    hid, lg = ora.prefill(pre, kvo)
+    so = osamp.Sampling(temperature=0.0, cp_temperature=0.0, repetition_penalty=1.05, min_frames=n)
+    ora.reset()
+    codes, step = [], None
+    with torch.no_grad():
+        for i in range(n):
+            th = trail[i] if i < trail.shape[0] else pad
+            if i == 0:
+                c, step = ora.frame(so, 6, 0, th, hidden=hid, logits=lg)
+            else:
+                c, step = ora.frame(so, 6, i, th, kv=kvo, n_past=pre.shape[0] + i - 1, step_in=step)
+            codes.append(c)
+    want = _to_s16(OVoc(path).decode(np.array(codes))).astype(np.float64)
+    got = pcm.astype(np.float64)
+    snr = 10 * np.log10(np.sum(want ** 2) / max(np.sum((got - want) ** 2), 1e-300))
+    voc.reset()
+    b = np.asarray(codes)
+    dev = np.concatenate([voc.decode(b[:4]), voc.decode(b[4:20]), voc.decode(b[20:36]), voc.decode(b[36:])])
+    same = np.array_equal(_to_s16(dev), pcm)
+    log(f"  server stream vs oracle: SNR {snr:.1f} dB (s16); device vocoder on the oracle's codes == stream: {same}")
+    assert snr >= 40.0
+    assert same
