@@ -375,6 +375,90 @@ def cpu_baseline(path: Path, frames: int) -> dict:
                       "a 10-row prefill and an 8-frame codec decode, each once after a warm-up call"}
 
 
+def frame_phase_table(P: np.ndarray, n_tl: int, n_cl: int, n_cb: int = 16) -> dict:
+    """Reduces one profiled frame's stamps (navi_frame_set_profile: per block, the 100 MHz real-time
+    counter at the start and end of every wait, in the kernel's phase order) to a phase table in
+    microseconds: medians over the blocks of when each phase ended, relative to the moment the
+    layer's input vector arrived, averaged over the talker layers 1.. and over the code predictor's
+    one-row layers that are not the first of their pass; then the time per code-predictor pass with
+    its logits hop and sampling. Blocks 0..15 run the attention combines (talker) and the cp
+    attention, so their stamp sequences carry those marks too."""
+    NB = P.shape[0]
+    t0 = P[:, 0][P[:, 0] > 0].min()
+    per_block = []
+    for b in range(NB):
+        row = P[b]
+        n = int((row > 0).sum())
+        t = (row[:n].astype(np.int64) - int(t0)) / 100.0
+        i, L, C = 0, [], []
+        att = b < 16
+        for _ in range(n_tl):
+            d = dict(zip(("att_start", "qkv_arrived", "kv_staged", "values", "partial_put"), t[i:i + 5])); i += 5
+            if att:
+                d.update(zip(("partials_wait", "partials_got", "head_put"), t[i:i + 3])); i += 3
+            d.update(zip(("att_gs", "att_ge", "x2_gs", "x2_ge", "h_gs", "h_ge", "x_gs", "x_ge"), t[i:i + 8])); i += 8
+            L.append(d)
+        head = dict(zip(("lg_gs", "lg_ge", "s0", "s1"), t[i:i + 4])); i += 4
+        for p in range(n_cb - 1):
+            rows = 2 if p == 0 else 1
+            for _ in range(n_cl):
+                d = {}
+                if att:
+                    d.update(zip(("cpa_start", "cpa_qkv", "cpa_put"), t[i:i + 3])); i += 3
+                v = t[i:i + 8 * rows]; i += 8 * rows
+                d.update({"att_gs": v[0], "att_ge": v[2 * rows - 1], "x2_gs": v[2 * rows], "x2_ge": v[4 * rows - 1],
+                          "h_gs": v[4 * rows], "h_ge": v[6 * rows - 1], "x_gs": v[6 * rows], "x_ge": v[8 * rows - 1]})
+                C.append(d)
+            C[-1].update(zip(("lg_gs", "lg_ge", "s0", "s1"), t[i:i + 4])); i += 4
+        per_block.append((L, head, C, t[i] if i < n else np.nan))
+
+    def med(kind, idx, key, blocks):
+        return float(np.median([per_block[b][kind][idx][key] for b in blocks]))
+
+    def layer_table(kind, idxs, steps):
+        out = {}
+        for name, key, blocks in steps:
+            out[name] = round(float(np.mean([med(kind, li, key, blocks) - med(kind, li - 1, "x_ge", range(NB))
+                                              for li in idxs])), 2)
+        return out
+    allb, att = range(NB), range(16)
+    talker = layer_table(0, range(1, n_tl), [
+        ("qkv published, K/V staging issued", "att_start", allb), ("q/k/v arrived", "qkv_arrived", allb),
+        ("range partial published", "partial_put", allb), ("partials combined, head published", "head_put", att),
+        ("attention output gathered", "att_ge", allb), ("o published", "x2_gs", allb), ("x2 gathered", "x2_ge", allb),
+        ("gate/up published", "h_gs", allb), ("h gathered", "h_ge", allb), ("down published", "x_gs", allb),
+        ("x gathered (layer end)", "x_ge", allb)])
+    cp_idx = [i for i in range(1, (n_cb - 1) * n_cl) if i % n_cl != 0 and i >= n_cl]
+    cp = layer_table(2, cp_idx, [
+        ("qkv published", "att_gs", range(16, NB)), ("q/k/v arrived at the attention blocks", "cpa_qkv", att),
+        ("attention output published", "cpa_put", att), ("attention output gathered", "att_ge", allb),
+        ("o published", "x2_gs", allb), ("x2 gathered", "x2_ge", allb), ("gate/up published", "h_gs", allb),
+        ("h gathered", "h_ge", allb), ("down published", "x_gs", allb), ("x gathered (layer end)", "x_ge", allb)])
+    prev = float(np.median([per_block[b][1]["s1"] for b in allb]))
+    talker_end = prev
+    passes = []
+    for p in range(n_cb - 1):
+        last = p * n_cl + n_cl - 1
+        s1, lg, xe = (med(2, last, k, allb) for k in ("s1", "lg_ge", "x_ge"))
+        passes.append({"pass": p, "us": round(s1 - prev, 1), "logits_hop_us": round(lg - xe, 2),
+                       "sampling_us": round(s1 - lg, 2)})
+        prev = s1
+    end = float(np.nanmedian([pb[3] for pb in per_block]))
+    return {"unit": "us", "talker_layer_cumulative": talker, "cp_layer_cumulative": cp,
+            "talker_and_cb0_us": round(talker_end, 1), "cp_passes": passes, "frame_us": round(end, 1)}
+
+
+def frame_profile(frame, kv, trail, s, warmup: int) -> dict:
+    """One frame at n_past 256 with the kernel's own phase stamps on (no profiler attached)."""
+    frame.set_profile(True)
+    r = frame.run(kv, N_PAST, trail.ptr, s, 2, warmup + 1000)
+    if not r.ok:
+        raise SystemExit(f"profiled frame failed: {r.error.decode()}")
+    P = frame.profile(frame.grid_blocks(), 4096)
+    frame.set_profile(False)
+    return {"frame_phases": {"profiled_frame_device_us": round(r.us, 1), **frame_phase_table(P, 28, 5)}}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
@@ -387,6 +471,9 @@ def main():
     ap.add_argument("--no-streaming", action="store_true", help="skip the prefill / streaming / vocoder extras")
     ap.add_argument("--only", choices=("prefill", "streaming", "vocoder", "multistream", "speaker"), default="",
                     help="run only this part (for a profiler run) and print its JSON instead of the bench line")
+    ap.add_argument("--frame-profile", action="store_true",
+                    help="after the warm-up, run one frame with the kernel's phase stamps on, print the phase table "
+                         "(JSON) and exit")
     ap.add_argument("--copy-calibration", type=float, default=0.0, metavar="GIB",
                     help="only run the counter-calibration copy kernel over GIB GiB and exit")
     args = ap.parse_args()
@@ -436,6 +523,9 @@ def main():
             if not r.ok:
                 raise SystemExit(f"warm-up frame {i} failed: {r.error.decode()}")
         abi.lib().navi_device_synchronize()
+        if args.frame_profile:
+            print(json.dumps(frame_profile(frame, kv, trail, s, args.warmup)), flush=True)
+            return
         dev_us = []
         t0 = time.perf_counter()
         for i in range(args.steps):
