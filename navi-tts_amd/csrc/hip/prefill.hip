@@ -348,27 +348,90 @@ __global__ void __launch_bounds__(BT) k_attn_prefill(const float *q, const uint1
 // every key of the launch falls in wave 0's range (FEW: prompts of up to 64 rows), per wave
 // otherwise (a per-group exit in the unrolled loops of the longer rows measured slower).
 constexpr int SHORT_KEYS = 256;
-template <bool FEW>
-__global__ void __launch_bounds__(BT) k_attn_prefill_short(const float *q, const uint16_t *kc, const uint16_t *vc, int nq,
-                                                           int nkv, int pos0, float scale, float *out, int ldo) {
+// FUSED (prompts of up to FUSED_ROWS rows from position 0; FEW): the q/k head norms, RoPE and the
+// f16 K/V store of k_qkv_finish are folded in, one launch fewer per layer. The block of row m
+// forms, from the raw q|k|v rows of the projection (`raw`, [rows][nq + 2 nkv heads] f32), its two
+// q heads and the normed, rotated f16 keys and the f16 values 0..m of kv group g in LDS, one wave
+// per head row with k_qkv_finish's arithmetic (lane l holding dims l and l + 64, the values
+// 0 + x), so q, K and V carry that pass's bits, and it stores K/V row m into the cache; the
+// attention then reads its keys and values from LDS instead of the cache. Same outputs, bit for bit.
+constexpr int FUSED_ROWS = 64;
+struct HeadNorm {
+    const float *raw, *qn, *kn, *invf;
+    float eps;
+};
+template <bool FEW, bool FUSED = false>
+__global__ void __launch_bounds__(BT) k_attn_prefill_short(const float *q, uint16_t *kc, uint16_t *vc, int nq,
+                                                           int nkv, int pos0, float scale, float *out, int ldo,
+                                                           HeadNorm hn = {}) {
     constexpr int NWV = BT / WAVE, KW = SHORT_KEYS / NWV, KI = KW / 4;
     static_assert(SHORT_KEYS == BT, "one key per thread in the softmax");
+    static_assert(!FUSED || (FEW && FUSED_ROWS <= KW), "fused: every key in wave 0's range");
     __shared__ float qs[2][HD], sc[2][SHORT_KEYS], red[2][NWV], opart[NWV][4][2][HD];
+    __shared__ uint16_t ks[FUSED ? FUSED_ROWS : 1][HD], vs[FUSED ? FUSED_ROWS : 1][HD];
     const int m = blockIdx.x, g = blockIdx.y, n = pos0 + m + 1;
     const int QD = nq * HD, KVD = nkv * HD;
     const int wv = threadIdx.x >> 6, l = threadIdx.x & 63, c = l & 15, r = l >> 4;
-    qs[threadIdx.x >> 7][threadIdx.x & (HD - 1)] = gld(q + static_cast<size_t>(m) * QD + g * 2 * HD + threadIdx.x);
-    const uint16_t *kb = kc + g * HD + c * 8, *vb = vc + g * HD + c * 8;
     u32x4_t kr[KI], vr[KI];
+    if constexpr (FUSED) {
+        // task t: q head 2g + t of row m (t < 2), else key / value row j = t - 2 of kv group g
+        const int W = QD + 2 * KVD;
+        for (int t = wv; t < 2 + n; t += NWV) {
+            const bool isq = t < 2;
+            const int row = isq ? m : t - 2;
+            const float *hp = hn.raw + static_cast<size_t>(row) * W + (isq ? (2 * g + t) * HD : QD + g * HD);
+            const float *vp = hn.raw + static_cast<size_t>(row) * W + QD + KVD + g * HD;
+            const float a0 = 0.f + gld(hp + l), a1 = 0.f + gld(hp + l + HD / 2);
+            float b0 = 0.f, b1 = 0.f;
+            if (!isq) {
+                b0 = 0.f + gld(vp + l);
+                b1 = 0.f + gld(vp + l + HD / 2);
+            }
+            float sn, cs;
+            sincosf(static_cast<float>(row) * gld(hn.invf + l), &sn, &cs);
+            const float *nw = isq ? hn.qn : hn.kn;
+            const float scl = rsqrtf(wave_sum(fmaf(a0, a0, a1 * a1)) / static_cast<float>(HD) + hn.eps);
+            const float x0 = a0 * scl * gld(nw + l), x1 = a1 * scl * gld(nw + l + HD / 2);
+            const float y0 = x0 * cs - x1 * sn;
+            const float y1 = x1 * cs + x0 * sn;
+            if (isq) {
+                qs[t][l] = y0;
+                qs[t][l + HD / 2] = y1;
+            } else {
+                const uint16_t k0 = f2h(y0), k1 = f2h(y1), v0 = f2h(b0), v1 = f2h(b1);
+                ks[row][l] = k0;
+                ks[row][l + HD / 2] = k1;
+                vs[row][l] = v0;
+                vs[row][l + HD / 2] = v1;
+                if (row == m) {
+                    uint16_t *kd = kc + static_cast<size_t>(m) * KVD + g * HD, *vd = vc + static_cast<size_t>(m) * KVD + g * HD;
+                    gst(kd + l, k0);
+                    gst(kd + l + HD / 2, k1);
+                    gst(vd + l, v0);
+                    gst(vd + l + HD / 2, v1);
+                }
+            }
+        }
+        __syncthreads();                                  // qs, ks, vs
 #pragma unroll
-    for (int i = 0; i < KI; ++i) {
-        const int j = wv * KW + 4 * i + r;
-        kr[i] = j < n ? *(const NAVI_GLOBAL u32x4_t *) (kb + static_cast<size_t>(j) * KVD) : u32x4_t{0u, 0u, 0u, 0u};
-    }
+        for (int i = 0; i < KI; ++i) {
+            const int j = wv * KW + 4 * i + r;
+            kr[i] = j < n ? *reinterpret_cast<const u32x4_t *>(&ks[j][c * 8]) : u32x4_t{0u, 0u, 0u, 0u};
+            vr[i] = j < n ? *reinterpret_cast<const u32x4_t *>(&vs[j][c * 8]) : u32x4_t{0u, 0u, 0u, 0u};
+        }
+    } else {
+        qs[threadIdx.x >> 7][threadIdx.x & (HD - 1)] = gld(q + static_cast<size_t>(m) * QD + g * 2 * HD + threadIdx.x);
+        const uint16_t *kb = kc + g * HD + c * 8, *vb = vc + g * HD + c * 8;
 #pragma unroll
-    for (int i = 0; i < KI; ++i) {
-        const int j = wv * KW + 4 * i + r;
-        vr[i] = j < n ? *(const NAVI_GLOBAL u32x4_t *) (vb + static_cast<size_t>(j) * KVD) : u32x4_t{0u, 0u, 0u, 0u};
+        for (int i = 0; i < KI; ++i) {
+            const int j = wv * KW + 4 * i + r;
+            kr[i] = j < n ? *(const NAVI_GLOBAL u32x4_t *) (kb + static_cast<size_t>(j) * KVD) : u32x4_t{0u, 0u, 0u, 0u};
+        }
+#pragma unroll
+        for (int i = 0; i < KI; ++i) {
+            const int j = wv * KW + 4 * i + r;
+            vr[i] = j < n ? *(const NAVI_GLOBAL u32x4_t *) (vb + static_cast<size_t>(j) * KVD) : u32x4_t{0u, 0u, 0u, 0u};
+        }
     }
     __syncthreads();                                      // qs
     {
@@ -868,14 +931,20 @@ void prefill_layers(navi_talker &t, int T, hipStream_t s) {
         const LayerW &w = t.layers[l];
         rows::launch_rows(rows::EPI_PLAIN, true, t.x, t.lx, T, H, w.ln1, t.eps, w.wq, t.QD, w.wk, t.KVD, w.wv, t.KVD, t.part,
                           QKVW, t.flag, s);
-        hipLaunchKernelGGL(k_qkv_finish, dim3(T, (t.NQ + 2 * t.NKV + BT / WAVE - 1) / (BT / WAVE)), dim3(BT), 0, s, t.part,
-                           t.NQ, t.NKV, w.qn, w.kn, t.eps, t.invf, 0, t.q, t.kk[l], t.vv[l]);
-        if (T <= SHORT_KEYS)
-            hipLaunchKernelGGL(T <= SHORT_KEYS / (BT / WAVE) ? k_attn_prefill_short<true> : k_attn_prefill_short<false>,
-                               dim3(T, t.NKV), dim3(BT), 0, s, t.q, t.kk[l], t.vv[l], t.NQ, t.NKV, 0, scale, t.att, t.la);
-        else
-            hipLaunchKernelGGL(k_attn_prefill, dim3(T, t.NKV), dim3(BT), att_lds, s, t.q, t.kk[l], t.vv[l], t.NQ,
-                               t.NKV, 0, scale, t.att, t.la);
+        if (T <= FUSED_ROWS) {         // the q/k norms, RoPE and K/V store inside the attention
+            hipLaunchKernelGGL((k_attn_prefill_short<true, true>), dim3(T, t.NKV), dim3(BT), 0, s, nullptr, t.kk[l],
+                               t.vv[l], t.NQ, t.NKV, 0, scale, t.att, t.la, HeadNorm{t.part, w.qn, w.kn, t.invf, t.eps});
+        } else {
+            hipLaunchKernelGGL(k_qkv_finish, dim3(T, (t.NQ + 2 * t.NKV + BT / WAVE - 1) / (BT / WAVE)), dim3(BT), 0, s,
+                               t.part, t.NQ, t.NKV, w.qn, w.kn, t.eps, t.invf, 0, t.q, t.kk[l], t.vv[l]);
+            if (T <= SHORT_KEYS)
+                hipLaunchKernelGGL(T <= SHORT_KEYS / (BT / WAVE) ? k_attn_prefill_short<true> : k_attn_prefill_short<false>,
+                                   dim3(T, t.NKV), dim3(BT), 0, s, t.q, t.kk[l], t.vv[l], t.NQ, t.NKV, 0, scale, t.att,
+                                   t.la, HeadNorm{});
+            else
+                hipLaunchKernelGGL(k_attn_prefill, dim3(T, t.NKV), dim3(BT), att_lds, s, t.q, t.kk[l], t.vv[l], t.NQ,
+                                   t.NKV, 0, scale, t.att, t.la);
+        }
         rows::launch_rows(rows::EPI_RESID, false, t.att, t.la, T, t.QD, nullptr, 0.f, w.wo, H, nullptr, 0, nullptr, 0, t.x,
                           t.lx, t.flag, s);
         rows::launch_rows(rows::EPI_SWIGLU, true, t.x, t.lx, T, H, w.ln2, t.eps, w.wg, t.F, w.wu, t.F, nullptr, 0, t.h, t.lf,
