@@ -212,7 +212,7 @@ __global__ void __launch_bounds__(BT) k_conv_mfma(ConvArgs a) {
         const int cc = min(CCH, ce - ci0);
 #pragma unroll
         for (int s = 0; s < CCH / 32; ++s)   // past the chunk's channels: zeros (the staged A is zero there too)
-            bq[j][s] = s * 32 < cc ? __builtin_nontemporal_load((const NAVI_GLOBAL u32x4_t *) (wbase + static_cast<size_t>(j) * a.Cin + ci0 + s * 32))
+            bq[j][s] = s * 32 < cc ? *((const NAVI_GLOBAL u32x4_t *) (wbase + static_cast<size_t>(j) * a.Cin + ci0 + s * 32))
                                    : u32x4_t{0u, 0u, 0u, 0u};
     };
     auto load_a = [&](int ci0) {
@@ -403,7 +403,7 @@ __global__ void __launch_bounds__(BT) k_conv_wide(ConvArgs a) {
 #pragma unroll
         for (int it = 0; it < ITB; ++it)
             if (ITB * BT == NBI || static_cast<int>(threadIdx.x) + BT * it < NBI)
-                bv[it] = __builtin_nontemporal_load((const NAVI_GLOBAL u32x4_t *) (a.w + boff[it] + ci0));
+                bv[it] = *((const NAVI_GLOBAL u32x4_t *) (a.w + boff[it] + ci0));
     };
     f32x16_t acc[NCT], racc[SM == 2 ? NCT : 1];
 #pragma unroll
@@ -712,7 +712,7 @@ __global__ void __launch_bounds__(BT) k_unit(UnitArgs u) {
 #pragma unroll
         for (int it = 0; it < ITB; ++it)
             if (ITB * BT == NBI || static_cast<int>(threadIdx.x) + BT * it < NBI)
-                bv[it] = __builtin_nontemporal_load((const NAVI_GLOBAL u32x4_t *) (u.w7 + boff[it] + ci0));
+                bv[it] = *((const NAVI_GLOBAL u32x4_t *) (u.w7 + boff[it] + ci0));
     };
     // the k1's weights, 32 input channels (CC1) at a time: [C][CC1] in 16-byte pieces
     constexpr int W1Q = C * CC1 / 8, ITW = (W1Q + BT - 1) / BT;
