@@ -247,15 +247,22 @@ __device__ __forceinline__ NormW normw(const float (&w)[H / BT]) {
     return n;
 }
 
+// How a gather waits for its vector (written in chunks of CH words by N/CH producers):
+// WORDS: every thread issues the loads of all its words at once and, round by round, re-issues
+// only those whose tag is not yet this phase's: the vector is in LDS one coherent round trip
+// after the last producer's store becomes visible. SENTINELS: wave 0 first polls one word per
+// producer (its chunk's last) while the other waves sleep in the barrier, then every thread
+// reads the whole vector once, re-polling only the rare stale word: a second round trip, but
+// 1/CH of the polling traffic while the producers are still working. Frame at n_past 256 on
+// MI355X: sentinels everywhere 1.775 ms; WORDS for the residual (1024), MLP (3072), talker
+// logits (3072) and attention-partial (2304) gathers 1.612 ms; WORDS also for the attention
+// output (16 late producers of 128 words) 1.707 ms; also for the cp logits 1.622 ms.
+enum class Wait { WORDS, SENTINELS };
+
 // Block-wide: N tagged words at mailbox offset `off` -> dst (LDS f32). Uniform result.
 // With NORM (N == H) the same pass does norm_prep's work: xn[i] = x[i] * w[i] and this wave's
 // sum of x^2 in S.red[red + wave] (same order, so the same bits), published by the final barrier.
-// The vector is written in chunks of CH words by N/CH producers. Wave 0 first polls
-// one sentinel per producer (its chunk's last word) while the other waves sleep in
-// the barrier; then every thread reads the whole vector once, re-polling only the
-// rare word whose tag is not yet visible. Polling N words from every thread instead
-// floods the coherent path: 4.9 us vs 2.8 us for N = 3072 on MI355X.
-template <int N, int CH, bool REPL = true, bool NORM = false>
+template <int N, int CH, Wait WAIT, bool REPL = true, bool NORM = false>
 __device__ __forceinline__ bool gather(const Args &a, int off, uint32_t tag, float *dst, Smem &S, NormW nw = {},
                                        float *xn = nullptr, int red = 0) {
     static_assert(N % BT == 0 && N % CH == 0, "gather size");
@@ -263,6 +270,46 @@ __device__ __forceinline__ bool gather(const Args &a, int off, uint32_t tag, flo
     constexpr int PER = N / BT, NPROD = N / CH;
     uint64_t *const mb = sgpr_ptr(a.mb + (REPL ? xcc_copy() * MB_WORDS : 0) + off);
     PROF_MARK(a, S);
+    if constexpr (WAIT == Wait::WORDS) {
+        uint64_t w[PER];
+#pragma unroll
+        for (int k = 0; k < PER; ++k) w[k] = mb_peek(mb + tid() + k * BT);
+        uint64_t spins = 0;
+        bool ok = true;
+        for (;;) {                                 // per thread: the wave runs until every lane is done
+            bool done = true;
+#pragma unroll
+            for (int k = 0; k < PER; ++k) done &= tag_of(w[k]) == tag;
+            if (done) break;
+            if (++spins >= a.spin_cap || ((spins & 63u) == 0 && aborted(a))) {
+                abort_frame(a);
+                ok = false;
+                break;
+            }
+#pragma unroll
+            for (int k = 0; k < PER; ++k)
+                if (tag_of(w[k]) != tag) w[k] = mb_peek(mb + tid() + k * BT);
+        }
+        float ss = 0.f;
+#pragma unroll
+        for (int k = 0; k < PER; ++k) {
+            const int i = tid() + k * BT;
+            const float v = val_of(w[k]);
+            dst[i] = v;
+            if constexpr (NORM) {
+                ss = fmaf(v, v, ss);
+                xn[i] = v * nw.v[k];
+            }
+        }
+        if constexpr (NORM) {
+            ss = wave_sum(ss);
+            if (lane() == 0) S.red[red + wave()] = ss;
+        }
+        if (!ok) S.fail = 1;
+        __syncthreads();
+        PROF_MARK(a, S);
+        return S.fail == 0;
+    }
     if (wave() == 0) {
         // every sentinel of this lane in flight at once; only the stale ones are read again
         constexpr int NQ = (NPROD + WAVE - 1) / WAVE;
@@ -319,12 +366,12 @@ __device__ __forceinline__ bool gather(const Args &a, int off, uint32_t tag, flo
 }
 
 // T rows of N words each (row stride N in the mailbox and in dst), one row at a time.
-template <int T, int N, int CH, bool NORM = false>
+template <int T, int N, int CH, Wait WAIT, bool NORM = false>
 __device__ __forceinline__ bool gather_rows(const Args &a, int off, uint32_t tag, float *dst, Smem &S, NormW nw = {},
                                             float *xn = nullptr) {
 #pragma unroll
     for (int t = 0; t < T; ++t)
-        if (!gather<N, CH, true, NORM>(a, off + t * N, tag, dst + t * N, S, nw, NORM ? xn + t * N : nullptr, t * NW))
+        if (!gather<N, CH, WAIT, true, NORM>(a, off + t * N, tag, dst + t * N, S, nw, NORM ? xn + t * N : nullptr, t * NW))
             return false;
     return true;
 }
@@ -743,7 +790,7 @@ __device__ bool talker_attention(const Args &a, const Ctx &cx, float qkw, int il
     if (r != 0) return true;
     // combine head h's NR partials in range order: out = sum_r o_r e^(m_r - M) / sum_r l_r e^(m_r - M)
     float *P = S.u.m.big;
-    if (!gather<NR * AP_W, AP_W, false>(a, MB_AP + h * NR * AP_W, tag_ap, P, S)) return false;
+    if (!gather<NR * AP_W, AP_W, Wait::WORDS, false>(a, MB_AP + h * NR * AP_W, tag_ap, P, S)) return false;
     if (tid() < HD) {
         // lane k (mod 16) computes partial k's weight once; the weights go round by readlane
         static_assert(NR == 16, "one partial per lane of a 16-lane row");
@@ -896,18 +943,18 @@ __device__ __forceinline__ bool run_layer(const Args &a, const Ctx &cx, Regs &R,
     } else if (blk() < NH) {
         if (!cp_attention<T>(a, qkw, (gi - a.n_tl) % a.n_cl, p0, t_qkv, t_att, S)) return false;
     }
-    if (!gather_rows<T, QD, HD>(a, MB_ATT, t_att, S.u.m.big, S)) return false;
+    if (!gather_rows<T, QD, HD, Wait::SENTINELS>(a, MB_ATT, t_att, S.u.m.big, S)) return false;
     const uint32_t t_x2 = seq.next();
     o_phase<T>(a, R, S, t_x2);
     if (has_next) load_o(R, N, next_cp);
 
-    if (!gather_rows<T, H, H / NB, true>(a, MB_X2, t_x2, &S.x[0][0], S, normw(R.ln2), &S.xn[0][0])) return false;
+    if (!gather_rows<T, H, H / NB, Wait::WORDS, true>(a, MB_X2, t_x2, &S.x[0][0], S, normw(R.ln2), &S.xn[0][0])) return false;
     norm_scale<T>(eps, sc, S);
     const uint32_t t_h = seq.next();
     gu_phase<T>(a, R, S, t_h, sc);
     if (has_next) load_gu(R, N, next_cp);
 
-    if (!gather_rows<T, FF, FF / NB>(a, MB_H, t_h, S.u.m.big, S)) return false;
+    if (!gather_rows<T, FF, FF / NB, Wait::WORDS>(a, MB_H, t_h, S.u.m.big, S)) return false;
     const uint32_t t_x = seq.next();
     down_phase<T>(a, R, S, t_x);
     if (has_next) load_dn(R, N, next_cp);
@@ -918,7 +965,7 @@ __device__ __forceinline__ bool run_layer(const Args &a, const Ctx &cx, Regs &R,
 
     // R.ln1 holds the next layer's weights by now (load_qkv above); the last layer of the frame
     // is always next_final
-    return gather_rows<T, H, H / NB, true>(a, MB_X, t_x, &S.x[0][0], S, next_final ? normw(R.fn) : normw(R.ln1),
+    return gather_rows<T, H, H / NB, Wait::WORDS, true>(a, MB_X, t_x, &S.x[0][0], S, next_final ? normw(R.fn) : normw(R.ln1),
                                            &S.xn[0][0]);
 }
 
@@ -987,7 +1034,7 @@ __global__ void __launch_bounds__(BT, 1) k_frame(Args a, const Weights *__restri
             for (int r = 0; r < 3; ++r)
                 if (lane() < NREP) mb_put(a.mb + lane() * MB_WORDS + MB_LG + blk() * (VT / NB) + wave() * 3 + r, d[r] * hsc[0], t_lg);
         }
-        if (!gather<VT, VT / NB>(a, MB_LG, t_lg, S.u.m.samp.lg, S)) return;
+        if (!gather<VT, VT / NB, Wait::WORDS>(a, MB_LG, t_lg, S.u.m.samp.lg, S)) return;
         // the post-norm hidden the code predictor takes: each thread scales the elements it wrote
         // (and is the only one to read below), after the gather's barriers ended the head's reads
         for (int i = tid(); i < H; i += BT) S.xn[0][i] *= hsc[0];
@@ -1059,7 +1106,7 @@ __global__ void __launch_bounds__(BT, 1) k_frame(Args a, const Weights *__restri
             for (int r = 0; r < 2; ++r)
                 if (lane() < NREP) mb_put(a.mb + lane() * MB_WORDS + MB_LG + blk() * (VC / NB) + wave() * 2 + r, d[r] * hsc0, t_lg);
         }
-        if (!gather<VC, VC / NB>(a, MB_LG, t_lg, S.u.m.samp.lg, S)) return;
+        if (!gather<VC, VC / NB, Wait::SENTINELS>(a, MB_LG, t_lg, S.u.m.samp.lg, S)) return;
         if (a.tap_cp_logits && blk() == 0) {
             for (int i = tid(); i < VC; i += BT) gst(a.tap_cp_logits + (pos - 1) * VC + i, S.u.m.samp.lg[i]);
             __syncthreads();
