@@ -365,15 +365,79 @@ __device__ __forceinline__ bool gather(const Args &a, int off, uint32_t tag, flo
     return S.fail == 0;
 }
 
-// T rows of N words each (row stride N in the mailbox and in dst), one row at a time.
+// Two rows of N words (row stride N in the mailbox and in dst) in one WORDS wait: both rows' words
+// of a thread in flight at once, so the second row costs no round trip of its own. Per row the
+// same values, order and norm partial sums (S.red[t * NW + wave]) as gather<>.
+template <int N, bool NORM>
+__device__ __forceinline__ bool gather_two_rows(const Args &a, int off, uint32_t tag, float *dst, Smem &S, NormW nw,
+                                                float *xn) {
+    static_assert(N % BT == 0, "gather size");
+    constexpr int PER = N / BT;
+    uint64_t *const mb = sgpr_ptr(a.mb + xcc_copy() * MB_WORDS + off);
+    PROF_MARK(a, S);
+    uint64_t w[2][PER];
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int k = 0; k < PER; ++k) w[t][k] = mb_peek(mb + t * N + tid() + k * BT);
+    uint64_t spins = 0;
+    bool ok = true;
+    for (;;) {
+        bool done = true;
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int k = 0; k < PER; ++k) done &= tag_of(w[t][k]) == tag;
+        if (done) break;
+        if (++spins >= a.spin_cap || ((spins & 63u) == 0 && aborted(a))) {
+            abort_frame(a);
+            ok = false;
+            break;
+        }
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int k = 0; k < PER; ++k)
+                if (tag_of(w[t][k]) != tag) w[t][k] = mb_peek(mb + t * N + tid() + k * BT);
+    }
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        float ss = 0.f;
+#pragma unroll
+        for (int k = 0; k < PER; ++k) {
+            const int i = t * N + tid() + k * BT;
+            const float v = val_of(w[t][k]);
+            dst[i] = v;
+            if constexpr (NORM) {
+                ss = fmaf(v, v, ss);
+                xn[i] = v * nw.v[k];
+            }
+        }
+        if constexpr (NORM) {
+            ss = wave_sum(ss);
+            if (lane() == 0) S.red[t * NW + wave()] = ss;
+        }
+    }
+    if (!ok) S.fail = 1;
+    __syncthreads();
+    PROF_MARK(a, S);
+    return S.fail == 0;
+}
+
+// T rows of N words each (row stride N in the mailbox and in dst): two rows in one WORDS wait,
+// otherwise one row at a time.
 template <int T, int N, int CH, Wait WAIT, bool NORM = false>
 __device__ __forceinline__ bool gather_rows(const Args &a, int off, uint32_t tag, float *dst, Smem &S, NormW nw = {},
                                             float *xn = nullptr) {
+    if constexpr (T == 2 && WAIT == Wait::WORDS) {
+        return gather_two_rows<N, NORM>(a, off, tag, dst, S, nw, xn);
+    } else {
 #pragma unroll
-    for (int t = 0; t < T; ++t)
-        if (!gather<N, CH, WAIT, true, NORM>(a, off + t * N, tag, dst + t * N, S, nw, NORM ? xn + t * N : nullptr, t * NW))
-            return false;
-    return true;
+        for (int t = 0; t < T; ++t)
+            if (!gather<N, CH, WAIT, true, NORM>(a, off + t * N, tag, dst + t * N, S, nw, NORM ? xn + t * N : nullptr, t * NW))
+                return false;
+        return true;
+    }
 }
 
 // ---- RMSNorm of T rows (every block, redundantly) ---------------------------
