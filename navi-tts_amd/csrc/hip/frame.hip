@@ -259,10 +259,29 @@ __device__ __forceinline__ NormW normw(const float (&w)[H / BT]) {
 // output (16 late producers of 128 words) 1.707 ms; also for the cp logits 1.622 ms.
 enum class Wait { WORDS, SENTINELS };
 
+// A pause before a gather's first poll, in s_sleep units of 64 clocks, per gather site. Polls that
+// go out while the producers are still computing only add coherent traffic to the mailbox lines
+// the producers' stores are headed for, and slow those stores down. A frame at n_past 256 on
+// MI355X: no pause 1.614 ms; 16 before the residual, MLP, talker-logit and attention-partial
+// gathers 1.564; the values below 1.534 (32 before the residual gathers: 1.558).
+constexpr int D_X2 = 24;    // x2 (after o; its prefetch is 16 KB per CU)
+constexpr int D_H = 16;     // MLP activation (after gate|up and its 48 KB prefetch)
+constexpr int D_X = 24;     // x (after down)
+constexpr int D_ATT = 24;   // attention output (every block; the 16 attention blocks publish it)
+constexpr int D_AP = 24;    // talker attention partials (the combining blocks)
+constexpr int D_TLG = 32;   // talker logits
+constexpr int D_CLG = 32;   // code-predictor logits
+constexpr int D_QKV = 8;    // q/k/v at the attention blocks
+
+template <int D>
+__device__ __forceinline__ void pause() {
+    if constexpr (D > 0) __builtin_amdgcn_s_sleep(D);
+}
+
 // Block-wide: N tagged words at mailbox offset `off` -> dst (LDS f32). Uniform result.
 // With NORM (N == H) the same pass does norm_prep's work: xn[i] = x[i] * w[i] and this wave's
 // sum of x^2 in S.red[red + wave] (same order, so the same bits), published by the final barrier.
-template <int N, int CH, Wait WAIT, bool REPL = true, bool NORM = false>
+template <int N, int CH, Wait WAIT, bool REPL = true, bool NORM = false, int D = 0>
 __device__ __forceinline__ bool gather(const Args &a, int off, uint32_t tag, float *dst, Smem &S, NormW nw = {},
                                        float *xn = nullptr, int red = 0) {
     static_assert(N % BT == 0 && N % CH == 0, "gather size");
@@ -272,6 +291,7 @@ __device__ __forceinline__ bool gather(const Args &a, int off, uint32_t tag, flo
     PROF_MARK(a, S);
     if constexpr (WAIT == Wait::WORDS) {
         uint64_t w[PER];
+        pause<D>();
 #pragma unroll
         for (int k = 0; k < PER; ++k) w[k] = mb_peek(mb + tid() + k * BT);
         uint64_t spins = 0;
@@ -314,6 +334,7 @@ __device__ __forceinline__ bool gather(const Args &a, int off, uint32_t tag, flo
         // every sentinel of this lane in flight at once; only the stale ones are read again
         constexpr int NQ = (NPROD + WAVE - 1) / WAVE;
         uint64_t sw[NQ];
+        pause<D>();
 #pragma unroll
         for (int q = 0; q < NQ; ++q) {
             const int pr = lane() + q * WAVE;
@@ -368,7 +389,7 @@ __device__ __forceinline__ bool gather(const Args &a, int off, uint32_t tag, flo
 // Two rows of N words (row stride N in the mailbox and in dst) in one WORDS wait: both rows' words
 // of a thread in flight at once, so the second row costs no round trip of its own. Per row the
 // same values, order and norm partial sums (S.red[t * NW + wave]) as gather<>.
-template <int N, bool NORM>
+template <int N, bool NORM, int D>
 __device__ __forceinline__ bool gather_two_rows(const Args &a, int off, uint32_t tag, float *dst, Smem &S, NormW nw,
                                                 float *xn) {
     static_assert(N % BT == 0, "gather size");
@@ -376,6 +397,7 @@ __device__ __forceinline__ bool gather_two_rows(const Args &a, int off, uint32_t
     uint64_t *const mb = sgpr_ptr(a.mb + xcc_copy() * MB_WORDS + off);
     PROF_MARK(a, S);
     uint64_t w[2][PER];
+    pause<D>();
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
@@ -426,16 +448,15 @@ __device__ __forceinline__ bool gather_two_rows(const Args &a, int off, uint32_t
 
 // T rows of N words each (row stride N in the mailbox and in dst): two rows in one WORDS wait,
 // otherwise one row at a time.
-template <int T, int N, int CH, Wait WAIT, bool NORM = false>
+template <int T, int N, int CH, Wait WAIT, bool NORM = false, int D = 0>
 __device__ __forceinline__ bool gather_rows(const Args &a, int off, uint32_t tag, float *dst, Smem &S, NormW nw = {},
                                             float *xn = nullptr) {
     if constexpr (T == 2 && WAIT == Wait::WORDS) {
-        return gather_two_rows<N, NORM>(a, off, tag, dst, S, nw, xn);
+        return gather_two_rows<N, NORM, D>(a, off, tag, dst, S, nw, xn);
     } else {
-#pragma unroll
-        for (int t = 0; t < T; ++t)
-            if (!gather<N, CH, WAIT, true, NORM>(a, off + t * N, tag, dst + t * N, S, nw, NORM ? xn + t * N : nullptr, t * NW))
-                return false;
+        static_assert(T == 1 || T == 2, "one or two rows");
+        if (!gather<N, CH, WAIT, true, NORM, D>(a, off, tag, dst, S, nw, NORM ? xn : nullptr, 0)) return false;
+        if constexpr (T == 2) return gather<N, CH, WAIT, true, NORM>(a, off + N, tag, dst + N, S, nw, NORM ? xn + N : nullptr, NW);
         return true;
     }
 }
@@ -664,6 +685,7 @@ __device__ __forceinline__ bool gather_head(const Args &a, int h, int g, uint32_
     constexpr int PER = (T * 3 * HD + BT - 1) / BT;
     int off[PER];
     uint64_t w[PER];
+    pause<D_QKV>();
 #pragma unroll
     for (int k = 0; k < PER; ++k) {                   // all of this thread's words in flight at once
         const int i = tid() + k * BT;
@@ -854,7 +876,7 @@ __device__ bool talker_attention(const Args &a, const Ctx &cx, float qkw, int il
     if (r != 0) return true;
     // combine head h's NR partials in range order: out = sum_r o_r e^(m_r - M) / sum_r l_r e^(m_r - M)
     float *P = S.u.m.big;
-    if (!gather<NR * AP_W, AP_W, Wait::WORDS, false>(a, MB_AP + h * NR * AP_W, tag_ap, P, S)) return false;
+    if (!gather<NR * AP_W, AP_W, Wait::WORDS, false, false, D_AP>(a, MB_AP + h * NR * AP_W, tag_ap, P, S)) return false;
     if (tid() < HD) {
         // lane k (mod 16) computes partial k's weight once; the weights go round by readlane
         static_assert(NR == 16, "one partial per lane of a 16-lane row");
@@ -1007,18 +1029,18 @@ __device__ __forceinline__ bool run_layer(const Args &a, const Ctx &cx, Regs &R,
     } else if (blk() < NH) {
         if (!cp_attention<T>(a, qkw, (gi - a.n_tl) % a.n_cl, p0, t_qkv, t_att, S)) return false;
     }
-    if (!gather_rows<T, QD, HD, Wait::SENTINELS>(a, MB_ATT, t_att, S.u.m.big, S)) return false;
+    if (!gather_rows<T, QD, HD, Wait::SENTINELS, false, D_ATT>(a, MB_ATT, t_att, S.u.m.big, S)) return false;
     const uint32_t t_x2 = seq.next();
     o_phase<T>(a, R, S, t_x2);
     if (has_next) load_o(R, N, next_cp);
 
-    if (!gather_rows<T, H, H / NB, Wait::WORDS, true>(a, MB_X2, t_x2, &S.x[0][0], S, normw(R.ln2), &S.xn[0][0])) return false;
+    if (!gather_rows<T, H, H / NB, Wait::WORDS, true, D_X2>(a, MB_X2, t_x2, &S.x[0][0], S, normw(R.ln2), &S.xn[0][0])) return false;
     norm_scale<T>(eps, sc, S);
     const uint32_t t_h = seq.next();
     gu_phase<T>(a, R, S, t_h, sc);
     if (has_next) load_gu(R, N, next_cp);
 
-    if (!gather_rows<T, FF, FF / NB, Wait::WORDS>(a, MB_H, t_h, S.u.m.big, S)) return false;
+    if (!gather_rows<T, FF, FF / NB, Wait::WORDS, false, D_H>(a, MB_H, t_h, S.u.m.big, S)) return false;
     const uint32_t t_x = seq.next();
     down_phase<T>(a, R, S, t_x);
     if (has_next) load_dn(R, N, next_cp);
@@ -1029,7 +1051,7 @@ __device__ __forceinline__ bool run_layer(const Args &a, const Ctx &cx, Regs &R,
 
     // R.ln1 holds the next layer's weights by now (load_qkv above); the last layer of the frame
     // is always next_final
-    return gather_rows<T, H, H / NB, Wait::WORDS, true>(a, MB_X, t_x, &S.x[0][0], S, next_final ? normw(R.fn) : normw(R.ln1),
+    return gather_rows<T, H, H / NB, Wait::WORDS, true, D_X>(a, MB_X, t_x, &S.x[0][0], S, next_final ? normw(R.fn) : normw(R.ln1),
                                            &S.xn[0][0]);
 }
 
@@ -1098,7 +1120,7 @@ __global__ void __launch_bounds__(BT, 1) k_frame(Args a, const Weights *__restri
             for (int r = 0; r < 3; ++r)
                 if (lane() < NREP) mb_put(a.mb + lane() * MB_WORDS + MB_LG + blk() * (VT / NB) + wave() * 3 + r, d[r] * hsc[0], t_lg);
         }
-        if (!gather<VT, VT / NB, Wait::WORDS>(a, MB_LG, t_lg, S.u.m.samp.lg, S)) return;
+        if (!gather<VT, VT / NB, Wait::WORDS, true, false, D_TLG>(a, MB_LG, t_lg, S.u.m.samp.lg, S)) return;
         // the post-norm hidden the code predictor takes: each thread scales the elements it wrote
         // (and is the only one to read below), after the gather's barriers ended the head's reads
         for (int i = tid(); i < H; i += BT) S.xn[0][i] *= hsc[0];
@@ -1170,7 +1192,7 @@ __global__ void __launch_bounds__(BT, 1) k_frame(Args a, const Weights *__restri
             for (int r = 0; r < 2; ++r)
                 if (lane() < NREP) mb_put(a.mb + lane() * MB_WORDS + MB_LG + blk() * (VC / NB) + wave() * 2 + r, d[r] * hsc0, t_lg);
         }
-        if (!gather<VC, VC / NB, Wait::SENTINELS>(a, MB_LG, t_lg, S.u.m.samp.lg, S)) return;
+        if (!gather<VC, VC / NB, Wait::SENTINELS, true, false, D_CLG>(a, MB_LG, t_lg, S.u.m.samp.lg, S)) return;
         if (a.tap_cp_logits && blk() == 0) {
             for (int i = tid(); i < VC; i += BT) gst(a.tap_cp_logits + (pos - 1) * VC + i, S.u.m.samp.lg[i]);
             __syncthreads();
