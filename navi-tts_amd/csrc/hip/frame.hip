@@ -1020,7 +1020,12 @@ __device__ __forceinline__ bool run_layer(const Args &a, const Ctx &cx, Regs &R,
     const uint32_t t_qkv = seq.next();
     qkv_phase<T>(a, R, S, t_qkv, sc);
     const float qkw = R.qkw;     // this layer's q/k norm weight; the prefetch below replaces it
-    if (has_next) load_qkv(R, N, next_cp);
+    // The next layer's q|k|v slice. Blocks with attention work of their own (the talker's key-range
+    // blocks, the code predictor's attention blocks) issue it once that work is published, so its
+    // loads do not sit in front of their q/k/v polls; the talker's combining blocks and the code
+    // predictor's other blocks issue it now (1.537 -> 1.518 ms per frame at n_past 256).
+    const bool pf_late = TALKER ? blk() >= NH : blk() < NH;
+    if (has_next && !pf_late) load_qkv(R, N, next_cp);
 
     const uint32_t t_ap = TALKER ? seq.next() : 0u;
     const uint32_t t_att = seq.next();
@@ -1029,6 +1034,7 @@ __device__ __forceinline__ bool run_layer(const Args &a, const Ctx &cx, Regs &R,
     } else if (blk() < NH) {
         if (!cp_attention<T>(a, qkw, (gi - a.n_tl) % a.n_cl, p0, t_qkv, t_att, S)) return false;
     }
+    if (has_next && pf_late) load_qkv(R, N, next_cp);
     if (!gather_rows<T, QD, HD, Wait::SENTINELS, false, D_ATT>(a, MB_ATT, t_att, S.u.m.big, S)) return false;
     const uint32_t t_x2 = seq.next();
     o_phase<T>(a, R, S, t_x2);
