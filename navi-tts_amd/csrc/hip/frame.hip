@@ -263,11 +263,13 @@ enum class Wait { WORDS, SENTINELS };
 // go out while the producers are still computing only add coherent traffic to the mailbox lines
 // the producers' stores are headed for, and slow those stores down. A frame at n_past 256 on
 // MI355X: no pause 1.614 ms; 16 before the residual, MLP, talker-logit and attention-partial
-// gathers 1.564; the values below 1.534 (32 before the residual gathers: 1.558).
+// gathers 1.564; the values below 1.534 (32 before the residual gathers: 1.558); with the late
+// q|k|v prefetch of the attention blocks (run_layer) the attention output's pause went from 24
+// to 12 (1.509 -> 1.487 ms; 32: 1.532).
 constexpr int D_X2 = 24;    // x2 (after o; its prefetch is 16 KB per CU)
 constexpr int D_H = 16;     // MLP activation (after gate|up and its 48 KB prefetch)
 constexpr int D_X = 24;     // x (after down)
-constexpr int D_ATT = 24;   // attention output (every block; the 16 attention blocks publish it)
+constexpr int D_ATT = 12;   // attention output (every block; the 16 attention blocks publish it)
 constexpr int D_AP = 24;    // talker attention partials (the combining blocks)
 constexpr int D_TLG = 32;   // talker logits
 constexpr int D_CLG = 32;   // code-predictor logits
@@ -877,26 +879,29 @@ __device__ bool talker_attention(const Args &a, const Ctx &cx, float qkw, int il
     // combine head h's NR partials in range order: out = sum_r o_r e^(m_r - M) / sum_r l_r e^(m_r - M)
     float *P = S.u.m.big;
     if (!gather<NR * AP_W, AP_W, Wait::WORDS, false, false, D_AP>(a, MB_AP + h * NR * AP_W, tag_ap, P, S)) return false;
-    if (tid() < HD) {
-        // lane k (mod 16) computes partial k's weight once; the weights go round by readlane
+    {
+        // every thread combines dim tid % 128 (the two halves of the block identically) and
+        // publishes it to half of the copies; lane k (mod 16) computes partial k's weight once,
+        // the weights go round by readlane
         static_assert(NR == 16, "one partial per lane of a 16-lane row");
-        const int k = L & (NR - 1);
+        const int k = L & (NR - 1), d = tid() & (HD - 1);
         const float mk = P[k * AP_W + HD], lk = P[k * AP_W + HD + 1];
         const float M = wave_max(mk);
         const float wk = mk == -INFINITY ? 0.f : expf(mk - M);
+        float pv[NR];
+#pragma unroll
+        for (int k2 = 0; k2 < NR; ++k2) pv[k2] = P[k2 * AP_W + d];
         float num = 0.f, den = 0.f;
 #pragma unroll
         for (int k2 = 0; k2 < NR; ++k2) {
             const float wv = lane_value(wk, k2);
             den = fmaf(lane_value(lk, k2), wv, den);
-            num = fmaf(P[k2 * AP_W + tid()], wv, num);
+            num = fmaf(pv[k2], wv, num);
         }
-        S.opart[0][tid()] = num / den;
-    }
-    __syncthreads();
-    for (int i = tid(); i < HD * NREP; i += BT) {      // one (value, copy) per iteration
-        const int d = i % HD, c = i / HD;
-        mb_put(a.mb + c * MB_WORDS + MB_ATT + h * HD + d, S.opart[0][d], tag_att);
+        const float o = num / den;
+        const int c0 = (tid() >> 7) * (NREP / 2);
+#pragma unroll
+        for (int c = 0; c < NREP / 2; ++c) mb_put(a.mb + (c0 + c) * MB_WORDS + MB_ATT + h * HD + d, o, tag_att);
     }
     PROF_MARK(a, S);
     return true;
