@@ -32,7 +32,7 @@ extern "C" {
 typedef enum {
     NAVI_OK = 0,
     NAVI_ERR_TIMEOUT = 1,        /* a dataflow wait hit its spin cap (frame.hip:673 "timed out") */
-    NAVI_ERR_LAUNCH = 2,         /* cooperative launch refused (frame.hip:664) */
+    NAVI_ERR_LAUNCH = 2,         /* frame launch refused (the reference's cooperative launch, frame.hip:664) */
     NAVI_ERR_KV_FULL = 3,        /* n_past >= max_pos (frame.hip:800) */
     NAVI_ERR_INVALID = 4,        /* bad argument / shape / missing tensor */
     NAVI_ERR_HIP = 5,            /* a HIP runtime call failed */

@@ -1,6 +1,6 @@
 // The per-frame token loop on gfx950: talker decode step at n_past -> codebook-0
 // sampling -> 16-position code-predictor pass with 15 sampled codebooks ->
-// next step embedding, in one persistent cooperative launch.
+// next step embedding, in one persistent launch.
 //
 // Replaces k_frame and its phases (model/qwen3tts/frame.hip:85-579) and the
 // host side of Frame (frame.hip:590-810). MI355X design:
@@ -28,6 +28,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <string>
 #include <vector>
@@ -1542,12 +1543,32 @@ hipError_t advance_epoch(navi_frame *f) {
     return hipSuccess;
 }
 
+// The frame's grid is one block per CU and every block waits for the others, so all of them must
+// be resident at once. navi_frame_create checked that one block fits on every CU; kernels on one
+// stream run one after the other; and a block whose peers never become resident ends at the spin
+// cap with "timed out" rather than hanging. So the grid goes out as an ordinary launch: on MI355X
+// it measured 1.464 against 1.479 ms per frame for a cooperative launch (the reference's
+// Impl::launch, frame.hip:663), and rocprofv3 ends a process that made cooperative launches with
+// SIGSEGV inside exit() while the same process with ordinary launches exits cleanly.
+// NAVI_FRAME_LAUNCH=cooperative in the environment selects the cooperative launch.
+bool cooperative_launch() {
+    static const bool coop = [] {
+        const char *e = std::getenv("NAVI_FRAME_LAUNCH");
+        return e && std::strcmp(e, "cooperative") == 0;
+    }();
+    return coop;
+}
+
 hipError_t frame_launch(navi_frame *f, Args &a) {
     const Weights *wp = f->dw;
     uint16_t *const *kvp = f->kv_dev;
-    void *args[] = {&a, &wp, &kvp};
-    return hipLaunchCooperativeKernel(reinterpret_cast<const void *>(k_frame), dim3(f->grid), dim3(BT), args, 0,
-                                      device_state().stream);
+    if (cooperative_launch()) {
+        void *args[] = {&a, &wp, &kvp};
+        return hipLaunchCooperativeKernel(reinterpret_cast<const void *>(k_frame), dim3(f->grid), dim3(BT), args, 0,
+                                          device_state().stream);
+    }
+    hipLaunchKernelGGL(k_frame, dim3(f->grid), dim3(BT), 0, device_state().stream, a, wp, kvp);
+    return hipGetLastError();
 }
 
 } // namespace
@@ -1580,7 +1601,7 @@ navi_status navi_frame_run(navi_frame *f, const navi_kv_view *kv, int32_t n_past
     if (hipEventRecord(f->ev0, st) != hipSuccess) return fail(NAVI_ERR_HIP, "frame: hipEventRecord failed");
     const hipError_t e = frame_launch(f, a);
     if (e != hipSuccess) {
-        std::string m = std::string("cooperative launch failed: ") + hipGetErrorString(e);
+        std::string m = std::string("frame launch failed: ") + hipGetErrorString(e);
         return fail(NAVI_ERR_LAUNCH, m.c_str());
     }
     uint32_t h[NCB + 1] = {};
@@ -1642,7 +1663,7 @@ navi_status navi_frame_run_many(navi_frame *f, const navi_kv_view *kv, int32_t n
         const hipError_t e = frame_launch(f, a);
         if (e != hipSuccess) {
             (void) hipStreamSynchronize(st);
-            set_err(err, errlen, "cooperative launch failed: %s", hipGetErrorString(e));
+            set_err(err, errlen, "frame launch failed: %s", hipGetErrorString(e));
             return NAVI_ERR_LAUNCH;
         }
     }

@@ -18,10 +18,6 @@ def _bench():
     return mod
 
 
-@pytest.mark.skip(reason="no further rocprofv3 counter runs of a process that launches k_frame: every such run "
-                         "ended in SIGSEGV inside exit() after the profiler's finalization, with the cause not "
-                         "shown; bench.py reports roofline.traffic as null while the frame sources differ from the "
-                         "ones the committed counters were measured on")
 def test_traffic_file_matches_the_frame_sources():
     b = _bench()
     t = json.loads(b.TRAFFIC_FILE.read_text())
