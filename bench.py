@@ -400,16 +400,14 @@ def frame_phase_table(P: np.ndarray, n_tl: int, n_cl: int, n_cb: int = 16) -> di
             L.append(d)
         head = dict(zip(("lg_gs", "lg_ge", "s0", "s1"), t[i:i + 4])); i += 4
         for p in range(n_cb - 1):
-            rows = 2 if p == 0 else 1
             for _ in range(n_cl):
                 d = {}
                 if att:
                     d.update(zip(("cpa_start", "cpa_qkv", "cpa_put"), t[i:i + 3])); i += 3
-                # the attention output is gathered row by row, x2 / h / x with both rows in one wait
-                v = t[i:i + 2 * rows + 6]; i += 2 * rows + 6
-                a0 = 2 * rows
-                d.update({"att_gs": v[0], "att_ge": v[a0 - 1], "x2_gs": v[a0], "x2_ge": v[a0 + 1],
-                          "h_gs": v[a0 + 2], "h_ge": v[a0 + 3], "x_gs": v[a0 + 4], "x_ge": v[a0 + 5]})
+                # every gather takes both rows of a two-row pass in one wait: two stamps each
+                v = t[i:i + 8]; i += 8
+                d.update({"att_gs": v[0], "att_ge": v[1], "x2_gs": v[2], "x2_ge": v[3],
+                          "h_gs": v[4], "h_ge": v[5], "x_gs": v[6], "x_ge": v[7]})
                 C.append(d)
             C[-1].update(zip(("lg_gs", "lg_ge", "s0", "s1"), t[i:i + 4])); i += 4
         per_block.append((L, head, C, t[i] if i < n else np.nan))

@@ -248,17 +248,14 @@ __device__ __forceinline__ NormW normw(const float (&w)[H / BT]) {
     return n;
 }
 
-// How a gather waits for its vector (written in chunks of CH words by N/CH producers):
-// WORDS: every thread issues the loads of all its words at once and, round by round, re-issues
-// only those whose tag is not yet this phase's: the vector is in LDS one coherent round trip
-// after the last producer's store becomes visible. SENTINELS: wave 0 first polls one word per
-// producer (its chunk's last) while the other waves sleep in the barrier, then every thread
-// reads the whole vector once, re-polling only the rare stale word: a second round trip, but
-// 1/CH of the polling traffic while the producers are still working. Frame at n_past 256 on
-// MI355X: sentinels everywhere 1.775 ms; WORDS for the residual (1024), MLP (3072), talker
-// logits (3072) and attention-partial (2304) gathers 1.612 ms; WORDS also for the attention
-// output (16 late producers of 128 words) 1.707 ms; also for the cp logits 1.622 ms.
-enum class Wait { WORDS, SENTINELS };
+// How a gather waits for its vector: every thread issues the loads of all its words at once and,
+// round by round, re-issues only those whose tag is not yet this phase's, so the vector is in LDS
+// one coherent round trip after the last producer's store becomes visible. The alternative, wave 0
+// polling one sentinel word per producer and then every thread reading the vector (a second round
+// trip, but 1/CH of the polling traffic while the producers still compute), measured on MI355X at
+// n_past 256: sentinels everywhere 1.775 ms; words for the residual, MLP, talker-logit and
+// attention-partial gathers 1.612 ms; once every first poll waited a pause (below), words for the
+// attention output and the code-predictor logits too: 1.462 -> 1.438 ms.
 
 // A pause before a gather's first poll, in s_sleep units of 64 clocks, per gather site. Polls that
 // go out while the producers are still computing only add coherent traffic to the mailbox lines
@@ -284,94 +281,38 @@ __device__ __forceinline__ void pause() {
 // Block-wide: N tagged words at mailbox offset `off` -> dst (LDS f32). Uniform result.
 // With NORM (N == H) the same pass does norm_prep's work: xn[i] = x[i] * w[i] and this wave's
 // sum of x^2 in S.red[red + wave] (same order, so the same bits), published by the final barrier.
-template <int N, int CH, Wait WAIT, bool REPL = true, bool NORM = false, int D = 0>
+template <int N, bool REPL = true, bool NORM = false, int D = 0>
 __device__ __forceinline__ bool gather(const Args &a, int off, uint32_t tag, float *dst, Smem &S, NormW nw = {},
                                        float *xn = nullptr, int red = 0) {
-    static_assert(N % BT == 0 && N % CH == 0, "gather size");
+    static_assert(N % BT == 0, "gather size");
     static_assert(!NORM || N == H, "norm of the residual stream");
-    constexpr int PER = N / BT, NPROD = N / CH;
+    constexpr int PER = N / BT;
     uint64_t *const mb = sgpr_ptr(a.mb + (REPL ? xcc_copy() * MB_WORDS : 0) + off);
     PROF_MARK(a, S);
-    if constexpr (WAIT == Wait::WORDS) {
-        uint64_t w[PER];
-        pause<D>();
-#pragma unroll
-        for (int k = 0; k < PER; ++k) w[k] = mb_peek(mb + tid() + k * BT);
-        uint64_t spins = 0;
-        bool ok = true;
-        for (;;) {                                 // per thread: the wave runs until every lane is done
-            bool done = true;
-#pragma unroll
-            for (int k = 0; k < PER; ++k) done &= tag_of(w[k]) == tag;
-            if (done) break;
-            if (++spins >= a.spin_cap || ((spins & 63u) == 0 && aborted(a))) {
-                abort_frame(a);
-                ok = false;
-                break;
-            }
-#pragma unroll
-            for (int k = 0; k < PER; ++k)
-                if (tag_of(w[k]) != tag) w[k] = mb_peek(mb + tid() + k * BT);
-        }
-        float ss = 0.f;
-#pragma unroll
-        for (int k = 0; k < PER; ++k) {
-            const int i = tid() + k * BT;
-            const float v = val_of(w[k]);
-            dst[i] = v;
-            if constexpr (NORM) {
-                ss = fmaf(v, v, ss);
-                xn[i] = v * nw.v[k];
-            }
-        }
-        if constexpr (NORM) {
-            ss = wave_sum(ss);
-            if (lane() == 0) S.red[red + wave()] = ss;
-        }
-        if (!ok) S.fail = 1;
-        __syncthreads();
-        PROF_MARK(a, S);
-        return S.fail == 0;
-    }
-    if (wave() == 0) {
-        // every sentinel of this lane in flight at once; only the stale ones are read again
-        constexpr int NQ = (NPROD + WAVE - 1) / WAVE;
-        uint64_t sw[NQ];
-        pause<D>();
-#pragma unroll
-        for (int q = 0; q < NQ; ++q) {
-            const int pr = lane() + q * WAVE;
-            sw[q] = pr < NPROD ? mb_peek(mb + pr * CH + CH - 1) : static_cast<uint64_t>(tag) << 32;
-        }
-        uint64_t spins = 0;
-        bool ok = true;
-        for (;;) {
-            bool done = true;
-#pragma unroll
-            for (int q = 0; q < NQ; ++q) done &= tag_of(sw[q]) == tag;
-            if (done) break;
-            if (++spins >= a.spin_cap || ((spins & 63u) == 0 && aborted(a))) {
-                abort_frame(a);
-                ok = false;
-                break;
-            }
-#pragma unroll
-            for (int q = 0; q < NQ; ++q)
-                if (tag_of(sw[q]) != tag) sw[q] = mb_peek(mb + (lane() + q * WAVE) * CH + CH - 1);
-        }
-        if (!ok) S.fail = 1;
-    }
-    __syncthreads();
-    if (S.fail) return false;
     uint64_t w[PER];
+    pause<D>();
 #pragma unroll
     for (int k = 0; k < PER; ++k) w[k] = mb_peek(mb + tid() + k * BT);
+    uint64_t spins = 0;
     bool ok = true;
+    for (;;) {                                 // per thread: the wave runs until every lane is done
+        bool done = true;
+#pragma unroll
+        for (int k = 0; k < PER; ++k) done &= tag_of(w[k]) == tag;
+        if (done) break;
+        if (++spins >= a.spin_cap || ((spins & 63u) == 0 && aborted(a))) {
+            abort_frame(a);
+            ok = false;
+            break;
+        }
+#pragma unroll
+        for (int k = 0; k < PER; ++k)
+            if (tag_of(w[k]) != tag) w[k] = mb_peek(mb + tid() + k * BT);
+    }
     float ss = 0.f;
 #pragma unroll
     for (int k = 0; k < PER; ++k) {
         const int i = tid() + k * BT;
-        if (ok) ok = poll_word(a, mb + i, tag, w[k]);
         const float v = val_of(w[k]);
         dst[i] = v;
         if constexpr (NORM) {
@@ -389,7 +330,7 @@ __device__ __forceinline__ bool gather(const Args &a, int off, uint32_t tag, flo
     return S.fail == 0;
 }
 
-// Two rows of N words (row stride N in the mailbox and in dst) in one WORDS wait: both rows' words
+// Two rows of N words (row stride N in the mailbox and in dst) in one wait: both rows' words
 // of a thread in flight at once, so the second row costs no round trip of its own. Per row the
 // same values, order and norm partial sums (S.red[t * NW + wave]) as gather<>.
 template <int N, bool NORM, int D>
@@ -449,19 +390,13 @@ __device__ __forceinline__ bool gather_two_rows(const Args &a, int off, uint32_t
     return S.fail == 0;
 }
 
-// T rows of N words each (row stride N in the mailbox and in dst): two rows in one WORDS wait,
-// otherwise one row at a time.
-template <int T, int N, int CH, Wait WAIT, bool NORM = false, int D = 0>
+// T rows of N words each (row stride N in the mailbox and in dst), two rows in one wait.
+template <int T, int N, bool NORM = false, int D = 0>
 __device__ __forceinline__ bool gather_rows(const Args &a, int off, uint32_t tag, float *dst, Smem &S, NormW nw = {},
                                             float *xn = nullptr) {
-    if constexpr (T == 2 && WAIT == Wait::WORDS) {
-        return gather_two_rows<N, NORM, D>(a, off, tag, dst, S, nw, xn);
-    } else {
-        static_assert(T == 1 || T == 2, "one or two rows");
-        if (!gather<N, CH, WAIT, true, NORM, D>(a, off, tag, dst, S, nw, NORM ? xn : nullptr, 0)) return false;
-        if constexpr (T == 2) return gather<N, CH, WAIT, true, NORM>(a, off + N, tag, dst + N, S, nw, NORM ? xn + N : nullptr, NW);
-        return true;
-    }
+    static_assert(T == 1 || T == 2, "one or two rows");
+    if constexpr (T == 2) return gather_two_rows<N, NORM, D>(a, off, tag, dst, S, nw, xn);
+    else return gather<N, true, NORM, D>(a, off, tag, dst, S, nw, NORM ? xn : nullptr, 0);
 }
 
 // ---- RMSNorm of T rows (every block, redundantly) ---------------------------
@@ -879,7 +814,7 @@ __device__ bool talker_attention(const Args &a, const Ctx &cx, float qkw, int il
     if (r != 0) return true;
     // combine head h's NR partials in range order: out = sum_r o_r e^(m_r - M) / sum_r l_r e^(m_r - M)
     float *P = S.u.m.big;
-    if (!gather<NR * AP_W, AP_W, Wait::WORDS, false, false, D_AP>(a, MB_AP + h * NR * AP_W, tag_ap, P, S)) return false;
+    if (!gather<NR * AP_W, false, false, D_AP>(a, MB_AP + h * NR * AP_W, tag_ap, P, S)) return false;
     {
         // every thread combines dim tid % 128 (the two halves of the block identically) and
         // publishes it to half of the copies; lane k (mod 16) computes partial k's weight once,
@@ -1041,18 +976,18 @@ __device__ __forceinline__ bool run_layer(const Args &a, const Ctx &cx, Regs &R,
         if (!cp_attention<T>(a, qkw, (gi - a.n_tl) % a.n_cl, p0, t_qkv, t_att, S)) return false;
     }
     if (has_next && pf_late) load_qkv(R, N, next_cp);
-    if (!gather_rows<T, QD, HD, Wait::SENTINELS, false, D_ATT>(a, MB_ATT, t_att, S.u.m.big, S)) return false;
+    if (!gather_rows<T, QD, false, D_ATT>(a, MB_ATT, t_att, S.u.m.big, S)) return false;
     const uint32_t t_x2 = seq.next();
     o_phase<T>(a, R, S, t_x2);
     if (has_next) load_o(R, N, next_cp);
 
-    if (!gather_rows<T, H, H / NB, Wait::WORDS, true, D_X2>(a, MB_X2, t_x2, &S.x[0][0], S, normw(R.ln2), &S.xn[0][0])) return false;
+    if (!gather_rows<T, H, true, D_X2>(a, MB_X2, t_x2, &S.x[0][0], S, normw(R.ln2), &S.xn[0][0])) return false;
     norm_scale<T>(eps, sc, S);
     const uint32_t t_h = seq.next();
     gu_phase<T>(a, R, S, t_h, sc);
     if (has_next) load_gu(R, N, next_cp);
 
-    if (!gather_rows<T, FF, FF / NB, Wait::WORDS, false, D_H>(a, MB_H, t_h, S.u.m.big, S)) return false;
+    if (!gather_rows<T, FF, false, D_H>(a, MB_H, t_h, S.u.m.big, S)) return false;
     const uint32_t t_x = seq.next();
     down_phase<T>(a, R, S, t_x);
     if (has_next) load_dn(R, N, next_cp);
@@ -1063,7 +998,7 @@ __device__ __forceinline__ bool run_layer(const Args &a, const Ctx &cx, Regs &R,
 
     // R.ln1 holds the next layer's weights by now (load_qkv above); the last layer of the frame
     // is always next_final
-    return gather_rows<T, H, H / NB, Wait::WORDS, true, D_X>(a, MB_X, t_x, &S.x[0][0], S, next_final ? normw(R.fn) : normw(R.ln1),
+    return gather_rows<T, H, true, D_X>(a, MB_X, t_x, &S.x[0][0], S, next_final ? normw(R.fn) : normw(R.ln1),
                                            &S.xn[0][0]);
 }
 
@@ -1132,7 +1067,7 @@ __global__ void __launch_bounds__(BT, 1) k_frame(Args a, const Weights *__restri
             for (int r = 0; r < 3; ++r)
                 if (lane() < NREP) mb_put(a.mb + lane() * MB_WORDS + MB_LG + blk() * (VT / NB) + wave() * 3 + r, d[r] * hsc[0], t_lg);
         }
-        if (!gather<VT, VT / NB, Wait::WORDS, true, false, D_TLG>(a, MB_LG, t_lg, S.u.m.samp.lg, S)) return;
+        if (!gather<VT, true, false, D_TLG>(a, MB_LG, t_lg, S.u.m.samp.lg, S)) return;
         // the post-norm hidden the code predictor takes: each thread scales the elements it wrote
         // (and is the only one to read below), after the gather's barriers ended the head's reads
         for (int i = tid(); i < H; i += BT) S.xn[0][i] *= hsc[0];
@@ -1204,7 +1139,7 @@ __global__ void __launch_bounds__(BT, 1) k_frame(Args a, const Weights *__restri
             for (int r = 0; r < 2; ++r)
                 if (lane() < NREP) mb_put(a.mb + lane() * MB_WORDS + MB_LG + blk() * (VC / NB) + wave() * 2 + r, d[r] * hsc0, t_lg);
         }
-        if (!gather<VC, VC / NB, Wait::SENTINELS, true, false, D_CLG>(a, MB_LG, t_lg, S.u.m.samp.lg, S)) return;
+        if (!gather<VC, true, false, D_CLG>(a, MB_LG, t_lg, S.u.m.samp.lg, S)) return;
         if (a.tap_cp_logits && blk() == 0) {
             for (int i = tid(); i < VC; i += BT) gst(a.tap_cp_logits + (pos - 1) * VC + i, S.u.m.samp.lg[i]);
             __syncthreads();

@@ -24,7 +24,7 @@ def _stamps(n_tl=28, n_cl=5, step=10):
         att = b < 16
         n = n_tl * (5 + (3 if att else 0) + 8) + 4
         for p in range(15):
-            n += n_cl * ((3 if att else 0) + 2 * (2 if p == 0 else 1) + 6) + 4
+            n += n_cl * ((3 if att else 0) + 8) + 4
         n += 1
         P[b, :n] = 1000 + step * np.arange(n, dtype=np.uint64)
     return P
