@@ -15,9 +15,13 @@
 //    N = 1024 fills the 256 CUs. Split-K partials go to a workspace and are summed in a fixed
 //    order by the "finish" kernels, which also apply the epilogue (bias, SiLU, residual):
 //    deterministic results.
-//  * The prefill's layers: six launches each. q|k|v, o, gate|up and down are whole-K row
-//    projections (rows.h) with the input RMSNorm, SwiGLU and the residual add fused in; one
-//    kernel applies the q/k head norms + RoPE and stores K/V as f16; then the attention.
+//  * The prefill's layers: five launches each. q|k|v, o, gate|up and down are whole-K row
+//    projections (rows.h) with the input RMSNorm, SwiGLU and the residual add fused in; the q/k
+//    head norms + RoPE and the f16 K/V store run in the q|k|v projection's epilogue (above 64 rows)
+//    or inside the attention (up to 64 rows); then the attention. The
+//    projections read their operands in the MFMA tile layouts (rows.h pk_a / pk_w): a copy of
+//    every layer's weights tiled at create, and the residual stream, the attention output and the
+//    MLP hidden stored tiled by the kernels that write them.
 //  * Causal prefill attention: one block per (row, q head), scores over keys 0..row from the
 //    f16 cache, exactly as the frame's decode attention will later read them.
 #include "dev_common.h"
@@ -37,10 +41,6 @@ constexpr int BT = 256;                 // 4 wave64s
 constexpr int KC = 256;                 // K elements staged in LDS per step
 constexpr int LDA = KC + 8;             // padded LDS row (halves): rotates banks between rows
 constexpr int HD = 128;                 // head dim the norm/rope/attention kernels are built for
-// Row padding of the prompt activations the projections read (residual rows, attention output,
-// MLP hidden): row strides that are multiples of 4 KB put the 16 rows one MFMA operand load reads
-// on the same memory channels; 8 floats more per row made the row projections ~15-25 % faster.
-constexpr int ROW_PAD = 8;
 
 typedef _Float16 half8v __attribute__((ext_vector_type(8)));
 
@@ -210,50 +210,12 @@ __global__ void __launch_bounds__(BT) k_swiglu(const float *part, int S, int M, 
     }
 }
 
-// Row m of [q | k | v] (nq + 2 nkv heads of 128 in one row of the q|k|v projection): per-head
-// RMSNorm of q and k, rotate-half RoPE at position pos0 + m, q kept f32, k and v rounded to f16
-// into the cache (k_qk_norm_rope, talker.hip:46-82). One wave per head slice (q heads, then k,
-// then v; block (m, b) takes slices 4b .. 4b + 3), lane l holding dims l and l + 64: no LDS and no
-// barrier, so the launch is one load latency deep. The values are 0 + x, as the split-K sum of
-// one partial was, so a -0 partial is stored as +0 exactly as before.
-__global__ void __launch_bounds__(BT) k_qkv_finish(const float *qkv, int nq, int nkv, const float *qn, const float *kn,
-                                                   float eps, const float *invf, int pos0, float *q, uint16_t *kc,
-                                                   uint16_t *vc) {
-    const int m = blockIdx.x, pos = pos0 + m;
-    const int hh = blockIdx.y * (BT / WAVE) + (threadIdx.x >> 6), l = threadIdx.x & 63;
-    if (hh >= nq + 2 * nkv) return;
-    const int QD = nq * HD, KVD = nkv * HD, W = QD + 2 * KVD;
-    const float *hp = qkv + static_cast<size_t>(m) * W + hh * HD;
-    const float a0 = 0.f + gld(hp + l), a1 = 0.f + gld(hp + l + HD / 2);
-    if (hh >= nq + nkv) {
-        uint16_t *vd = vc + static_cast<size_t>(pos) * KVD + (hh - nq - nkv) * HD;
-        gst(vd + l, f2h(a0));
-        gst(vd + l + HD / 2, f2h(a1));
-        return;
-    }
-    float sn, cs;
-    sincosf(static_cast<float>(pos) * gld(invf + l), &sn, &cs);
-    const float *nw = hh < nq ? qn : kn;
-    const float sc = rsqrtf(wave_sum(fmaf(a0, a0, a1 * a1)) / static_cast<float>(HD) + eps);
-    const float x0 = a0 * sc * gld(nw + l), x1 = a1 * sc * gld(nw + l + HD / 2);
-    const float y0 = x0 * cs - x1 * sn;
-    const float y1 = x1 * cs + x0 * sn;
-    if (hh < nq) {
-        float *qd = q + static_cast<size_t>(m) * QD + hh * HD;
-        gst(qd + l, y0);
-        gst(qd + l + HD / 2, y1);
-    } else {
-        uint16_t *kd = kc + static_cast<size_t>(pos) * KVD + (hh - nq) * HD;
-        gst(kd + l, f2h(y0));
-        gst(kd + l + HD / 2, f2h(y1));
-    }
-}
-
 // Causal GQA attention of row m for the two q heads of kv group g over keys 0..pos0 + m of the
 // f16 cache (k_prefill_attention, talker.hip:88-117). 256 threads. Scores: one key per thread
 // (its 256-byte K row loaded at once, dotted with both q heads). V: each wave sums every 4th key
 // for both heads (a lane owns 2 dims), eight keys' loads in flight, then the four waves'
-// partial sums are added in wave order.
+// partial sums are added in wave order. The output row goes to `out` in the tile layout of width
+// ldo (rows.h pk_a), the layout the o projection reads.
 __global__ void __launch_bounds__(BT) k_attn_prefill(const float *q, const uint16_t *kc, const uint16_t *vc, int nq,
                                                      int nkv, int pos0, float scale, float *out, int ldo) {
     extern __shared__ float sc[];                        // [2][n] scores, then probabilities
@@ -336,7 +298,7 @@ __global__ void __launch_bounds__(BT) k_attn_prefill(const float *q, const uint1
     __syncthreads();
     const int hh = threadIdx.x >> 7, d = threadIdx.x & (HD - 1);
     const float acc = part[0][hh][d] + part[1][hh][d] + part[2][hh][d] + part[3][hh][d];
-    gst(out + static_cast<size_t>(m) * ldo + (g * 2 + hh) * HD + d, acc / (hh ? s1 : s0));
+    gst(out + rows::pk_a(m, (g * 2 + hh) * HD + d, ldo), acc / (hh ? s1 : s0));
 }
 
 // k_attn_prefill for rows with at most SHORT_KEYS keys (prompts of up to 256 rows). Wave w takes
@@ -349,12 +311,12 @@ __global__ void __launch_bounds__(BT) k_attn_prefill(const float *q, const uint1
 // otherwise (a per-group exit in the unrolled loops of the longer rows measured slower).
 constexpr int SHORT_KEYS = 256;
 // FUSED (prompts of up to FUSED_ROWS rows from position 0; FEW): the q/k head norms, RoPE and the
-// f16 K/V store of k_qkv_finish are folded in, one launch fewer per layer. The block of row m
-// forms, from the raw q|k|v rows of the projection (`raw`, [rows][nq + 2 nkv heads] f32), its two
-// q heads and the normed, rotated f16 keys and the f16 values 0..m of kv group g in LDS, one wave
-// per head row with k_qkv_finish's arithmetic (lane l holding dims l and l + 64, the values
-// 0 + x), so q, K and V carry that pass's bits, and it stores K/V row m into the cache; the
-// attention then reads its keys and values from LDS instead of the cache. Same outputs, bit for bit.
+// f16 K/V store are folded in (k_qk_norm_rope, talker.hip:46-82). The block of row m forms, from
+// the raw q|k|v rows of the projection (`raw`, [rows][nq + 2 nkv heads] f32), its two q heads and
+// the normed, rotated f16 keys and the f16 values 0..m of kv group g in LDS, one wave per head row
+// with the arithmetic of the EPI_QKV epilogue (rows.h: lane l holding dims l and l + 64, the values
+// 0 + x), and it stores K/V row m into the cache; the attention then reads its keys and values from
+// LDS instead of the cache.
 constexpr int FUSED_ROWS = 64;
 struct HeadNorm {
     const float *raw, *qn, *kn, *invf;
@@ -508,7 +470,7 @@ __global__ void __launch_bounds__(BT) k_attn_prefill_short(const float *q, uint1
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) acc += opart[w][rr][hh][d];
     const float sum = red[hh][0] + red[hh][1] + red[hh][2] + red[hh][3];
-    gst(out + static_cast<size_t>(m) * ldo + (g * 2 + hh) * HD + d, acc / sum);
+    gst(out + rows::pk_a(m, (g * 2 + hh) * HD + d, ldo), acc / sum);
 }
 
 // rows[t] = table[ids[t]] (f16 -> f32), k_gather_rows (talker.hip:20-25).
@@ -610,7 +572,44 @@ __global__ void k_clear_word(uint32_t *w) {
 struct LayerW {
     const float *ln1, *ln2, *qn, *kn;
     const uint16_t *wq, *wk, *wv, *wo, *wg, *wu, *wd;
+    uint16_t *qkv_t, *o_t, *gu_t, *d_t;   // the tiled copies: [q; k; v], o, [gate; up], down
 };
+
+// dst (tile layout, rows.h pk_w) = rows [0, n) of the row-major f16 matrix src [n][K]: one thread
+// per 16-byte lane slot (8 halves of one weight row).
+__global__ void __launch_bounds__(BT) k_tile_w(const uint16_t *src, int n, int K, uint16_t *dst) {
+    const size_t i = static_cast<size_t>(blockIdx.x) * BT + threadIdx.x, slots = static_cast<size_t>(n) * K / 8;
+    if (i >= slots) return;
+    const int ln = static_cast<int>(i & 63), steps = K / 32;
+    const size_t tile = i / 64;
+    const int row = static_cast<int>(tile / steps) * 16 + (ln & 15), k = static_cast<int>(tile % steps) * 32 + 8 * (ln >> 4);
+    *reinterpret_cast<u32x4_t *>(dst + i * 8) = *reinterpret_cast<const u32x4_t *>(src + static_cast<size_t>(row) * K + k);
+}
+
+// x (tile layout of width H) = the T prompt rows src [T][H]: one thread per 4 floats.
+__global__ void __launch_bounds__(BT) k_tile_rows(const float *src, int T, int H, float *x) {
+    const int i = blockIdx.x * BT + threadIdx.x, m = i / (H / 4), k = 4 * (i % (H / 4));
+    if (m >= T) return;
+    st4(x + rows::pk_a(m, k, H), ld4(src + static_cast<size_t>(m) * H + k));
+}
+
+// xn = RMSNorm(row m of the tiled residual stream x) * w: k_resid_norm's arithmetic for one row
+// (thread i holds elements 4i .. 4i + 3, the same sum order), reading x in the tile layout.
+__global__ void __launch_bounds__(BT) k_tiled_row_norm(const float *x, int m, const float *w, float eps, float *xn, int H) {
+    __shared__ float red[4];
+    const int i = threadIdx.x * 4;                            // H == 4 * BT
+    const f32x4_t v = ld4(x + rows::pk_a(m, i, H));
+    const f32x4_t wv = ld4(w + i);
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) ss = fmaf(v[j], v[j], ss);
+    ss = block_sum256(ss, red);
+    const float scale = rsqrtf(ss / static_cast<float>(H) + eps);
+    f32x4_t o;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) o[j] = v[j] * scale * wv[j];
+    st4(xn + i, o);
+}
 
 } // namespace pf
 } // namespace navi_amd
@@ -629,12 +628,13 @@ struct navi_talker {
     const uint16_t *text_emb = nullptr, *codec_emb = nullptr, *fc1 = nullptr, *fc2 = nullptr, *head = nullptr;
     const float *fc1_b = nullptr, *fc2_b = nullptr, *final_norm = nullptr;
     std::vector<LayerW> layers;
+    uint16_t *tiled = nullptr;         // every layer's tiled weight copies, one allocation
     // cache
     std::vector<uint16_t *> kk, vv;
     int n_used = 0;
     // work buffers
+    // x (the residual stream), att and h in the tile layout (rows.h pk_a), the rest row-major
     float *x = nullptr, *xn = nullptr, *q = nullptr, *att = nullptr, *h = nullptr, *part = nullptr, *invf = nullptr;
-    int lx = 0, la = 0, lf = 0;    // row strides of x, att and h (ROW_PAD floats past the row)
     size_t part_floats = 0;
     uint32_t *flag = nullptr;
     int32_t *d_ids = nullptr, *d_cids = nullptr, *d_ia = nullptr, *d_ib = nullptr, *d_ta = nullptr, *d_tb = nullptr;
@@ -774,14 +774,15 @@ navi_status navi_talker_create(const navi_model_params *p, const navi_tensor_ref
     do {                                                                         \
         if ((st = t->alloc(ptr, (n), err, errlen)) != NAVI_OK) return fail(st);  \
     } while (0)
-    t->lx = t->H + ROW_PAD;
-    t->la = t->QD + ROW_PAD;
-    t->lf = t->F + ROW_PAD;
-    TALLOC(t->x, M * t->lx);
+    const size_t MT16 = (M + 15) / 16 * 16;     // x, att and h (tile layout) hold whole 16-row tiles
+    TALLOC(t->x, MT16 * t->H);
     TALLOC(t->xn, M * t->H);
     TALLOC(t->q, M * t->QD);
-    TALLOC(t->att, M * t->la);
-    TALLOC(t->h, M * t->lf);
+    TALLOC(t->att, MT16 * t->QD);
+    TALLOC(t->h, MT16 * t->F);
+    const size_t per_layer = static_cast<size_t>(t->QD + 2 * t->KVD) * t->H + static_cast<size_t>(t->H) * t->QD +
+                             static_cast<size_t>(2 * t->F) * t->H + static_cast<size_t>(t->H) * t->F;
+    TALLOC(t->tiled, per_layer * t->L);
     TALLOC(t->part, t->part_floats);
     TALLOC(t->invf, HD / 2);
     TALLOC(t->flag, 1);
@@ -805,6 +806,33 @@ navi_status navi_talker_create(const navi_model_params *p, const navi_tensor_ref
     float invf[HD / 2];
     for (int i = 0; i < HD / 2; ++i) invf[i] = static_cast<float>(1.0 / std::pow(x.rope_theta, (2.0 * i) / HD));
     hipStream_t s = device_state().stream;
+    {
+        // the tiled copies of the layer weights the prefill's projections read
+        auto tile = [&](const uint16_t *src, int n, int K, uint16_t *dst) {
+            const size_t slots = static_cast<size_t>(n) * K / 8;
+            hipLaunchKernelGGL(k_tile_w, dim3(static_cast<unsigned>((slots + BT - 1) / BT)), dim3(BT), 0, s, src, n, K, dst);
+        };
+        uint16_t *p = t->tiled;
+        const size_t q_el = static_cast<size_t>(t->QD) * t->H, kv_el = static_cast<size_t>(t->KVD) * t->H,
+                     f_el = static_cast<size_t>(t->F) * t->H;
+        for (LayerW &w : t->layers) {
+            w.qkv_t = p;
+            tile(w.wq, t->QD, t->H, p);
+            tile(w.wk, t->KVD, t->H, p + q_el);
+            tile(w.wv, t->KVD, t->H, p + q_el + kv_el);
+            p += q_el + 2 * kv_el;
+            w.o_t = p;
+            tile(w.wo, t->H, t->QD, p);
+            p += static_cast<size_t>(t->H) * t->QD;
+            w.gu_t = p;
+            tile(w.wg, t->F, t->H, p);
+            tile(w.wu, t->F, t->H, p + f_el);
+            p += 2 * f_el;
+            w.d_t = p;
+            tile(w.wd, t->H, t->F, p);
+            p += static_cast<size_t>(t->H) * t->F;
+        }
+    }
     if (hipMemcpyAsync(t->invf, invf, sizeof invf, hipMemcpyHostToDevice, s) != hipSuccess ||
         hipEventCreate(&t->ev0) != hipSuccess || hipEventCreate(&t->ev1) != hipSuccess || hipStreamSynchronize(s) != hipSuccess) {
         set_err(err, errlen, "talker: HIP setup failed");
@@ -919,45 +947,47 @@ navi_status navi_talker_build_prompt(navi_talker *t, const int32_t *ids, int32_t
 
 namespace {
 
-// The prefill's kernels for T rows already in t.x: six launches per layer (q|k|v with the RMSNorm
-// fused -> q/k norms + RoPE + K/V store -> attention -> o (+ residual) -> gate|up with the RMSNorm
-// and SwiGLU fused -> down (+ residual); every projection one whole-K MFMA kernel, rows.h), then
-// the last row's final RMSNorm (the post-norm hidden the frame takes) and the codec head.
-void prefill_layers(navi_talker &t, int T, hipStream_t s) {
+// The prefill's kernels for T rows already in t.x (tile layout): five launches per layer (q|k|v
+// with the RMSNorm fused, and above 64 rows the q/k norms + RoPE + K/V store in its epilogue ->
+// attention (up to 64 rows with the norms, RoPE and K/V store) -> o (+ residual) -> gate|up with
+// the RMSNorm and SwiGLU fused -> down (+ residual); every projection one whole-K MFMA kernel on
+// the tiled operands, rows.h), then the last row's final RMSNorm (the post-norm hidden the frame
+// takes) and the codec head. false: a projection shape the tiled kernels do not take (nothing
+// after it was launched).
+bool prefill_layers(navi_talker &t, int T, hipStream_t s) {
     const int H = t.H, QKVW = t.QD + 2 * t.KVD;
     const float scale = 1.f / std::sqrt(static_cast<float>(HD));
     const size_t att_lds = static_cast<size_t>(2) * T * sizeof(float);
     for (int l = 0; l < t.L; ++l) {
         const LayerW &w = t.layers[l];
-        rows::launch_rows(rows::EPI_PLAIN, true, t.x, t.lx, T, H, w.ln1, t.eps, w.wq, t.QD, w.wk, t.KVD, w.wv, t.KVD, t.part,
-                          QKVW, t.flag, s);
         if (T <= FUSED_ROWS) {         // the q/k norms, RoPE and K/V store inside the attention
+            if (!rows::launch_rows_pk(rows::EPI_PLAIN, true, t.x, T, H, w.ln1, t.eps, w.qkv_t, QKVW, t.part, QKVW, t.flag, s))
+                return false;
             hipLaunchKernelGGL((k_attn_prefill_short<true, true>), dim3(T, t.NKV), dim3(BT), 0, s, nullptr, t.kk[l],
-                               t.vv[l], t.NQ, t.NKV, 0, scale, t.att, t.la, HeadNorm{t.part, w.qn, w.kn, t.invf, t.eps});
-        } else {
-            hipLaunchKernelGGL(k_qkv_finish, dim3(T, (t.NQ + 2 * t.NKV + BT / WAVE - 1) / (BT / WAVE)), dim3(BT), 0, s,
-                               t.part, t.NQ, t.NKV, w.qn, w.kn, t.eps, t.invf, 0, t.q, t.kk[l], t.vv[l]);
+                               t.vv[l], t.NQ, t.NKV, 0, scale, t.att, t.QD, HeadNorm{t.part, w.qn, w.kn, t.invf, t.eps});
+        } else {                       // ... or in the q|k|v projection's epilogue
+            const rows::HeadOut ho{w.qn, w.kn, t.invf, t.q, t.kk[l], t.vv[l], t.NQ, t.NKV, 0};
+            if (!rows::launch_rows_pk(rows::EPI_QKV, true, t.x, T, H, w.ln1, t.eps, w.qkv_t, QKVW, nullptr, 0, t.flag, s, ho))
+                return false;
             if (T <= SHORT_KEYS)
                 hipLaunchKernelGGL(T <= SHORT_KEYS / (BT / WAVE) ? k_attn_prefill_short<true> : k_attn_prefill_short<false>,
                                    dim3(T, t.NKV), dim3(BT), 0, s, t.q, t.kk[l], t.vv[l], t.NQ, t.NKV, 0, scale, t.att,
-                                   t.la, HeadNorm{});
+                                   t.QD, HeadNorm{});
             else
                 hipLaunchKernelGGL(k_attn_prefill, dim3(T, t.NKV), dim3(BT), att_lds, s, t.q, t.kk[l], t.vv[l], t.NQ,
-                                   t.NKV, 0, scale, t.att, t.la);
+                                   t.NKV, 0, scale, t.att, t.QD);
         }
-        rows::launch_rows(rows::EPI_RESID, false, t.att, t.la, T, t.QD, nullptr, 0.f, w.wo, H, nullptr, 0, nullptr, 0, t.x,
-                          t.lx, t.flag, s);
-        rows::launch_rows(rows::EPI_SWIGLU, true, t.x, t.lx, T, H, w.ln2, t.eps, w.wg, t.F, w.wu, t.F, nullptr, 0, t.h, t.lf,
-                          t.flag, s);
-        rows::launch_rows(rows::EPI_RESID, false, t.h, t.lf, T, t.F, nullptr, 0.f, w.wd, H, nullptr, 0, nullptr, 0, t.x, t.lx,
-                          t.flag, s);
+        if (!rows::launch_rows_pk(rows::EPI_RESID, false, t.att, T, t.QD, nullptr, 0.f, w.o_t, H, t.x, 0, t.flag, s) ||
+            !rows::launch_rows_pk(rows::EPI_SWIGLU, true, t.x, T, H, w.ln2, t.eps, w.gu_t, t.F, t.h, 0, t.flag, s) ||
+            !rows::launch_rows_pk(rows::EPI_RESID, false, t.h, T, t.F, nullptr, 0.f, w.d_t, H, t.x, 0, t.flag, s))
+            return false;
     }
     // the last row: final RMSNorm (the post-norm hidden the frame takes), then the codec head
     float *last = t.xn + static_cast<size_t>(T - 1) * H;
-    hipLaunchKernelGGL(k_resid_norm, dim3(1), dim3(BT), 0, s, nullptr, 0, t.x + static_cast<size_t>(T - 1) * t.lx,
-                       t.x + static_cast<size_t>(T - 1) * t.lx, t.final_norm, t.eps, last, 1, H);
+    hipLaunchKernelGGL(k_tiled_row_norm, dim3(1), dim3(BT), 0, s, t.x, T - 1, t.final_norm, t.eps, last, H);
     rows::launch_rows(rows::EPI_PLAIN, false, last, H, 1, H, nullptr, 0.f, t.head, t.V, nullptr, 0, nullptr, 0, t.logits, t.V,
                       t.flag, s);
+    return true;
 }
 
 } // namespace
@@ -977,8 +1007,7 @@ navi_status navi_talker_prefill(navi_talker *t, const float *d_rows, int32_t n_r
     hipStream_t s = device_state().stream;
     NAVI_TRY_HIP(hipMemsetAsync(t->flag, 0, 4, s), err, errlen);
     NAVI_TRY_HIP(hipEventRecord(t->ev0, s), err, errlen);
-    NAVI_TRY_HIP(hipMemcpy2DAsync(t->x, static_cast<size_t>(t->lx) * sizeof(float), d_rows, static_cast<size_t>(H) * sizeof(float),
-                                  static_cast<size_t>(H) * sizeof(float), T, hipMemcpyDeviceToDevice, s), err, errlen);
+    hipLaunchKernelGGL(k_tile_rows, dim3((T * (H / 4) + BT - 1) / BT), dim3(BT), 0, s, d_rows, T, H, t->x);
     // The layers and the head: a launch sequence that depends only on T (every buffer is the
     // handle's), so it can be captured once per row count as a HIP graph and replayed
     // (navi_talker_set_graphs; off by default, measured no faster than host launches).
@@ -988,17 +1017,23 @@ navi_status navi_talker_prefill(navi_talker *t, const float *d_rows, int32_t n_r
             if (g.first == T) ex = g.second;
         if (!ex) {
             NAVI_TRY_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal), err, errlen);
-            prefill_layers(*t, T, s);
+            const bool ok = prefill_layers(*t, T, s);
             hipGraph_t graph = nullptr;
             NAVI_TRY_HIP(hipStreamEndCapture(s, &graph), err, errlen);
+            if (!ok) {
+                (void) hipGraphDestroy(graph);
+                set_err(err, errlen, "talker: a projection shape the prefill's tiled kernels do not take");
+                return NAVI_ERR_UNSUPPORTED;
+            }
             const hipError_t ei = hipGraphInstantiateWithFlags(&ex, graph, 0);
             (void) hipGraphDestroy(graph);
             NAVI_TRY_HIP(ei, err, errlen);
             t->graphs.push_back({T, ex});
         }
         NAVI_TRY_HIP(hipGraphLaunch(ex, s), err, errlen);
-    } else {
-        prefill_layers(*t, T, s);
+    } else if (!prefill_layers(*t, T, s)) {
+        set_err(err, errlen, "talker: a projection shape the prefill's tiled kernels do not take");
+        return NAVI_ERR_UNSUPPORTED;
     }
     NAVI_TRY_HIP(hipMemcpyAsync(t->hidden, t->xn + static_cast<size_t>(T - 1) * H, H * 4, hipMemcpyDeviceToDevice, s), err,
                  errlen);
