@@ -575,24 +575,6 @@ struct LayerW {
     uint16_t *qkv_t, *o_t, *gu_t, *d_t;   // the tiled copies: [q; k; v], o, [gate; up], down
 };
 
-// dst (tile layout, rows.h pk_w) = rows [0, n) of the row-major f16 matrix src [n][K]: one thread
-// per 16-byte lane slot (8 halves of one weight row).
-__global__ void __launch_bounds__(BT) k_tile_w(const uint16_t *src, int n, int K, uint16_t *dst) {
-    const size_t i = static_cast<size_t>(blockIdx.x) * BT + threadIdx.x, slots = static_cast<size_t>(n) * K / 8;
-    if (i >= slots) return;
-    const int ln = static_cast<int>(i & 63), steps = K / 32;
-    const size_t tile = i / 64;
-    const int row = static_cast<int>(tile / steps) * 16 + (ln & 15), k = static_cast<int>(tile % steps) * 32 + 8 * (ln >> 4);
-    *reinterpret_cast<u32x4_t *>(dst + i * 8) = *reinterpret_cast<const u32x4_t *>(src + static_cast<size_t>(row) * K + k);
-}
-
-// x (tile layout of width H) = the T prompt rows src [T][H]: one thread per 4 floats.
-__global__ void __launch_bounds__(BT) k_tile_rows(const float *src, int T, int H, float *x) {
-    const int i = blockIdx.x * BT + threadIdx.x, m = i / (H / 4), k = 4 * (i % (H / 4));
-    if (m >= T) return;
-    st4(x + rows::pk_a(m, k, H), ld4(src + static_cast<size_t>(m) * H + k));
-}
-
 // xn = RMSNorm(row m of the tiled residual stream x) * w: k_resid_norm's arithmetic for one row
 // (thread i holds elements 4i .. 4i + 3, the same sum order), reading x in the tile layout.
 __global__ void __launch_bounds__(BT) k_tiled_row_norm(const float *x, int m, const float *w, float eps, float *xn, int H) {
@@ -808,10 +790,7 @@ navi_status navi_talker_create(const navi_model_params *p, const navi_tensor_ref
     hipStream_t s = device_state().stream;
     {
         // the tiled copies of the layer weights the prefill's projections read
-        auto tile = [&](const uint16_t *src, int n, int K, uint16_t *dst) {
-            const size_t slots = static_cast<size_t>(n) * K / 8;
-            hipLaunchKernelGGL(k_tile_w, dim3(static_cast<unsigned>((slots + BT - 1) / BT)), dim3(BT), 0, s, src, n, K, dst);
-        };
+        auto tile = [&](const uint16_t *src, int n, int K, uint16_t *dst) { rows::tile_weights(src, n, K, dst, s); };
         uint16_t *p = t->tiled;
         const size_t q_el = static_cast<size_t>(t->QD) * t->H, kv_el = static_cast<size_t>(t->KVD) * t->H,
                      f_el = static_cast<size_t>(t->F) * t->H;
@@ -1007,7 +986,7 @@ navi_status navi_talker_prefill(navi_talker *t, const float *d_rows, int32_t n_r
     hipStream_t s = device_state().stream;
     NAVI_TRY_HIP(hipMemsetAsync(t->flag, 0, 4, s), err, errlen);
     NAVI_TRY_HIP(hipEventRecord(t->ev0, s), err, errlen);
-    hipLaunchKernelGGL(k_tile_rows, dim3((T * (H / 4) + BT - 1) / BT), dim3(BT), 0, s, d_rows, T, H, t->x);
+    rows::tile_rows(d_rows, T, H, t->x, s);
     // The layers and the head: a launch sequence that depends only on T (every buffer is the
     // handle's), so it can be captured once per row count as a HIP graph and replayed
     // (navi_talker_set_graphs; off by default, measured no faster than host launches).

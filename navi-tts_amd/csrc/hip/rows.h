@@ -43,6 +43,7 @@ struct RowArgs {
     const float *rs;                  // RESID: per-column scale of the added product (a layer scale), or null
     int ypk;                          // packed kernels: y's width for a SWIGLU / RESID output in the tile layout
     HeadOut ho;                       // EPI_QKV
+    int ars = 1, aoff = 0;            // packed kernels: row m of the product reads row m * ars + aoff of A
 };
 
 // Tile layouts of the packed kernels (the prompt prefill): every operand load of a wave is one
@@ -118,7 +119,9 @@ __global__ void __launch_bounds__(NWV * WAVE) k_rows(RowArgs a) {
             for (int i = 0; i < MT; ++i) {
                 const int m = m0 + 16 * i + c;
                 if (PK && m < a.M) {
-                    const NAVI_GLOBAL f32x4_t *p = (const NAVI_GLOBAL f32x4_t *) (a.a + (static_cast<size_t>((m0 >> 4) + i) * (K / 32) + w * KS + st) * 512 + l * 4);
+                    // lanes of a 16-row tile read one contiguous 1 KB when ars == 1 and aoff == 0
+                    const int r = m * a.ars + a.aoff;
+                    const NAVI_GLOBAL f32x4_t *p = (const NAVI_GLOBAL f32x4_t *) (a.a + (static_cast<size_t>(r >> 4) * (K / 32) + w * KS + st) * 512 + ((r & 15) + 16 * kq) * 4);
                     av[st][i][0] = p[0];
                     av[st][i][1] = p[64];
                 } else if (m < a.M) {
@@ -335,6 +338,32 @@ void launch_rows(int epi, bool norm, const float *A, int lda, int M, int K, cons
     }
 }
 
+// dst (tile layout pk_w) = the row-major f16 matrix src [n][K]: one thread per 16-byte lane slot.
+__global__ void __launch_bounds__(256) k_tile_w(const uint16_t *src, int n, int K, uint16_t *dst) {
+    const size_t i = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x, slots = static_cast<size_t>(n) * K / 8;
+    if (i >= slots) return;
+    const int ln = static_cast<int>(i & 63), steps = K / 32;
+    const size_t tile = i / 64;
+    const int row = static_cast<int>(tile / steps) * 16 + (ln & 15), k = static_cast<int>(tile % steps) * 32 + 8 * (ln >> 4);
+    *reinterpret_cast<u32x4_t *>(dst + i * 8) = *reinterpret_cast<const u32x4_t *>(src + static_cast<size_t>(row) * K + k);
+}
+
+void tile_weights(const uint16_t *src, int n, int K, uint16_t *dst, hipStream_t s) {
+    const size_t slots = static_cast<size_t>(n) * K / 8;
+    hipLaunchKernelGGL(k_tile_w, dim3(static_cast<unsigned>((slots + 255) / 256)), dim3(256), 0, s, src, n, K, dst);
+}
+
+// x (tile layout pk_a of width H) = the rows src [T][H]: one thread per 4 floats.
+__global__ void __launch_bounds__(256) k_tile_rows(const float *src, int T, int H, float *x) {
+    const int i = blockIdx.x * 256 + threadIdx.x, m = i / (H / 4), k = 4 * (i % (H / 4));
+    if (m >= T) return;
+    *(NAVI_GLOBAL f32x4_t *) (x + pk_a(m, k, H)) = *(const NAVI_GLOBAL f32x4_t *) (src + static_cast<size_t>(m) * H + k);
+}
+
+void tile_rows(const float *src, int T, int H, float *x, hipStream_t s) {
+    hipLaunchKernelGGL(k_tile_rows, dim3((T * (H / 4) + 255) / 256), dim3(256), 0, s, src, T, H, x);
+}
+
 template <int MT, int EPI, bool NORM, int NWV, int KS, int CG>
 void launch_pk(int M, int N, const RowArgs &ra, hipStream_t s) {
     const dim3 grid(N / (16 * CG), (M + 16 * MT - 1) / (16 * MT));
@@ -352,31 +381,29 @@ void launch_pk(int M, int N, const RowArgs &ra, hipStream_t s) {
 // EPI_QKV (above 64 rows, talker heads of 128 with ho): the q|k|v projection with the head norms,
 // RoPE and the K/V store in its epilogue; y is not written.
 bool launch_rows_pk(int epi, bool norm, const float *A, int M, int K, const float *ln, float eps, const uint16_t *w, int N,
-                    float *y, int ldy, uint32_t *flag, hipStream_t s, const HeadOut &ho = {}) {
+                    float *y, int ldy, uint32_t *flag, hipStream_t s, const HeadOut &ho = {}, int ars = 1, int aoff = 0) {
     const int F = epi == EPI_SWIGLU ? N : 0;
     const RowArgs ra{A, ln, w, nullptr, nullptr, y, flag, 0, M, K, epi == EPI_SWIGLU ? 2 * N : N, epi == EPI_SWIGLU ? 2 * N : N,
-                     F, ldy, eps, nullptr, N, ho};
-    if (M < 1 || N % 128 != 0 || (epi == EPI_SWIGLU && !norm)) return false;
+                     F, ldy, eps, nullptr, N, ho, ars, aoff};
+    if (M < 1 || N % 128 != 0 || (epi == EPI_SWIGLU && !norm) || ars < 1 || aoff < 0) return false;
     const bool wide = M > 64;
-    const int mt = M <= 16 ? 1 : M <= 32 ? 2 : M <= 48 ? 3 : 4;
     if (epi == EPI_QKV) {
         if (!wide || !norm || K != 1024 || N != 128 * (ho.nq + 2 * ho.nkv)) return false;
         launch_pk<1, EPI_QKV, true, 8, 4, 8>(M, N, ra, s);
         return true;
     }
+    // up to 64 rows: 16-row tiles up to 32 rows (faster than 32-row tiles there), 32-row tiles for
+    // q|k|v and a whole-M tile for gate|up above (the sweep's best at 64 rows)
     if (epi == EPI_PLAIN && norm && K == 1024) {
         if (wide) launch_pk<1, EPI_PLAIN, true, 8, 4, 8>(M, N, ra, s);
-        else if (mt == 1) launch_pk<1, EPI_PLAIN, true, 8, 4, 1>(M, N, ra, s);
-        else if (mt == 2) launch_pk<2, EPI_PLAIN, true, 8, 4, 1>(M, N, ra, s);
-        else if (mt == 3) launch_pk<3, EPI_PLAIN, true, 8, 4, 1>(M, N, ra, s);
-        else launch_pk<4, EPI_PLAIN, true, 8, 4, 1>(M, N, ra, s);
+        else if (M <= 32) launch_pk<1, EPI_PLAIN, true, 8, 4, 1>(M, N, ra, s);
+        else launch_pk<2, EPI_PLAIN, true, 8, 4, 1>(M, N, ra, s);
         return true;
     }
     if (epi == EPI_SWIGLU && K == 1024) {
         if (wide) launch_pk<1, EPI_SWIGLU, true, 8, 4, 4>(M, N, ra, s);
-        else if (mt == 1) launch_pk<1, EPI_SWIGLU, true, 8, 4, 1>(M, N, ra, s);
-        else if (mt == 2) launch_pk<2, EPI_SWIGLU, true, 8, 4, 1>(M, N, ra, s);
-        else if (mt == 3) launch_pk<3, EPI_SWIGLU, true, 8, 4, 1>(M, N, ra, s);
+        else if (M <= 32) launch_pk<1, EPI_SWIGLU, true, 8, 4, 1>(M, N, ra, s);
+        else if (M <= 48) launch_pk<3, EPI_SWIGLU, true, 8, 4, 1>(M, N, ra, s);
         else launch_pk<4, EPI_SWIGLU, true, 8, 4, 1>(M, N, ra, s);
         return true;
     }

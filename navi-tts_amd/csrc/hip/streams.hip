@@ -9,9 +9,12 @@
 //
 //  * Projections: the whole-K MFMA row kernels of rows.h (activations as f16 hi + lo pairs, f16
 //    weights) with M = n streams (code-predictor positions 0 and 1: 2n rows), the RMSNorm, SwiGLU
-//    and residual add fused in. Every weight byte streams from HBM once per step for all streams
-//    (twice for the residual projections above 16 rows), so the weights cost ~3.3 GB per step
-//    whatever n. The step (582 launches) is captured once as a HIP graph and replayed.
+//    and residual add fused in, on the MFMA tile layouts (rows.h pk_a / pk_w: a tiled copy of the
+//    weights made at create; the residual stream, attention output and MLP hidden stored tiled), so
+//    every operand load of a wave is one contiguous 1 KB. Every weight byte streams from HBM once
+//    per step for all streams (twice for the residual projections above 16 rows), so the weights
+//    cost ~3.3 GB per step whatever n. The step (582 launches) is captured once as a HIP graph and
+//    replayed.
 //  * Talker attention: split-KV decode attention, one block per (stream, kv head, key range), with
 //    the q/k head norms, RoPE and the step's f16 K/V store folded in (the range holding the new key
 //    stores it); the two q heads of a GQA group share the K/V loads (16 lanes per key for the
@@ -42,11 +45,6 @@ constexpr int HD = 128, NCB = 16, CPH = NCB - 1;
 constexpr int MAX_TL = 32, MAX_CL = 8;
 constexpr int KPS = 256;               // keys per attention split (one per thread)
 constexpr float ATT_SCALE = 0.08838834764831845f;   // 1/sqrt(128)
-// Row padding of the activations the projections read (residual stream, attention output, MLP
-// hidden): with row strides that are multiples of 4 KB (1024, 2048, 3072 floats) the 16 rows one
-// MFMA operand load reads fall on the same memory channels; 8 floats more per row made the
-// 32-row projections 20-25 % faster on MI355X (7.6 -> 6.1 us for q|k|v, 10.7 -> 8.7 us for down).
-constexpr int ROW_PAD = 8;
 
 // Per-stream state the kernels read: position, frame index, seeds, cache pointers.
 struct StreamMeta {
@@ -232,9 +230,10 @@ __global__ void __launch_bounds__(BT) k_st_attn(const float *part, const StreamM
     }
 }
 
-// att[m][(2g + h) * HD + d] = sum_s o_s e^(m_s - M) / sum_s l_s e^(m_s - M) over the key ranges.
+// att[m][(2g + h) * HD + d] = sum_s o_s e^(m_s - M) / sum_s l_s e^(m_s - M) over the key ranges
+// (att in the tile layout of width nq * HD).
 __global__ void __launch_bounds__(BT) k_st_attn_combine(const float *part, const StreamMeta *meta, int nq, int nkv, int splits,
-                                                        float *att, int lda) {
+                                                        float *att) {
     const int m = blockIdx.x, g = blockIdx.y, hh = threadIdx.x >> 7, d = threadIdx.x & (HD - 1);
     const int used = (meta[m].n_past + 1 + KPS - 1) / KPS;
     const float *p = part + (static_cast<size_t>(m) * nkv + g) * splits * 2 * (HD + 2) + hh * (HD + 2);
@@ -286,7 +285,7 @@ __global__ void __launch_bounds__(BT) k_st_attn_combine(const float *part, const
                 num = fmaf(ob[s], w, num);
             }
     }
-    gst(att + static_cast<size_t>(m) * lda + (g * 2 + hh) * HD + d, num / den);
+    gst(att + pk_a(m, (g * 2 + hh) * HD + d, nq * HD), num / den);
 }
 
 // ---- code predictor: norms + RoPE + K/V store + attention, per (stream, kv head) -----------
@@ -304,7 +303,7 @@ __global__ void __launch_bounds__(BT) k_st_attn_combine(const float *part, const
 // weight 0), even and odd keys in two chains.
 __global__ void __launch_bounds__(BT) k_st_cp_attn(const float *part, int T, int p0, int nq, int nkv, const float *qn,
                                                    const float *kn, float eps, const float *invf, int layer, int n_layer,
-                                                   uint16_t *cpk, uint16_t *cpv, float *att, int lda) {
+                                                   uint16_t *cpk, uint16_t *cpv, float *att) {
     __shared__ __align__(16) float lq[NW][HD], lk[NW][2][HD], lv[NW][2][HD];
     const int m = blockIdx.x, g = blockIdx.y, w = threadIdx.x >> 6, l = threadIdx.x & 63;
     if (w >= 2 * T) return;
@@ -420,7 +419,7 @@ __global__ void __launch_bounds__(BT) k_st_cp_attn(const float *part, int T, int
         q0 = fmaf(pb, b0, q0);
         q1 = fmaf(pb, b1, q1);
     }
-    float *dst = att + static_cast<size_t>(m * T + t) * lda + (g * 2 + hh) * HD + 2 * l;
+    float *dst = att + pk_a(m * T + t, (g * 2 + hh) * HD + 2 * l, QD);   // dims 2l, 2l + 1: adjacent in the tile layout
     gst(dst, (o0 + q0) * inv);
     gst(dst + 1, (o1 + q1) * inv);
 }
@@ -434,10 +433,11 @@ struct SampleArgs {
 
 // Talker codebook 0 of stream m (tl_modified_logit + tl_sample, frame.hip:413-454): control range
 // suppressed except EOS, EOS suppressed before min_frames, repetition penalty over the stream's
-// set; then the cp input rows of the stream: x[2m] = post-norm hidden, x[2m + 1] = codec_emb[cb0].
+// set; then the cp input rows of the stream: x[2m] = post-norm hidden, x[2m + 1] = codec_emb[cb0]
+// (x in the tile layout of width H).
 __global__ void __launch_bounds__(BT) k_st_talker_sample(const float *logits, int V, const StreamMeta *meta, uint8_t *seen,
                                                          SampleArgs sa, const float *hidden, const uint16_t *codec_emb, int H,
-                                                         float *cp_x, int ldx, int32_t *codes) {
+                                                         float *cp_x, int32_t *codes) {
     constexpr int VT = 3072;
     __shared__ float lg[VT];
     __shared__ __align__(16) unsigned hist[SAMPLE_LDS_WORDS];
@@ -463,16 +463,16 @@ __global__ void __launch_bounds__(BT) k_st_talker_sample(const float *logits, in
     const float *hr = hidden + static_cast<size_t>(m) * H;
     const uint16_t *er = codec_emb + static_cast<size_t>(cb0) * H;
     for (int i = threadIdx.x; i < H; i += BT) {
-        gst(cp_x + static_cast<size_t>(2 * m) * ldx + i, gld(hr + i));
-        gst(cp_x + static_cast<size_t>(2 * m + 1) * ldx + i, h2f(gld(er + i)));
+        gst(cp_x + pk_a(2 * m, i, H), gld(hr + i));
+        gst(cp_x + pk_a(2 * m + 1, i, H), h2f(gld(er + i)));
     }
 }
 
 // Code pos of stream m from lm_head[pos - 1]'s logits (cp_sample, frame.hip:483-500: no
 // suppression, penalty or EOS gate; seed cp_seed + pos * 0xD1B54A32D192ED03); then, if next_emb,
-// the next cp input row x[m] = next_emb[code].
+// the next cp input row x[m] = next_emb[code] (x in the tile layout of width H).
 __global__ void __launch_bounds__(BT) k_st_cp_sample(const float *logits, const StreamMeta *meta, SampleArgs sa, int pos,
-                                                     const uint16_t *next_emb, int H, float *x, int ldx, int32_t *codes) {
+                                                     const uint16_t *next_emb, int H, float *x, int32_t *codes) {
     constexpr int VC = 2048;
     __shared__ float lg[VC];
     __shared__ __align__(16) unsigned hist[SAMPLE_LDS_WORDS];
@@ -487,16 +487,16 @@ __global__ void __launch_bounds__(BT) k_st_cp_sample(const float *logits, const 
     if (threadIdx.x == 0) gst(codes + static_cast<size_t>(m) * NCB + pos, code);
     if (next_emb) {
         const uint16_t *er = next_emb + static_cast<size_t>(code) * H;
-        for (int i = threadIdx.x; i < H; i += BT) gst(x + static_cast<size_t>(m) * ldx + i, h2f(gld(er + i)));
+        for (int i = threadIdx.x; i < H; i += BT) gst(x + pk_a(m, i, H), h2f(gld(er + i)));
     }
 }
 
-// xn[m] = RMSNorm(x[m]) * w for the residual rows x (row stride ldx) into xn (row stride H): the
-// talker's final norm (k_rmsnorm, kernels.h:342-350); H == 4 * BT.
-__global__ void __launch_bounds__(BT) k_st_final_norm(const float *x, int ldx, const float *w, float eps, float *xn, int H) {
+// xn[m] = RMSNorm(x[m]) * w for the residual rows x (tile layout of width H) into xn (row stride
+// H): the talker's final norm (k_rmsnorm, kernels.h:342-350); H == 4 * BT.
+__global__ void __launch_bounds__(BT) k_st_final_norm(const float *x, const float *w, float eps, float *xn, int H) {
     __shared__ float red[NW];
     const int m = blockIdx.x, i = threadIdx.x * 4;
-    const f32x4_t v = ld4(x + static_cast<size_t>(m) * ldx + i), wv = ld4(w + i);
+    const f32x4_t v = ld4(x + pk_a(m, i, H)), wv = ld4(w + i);
     float ss = 0.f;
 #pragma unroll
     for (int j = 0; j < 4; ++j) ss = fmaf(v[j], v[j], ss);
@@ -534,6 +534,7 @@ __global__ void __launch_bounds__(BT) k_st_assemble(const int32_t *codes, const 
 struct LayerW {
     const float *ln1, *ln2, *qn, *kn;
     const uint16_t *wq, *wk, *wv, *wo, *wg, *wu, *wd;
+    uint16_t *qkv_t, *o_t, *gu_t, *d_t;   // the tiled copies: [q; k; v], o, [gate; up], down
 };
 
 } // namespace ms
@@ -543,10 +544,10 @@ using namespace navi_amd;
 using namespace navi_amd::ms;
 
 // The step's activations and split-K workspace, and the HIP stream it runs on.
+// x (the residual stream), att and h in the tile layout (rows.h pk_a), the rest row-major.
 struct StreamWork {
     float *x = nullptr, *xn = nullptr, *att = nullptr, *h = nullptr, *part = nullptr, *apart = nullptr;
     float *lg = nullptr;
-    int lx = 0, la = 0, lf = 0;       // row strides of x, att and h (ROW_PAD floats past the row)
     hipStream_t st = nullptr;
 };
 
@@ -560,6 +561,8 @@ struct navi_streams {
     const uint16_t *codec_head = nullptr, *codec_emb = nullptr;
     EmbTable cp_emb{};
     const uint16_t *lm_head[CPH] = {};
+    uint16_t *lm_head_t[CPH] = {};                  // tiled copies of lm_head
+    uint16_t *tiled = nullptr;                      // every tiled weight copy, one allocation
     StreamWork work;
     float *step = nullptr, *invf_t = nullptr, *invf_c = nullptr;
     size_t part_floats = 0;
@@ -640,15 +643,21 @@ navi_status bind_layers(const char *who, const navi_tensor_ref *t, int n, const 
 
 // One decoder layer over `rows` rows: x (the residual stream) in and out. attend() turns the
 // q|k|v rows in g.part into the attention output rows in g.att.
+// false: a projection shape the tiled kernels do not take (the shapes checked at create all are).
 template <class Attend>
-void layer(navi_streams &h, StreamWork &g, const LayerW &w, float eps, int rows, Attend attend) {
+bool layer(navi_streams &h, StreamWork &g, const LayerW &w, float eps, int rows, Attend attend) {
     const int H = h.H, QKVW = h.QD + 2 * h.KVD;
     hipStream_t s = g.st;
-    launch_rows(EPI_PLAIN, true, g.x, g.lx, rows, H, w.ln1, eps, w.wq, h.QD, w.wk, h.KVD, w.wv, h.KVD, g.part, QKVW, h.flag, s);
+    if (!launch_rows_pk(EPI_PLAIN, true, g.x, rows, H, w.ln1, eps, w.qkv_t, QKVW, g.part, QKVW, h.flag, s)) return false;
     attend();
-    launch_rows(EPI_RESID, false, g.att, g.la, rows, h.QD, nullptr, 0.f, w.wo, H, nullptr, 0, nullptr, 0, g.x, g.lx, h.flag, s);
-    launch_rows(EPI_SWIGLU, true, g.x, g.lx, rows, H, w.ln2, eps, w.wg, h.F, w.wu, h.F, nullptr, 0, g.h, g.lf, h.flag, s);
-    launch_rows(EPI_RESID, false, g.h, g.lf, rows, h.F, nullptr, 0.f, w.wd, H, nullptr, 0, nullptr, 0, g.x, g.lx, h.flag, s);
+    return launch_rows_pk(EPI_RESID, false, g.att, rows, h.QD, nullptr, 0.f, w.o_t, H, g.x, 0, h.flag, s) &&
+           launch_rows_pk(EPI_SWIGLU, true, g.x, rows, H, w.ln2, eps, w.gu_t, h.F, g.h, 0, h.flag, s) &&
+           launch_rows_pk(EPI_RESID, false, g.h, rows, h.F, nullptr, 0.f, w.d_t, H, g.x, 0, h.flag, s);
+}
+
+navi_status unsupported(char *err, size_t errlen) {
+    set_err(err, errlen, "streams: a projection shape the tiled row kernels do not take");
+    return NAVI_ERR_UNSUPPORTED;
 }
 
 // The frame of streams i0 .. i0 + n - 1 (per-stream state at those offsets), on g.st.
@@ -664,20 +673,20 @@ navi_status run_group(navi_streams *h, StreamWork &g, int i0, int n, int zsplits
     uint16_t *cpv = h->cpv + static_cast<size_t>(i0) * h->CL * NCB * h->KVD;
 
     // talker step over the group's streams
-    NAVI_TRY_HIP(hipMemcpy2DAsync(g.x, static_cast<size_t>(g.lx) * 4, step_in, static_cast<size_t>(H) * 4,
-                                  static_cast<size_t>(H) * 4, n, hipMemcpyDeviceToDevice, s), err, errlen);
+    tile_rows(step_in, n, H, g.x, s);
     for (int l = 0; l < h->TL; ++l) {
         uint16_t *const *kt = h->ktab + static_cast<size_t>(l) * h->ms + i0;
         uint16_t *const *vt = h->vtab + static_cast<size_t>(l) * h->ms + i0;
-        layer(*h, g, h->tl[l], et, n, [&]() {
+        const bool ok = layer(*h, g, h->tl[l], et, n, [&]() {
             hipLaunchKernelGGL(k_st_attn, dim3(n, h->NKV, zsplits), dim3(BT), 0, s, g.part, meta, kt, vt, h->NQ, h->NKV,
                                h->splits, h->tl[l].qn, h->tl[l].kn, et, h->invf_t, g.apart);
             hipLaunchKernelGGL(k_st_attn_combine, dim3(n, h->NKV), dim3(BT), 0, s, g.apart, meta, h->NQ, h->NKV, h->splits,
-                               g.att, g.la);
+                               g.att);
         });
+        if (!ok) return unsupported(err, errlen);
     }
     // final norm (the post-norm hidden rows are the cp's first input rows), head, codebook 0
-    hipLaunchKernelGGL(k_st_final_norm, dim3(n), dim3(BT), 0, s, g.x, g.lx, h->tl_norm, et, g.xn, H);
+    hipLaunchKernelGGL(k_st_final_norm, dim3(n), dim3(BT), 0, s, g.x, h->tl_norm, et, g.xn, H);
     launch_rows(EPI_PLAIN, false, g.xn, H, n, H, nullptr, 0.f, h->codec_head, h->VT, nullptr, 0, nullptr, 0, g.lg, h->VT,
                 h->flag, s);
     if (h->taps_on) {
@@ -687,27 +696,29 @@ navi_status run_group(navi_streams *h, StreamWork &g, int i0, int n, int zsplits
                                     hipMemcpyDeviceToDevice, s), err, errlen);
     }
     hipLaunchKernelGGL(k_st_talker_sample, dim3(n), dim3(BT), 0, s, g.lg, h->VT, meta, seen, sa, g.xn, h->codec_emb, H, g.x,
-                       g.lx, codes);
+                       codes);
 
     // code predictor: positions 0 and 1 as one 2-row pass per stream, then one row per position
     for (int pos = 1; pos < NCB; ++pos) {
         const int T = pos == 1 ? 2 : 1, p0 = pos == 1 ? 0 : pos, rows = n * T;
         for (int l = 0; l < h->CL; ++l) {
-            layer(*h, g, h->cl[l], ec, rows, [&]() {
+            const bool ok = layer(*h, g, h->cl[l], ec, rows, [&]() {
                 hipLaunchKernelGGL(k_st_cp_attn, dim3(n, h->NKV), dim3(2 * T * WAVE), 0, s, g.part, T, p0, h->NQ, h->NKV,
-                                   h->cl[l].qn, h->cl[l].kn, ec, h->invf_c, l, h->CL, cpk, cpv, g.att, g.la);
+                                   h->cl[l].qn, h->cl[l].kn, ec, h->invf_c, l, h->CL, cpk, cpv, g.att);
             });
+            if (!ok) return unsupported(err, errlen);
         }
-        // the cp norm and lm_head[pos - 1] on the last row of each stream
-        launch_rows(EPI_PLAIN, true, g.x + static_cast<size_t>(T - 1) * g.lx, T * g.lx, n, H, h->cp_norm, ec, h->lm_head[pos - 1],
-                    h->VC, nullptr, 0, nullptr, 0, g.lg, h->VC, h->flag, s);
+        // the cp norm and lm_head[pos - 1] on the last row of each stream (row m T + T - 1 of x)
+        if (!launch_rows_pk(EPI_PLAIN, true, g.x, n, H, h->cp_norm, ec, h->lm_head_t[pos - 1], h->VC, g.lg, h->VC, h->flag, s, {},
+                            T, T - 1))
+            return unsupported(err, errlen);
         if (h->taps_on)
             NAVI_TRY_HIP(hipMemcpy2DAsync(h->tap_cp() + (static_cast<size_t>(i0) * CPH + (pos - 1)) * h->VC,
                                           static_cast<size_t>(CPH) * h->VC * 4, g.lg, static_cast<size_t>(h->VC) * 4,
                                           static_cast<size_t>(h->VC) * 4, n, hipMemcpyDeviceToDevice, s),
                          err, errlen);
         hipLaunchKernelGGL(k_st_cp_sample, dim3(n), dim3(BT), 0, s, g.lg, meta, sa, pos,
-                           pos < CPH ? h->cp_emb.cp_emb[pos - 1] : nullptr, H, g.x, g.lx, codes);
+                           pos < CPH ? h->cp_emb.cp_emb[pos - 1] : nullptr, H, g.x, codes);
     }
     hipLaunchKernelGGL(k_st_assemble, dim3(n), dim3(BT), 0, s, codes, h->codec_emb, h->cp_emb,
                        d_trailing + static_cast<size_t>(i0) * H, H, h->step + static_cast<size_t>(i0) * H);
@@ -781,13 +792,14 @@ navi_status navi_streams_create(const navi_model_params *p, const navi_tensor_re
 #define SA(ptr, n_) \
     if ((st = h->alloc(ptr, (n_), err, errlen)) != NAVI_OK) return fail(st)
     StreamWork &g = h->work;
-    g.lx = H + ROW_PAD;
-    g.la = h->QD + ROW_PAD;
-    g.lf = h->F + ROW_PAD;
-    SA(g.x, R * g.lx);
+    const size_t R16 = (R + 15) / 16 * 16;          // x, att and h (tile layout) hold whole 16-row tiles
+    SA(g.x, R16 * H);
     SA(g.xn, R * H);
-    SA(g.att, R * g.la);
-    SA(g.h, R * g.lf);
+    SA(g.att, R16 * h->QD);
+    SA(g.h, R16 * h->F);
+    const size_t per_layer = static_cast<size_t>(QKVW) * H + static_cast<size_t>(H) * h->QD + static_cast<size_t>(2 * h->F) * H +
+                             static_cast<size_t>(H) * h->F;
+    SA(h->tiled, per_layer * (h->TL + h->CL) + static_cast<size_t>(CPH) * h->VC * H);
     SA(g.part, pf_need);
     SA(g.apart, static_cast<size_t>(max_streams) * h->NKV * h->splits * 2 * (HD + 2));
     SA(g.lg, static_cast<size_t>(max_streams) * h->VT);
@@ -813,6 +825,32 @@ navi_status navi_streams_create(const navi_model_params *p, const navi_tensor_re
         ic[i] = static_cast<float>(1.0 / std::pow(c.rope_theta, 2.0 * i / HD));
     }
     hipStream_t s = device_state().stream;
+    {
+        // the tiled copies the row projections read
+        uint16_t *q = h->tiled;
+        auto put = [&](const uint16_t *src, int rows_, int K) {
+            tile_weights(src, rows_, K, q, s);
+            q += static_cast<size_t>(rows_) * K;
+        };
+        for (std::vector<LayerW> *ls : {&h->tl, &h->cl})
+            for (LayerW &w : *ls) {
+                w.qkv_t = q;
+                put(w.wq, h->QD, H);
+                put(w.wk, h->KVD, H);
+                put(w.wv, h->KVD, H);
+                w.o_t = q;
+                put(w.wo, H, h->QD);
+                w.gu_t = q;
+                put(w.wg, h->F, H);
+                put(w.wu, h->F, H);
+                w.d_t = q;
+                put(w.wd, H, h->F);
+            }
+        for (int i = 0; i < CPH; ++i) {
+            h->lm_head_t[i] = q;
+            put(h->lm_head[i], h->VC, H);
+        }
+    }
     if (hipMemcpyAsync(h->invf_t, it, sizeof it, hipMemcpyHostToDevice, s) != hipSuccess ||
         hipMemcpyAsync(h->invf_c, ic, sizeof ic, hipMemcpyHostToDevice, s) != hipSuccess || hipEventCreate(&h->ev0) != hipSuccess ||
         hipEventCreate(&h->ev1) != hipSuccess || hipStreamSynchronize(s) != hipSuccess) {
