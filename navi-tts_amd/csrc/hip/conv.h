@@ -636,8 +636,10 @@ __global__ void __launch_bounds__(BT) k_conv_c96(ConvArgs a) {
 // One residual unit of the codec decoder's narrow blocks (C = 96 or 192 channels) in one kernel:
 // the Snake'd residual stream x -> k7 conv (dilation dil) + bias -> Snake with the k1's parameters
 // -> k1 conv + bias + the residual -> y, and y's Snake with the next conv's parameters -> z. A block
-// owns BM rows and all C output channels (C = 96: 128 rows, waves 4 x 1; C = 192: 64 rows, waves
-// 2 x 2; each wave 32 rows x 96 columns). The k7 stages its time window and every tap's weights per
+// owns BM rows and all C output channels (C = 96: 128 rows, waves 4 x 1, each wave 32 rows x 96
+// columns, or 32 rows, waves 1 x 3, each wave 32 rows x 32 columns and the fourth wave staging only;
+// C = 192: 64 rows, waves 2 x 2, each wave 32 rows x 96 columns). An output's sums run the same
+// MFMA chain whatever BM. The k7 stages its time window and every tap's weights per
 // CC7-channel chunk as k_conv_wide does; its output tile goes through the Snake into LDS as f16 hi
 // + lo, where the k1 reads it as its A operand while the k1's weights are staged 32 channels at a
 // time, the next piece in flight during the MFMAs: the intermediate never goes to memory and the
@@ -659,9 +661,11 @@ struct UnitArgs {
 
 template <int C, int BM, int CC7>
 __global__ void __launch_bounds__(BT) k_unit(UnitArgs u) {
-    constexpr int K = 7, LDA = CC7 + 8, NCT = 3;
-    constexpr int WRW = BM / 32, WCW = 4 / WRW;             // waves along rows, along columns
-    static_assert(WRW * WCW == 4 && C == WCW * 32 * NCT, "each wave 32 rows x 96 columns");
+    constexpr int K = 7, LDA = CC7 + 8;
+    constexpr int WRW = BM / 32;                            // waves along rows
+    constexpr int WCW = 4 / WRW < C / 32 ? 4 / WRW : C / 32;   // waves along columns
+    constexpr int NCT = C / (WCW * 32);                     // 32-column tiles per wave
+    static_assert(WRW * WCW <= 4 && C == WCW * 32 * NCT, "each computing wave 32 rows x 32 NCT columns");
     constexpr int MAXWR = BM + (K - 1) * 9, LDM = C + 8, CC1 = 32, LDW = CC1 + 8;
     constexpr int A_BYTES = MAXWR * LDA * 2 * 2, B_BYTES = K * C * LDA * 2;           // k7 staging
     constexpr int M_BYTES = BM * LDM * 2 * 2, W_BYTES = C * LDW * 2;                  // k1 operands
@@ -671,6 +675,7 @@ __global__ void __launch_bounds__(BT) k_unit(UnitArgs u) {
     _Float16 *mhi = reinterpret_cast<_Float16 *>(smem), *mlo = mhi + BM * LDM, *w1s = mlo + BM * LDM;
     const int wv = threadIdx.x >> 6, l = threadIdx.x & 63;
     const int wr = 32 * (wv % WRW), wc = 32 * NCT * (wv / WRW);
+    const bool mma = wv < WRW * WCW;                        // a computing wave (the rest stage only)
     const int t0 = blockIdx.x * BM;
     const int H = (K - 1) * u.dil, rows = BM + H, lpad = H;
     // ---- k7: the staging and step order of k_conv_wide ----
@@ -754,6 +759,7 @@ __global__ void __launch_bounds__(BT) k_unit(UnitArgs u) {
         __syncthreads();
         if (ci0 + CC7 < C) load(ci0 + CC7);
         else load_w1(0);                                    // the k1's first weight piece, during the last MFMAs
+        if (!mma) continue;
 #pragma unroll
         for (int j = 0; j < K; ++j) {
 #pragma unroll
@@ -784,6 +790,7 @@ __global__ void __launch_bounds__(BT) k_unit(UnitArgs u) {
     for (int c = 0; c < NCT; ++c)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
+            if (!mma) break;
             const int row = wr + 8 * (r / 4) + 4 * (l >> 5) + (r & 3), co = wc + 32 * c + (l & 31);
             const float m = snake(acc[c][r] + b7c[c], zam[c], zbm[c]);
             if (t0 + row < u.T) bad |= !(fabsf(m) < 65504.f);
@@ -807,6 +814,7 @@ __global__ void __launch_bounds__(BT) k_unit(UnitArgs u) {
         }
         __syncthreads();                                    // the piece (and, first time, the tile) in LDS
         if (ci0 + CC1 < C) load_w1(ci0 + CC1);
+        if (!mma) continue;
 #pragma unroll
         for (int ks = 0; ks < CC1 / 16; ++ks) {
             const int ar = (wr + (l & 31)) * LDM + ci0 + 16 * ks + 8 * (l >> 5);
@@ -821,6 +829,10 @@ __global__ void __launch_bounds__(BT) k_unit(UnitArgs u) {
         }
     }
     // ---- epilogue: every load first (column operands, residuals), then the stores ----
+    if (!mma) {
+        if (u.hnext) carry_rows(u.hist, u.x, C, u.T, H, C, u.hnext);
+        return;
+    }
     float b1c[NCT], zac[NCT], zbc[NCT], rs[NCT][16];
 #pragma unroll
     for (int c = 0; c < NCT; ++c) {

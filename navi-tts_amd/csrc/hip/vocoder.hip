@@ -592,7 +592,9 @@ void launch_unit(navi_vocoder &v, Unit &u, const float *x, int T, const float *r
     a.x = x; a.hist = u.c1.hbuf[v.parity]; a.hnext = u.c1.H > 0 ? u.c1.hbuf[v.parity ^ 1] : nullptr;
     a.w7 = u.c1.w; a.w1 = u.c2.w; a.b7 = u.c1.bias; a.b1 = u.c2.bias; a.za_mid = u.c2.sa; a.zb_mid = u.c2.sb;
     a.res = res; a.y = y; a.z = z; a.za = next.sa; a.zb = next.sb; a.flag = v.flag; a.T = T; a.dil = u.c1.dil;
-    hipLaunchKernelGGL((k_unit<96, 128, 16>), dim3((T + 127) / 128), dim3(BT), 0, device_state().stream, a);
+    // 32-row tiles when 128-row ones would leave half the CUs idle (a short chunk): the same sums
+    if (T < 128 * 128) hipLaunchKernelGGL((k_unit<96, 32, 16>), dim3((T + 31) / 32), dim3(BT), 0, device_state().stream, a);
+    else hipLaunchKernelGGL((k_unit<96, 128, 16>), dim3((T + 127) / 128), dim3(BT), 0, device_state().stream, a);
 }
 
 // Input-channel splits of a conv over T rows: when the output tiles alone would leave most of the
