@@ -78,11 +78,13 @@ def build_hip(jobs: int = 8) -> Path:
 def build_bench() -> list[Path]:
     """The microbenchmarks behind the design's latency figures (standalone programs): the frame
     kernel's exchange hop, the dependent-launch floor of the row-projection chains, the cost
-    of a grid-wide barrier phase in a persistent grid exchanging 32-row activations, and how a
-    poll's round trip grows with other waves' or its own wave's weight loads in flight."""
+    of a grid-wide barrier phase in a persistent grid exchanging 32-row activations, how a
+    poll's round trip grows with other waves' or its own wave's weight loads in flight, the read
+    rate of the row projections' operand loads by memory layout, and the projections on the
+    row-major and the tile layouts."""
     LIB.mkdir(parents=True, exist_ok=True)
     outs = []
-    for name in ("hop_latency", "launch_floor", "grid_barrier", "load_coupling"):
+    for name in ("hop_latency", "launch_floor", "grid_barrier", "load_coupling", "operand_layout", "row_tiles"):
         out = LIB / name
         _run([HIPCC, "-O3", "-std=c++17", f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
               "-I", str(ROOT / "include"), "-I", str(PKG / "csrc" / "hip"),
