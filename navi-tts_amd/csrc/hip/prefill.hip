@@ -389,10 +389,12 @@ __global__ void __launch_bounds__(BT) k_attn_prefill_short(const float *q, uint1
             const int j = wv * KW + 4 * i + r;
             kr[i] = j < n ? *(const NAVI_GLOBAL u32x4_t *) (kb + static_cast<size_t>(j) * KVD) : u32x4_t{0u, 0u, 0u, 0u};
         }
+        if constexpr (FEW) {
 #pragma unroll
-        for (int i = 0; i < KI; ++i) {
-            const int j = wv * KW + 4 * i + r;
-            vr[i] = j < n ? *(const NAVI_GLOBAL u32x4_t *) (vb + static_cast<size_t>(j) * KVD) : u32x4_t{0u, 0u, 0u, 0u};
+            for (int i = 0; i < KI; ++i) {
+                const int j = wv * KW + 4 * i + r;
+                vr[i] = j < n ? *(const NAVI_GLOBAL u32x4_t *) (vb + static_cast<size_t>(j) * KVD) : u32x4_t{0u, 0u, 0u, 0u};
+            }
         }
     }
     __syncthreads();                                      // qs
@@ -422,6 +424,17 @@ __global__ void __launch_bounds__(BT) k_attn_prefill_short(const float *q, uint1
                 sc[0][j] = a0 * scale;
                 sc[1][j] = a1 * scale;
             }
+        }
+    }
+    if constexpr (!FEW && !FUSED) {
+        // prompts of 65-256 rows: the V chunks go out after the scores and fly during the softmax,
+        // so K and V are never in registers together (about 100 VGPRs instead of 156: four blocks
+        // per CU instead of three; the sums are unchanged)
+        const uint16_t *vb = vc + g * HD + c * 8;
+#pragma unroll
+        for (int i = 0; i < KI; ++i) {
+            const int j = wv * KW + 4 * i + r;
+            vr[i] = j < n ? *(const NAVI_GLOBAL u32x4_t *) (vb + static_cast<size_t>(j) * KVD) : u32x4_t{0u, 0u, 0u, 0u};
         }
     }
     __syncthreads();

@@ -62,7 +62,7 @@ struct StreamMeta {
 // stream's cache at n_past and uses those values for that key; every other key comes from the
 // cache. Writes per head (max, sum of e^(score - max), unnormalised vector) to
 // out[m][g][s][h] = {m, l, o[HD]}.
-__global__ void __launch_bounds__(BT) k_st_attn(const float *part, const StreamMeta *meta, uint16_t *const *kcache,
+__global__ void __launch_bounds__(BT, 4) k_st_attn(const float *part, const StreamMeta *meta, uint16_t *const *kcache,
                                                 uint16_t *const *vcache, int nq, int nkv, int splits, const float *qn,
                                                 const float *kn, float eps, const float *invf, float *partials) {
     __shared__ float qs[2][HD], nkv_[2][HD], sc[2][KPS], red[2][NW], opart[NW][4][2][HD];
@@ -86,14 +86,6 @@ __global__ void __launch_bounds__(BT) k_st_attn(const float *part, const StreamM
         for (int i = 0; i < KI; ++i) {
             const int jl = wv * (KPS / NW) + 4 * i + r;
             kr[i] = jl < cnt && j0 + jl != pos ? *(const NAVI_GLOBAL u32x4_t *) (kb + static_cast<size_t>(j0 + jl) * KVD + c * 8)
-                                               : u32x4_t{0u, 0u, 0u, 0u};
-        }
-        // the same keys' V chunks are loaded now too (they do not depend on the scores): one
-        // memory latency per block instead of two
-#pragma unroll
-        for (int i = 0; i < KI; ++i) {
-            const int jl = wv * (KPS / NW) + 4 * i + r;
-            vr[i] = jl < cnt && j0 + jl != pos ? *(const NAVI_GLOBAL u32x4_t *) (vb + static_cast<size_t>(j0 + jl) * KVD + c * 8)
                                                : u32x4_t{0u, 0u, 0u, 0u};
         }
         // while those loads are in flight: q heads 2g, 2g + 1 and (own range) the step's k and v,
@@ -141,14 +133,10 @@ __global__ void __launch_bounds__(BT) k_st_attn(const float *part, const StreamM
             for (int i = 0; i < KI; ++i) {
                 const int jl = wv * (KPS / NW) + 4 * i + r;
                 if (j0 + jl == pos) {
-                    half8_t hk, hv;
+                    half8_t hk;
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) {
-                        hk[e] = static_cast<_Float16>(nkv_[0][c * 8 + e]);
-                        hv[e] = static_cast<_Float16>(nkv_[1][c * 8 + e]);
-                    }
+                    for (int e = 0; e < 8; ++e) hk[e] = static_cast<_Float16>(nkv_[0][c * 8 + e]);
                     __builtin_memcpy(&kr[i], &hk, 16);
-                    __builtin_memcpy(&vr[i], &hv, 16);
                 }
             }
         }
@@ -169,6 +157,23 @@ __global__ void __launch_bounds__(BT) k_st_attn(const float *part, const StreamM
             if (c == 0) {
                 sc[0][jl] = a0 * ATT_SCALE;
                 sc[1][jl] = a1 * ATT_SCALE;
+            }
+        }
+        // the same keys' V chunks go out after the scores and fly during the softmax, so K and V
+        // are never in registers together (about 110 VGPRs instead of 168: the whole grid of a
+        // 32-stream step resident at once, four blocks per CU instead of three; the sums are
+        // unchanged); the step's own value from LDS
+#pragma unroll
+        for (int i = 0; i < KI; ++i) {
+            const int jl = wv * (KPS / NW) + 4 * i + r;
+            if (own && j0 + jl == pos) {
+                half8_t hv;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) hv[e] = static_cast<_Float16>(nkv_[1][c * 8 + e]);
+                __builtin_memcpy(&vr[i], &hv, 16);
+            } else {
+                vr[i] = jl < cnt && j0 + jl != pos ? *(const NAVI_GLOBAL u32x4_t *) (vb + static_cast<size_t>(j0 + jl) * KVD + c * 8)
+                                                   : u32x4_t{0u, 0u, 0u, 0u};
             }
         }
     }
