@@ -303,12 +303,14 @@ __global__ void __launch_bounds__(BT) k_attn_prefill(const float *q, const uint1
 
 // k_attn_prefill for rows with at most SHORT_KEYS keys (prompts of up to 256 rows). Wave w takes
 // keys 64w .. 64w + 63; lane 16r + c reads 16-byte chunk c of key 4i + r, so one load instruction
-// covers four whole 256-byte key rows, and every K and V chunk of the block is issued before the
-// first score: one memory latency per block where the loop above pays one per 32 keys of V.
+// covers four whole 256-byte key rows, and every K chunk of the block is issued before the first
+// score (the fused variant stages K and V in LDS; the other issues its V chunks after the scores,
+// so they fly during the softmax and K and V never share the registers): one or two memory
+// latencies per block where the loop above pays one per 32 keys of V.
 // Scores are summed over a key's 16 lanes by DPP; thread t owns key t for the softmax.
 // The score and value loops skip the key groups past the row's keys: per group of four keys when
-// every key of the launch falls in wave 0's range (FEW: prompts of up to 64 rows), per wave
-// otherwise (a per-group exit in the unrolled loops of the longer rows measured slower).
+// every key of the launch falls in wave 0's range (FEW, the fused prompts of up to 64 rows), per
+// wave otherwise (a per-group exit in the unrolled loops of the longer rows measured slower).
 constexpr int SHORT_KEYS = 256;
 // FUSED (prompts of up to FUSED_ROWS rows from position 0; FEW): the q/k head norms, RoPE and the
 // f16 K/V store are folded in (k_qk_norm_rope, talker.hip:46-82). The block of row m forms, from
@@ -328,7 +330,7 @@ __global__ void __launch_bounds__(BT) k_attn_prefill_short(const float *q, uint1
                                                            HeadNorm hn = {}) {
     constexpr int NWV = BT / WAVE, KW = SHORT_KEYS / NWV, KI = KW / 4;
     static_assert(SHORT_KEYS == BT, "one key per thread in the softmax");
-    static_assert(!FUSED || (FEW && FUSED_ROWS <= KW), "fused: every key in wave 0's range");
+    static_assert(FEW == FUSED && (!FUSED || FUSED_ROWS <= KW), "fused (the only FEW case): every key in wave 0's range");
     __shared__ float qs[2][HD], sc[2][SHORT_KEYS], red[2][NWV], opart[NWV][4][2][HD];
     __shared__ uint16_t ks[FUSED ? FUSED_ROWS : 1][HD], vs[FUSED ? FUSED_ROWS : 1][HD];
     const int m = blockIdx.x, g = blockIdx.y, n = pos0 + m + 1;
@@ -383,18 +385,11 @@ __global__ void __launch_bounds__(BT) k_attn_prefill_short(const float *q, uint1
         }
     } else {
         qs[threadIdx.x >> 7][threadIdx.x & (HD - 1)] = gld(q + static_cast<size_t>(m) * QD + g * 2 * HD + threadIdx.x);
-        const uint16_t *kb = kc + g * HD + c * 8, *vb = vc + g * HD + c * 8;
+        const uint16_t *kb = kc + g * HD + c * 8;
 #pragma unroll
         for (int i = 0; i < KI; ++i) {
             const int j = wv * KW + 4 * i + r;
             kr[i] = j < n ? *(const NAVI_GLOBAL u32x4_t *) (kb + static_cast<size_t>(j) * KVD) : u32x4_t{0u, 0u, 0u, 0u};
-        }
-        if constexpr (FEW) {
-#pragma unroll
-            for (int i = 0; i < KI; ++i) {
-                const int j = wv * KW + 4 * i + r;
-                vr[i] = j < n ? *(const NAVI_GLOBAL u32x4_t *) (vb + static_cast<size_t>(j) * KVD) : u32x4_t{0u, 0u, 0u, 0u};
-            }
         }
     }
     __syncthreads();                                      // qs
@@ -426,7 +421,7 @@ __global__ void __launch_bounds__(BT) k_attn_prefill_short(const float *q, uint1
             }
         }
     }
-    if constexpr (!FEW && !FUSED) {
+    if constexpr (!FUSED) {
         // prompts of 65-256 rows: the V chunks go out after the scores and fly during the softmax,
         // so K and V are never in registers together (about 100 VGPRs instead of 156: four blocks
         // per CU instead of three; the sums are unchanged)
@@ -962,9 +957,8 @@ bool prefill_layers(navi_talker &t, int T, hipStream_t s) {
             if (!rows::launch_rows_pk(rows::EPI_QKV, true, t.x, T, H, w.ln1, t.eps, w.qkv_t, QKVW, nullptr, 0, t.flag, s, ho))
                 return false;
             if (T <= SHORT_KEYS)
-                hipLaunchKernelGGL(T <= SHORT_KEYS / (BT / WAVE) ? k_attn_prefill_short<true> : k_attn_prefill_short<false>,
-                                   dim3(T, t.NKV), dim3(BT), 0, s, t.q, t.kk[l], t.vv[l], t.NQ, t.NKV, 0, scale, t.att,
-                                   t.QD, HeadNorm{});
+                hipLaunchKernelGGL(k_attn_prefill_short<false>, dim3(T, t.NKV), dim3(BT), 0, s, t.q, t.kk[l], t.vv[l], t.NQ,
+                                   t.NKV, 0, scale, t.att, t.QD, HeadNorm{});
             else
                 hipLaunchKernelGGL(k_attn_prefill, dim3(T, t.NKV), dim3(BT), att_lds, s, t.q, t.kk[l], t.vv[l], t.NQ,
                                    t.NKV, 0, scale, t.att, t.QD);
