@@ -210,103 +210,14 @@ __global__ void __launch_bounds__(BT) k_swiglu(const float *part, int S, int M, 
     }
 }
 
-// Causal GQA attention of row m for the two q heads of kv group g over keys 0..pos0 + m of the
-// f16 cache (k_prefill_attention, talker.hip:88-117). 256 threads. Scores: one key per thread
-// (its 256-byte K row loaded at once, dotted with both q heads). V: each wave sums every 4th key
-// for both heads (a lane owns 2 dims), eight keys' loads in flight, then the four waves'
-// partial sums are added in wave order. The output row goes to `out` in the tile layout of width
-// ldo (rows.h pk_a), the layout the o projection reads.
-__global__ void __launch_bounds__(BT) k_attn_prefill(const float *q, const uint16_t *kc, const uint16_t *vc, int nq,
-                                                     int nkv, int pos0, float scale, float *out, int ldo) {
-    extern __shared__ float sc[];                        // [2][n] scores, then probabilities
-    __shared__ float qs[2][HD], red[2][4], part[4][2][HD];
-    const int m = blockIdx.x, g = blockIdx.y, n = pos0 + m + 1;
-    const int QD = nq * HD, KVD = nkv * HD;
-    const int wv = threadIdx.x >> 6, l = threadIdx.x & 63;
-    qs[threadIdx.x >> 7][threadIdx.x & (HD - 1)] = gld(q + static_cast<size_t>(m) * QD + g * 2 * HD + threadIdx.x);
-    __syncthreads();
-    float mx0 = -INFINITY, mx1 = -INFINITY;
-    for (int j = threadIdx.x; j < n; j += BT) {
-        const NAVI_GLOBAL u32x4_t *kp = (const NAVI_GLOBAL u32x4_t *) (kc + static_cast<size_t>(j) * KVD + g * HD);
-        u32x4_t kr[HD / 8];
-#pragma unroll
-        for (int c = 0; c < HD / 8; ++c) kr[c] = kp[c];
-        float d0 = 0.f, d1 = 0.f;
-#pragma unroll
-        for (int c = 0; c < HD / 8; ++c)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int i = c * 8 + e * 2;
-                const float k0 = h2f(static_cast<uint16_t>(kr[c][e])), k1 = h2f(static_cast<uint16_t>(kr[c][e] >> 16));
-                d0 = fmaf(qs[0][i + 1], k1, fmaf(qs[0][i], k0, d0));
-                d1 = fmaf(qs[1][i + 1], k1, fmaf(qs[1][i], k0, d1));
-            }
-        d0 *= scale;
-        d1 *= scale;
-        sc[j] = d0;
-        sc[n + j] = d1;
-        mx0 = fmaxf(mx0, d0);
-        mx1 = fmaxf(mx1, d1);
-    }
-    mx0 = wave_max(mx0);
-    mx1 = wave_max(mx1);
-    if (l == 0) { red[0][wv] = mx0; red[1][wv] = mx1; }
-    __syncthreads();
-    mx0 = fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3]));
-    mx1 = fmaxf(fmaxf(red[1][0], red[1][1]), fmaxf(red[1][2], red[1][3]));
-    __syncthreads();
-    float s0 = 0.f, s1 = 0.f;
-    for (int j = threadIdx.x; j < n; j += BT) {
-        const float e0 = expf(sc[j] - mx0), e1 = expf(sc[n + j] - mx1);
-        sc[j] = e0;
-        sc[n + j] = e1;
-        s0 += e0;
-        s1 += e1;
-    }
-    s0 = wave_sum(s0);
-    s1 = wave_sum(s1);
-    if (l == 0) { red[0][wv] = s0; red[1][wv] = s1; }
-    __syncthreads();                                      // also publishes the probabilities
-    s0 = red[0][0] + red[0][1] + red[0][2] + red[0][3];
-    s1 = red[1][0] + red[1][1] + red[1][2] + red[1][3];
-    const uint16_t *vp = vc + g * HD + 2 * l;
-    float a00 = 0.f, a01 = 0.f, a10 = 0.f, a11 = 0.f;
-    for (int j0 = wv; j0 < n; j0 += 4 * 8) {
-        uint32_t vv[8];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            const int j = j0 + 4 * u;
-            vv[u] = j < n ? gld(reinterpret_cast<const uint32_t *>(vp + static_cast<size_t>(j) * KVD)) : 0u;
-        }
-#pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            const int j = j0 + 4 * u;
-            if (j < n) {
-                const float p0 = sc[j], p1 = sc[n + j];
-                const float v0 = h2f(static_cast<uint16_t>(vv[u])), v1 = h2f(static_cast<uint16_t>(vv[u] >> 16));
-                a00 = fmaf(p0, v0, a00);
-                a01 = fmaf(p0, v1, a01);
-                a10 = fmaf(p1, v0, a10);
-                a11 = fmaf(p1, v1, a11);
-            }
-        }
-    }
-    part[wv][0][2 * l] = a00;
-    part[wv][0][2 * l + 1] = a01;
-    part[wv][1][2 * l] = a10;
-    part[wv][1][2 * l + 1] = a11;
-    __syncthreads();
-    const int hh = threadIdx.x >> 7, d = threadIdx.x & (HD - 1);
-    const float acc = part[0][hh][d] + part[1][hh][d] + part[2][hh][d] + part[3][hh][d];
-    gst(out + rows::pk_a(m, (g * 2 + hh) * HD + d, ldo), acc / (hh ? s1 : s0));
-}
-
-// k_attn_prefill for rows with at most SHORT_KEYS keys (prompts of up to 256 rows). Wave w takes
+// Causal GQA attention for rows with at most SHORT_KEYS keys (prompts of up to 256 rows; above,
+// k_attn_prefill_long), one block per (row m, kv group g) for its two q heads over keys 0..pos0 + m
+// of the f16 cache (k_prefill_attention, talker.hip:88-117). Wave w takes
 // keys 64w .. 64w + 63; lane 16r + c reads 16-byte chunk c of key 4i + r, so one load instruction
 // covers four whole 256-byte key rows, and every K chunk of the block is issued before the first
 // score (the fused variant stages K and V in LDS; the other issues its V chunks after the scores,
 // so they fly during the softmax and K and V never share the registers): one or two memory
-// latencies per block where the loop above pays one per 32 keys of V.
+// latencies per block.
 // Scores are summed over a key's 16 lanes by DPP; thread t owns key t for the softmax.
 // The score and value loops skip the key groups past the row's keys: per group of four keys when
 // every key of the launch falls in wave 0's range (FEW, the fused prompts of up to 64 rows), per
@@ -479,6 +390,159 @@ __global__ void __launch_bounds__(BT) k_attn_prefill_short(const float *q, uint1
         for (int rr = 0; rr < 4; ++rr) acc += opart[w][rr][hh][d];
     const float sum = red[hh][0] + red[hh][1] + red[hh][2] + red[hh][3];
     gst(out + rows::pk_a(m, (g * 2 + hh) * HD + d, ldo), acc / sum);
+}
+
+// Causal attention of prompts of more than 256 rows on the matrix cores: block (16-row tile qt,
+// q head h) over keys 0..min(T, 16 qt + 16) - 1 of kv group h / (nq / nkv), in chunks of 256 keys
+// with a running softmax. Per chunk: S = Q K^T on v_mfma_f32_16x16x32_f16 with q split into f16
+// hi + lo (f32-level products of the f32 q and the f16 keys; wave w takes the chunk's key tiles w,
+// w + 4, ...), scaled and causally masked into LDS; per row (16 lanes) the chunk's max m_c, the
+// new running max m = max(m_run, m_c), corr = e^(m_run - m), p = e^(s - m) in place, l_run =
+// l_run corr + sum p; the output rows scaled by corr, then O += P V with P split hi + lo against
+// the chunk's V staged transposed in LDS ([dim][key] f16: one 16-byte read per B fragment), wave w
+// taking dims 32w .. 32w + 31. Finally O / l_run to the tile layout of width ldo (rows.h pk_a).
+// Key 0 is in the first chunk of every row, so m_run is finite from the first chunk on.
+constexpr int LONG_CHUNK = 256;
+__global__ void __launch_bounds__(BT) k_attn_prefill_long(const float *q, const uint16_t *kc, const uint16_t *vc, int nq,
+                                                          int nkv, int T, float scale, float *out, int ldo) {
+    constexpr int KT = LONG_CHUNK / 16 / 4;              // key tiles per wave per chunk
+    constexpr int LDS_S = LONG_CHUNK + 4, LDV = LONG_CHUNK + 8;
+    constexpr int VCH = LONG_CHUNK * (HD / 8) / BT;       // 16-byte V chunks per thread per chunk
+    __shared__ float sS[16][LDS_S];
+    __shared__ __align__(16) _Float16 vt[HD][LDV];
+    __shared__ float mrun[16], lrun[16], corr[16];
+    const int qt = blockIdx.x, h = blockIdx.y, g = h / (nq / nkv), r0 = 16 * qt;
+    const int QD = nq * HD, KVD = nkv * HD;
+    const int nk = min(T, r0 + 16);
+    const int w = threadIdx.x >> 6, l = threadIdx.x & 63, c = l & 15, kq = l >> 4;
+    half8_t qh[4], ql[4];
+    {
+        const int row = min(r0 + c, T - 1);
+        const float *qp = q + static_cast<size_t>(row) * QD + h * HD + 8 * kq;
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+            const f32x4_t a0 = ld4(qp + 32 * st), a1 = ld4(qp + 32 * st + 4);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float v = j < 4 ? a0[j] : a1[j - 4];
+                const _Float16 hv = static_cast<_Float16>(v);
+                qh[st][j] = hv;
+                ql[st][j] = static_cast<_Float16>(v - static_cast<float>(hv));
+            }
+        }
+    }
+    if (threadIdx.x < 16) {
+        mrun[threadIdx.x] = -INFINITY;
+        lrun[threadIdx.x] = 0.f;
+    }
+    f32x4_t o[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+    for (int k0 = 0; k0 < nk; k0 += LONG_CHUNK) {
+        const int nkc = min(LONG_CHUNK, nk - k0), nkt = (nkc + 15) / 16, nks = (nkc + 31) / 32;
+        // the chunk's K fragments and V rows, every load before the first MFMA
+        u32x4_t kf[KT][4];
+#pragma unroll
+        for (int i = 0; i < KT; ++i) {
+            const int kt = w + 4 * i, key = 16 * kt + c;
+#pragma unroll
+            for (int st = 0; st < 4; ++st)
+                kf[i][st] = kt < nkt && key < nkc
+                                ? *(const NAVI_GLOBAL u32x4_t *) (kc + static_cast<size_t>(k0 + key) * KVD + g * HD + 32 * st + 8 * kq)
+                                : u32x4_t{0u, 0u, 0u, 0u};
+        }
+        u32x4_t vch[VCH];
+#pragma unroll
+        for (int i = 0; i < VCH; ++i) {
+            const int e = static_cast<int>(threadIdx.x) + BT * i, key = e / (HD / 8), d8 = e % (HD / 8);
+            vch[i] = key < nkc ? *(const NAVI_GLOBAL u32x4_t *) (vc + static_cast<size_t>(k0 + key) * KVD + g * HD + 8 * d8)
+                               : u32x4_t{0u, 0u, 0u, 0u};
+        }
+        __syncthreads();                                  // the previous chunk's readers of sS, vt are done
+#pragma unroll
+        for (int i = 0; i < KT; ++i) {
+            const int kt = w + 4 * i;
+            if (kt >= nkt) break;
+            f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int st = 0; st < 4; ++st) {
+                half8_t b;
+                __builtin_memcpy(&b, &kf[i][st], 16);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(qh[st], b, acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ql[st], b, acc, 0, 0, 0);
+            }
+            const int key = 16 * kt + c;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int row = 4 * kq + r;
+                sS[row][key] = key < nkc && k0 + key <= r0 + row ? acc[r] * scale : -INFINITY;
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < VCH; ++i) {
+            const int e = static_cast<int>(threadIdx.x) + BT * i, key = e / (HD / 8), d8 = e % (HD / 8);
+            if (key < 32 * nks) {
+                half8_t hv;
+                __builtin_memcpy(&hv, &vch[i], 16);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) vt[8 * d8 + j][key] = hv[j];
+            }
+        }
+        __syncthreads();
+        {
+            // row threadIdx / 16, its 16 lanes take keys lane % 16 + 16 m of the chunk
+            const int row = threadIdx.x >> 4, j0 = threadIdx.x & 15;
+            float mc = -INFINITY;
+            for (int j = j0; j < 32 * nks; j += 16) mc = fmaxf(mc, j < nkt * 16 ? sS[row][j] : -INFINITY);
+            mc = fmaxf(mc, dpp_red<0xB1>(mc));
+            mc = fmaxf(mc, dpp_red<0x4E>(mc));
+            mc = fmaxf(mc, dpp_red<0x141>(mc));
+            mc = fmaxf(mc, dpp_red<0x140>(mc));
+            const float mo = mrun[row], m = fmaxf(mo, mc), cr = expf(mo - m);
+            float sum = 0.f;
+            for (int j = j0; j < 32 * nks; j += 16) {
+                const float e = j < nkt * 16 ? expf(sS[row][j] - m) : 0.f;   // masked: e^-inf = 0
+                sS[row][j] = e;
+                sum += e;
+            }
+            sum += dpp_red<0xB1>(sum);
+            sum += dpp_red<0x4E>(sum);
+            sum += dpp_red<0x141>(sum);
+            sum += dpp_red<0x140>(sum);
+            __syncthreads();                              // every lane of the row has read mrun[row]
+            if (j0 == 0) {
+                mrun[row] = m;
+                lrun[row] = lrun[row] * cr + sum;
+                corr[row] = cr;
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) o[u][r] *= corr[4 * kq + r];
+        for (int t = 0; t < nks; ++t) {
+            half8_t ph, pl;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float v = sS[c][32 * t + 8 * kq + j];
+                const _Float16 hv = static_cast<_Float16>(v);
+                ph[j] = hv;
+                pl[j] = static_cast<_Float16>(v - static_cast<float>(hv));
+            }
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const half8_t b = *reinterpret_cast<const half8_t *>(&vt[32 * w + 16 * u + c][32 * t + 8 * kq]);
+                o[u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph, b, o[u], 0, 0, 0);
+                o[u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl, b, o[u], 0, 0, 0);
+            }
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int row = 4 * kq + r;
+            if (r0 + row < T) gst(out + rows::pk_a(r0 + row, h * HD + 32 * w + 16 * u + c, ldo), o[u][r] / lrun[row]);
+        }
 }
 
 // rows[t] = table[ids[t]] (f16 -> f32), k_gather_rows (talker.hip:20-25).
@@ -944,7 +1008,6 @@ namespace {
 bool prefill_layers(navi_talker &t, int T, hipStream_t s) {
     const int H = t.H, QKVW = t.QD + 2 * t.KVD;
     const float scale = 1.f / std::sqrt(static_cast<float>(HD));
-    const size_t att_lds = static_cast<size_t>(2) * T * sizeof(float);
     for (int l = 0; l < t.L; ++l) {
         const LayerW &w = t.layers[l];
         if (T <= FUSED_ROWS) {         // the q/k norms, RoPE and K/V store inside the attention
@@ -960,8 +1023,8 @@ bool prefill_layers(navi_talker &t, int T, hipStream_t s) {
                 hipLaunchKernelGGL(k_attn_prefill_short<false>, dim3(T, t.NKV), dim3(BT), 0, s, t.q, t.kk[l], t.vv[l], t.NQ,
                                    t.NKV, 0, scale, t.att, t.QD, HeadNorm{});
             else
-                hipLaunchKernelGGL(k_attn_prefill, dim3(T, t.NKV), dim3(BT), att_lds, s, t.q, t.kk[l], t.vv[l], t.NQ,
-                                   t.NKV, 0, scale, t.att, t.QD);
+                hipLaunchKernelGGL(k_attn_prefill_long, dim3((T + 15) / 16, t.NQ), dim3(BT), 0, s, t.q, t.kk[l], t.vv[l],
+                                   t.NQ, t.NKV, T, scale, t.att, t.QD);
         }
         if (!rows::launch_rows_pk(rows::EPI_RESID, false, t.att, T, t.QD, nullptr, 0.f, w.o_t, H, t.x, 0, t.flag, s) ||
             !rows::launch_rows_pk(rows::EPI_SWIGLU, true, t.x, T, H, w.ln2, t.eps, w.gu_t, t.F, t.h, 0, t.flag, s) ||
