@@ -6,9 +6,10 @@
 * build_prompt against Oracle.build_prompt (the reference's layout, talker.hip:283-352);
 * prefill against Oracle.prefill at T = 1, T = 10 (the reference's layout), T = 32 and 48 (the
   2- and 3-tile single-group row projections), T = 65, T = 130 (BASELINE's streaming
-  configuration), T = 256 and T = 264 (the most a 256-token handle takes), and on a handle sized as
-  the reference's (max_prompt_tokens 1024, talker.h:37; MAX_KEYS 1024, talker.hip:86) at T = 512,
-  1024 and 1032 (its maximum): post-norm hidden and logits within 2e-2 max abs and cosine > 0.9995
+  configuration), T = 256, 257 and 264 (the most a 256-token handle takes; above 256 rows the
+  attention walks 256-key chunks), and on a handle sized as the reference's (max_prompt_tokens
+  1024, talker.h:37; MAX_KEYS 1024, talker.hip:86) at T = 300, 512, 513, 1024 and 1032 (its
+  maximum): post-norm hidden and logits within 2e-2 max abs and cosine > 0.9995
   (the north star's bar), K/V cache rows within a few f16 ulps;
 * device prompt + device prefill + device frames == oracle codes (greedy).
 """
@@ -129,9 +130,9 @@ def test_prompt_matches_oracle(side, language):
 
 
 # 65: the first row count on the column-group row projections; 256: the most keys the
-# short-context attention takes (every thread owns a key); 264: the handle's maximum
-# (max_prompt_tokens 256 + 8), on the general attention kernel
-@pytest.mark.parametrize("T", [1, 10, 32, 48, 65, 130, 256, 264])
+# short-context attention takes (every thread owns a key); 257: one key into the long-prompt
+# attention's second 256-key chunk; 264: the handle's maximum (max_prompt_tokens 256 + 8)
+@pytest.mark.parametrize("T", [1, 10, 32, 48, 65, 130, 256, 257, 264])
 def test_prefill_matches_oracle(abi, side, T):
     _check_prefill(abi, side, T)
 
@@ -143,7 +144,8 @@ def side_long(abi, small_blob):
     s.talker.close()
 
 
-@pytest.mark.parametrize("T", [512, 1024, 1032])
+# 300: a ragged last 16-row tile and a partial second key chunk; 513: one key into the third chunk
+@pytest.mark.parametrize("T", [300, 512, 513, 1024, 1032])
 def test_long_prefill_matches_oracle(abi, side_long, T):
     _check_prefill(abi, side_long, T)
 
