@@ -1202,6 +1202,9 @@ struct navi_frame {
     uint64_t *prof = nullptr;      // [NB][PROF_SLOTS] when profiling is on
     int32_t *run_codes = nullptr;  // frame loop: [MAX_RUN][16] codes of each frame
     uint32_t *stop = nullptr;      // frame loop: 1 = EOS sampled, 2 = a frame timed out
+    // pinned host copies read back after a call's one synchronization: [MAX_RUN][16] loop codes,
+    // then ctl ([16] codes, abort epoch), then the loop's stop word
+    uint32_t *h_rb = nullptr;
     uint16_t *kv_host[2][MAX_TL] = {};
     uint32_t epoch = 0;
     int grid = NB, occ = 0;
@@ -1211,8 +1214,11 @@ struct navi_frame {
     ~navi_frame() {
         if (ev0) (void) hipEventDestroy(ev0);
         if (ev1) (void) hipEventDestroy(ev1);
+        if (h_rb) (void) hipHostFree(h_rb);
         for (void *q : owned) (void) hipFree(q);
     }
+    uint32_t *h_ctl() const { return h_rb + static_cast<size_t>(MAX_RUN) * NCB; }
+    uint32_t *h_stop() const { return h_ctl() + NCB + 1; }
     template <class T> navi_status alloc(T *&ptr, size_t n, char *err, size_t errlen) {
         void *q = nullptr;
         NAVI_TRY_HIP(hipMalloc(&q, n * sizeof(T)), err, errlen);
@@ -1331,8 +1337,10 @@ navi_status navi_frame_create(const navi_model_params *p, const navi_tensor_ref 
         set_err(err, errlen, "frame: weight table upload failed");
         return fail(NAVI_ERR_HIP);
     }
-    if (hipEventCreate(&f->ev0) != hipSuccess || hipEventCreate(&f->ev1) != hipSuccess) {
-        set_err(err, errlen, "frame: hipEventCreate failed");
+    if (hipEventCreate(&f->ev0) != hipSuccess || hipEventCreate(&f->ev1) != hipSuccess ||
+        hipHostMalloc(reinterpret_cast<void **>(&f->h_rb), sizeof(uint32_t) * (static_cast<size_t>(MAX_RUN) * NCB + NCB + 2),
+                      hipHostMallocDefault) != hipSuccess) {
+        set_err(err, errlen, "frame: hipEventCreate or the pinned readback allocation failed");
         return fail(NAVI_ERR_HIP);
     }
     f->grid = NB;
@@ -1539,8 +1547,9 @@ navi_status navi_frame_run(navi_frame *f, const navi_kv_view *kv, int32_t n_past
         std::string m = std::string("frame launch failed: ") + hipGetErrorString(e);
         return fail(NAVI_ERR_LAUNCH, m.c_str());
     }
-    uint32_t h[NCB + 1] = {};
-    if (hipEventRecord(f->ev1, st) != hipSuccess || hipMemcpyAsync(h, f->ctl, sizeof(h), hipMemcpyDeviceToHost, st) != hipSuccess ||
+    uint32_t *h = f->h_ctl();
+    if (hipEventRecord(f->ev1, st) != hipSuccess ||
+        hipMemcpyAsync(h, f->ctl, sizeof(uint32_t) * (NCB + 1), hipMemcpyDeviceToHost, st) != hipSuccess ||
         hipStreamSynchronize(st) != hipSuccess)
         return fail(NAVI_ERR_HIP, "frame: launch or readback failed");
     float ms = 0.f;
@@ -1602,13 +1611,14 @@ navi_status navi_frame_run_many(navi_frame *f, const navi_kv_view *kv, int32_t n
             return NAVI_ERR_LAUNCH;
         }
     }
-    uint32_t ctl[NCB + 1] = {}, stop = 0;
     NAVI_TRY_HIP(hipEventRecord(f->ev1, st), err, errlen);
-    NAVI_TRY_HIP(hipMemcpyAsync(codes_out, f->run_codes, static_cast<size_t>(n_frames) * NCB * sizeof(int32_t),
+    NAVI_TRY_HIP(hipMemcpyAsync(f->h_rb, f->run_codes, static_cast<size_t>(n_frames) * NCB * sizeof(int32_t),
                                 hipMemcpyDeviceToHost, st), err, errlen);
-    NAVI_TRY_HIP(hipMemcpyAsync(ctl, f->ctl, sizeof(ctl), hipMemcpyDeviceToHost, st), err, errlen);
-    NAVI_TRY_HIP(hipMemcpyAsync(&stop, f->stop, sizeof(stop), hipMemcpyDeviceToHost, st), err, errlen);
+    NAVI_TRY_HIP(hipMemcpyAsync(f->h_ctl(), f->ctl, sizeof(uint32_t) * (NCB + 1), hipMemcpyDeviceToHost, st), err, errlen);
+    NAVI_TRY_HIP(hipMemcpyAsync(f->h_stop(), f->stop, sizeof(uint32_t), hipMemcpyDeviceToHost, st), err, errlen);
     NAVI_TRY_HIP(hipStreamSynchronize(st), err, errlen);
+    std::memcpy(codes_out, f->h_rb, static_cast<size_t>(n_frames) * NCB * sizeof(int32_t));
+    const uint32_t *ctl = f->h_ctl(), stop = *f->h_stop();
     float ms = 0.f;
     (void) hipEventElapsedTime(&ms, f->ev0, f->ev1);
     if (us) *us = ms * 1000.0;

@@ -691,6 +691,7 @@ struct navi_talker {
     float *x = nullptr, *xn = nullptr, *q = nullptr, *att = nullptr, *h = nullptr, *part = nullptr, *invf = nullptr;
     size_t part_floats = 0;
     uint32_t *flag = nullptr;
+    uint32_t *h_flag = nullptr;        // pinned host copy of flag, read back with the call's last sync
     int32_t *d_ids = nullptr, *d_cids = nullptr, *d_ia = nullptr, *d_ib = nullptr, *d_ta = nullptr, *d_tb = nullptr;
     float *text_rows = nullptr, *fc1_out = nullptr, *proj = nullptr, *codec_rows = nullptr, *spk = nullptr;
     float *prefill = nullptr, *trailing = nullptr, *pad_row = nullptr, *hidden = nullptr, *logits = nullptr;
@@ -715,6 +716,7 @@ struct navi_talker {
         for (auto &g : graphs) (void) hipGraphExecDestroy(g.second);
         if (ev0) (void) hipEventDestroy(ev0);
         if (ev1) (void) hipEventDestroy(ev1);
+        if (h_flag) (void) hipHostFree(h_flag);
         for (void *p : owned) (void) hipFree(p);
     }
 };
@@ -768,15 +770,21 @@ size_t talker_part_floats(const navi_talker &t) {
     return best;
 }
 
-navi_status check_flag(navi_talker &t, const char *what, char *err, size_t errlen) {
-    uint32_t f = 0;
-    NAVI_TRY_HIP(hipMemcpyAsync(&f, t.flag, 4, hipMemcpyDeviceToHost, device_state().stream), err, errlen);
-    NAVI_TRY_HIP(hipStreamSynchronize(device_state().stream), err, errlen);
-    if (f) {
+// The f16-range flag as the stream's last copy left it in the pinned host word.
+navi_status flag_result(const navi_talker &t, const char *what, char *err, size_t errlen) {
+    if (*t.h_flag) {
         set_err(err, errlen, "talker: %s: an activation is outside the f16 range (|x| >= 65504 or NaN)", what);
         return NAVI_ERR_INVALID;
     }
     return NAVI_OK;
+}
+
+// The f16-range flag of the work enqueued so far: copied into the pinned host word on the stream
+// and read after one synchronization.
+navi_status check_flag(navi_talker &t, const char *what, char *err, size_t errlen) {
+    NAVI_TRY_HIP(hipMemcpyAsync(t.h_flag, t.flag, 4, hipMemcpyDeviceToHost, device_state().stream), err, errlen);
+    NAVI_TRY_HIP(hipStreamSynchronize(device_state().stream), err, errlen);
+    return flag_result(t, what, err, errlen);
 }
 
 } // namespace
@@ -885,7 +893,9 @@ navi_status navi_talker_create(const navi_model_params *p, const navi_tensor_ref
         }
     }
     if (hipMemcpyAsync(t->invf, invf, sizeof invf, hipMemcpyHostToDevice, s) != hipSuccess ||
-        hipEventCreate(&t->ev0) != hipSuccess || hipEventCreate(&t->ev1) != hipSuccess || hipStreamSynchronize(s) != hipSuccess) {
+        hipEventCreate(&t->ev0) != hipSuccess || hipEventCreate(&t->ev1) != hipSuccess ||
+        hipHostMalloc(reinterpret_cast<void **>(&t->h_flag), 64, hipHostMallocDefault) != hipSuccess ||
+        hipStreamSynchronize(s) != hipSuccess) {
         set_err(err, errlen, "talker: HIP setup failed");
         return fail(NAVI_ERR_HIP);
     }
@@ -1088,11 +1098,12 @@ navi_status navi_talker_prefill(navi_talker *t, const float *d_rows, int32_t n_r
                  errlen);
     NAVI_TRY_HIP(hipGetLastError(), err, errlen);
     NAVI_TRY_HIP(hipEventRecord(t->ev1, s), err, errlen);
-    NAVI_TRY_HIP(hipEventSynchronize(t->ev1), err, errlen);
+    NAVI_TRY_HIP(hipMemcpyAsync(t->h_flag, t->flag, 4, hipMemcpyDeviceToHost, s), err, errlen);
+    NAVI_TRY_HIP(hipStreamSynchronize(s), err, errlen);
     float ms = 0.f;
     NAVI_TRY_HIP(hipEventElapsedTime(&ms, t->ev0, t->ev1), err, errlen);
     t->last_ms = ms;
-    const navi_status st = check_flag(*t, "prefill", err, errlen);
+    const navi_status st = flag_result(*t, "prefill", err, errlen);
     if (st != NAVI_OK) return st;
     t->n_used = T;
     return NAVI_OK;

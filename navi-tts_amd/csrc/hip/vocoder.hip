@@ -41,6 +41,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstring>
 #include <string>
 #include <vector>
 
@@ -303,16 +304,23 @@ __global__ void __launch_bounds__(BT) k_zero_spans(const ZeroSpan *spans) {
     for (uint32_t i = threadIdx.x; i < z.n; i += BT) gst(z.p + i, 0u);
 }
 
-// The utterance position after a chunk of T frames (the last kernel of a chunk).
-__global__ void k_advance_pos(int *pos0, int T) {
-    if (threadIdx.x == 0) gst(pos0, gld(pos0) + T);
-}
-
-// pcm[t] = y[t][0]: the last conv runs on the matrix cores with its one output channel padded to
-// a 16-column tile (15 zero weight rows); this keeps column 0.
-__global__ void __launch_bounds__(BT) k_take_col0(const float *y, int T, int ld, float *pcm) {
+// The last kernel of a chunk. pcm[t] = y[t][0] for the T rows: the last conv runs on the matrix
+// cores with its one output channel padded to a 16-column tile (15 zero weight rows); this keeps
+// column 0, in device memory (the stage hook's copy) and in the caller's pinned host slot. Thread
+// 0 also moves the utterance position past the chunk's frames and copies the chunk's f16-range
+// flag into its pinned host word (every kernel that sets it ran before this one).
+__global__ void __launch_bounds__(BT) k_take_col0(const float *y, int T, int ld, float *pcm, float *pcm_host, int *pos0,
+                                                 int frames, const uint32_t *flag, uint32_t *flag_host) {
     const int t = blockIdx.x * BT + threadIdx.x;
-    if (t < T) gst(pcm + t, gld(y + static_cast<size_t>(t) * ld));
+    if (t < T) {
+        const float v = gld(y + static_cast<size_t>(t) * ld);
+        gst(pcm + t, v);
+        gst(pcm_host + t, v);
+    }
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        gst(pos0, gld(pos0) + frames);
+        gst(flag_host, gld(flag));
+    }
 }
 
 // ---- weight preparation (vocoder.hip:350-420, done here on the device) ----------------
@@ -407,8 +415,17 @@ struct navi_vocoder {
     float *pcm16 = nullptr;            // [rows][16] output of the padded final conv
     float *invf = nullptr;
     uint32_t *flag = nullptr;
+    // Pinned, coherent host slots that the kernels read and write directly: a chunk's codes (read by
+    // the RVQ front end) and its PCM (written by the last kernel), slot = the chunk's history
+    // parity, so consecutive chunks alternate and one can be handed over while the next runs; the
+    // f16-range flag word, copied there by a chunk's last kernel.
+    // (h_*: the host's addresses, dh_*: the same memory as the kernels address it)
+    int32_t *h_codes[2] = {}, *dh_codes[2] = {};
+    float *h_pcm[2] = {}, *dh_pcm[2] = {};
+    uint32_t *h_flag = nullptr, *dh_flag = nullptr;
+    void *h_buf = nullptr;
+    hipEvent_t ev_slot[2] = {};
     // activations of one chunk (time-major rows)
-    int32_t *d_codes = nullptr;
     float *lat_in = nullptr;           // RVQ rows gathered from the codebooks [T][CD]
     float *lat = nullptr;              // RVQ latent [T][CD]
     float *pre = nullptr;              // pre_conv output [T][L]
@@ -451,6 +468,9 @@ struct navi_vocoder {
         for (auto &g : graphs) (void) hipGraphExecDestroy(g.second);
         if (ev0) (void) hipEventDestroy(ev0);
         if (ev1) (void) hipEventDestroy(ev1);
+        for (hipEvent_t e : ev_slot)
+            if (e) (void) hipEventDestroy(e);
+        if (h_buf) (void) hipHostFree(h_buf);
         for (void *v : owned) (void) hipFree(v);
     }
 };
@@ -725,7 +745,8 @@ navi_status xf_rows(int epi, bool norm, const float *A, int lda, int M, int K, c
     return NAVI_OK;
 }
 
-// One chunk of T frames: codes (already in v.d_codes) -> T * samples_per_frame PCM samples in v.pcm
+// One chunk of T frames: codes (already in the pinned slot of the history parity) -> T *
+// samples_per_frame PCM samples in v.pcm and that pinned slot
 // (the stage order of decode_chunk, vocoder.hip:261-343, which is the model's).
 navi_status decode_chunk(navi_vocoder &v, int T, char *err, size_t errlen) {
     hipStream_t s = device_state().stream;
@@ -734,7 +755,7 @@ navi_status decode_chunk(navi_vocoder &v, int T, char *err, size_t errlen) {
     // RVQ front end and its two output projections, one conv gathering its rows from the codebooks
     {
         ConvArgs ra{};
-        ra.codes = v.d_codes; ra.cb0 = v.cb_first; ra.cbr = v.cb_rest; ra.nq = p.n_q; ra.cbsize = p.codebook_size;
+        ra.codes = v.dh_codes[v.parity]; ra.cb0 = v.cb_first; ra.cbr = v.cb_rest; ra.nq = p.n_q; ra.cbsize = p.codebook_size;
         ra.T = T; ra.Cin = CD;
         hipLaunchKernelGGL(k_rvq_rows, dim3((T * (CD / 4) + BT - 1) / BT), dim3(BT), 0, s, ra, v.lat_in);
     }
@@ -838,9 +859,9 @@ navi_status decode_chunk(navi_vocoder &v, int T, char *err, size_t errlen) {
         blk_in = unit_in;
     }
     VOC_TRY(run_conv(v, v.final_conv, PRO_NONE, EPI_CLAMP, blk_in, rows, ch, v.pcm16, 16, nullptr, nullptr, err, errlen));
-    hipLaunchKernelGGL(k_take_col0, dim3((rows + BT - 1) / BT), dim3(BT), 0, s, v.pcm16, rows, 16, v.pcm);
+    hipLaunchKernelGGL(k_take_col0, dim3((rows + BT - 1) / BT), dim3(BT), 0, s, v.pcm16, rows, 16, v.pcm, v.dh_pcm[v.parity],
+                       v.d_pos0, T, v.flag, v.dh_flag);
     VOC_TRY(snap(v, "pcm", v.pcm, rows, 1, err, errlen));
-    hipLaunchKernelGGL(k_advance_pos, dim3(1), dim3(64), 0, s, v.d_pos0, T);
     NAVI_TRY_HIP(hipGetLastError(), err, errlen);
     return NAVI_OK;
 }
@@ -1183,7 +1204,6 @@ navi_status navi_vocoder_create(const navi_vocoder_params *p, const navi_tensor_
     VA(v->invf, 64);
     VA(v->flag, 1);
     VA(v->d_pos0, 1);
-    VA(v->d_codes, C * p->n_q);
     VA(v->lat_in, C * CD);
     VA(v->lat, C * CD);
     VA(v->pre, C * L);
@@ -1265,9 +1285,34 @@ navi_status navi_vocoder_create(const navi_vocoder_params *p, const navi_tensor_
 #undef VB
 #undef VA
     if (hipMemcpyAsync(v->invf, invf, sizeof invf, hipMemcpyHostToDevice, s) != hipSuccess || hipEventCreate(&v->ev0) != hipSuccess ||
-        hipEventCreate(&v->ev1) != hipSuccess || hipGetLastError() != hipSuccess || hipStreamSynchronize(s) != hipSuccess) {
+        hipEventCreate(&v->ev1) != hipSuccess || hipEventCreate(&v->ev_slot[0]) != hipSuccess ||
+        hipEventCreate(&v->ev_slot[1]) != hipSuccess || hipGetLastError() != hipSuccess || hipStreamSynchronize(s) != hipSuccess) {
         set_err(err, errlen, "vocoder: HIP setup failed");
         return fail(NAVI_ERR_HIP);
+    }
+    {
+        // per slot: cmax frames of codes, then cmax frames of PCM (16-byte aligned), then the flag word
+        const size_t codes_b = (static_cast<size_t>(C) * p->n_q * 4 + 15) / 16 * 16;
+        const size_t pcm_b = (static_cast<size_t>(C) * p->samples_per_frame * 4 + 15) / 16 * 16;
+        if (hipHostMalloc(&v->h_buf, 2 * (codes_b + pcm_b) + 64, hipHostMallocCoherent) != hipSuccess) {
+            set_err(err, errlen, "vocoder: pinned staging allocation failed");
+            return fail(NAVI_ERR_HIP);
+        }
+        void *dbuf = nullptr;
+        if (hipHostGetDevicePointer(&dbuf, v->h_buf, 0) != hipSuccess) {
+            set_err(err, errlen, "vocoder: no device address for the pinned staging");
+            return fail(NAVI_ERR_HIP);
+        }
+        unsigned char *hb = static_cast<unsigned char *>(v->h_buf), *db = static_cast<unsigned char *>(dbuf);
+        for (int b = 0; b < 2; ++b) {
+            const size_t o = b * (codes_b + pcm_b);
+            v->h_codes[b] = reinterpret_cast<int32_t *>(hb + o);
+            v->dh_codes[b] = reinterpret_cast<int32_t *>(db + o);
+            v->h_pcm[b] = reinterpret_cast<float *>(hb + o + codes_b);
+            v->dh_pcm[b] = reinterpret_cast<float *>(db + o + codes_b);
+        }
+        v->h_flag = reinterpret_cast<uint32_t *>(hb + 2 * (codes_b + pcm_b));
+        v->dh_flag = reinterpret_cast<uint32_t *>(db + 2 * (codes_b + pcm_b));
     }
     *out = v;
     return NAVI_OK;
@@ -1304,23 +1349,36 @@ navi_status navi_vocoder_decode(navi_vocoder *v, const int32_t *codes, int32_t n
     hipStream_t s = device_state().stream;
     NAVI_TRY_HIP(hipMemsetAsync(v->flag, 0, 4, s), err, errlen);
     NAVI_TRY_HIP(hipEventRecord(v->ev0, s), err, errlen);
-    for (int f0 = 0; f0 < n_frames; f0 += v->cmax) {
-        const int T = std::min(v->cmax, n_frames - f0);
-        NAVI_TRY_HIP(hipMemcpyAsync(v->d_codes, codes + static_cast<size_t>(f0) * nq, static_cast<size_t>(T) * nq * 4,
-                                    hipMemcpyHostToDevice, s), err, errlen);
+    // Chunk k reads its codes from, and writes its PCM into, the pinned slot of its history parity
+    // (the parity alternates per chunk, so chunk k's slot is chunk k - 2's): before writing the
+    // slot's codes, the chunk that used it last has finished and its PCM is handed over, while
+    // chunk k - 1 still runs.
+    const int cmax = v->cmax, nch = (n_frames + cmax - 1) / cmax, b0 = v->parity;
+    auto hand_over = [&](int k) -> navi_status {
+        const int b = (b0 + k) & 1, T = std::min(cmax, n_frames - k * cmax);
+        NAVI_TRY_HIP(hipEventSynchronize(v->ev_slot[b]), err, errlen);
+        std::memcpy(pcm + static_cast<size_t>(k) * cmax * spf, v->h_pcm[b], static_cast<size_t>(T) * spf * 4);
+        return NAVI_OK;
+    };
+    *v->h_flag = 0;
+    for (int k = 0; k < nch; ++k) {
+        const int b = v->parity, f0 = k * cmax, T = std::min(cmax, n_frames - f0);
+        if (k >= 2) VOC_TRY(hand_over(k - 2));
+        std::memcpy(v->h_codes[b], codes + static_cast<size_t>(f0) * nq, static_cast<size_t>(T) * nq * 4);
         const navi_status st = run_chunk(*v, T, err, errlen);
-        if (st != NAVI_OK) return st;
-        NAVI_TRY_HIP(hipMemcpyAsync(pcm + static_cast<size_t>(f0) * spf, v->pcm, static_cast<size_t>(T) * spf * 4,
-                                    hipMemcpyDeviceToHost, s), err, errlen);
+        if (st != NAVI_OK) {
+            (void) hipStreamSynchronize(s);
+            return st;
+        }
+        NAVI_TRY_HIP(hipEventRecord(v->ev_slot[b], s), err, errlen);
     }
     NAVI_TRY_HIP(hipEventRecord(v->ev1, s), err, errlen);
-    NAVI_TRY_HIP(hipEventSynchronize(v->ev1), err, errlen);
+    NAVI_TRY_HIP(hipStreamSynchronize(s), err, errlen);
+    for (int k = std::max(0, nch - 2); k < nch; ++k) VOC_TRY(hand_over(k));
     float ms = 0.f;
     NAVI_TRY_HIP(hipEventElapsedTime(&ms, v->ev0, v->ev1), err, errlen);
     v->last_ms = ms;
-    uint32_t f = 0;
-    NAVI_TRY_HIP(hipMemcpy(&f, v->flag, 4, hipMemcpyDeviceToHost), err, errlen);
-    if (f) {
+    if (*v->h_flag) {
         set_err(err, errlen, "vocoder: an activation is outside the f16 range (|x| >= 65504 or NaN)");
         return NAVI_ERR_INVALID;
     }
