@@ -99,6 +99,33 @@ def test_bad_code_is_an_error(codec):
     assert e.value.status == abi.NAVI_ERR_INVALID
 
 
+def test_activation_outside_f16_is_an_error(codec, scratch_dir):
+    """A conv input at or above 65504 (outside f16, where the staging's hi/lo split breaks) is an
+    error, not an infinity in the PCM, also when only the third chunk of a call holds it; the next
+    call starts clean. Row 7 of the first two rest codebooks is set to 40000 in every channel, so a
+    frame whose codes 1 and 2 are both 7 sums to 80000 in the RVQ front end's rows."""
+    abi, _, _ = codec
+    W2 = abi.DeviceWeights(scratch_dir / "codec_gpu.navi", select=lambda t: t.name.startswith("codec.decoder."))
+    for q in (0, 1):
+        name = f"codec.decoder.quantizer.rvq_rest.vq.layers.{q}._codebook.codebook"
+        vq = W2.tensors[name][2][1]
+        abi.upload(W2.ptr(name) + 7 * vq * 2, np.full(vq, 40000, np.float16).view(np.uint16))
+    v = abi.Vocoder(W2, max_chunk_frames=4)
+    codes = np.random.default_rng(3).integers(0, 2048, (12, 16)).astype(np.int32)
+    codes[:, 1:3][codes[:, 1:3] == 7] = 8
+    log("vocoder f16-range flag: 8 clean frames, then 12 with the overflow in frame 9 (chunk 3 of 3)")
+    clean = v.decode(codes[:8])
+    assert np.isfinite(clean).all()
+    bad = codes.copy()
+    bad[9, 1] = bad[9, 2] = 7
+    v.reset()
+    with pytest.raises(abi.NaviError) as e:
+        v.decode(bad)
+    assert e.value.status == abi.NAVI_ERR_INVALID and "f16 range" in str(e.value)
+    v.reset()
+    assert np.array_equal(v.decode(codes[:8]), clean)
+
+
 def test_stage_hook_stages_match_oracle(codec):
     """Vocoder::set_stage_hook (vocoder.h:46-48): every stage of a chunk reaches the hook under the
     reference's stage names, in the model's order; the stages compare one by one with the oracle's
