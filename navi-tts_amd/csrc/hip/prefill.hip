@@ -649,7 +649,8 @@ struct LayerW {
 
 // xn = RMSNorm(row m of the tiled residual stream x) * w: k_resid_norm's arithmetic for one row
 // (thread i holds elements 4i .. 4i + 3, the same sum order), reading x in the tile layout.
-__global__ void __launch_bounds__(BT) k_tiled_row_norm(const float *x, int m, const float *w, float eps, float *xn, int H) {
+__global__ void __launch_bounds__(BT) k_tiled_row_norm(const float *x, int m, const float *w, float eps, float *xn, int H,
+                                                       float *xn2) {
     __shared__ float red[4];
     const int i = threadIdx.x * 4;                            // H == 4 * BT
     const f32x4_t v = ld4(x + rows::pk_a(m, i, H));
@@ -663,6 +664,7 @@ __global__ void __launch_bounds__(BT) k_tiled_row_norm(const float *x, int m, co
 #pragma unroll
     for (int j = 0; j < 4; ++j) o[j] = v[j] * scale * wv[j];
     st4(xn + i, o);
+    if (xn2) st4(xn2 + i, o);
 }
 
 } // namespace pf
@@ -1043,7 +1045,7 @@ bool prefill_layers(navi_talker &t, int T, hipStream_t s) {
     }
     // the last row: final RMSNorm (the post-norm hidden the frame takes), then the codec head
     float *last = t.xn + static_cast<size_t>(T - 1) * H;
-    hipLaunchKernelGGL(k_tiled_row_norm, dim3(1), dim3(BT), 0, s, t.x, T - 1, t.final_norm, t.eps, last, H);
+    hipLaunchKernelGGL(k_tiled_row_norm, dim3(1), dim3(BT), 0, s, t.x, T - 1, t.final_norm, t.eps, last, H, t.hidden);
     rows::launch_rows(rows::EPI_PLAIN, false, last, H, 1, H, nullptr, 0.f, t.head, t.V, nullptr, 0, nullptr, 0, t.logits, t.V,
                       t.flag, s);
     return true;
@@ -1064,9 +1066,8 @@ navi_status navi_talker_prefill(navi_talker *t, const float *d_rows, int32_t n_r
     }
     const int T = n_rows, H = t->H;
     hipStream_t s = device_state().stream;
-    NAVI_TRY_HIP(hipMemsetAsync(t->flag, 0, 4, s), err, errlen);
     NAVI_TRY_HIP(hipEventRecord(t->ev0, s), err, errlen);
-    rows::tile_rows(d_rows, T, H, t->x, s);
+    rows::tile_rows(d_rows, T, H, t->x, s, t->flag);       // also clears the f16-range flag
     // The layers and the head: a launch sequence that depends only on T (every buffer is the
     // handle's), so it can be captured once per row count as a HIP graph and replayed
     // (navi_talker_set_graphs; off by default, measured no faster than host launches).
@@ -1094,8 +1095,6 @@ navi_status navi_talker_prefill(navi_talker *t, const float *d_rows, int32_t n_r
         set_err(err, errlen, "talker: a projection shape the prefill's tiled kernels do not take");
         return NAVI_ERR_UNSUPPORTED;
     }
-    NAVI_TRY_HIP(hipMemcpyAsync(t->hidden, t->xn + static_cast<size_t>(T - 1) * H, H * 4, hipMemcpyDeviceToDevice, s), err,
-                 errlen);
     NAVI_TRY_HIP(hipGetLastError(), err, errlen);
     NAVI_TRY_HIP(hipEventRecord(t->ev1, s), err, errlen);
     NAVI_TRY_HIP(hipMemcpyAsync(t->h_flag, t->flag, 4, hipMemcpyDeviceToHost, s), err, errlen);

@@ -353,15 +353,17 @@ void tile_weights(const uint16_t *src, int n, int K, uint16_t *dst, hipStream_t 
     hipLaunchKernelGGL(k_tile_w, dim3(static_cast<unsigned>((slots + 255) / 256)), dim3(256), 0, s, src, n, K, dst);
 }
 
-// x (tile layout pk_a of width H) = the rows src [T][H]: one thread per 4 floats.
-__global__ void __launch_bounds__(256) k_tile_rows(const float *src, int T, int H, float *x) {
+// x (tile layout pk_a of width H) = the rows src [T][H]: one thread per 4 floats. clear (optional):
+// a word set to 0 by the first thread, for a sequence that starts with this launch (its flag).
+__global__ void __launch_bounds__(256) k_tile_rows(const float *src, int T, int H, float *x, uint32_t *clear) {
     const int i = blockIdx.x * 256 + threadIdx.x, m = i / (H / 4), k = 4 * (i % (H / 4));
+    if (clear && i == 0) *(NAVI_GLOBAL uint32_t *) clear = 0u;
     if (m >= T) return;
     *(NAVI_GLOBAL f32x4_t *) (x + pk_a(m, k, H)) = *(const NAVI_GLOBAL f32x4_t *) (src + static_cast<size_t>(m) * H + k);
 }
 
-void tile_rows(const float *src, int T, int H, float *x, hipStream_t s) {
-    hipLaunchKernelGGL(k_tile_rows, dim3((T * (H / 4) + 255) / 256), dim3(256), 0, s, src, T, H, x);
+void tile_rows(const float *src, int T, int H, float *x, hipStream_t s, uint32_t *clear = nullptr) {
+    hipLaunchKernelGGL(k_tile_rows, dim3((T * (H / 4) + 255) / 256), dim3(256), 0, s, src, T, H, x, clear);
 }
 
 template <int MT, int EPI, bool NORM, int NWV, int KS, int CG>

@@ -423,6 +423,9 @@ struct navi_vocoder {
     int32_t *h_codes[2] = {}, *dh_codes[2] = {};
     float *h_pcm[2] = {}, *dh_pcm[2] = {};
     uint32_t *h_flag = nullptr, *dh_flag = nullptr;
+    // The device flag is zero at the start of a call unless the previous call did not end with it
+    // read back as zero (then this call clears it first): no clearing launch on the normal path.
+    bool flag_dirty = false;
     void *h_buf = nullptr;
     hipEvent_t ev_slot[2] = {};
     // activations of one chunk (time-major rows)
@@ -1347,7 +1350,8 @@ navi_status navi_vocoder_decode(navi_vocoder *v, const int32_t *codes, int32_t n
             return NAVI_ERR_INVALID;
         }
     hipStream_t s = device_state().stream;
-    NAVI_TRY_HIP(hipMemsetAsync(v->flag, 0, 4, s), err, errlen);
+    if (v->flag_dirty) NAVI_TRY_HIP(hipMemsetAsync(v->flag, 0, 4, s), err, errlen);
+    v->flag_dirty = true;                                  // until the call ends with the flag read as zero
     NAVI_TRY_HIP(hipEventRecord(v->ev0, s), err, errlen);
     // Chunk k reads its codes from, and writes its PCM into, the pinned slot of its history parity
     // (the parity alternates per chunk, so chunk k's slot is chunk k - 2's): before writing the
@@ -1382,6 +1386,7 @@ navi_status navi_vocoder_decode(navi_vocoder *v, const int32_t *codes, int32_t n
         set_err(err, errlen, "vocoder: an activation is outside the f16 range (|x| >= 65504 or NaN)");
         return NAVI_ERR_INVALID;
     }
+    v->flag_dirty = false;
     return NAVI_OK;
 }
 
