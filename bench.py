@@ -244,10 +244,13 @@ def streaming(W, abi, talker, frame, rows, n_pre, trail, pr, pad, build_ms) -> d
     # warm-up: the first batch and full batches of both chunk sizes
     abi.synth(talker, frame, voc, prompt=prompt, seed=2, max_frames=52, sampling=s, vocoder_batch=16, first_batch=4)
     abi.synth(talker, frame, voc, prompt=prompt, seed=2, max_frames=52, sampling=s, vocoder_batch=16, first_batch=4)
-    st, pcm, _ = abi.synth(talker, frame, voc, prompt=prompt, seed=2, max_frames=240, sampling=s, vocoder_batch=16,
-                           first_batch=4)
+    # three identical utterances; the figures are those of the run with the median TTFA
+    runs = [abi.synth(talker, frame, voc, prompt=prompt, seed=2, max_frames=240, sampling=s, vocoder_batch=16,
+                      first_batch=4)[0] for _ in range(3)]
+    st = sorted(runs, key=lambda r: r.ttfa_ms)[1]
     return {"config": "configs[2]: 128 text ids prefilled (130 rows), speaker N(0,1), 240 frames, "
                       "top-k 50, T 0.9, seed 2, first vocoder batch 4 then 16",
+            "runs": 3, "ttfa_ms_each": [round(r.ttfa_ms, 2) for r in runs],
             "ttfa_ms": round(st.ttfa_ms, 2), "prompt_build_ms": round(build_ms, 3),
             # the reference's TTFA starts at the request, before the prompt rows exist
             "ttfa_with_prompt_build_ms": round(st.ttfa_ms + build_ms, 2),
