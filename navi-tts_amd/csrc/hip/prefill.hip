@@ -244,7 +244,10 @@ __global__ void __launch_bounds__(BT) k_attn_prefill_short(const float *q, uint1
     static_assert(FEW == FUSED && (!FUSED || FUSED_ROWS <= KW), "fused (the only FEW case): every key in wave 0's range");
     __shared__ float qs[2][HD], sc[2][SHORT_KEYS], red[2][NWV], opart[NWV][4][2][HD];
     __shared__ uint16_t ks[FUSED ? FUSED_ROWS : 1][HD], vs[FUSED ? FUSED_ROWS : 1][HD];
-    const int m = blockIdx.x, g = blockIdx.y, n = pos0 + m + 1;
+    // grid (kv groups, rows): blocks go out in row order from the last row (the most keys) down,
+    // every kv group of a row together, so the blocks that wait for a free slot are the shortest;
+    // and kv group g's blocks all land on XCD g (block id % 8), whose L2 then holds its keys
+    const int m = static_cast<int>(gridDim.y) - 1 - static_cast<int>(blockIdx.y), g = blockIdx.x, n = pos0 + m + 1;
     const int QD = nq * HD, KVD = nkv * HD;
     const int wv = threadIdx.x >> 6, l = threadIdx.x & 63, c = l & 15, r = l >> 4;
     u32x4_t kr[KI], vr[KI];
@@ -411,7 +414,10 @@ __global__ void __launch_bounds__(BT) k_attn_prefill_long(const float *q, const 
     __shared__ float sS[16][LDS_S];
     __shared__ __align__(16) _Float16 vt[HD][LDV];
     __shared__ float mrun[16], lrun[16], corr[16];
-    const int qt = blockIdx.x, h = blockIdx.y, g = h / (nq / nkv), r0 = 16 * qt;
+    // grid (q heads, row tiles): tiles go out from the last (the most keys) down, every head of a
+    // tile together
+    const int qt = static_cast<int>(gridDim.y) - 1 - static_cast<int>(blockIdx.y), h = blockIdx.x, g = h / (nq / nkv),
+              r0 = 16 * qt;
     const int QD = nq * HD, KVD = nkv * HD;
     const int nk = min(T, r0 + 16);
     const int w = threadIdx.x >> 6, l = threadIdx.x & 63, c = l & 15, kq = l >> 4;
@@ -1025,17 +1031,17 @@ bool prefill_layers(navi_talker &t, int T, hipStream_t s) {
         if (T <= FUSED_ROWS) {         // the q/k norms, RoPE and K/V store inside the attention
             if (!rows::launch_rows_pk(rows::EPI_PLAIN, true, t.x, T, H, w.ln1, t.eps, w.qkv_t, QKVW, t.part, QKVW, t.flag, s))
                 return false;
-            hipLaunchKernelGGL((k_attn_prefill_short<true, true>), dim3(T, t.NKV), dim3(BT), 0, s, nullptr, t.kk[l],
+            hipLaunchKernelGGL((k_attn_prefill_short<true, true>), dim3(t.NKV, T), dim3(BT), 0, s, nullptr, t.kk[l],
                                t.vv[l], t.NQ, t.NKV, 0, scale, t.att, t.QD, HeadNorm{t.part, w.qn, w.kn, t.invf, t.eps});
         } else {                       // ... or in the q|k|v projection's epilogue
             const rows::HeadOut ho{w.qn, w.kn, t.invf, t.q, t.kk[l], t.vv[l], t.NQ, t.NKV, 0};
             if (!rows::launch_rows_pk(rows::EPI_QKV, true, t.x, T, H, w.ln1, t.eps, w.qkv_t, QKVW, nullptr, 0, t.flag, s, ho))
                 return false;
             if (T <= SHORT_KEYS)
-                hipLaunchKernelGGL(k_attn_prefill_short<false>, dim3(T, t.NKV), dim3(BT), 0, s, t.q, t.kk[l], t.vv[l], t.NQ,
+                hipLaunchKernelGGL(k_attn_prefill_short<false>, dim3(t.NKV, T), dim3(BT), 0, s, t.q, t.kk[l], t.vv[l], t.NQ,
                                    t.NKV, 0, scale, t.att, t.QD, HeadNorm{});
             else
-                hipLaunchKernelGGL(k_attn_prefill_long, dim3((T + 15) / 16, t.NQ), dim3(BT), 0, s, t.q, t.kk[l], t.vv[l],
+                hipLaunchKernelGGL(k_attn_prefill_long, dim3(t.NQ, (T + 15) / 16), dim3(BT), 0, s, t.q, t.kk[l], t.vv[l],
                                    t.NQ, t.NKV, T, scale, t.att, t.QD);
         }
         if (!rows::launch_rows_pk(rows::EPI_RESID, false, t.att, T, t.QD, nullptr, 0.f, w.o_t, H, t.x, 0, t.flag, s) ||
