@@ -126,6 +126,19 @@ __device__ __forceinline__ void carry_rows(const float *hist, const float *x, in
     }
 }
 
+// The (column block, row tile) of this block in a gridDim.x x gridDim.y tile grid, remapped for
+// the round-robin dispatch of block ids over the 8 XCDs (block x + gridDim.x y goes to XCD
+// (x + gridDim.x y) % 8): XCD k's blocks take a contiguous run of the tiles in row-major order, so
+// the column blocks of a row tile, which read the same input window, share one L2.
+__device__ __forceinline__ void xcd_tile(int &col, int &row) {
+    const int ncol = static_cast<int>(gridDim.x), n = ncol * static_cast<int>(gridDim.y);
+    const int id = static_cast<int>(blockIdx.x) + ncol * static_cast<int>(blockIdx.y);
+    const int k = id & 7, slot = id >> 3, q = n >> 3, r = n & 7;
+    const int tile = k * q + min(k, r) + slot;           // XCD k holds q + (k < r) ids
+    col = tile % ncol;
+    row = tile / ncol;
+}
+
 // Four input channels ci..ci+3 of the RVQ front end at frame t: the semantic codebook's row, or
 // the rest codebooks' rows summed in f32 in codebook order (k_rvq, vocoder.hip:125-143).
 // Every code load first (indices clamped into the frame's row, so all of them run at once), then
@@ -167,8 +180,10 @@ __global__ void __launch_bounds__(BT) k_conv_mfma(ConvArgs a) {
     __shared__ __align__(16) _Float16 whi[WROWS][LDW];
     __shared__ __align__(16) _Float16 wlo[WROWS][LDW];
     const int wv = threadIdx.x >> 6, l = threadIdx.x & 63;
-    const int n0 = blockIdx.x * 64 + wv * 16;
-    const int t0 = blockIdx.y * (MT * 16);
+    int tcol, trow;
+    xcd_tile(tcol, trow);
+    const int n0 = tcol * 64 + wv * 16;
+    const int t0 = trow * (MT * 16);
     const int phase = blockIdx.z % a.phases, split = blockIdx.z / a.phases;
     const int cb = split * a.cps, ce = min(a.Cin, cb + a.cps);
     const int H = (K - 1) * a.dil, rows = MT * 16 + H;
@@ -359,7 +374,9 @@ __global__ void __launch_bounds__(BT) k_conv_wide(ConvArgs a) {
     const int wv = threadIdx.x >> 6, l = threadIdx.x & 63;
     const int wr = BM == 128 ? 32 * wv : 32 * (wv >> 1), wc = BM == 128 ? 0 : (BN / 2) * (wv & 1);
     const int S = SM == 1 ? static_cast<int>(gridDim.z) / a.phases : 1, sp = SM == 1 ? static_cast<int>(blockIdx.z) % S : 0;
-    const int n0 = blockIdx.x * BN, t0 = blockIdx.y * BM, phase = SM == 1 ? static_cast<int>(blockIdx.z) / S : blockIdx.z;
+    int tcol, trow;
+    xcd_tile(tcol, trow);
+    const int n0 = tcol * BN, t0 = trow * BM, phase = SM == 1 ? static_cast<int>(blockIdx.z) / S : blockIdx.z;
     const int cbeg = SM == 1 ? sp * a.cps : 0, cend = SM == 1 ? min(a.Cin, cbeg + a.cps) : a.Cin;
     const int H = (K - 1) * a.dil, rows = BM + H;
     // A staging: 8 float4 per window row, thread -> rows (tid / 8) + 32 it, channels 4 (tid % 8);
