@@ -410,7 +410,8 @@ bool launch_rows_pk(int epi, bool norm, const float *A, int M, int K, const floa
         return true;
     }
     if (epi == EPI_RESID && K == 2048) {
-        if (wide) launch_pk<1, EPI_RESID, false, 16, 4, 4>(M, N, ra, s);
+        if (wide && M <= 96) launch_pk<1, EPI_RESID, false, 16, 4, 2>(M, N, ra, s);   // more blocks where they are few
+        else if (wide) launch_pk<1, EPI_RESID, false, 16, 4, 4>(M, N, ra, s);
         else launch_pk<1, EPI_RESID, false, 16, 4, 1>(M, N, ra, s);
         return true;
     }
